@@ -1,0 +1,335 @@
+"""Pins the CPU oracle before anything is compared against it.
+
+Every check here is independent of the oracle's own code: IEEE conversions
+against numpy / torch, hand-computed block vectors, exact integer brute
+force, the reference's own argmax tie vectors (engine/src/engine.rs:3086-3128)
+and the closed form of the gate/up epilogue (engine/src/qwen35.rs:7002-7007).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+
+# ---------------------------------------------------------------- conversions
+def test_f16_decode_matches_numpy_exhaustive():
+    L = O.lib()
+    bits = np.arange(65536, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = np.array([L.o_f16_to_f32(int(b)) for b in bits], dtype=np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_f16_encode_matches_numpy():
+    L = O.lib()
+    rng = np.random.default_rng(1)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 20000),
+        np.array([0.0, -0.0, 65504.0, 65519.0, 65520.0, 1e9, -1e9, 6.1e-5, 5.96e-8, 2.98e-8, 2.99e-8,
+                  1.0 / 127, 0.02 / 127, np.inf, -np.inf], dtype=np.float32),
+        # exact ties between two f16 neighbours (round half to even)
+        (np.arange(1024, 1100, dtype=np.float32) + np.float32(0.5)) * np.float32(2.0 ** -10),
+    ]).astype(np.float32)
+    with np.errstate(over="ignore"):
+        ref = vals.astype(np.float16).view(np.uint16)
+    got = np.array([L.o_f32_to_f16(float(v)) for v in vals], dtype=np.uint16)
+    assert np.array_equal(got, ref)
+
+
+def test_bf16_encode_matches_torch():
+    L = O.lib()
+    rng = np.random.default_rng(2)
+    vals = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-30, 30, 20000),
+        np.array([0.0, -0.0, np.inf, -np.inf, 3.0e38, 1e-40, 21.03, 20.97], dtype=np.float32),
+        # exact ties: 1 + (2k+1) * 2^-8
+        (1.0 + (2 * np.arange(0, 64, dtype=np.float32) + 1) * np.float32(2.0 ** -8)).astype(np.float32),
+    ]).astype(np.float32)
+    ref = torch.from_numpy(vals).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got_c = np.array([L.o_f32_to_bf16(float(v)) for v in vals], dtype=np.uint16)
+    got_np = O.f32_to_bf16_bits(vals)
+    assert np.array_equal(got_c, ref)
+    assert np.array_equal(got_np, ref)
+
+
+def test_randn_is_seeded_normal():
+    a = O.randn(0, 1, 1.0, (1 << 20,))
+    b = O.randn(0, 1, 1.0, (1 << 20,))
+    c = O.randn(0, 2, 1.0, (1 << 20,))
+    assert np.array_equal(a, b)
+    assert not np.array_equal(a, c)
+    assert abs(float(a.mean())) < 5e-3 and abs(float(a.std()) - 1.0) < 5e-3
+    w = O.randn(0, 1, 0.02, (4096,))
+    assert abs(float(w.std()) - 0.02) < 2e-3
+
+
+# ---------------------------------------------------------------- Q8_0
+def test_q8_0_zero_block():
+    blk = O.quantize(O.Q8_0, np.zeros((1, 32), np.float32))
+    assert blk.shape == (1, 34) and not blk.any()
+    assert not O.dequantize(O.Q8_0, blk, 1, 32).any()
+
+
+def test_q8_0_exact_power_of_two_block():
+    # d = 1/128 is exact in f16; x = q*d for q in [-127, 127] survives exactly
+    q = np.array([127, -127, 0, 1, -1, 64, -64, 100] + list(range(-12, 12)), dtype=np.int8)
+    x = (q.astype(np.float32) / np.float32(128.0)).reshape(1, 32)
+    blk = O.quantize(O.Q8_0, x)
+    assert blk[0, 0] == 0x00 and blk[0, 1] == 0x20  # f16(2^-7) = 0x2000 little endian
+    assert np.array_equal(blk[0, 2:].view(np.int8), q)
+    assert np.array_equal(O.dequantize(O.Q8_0, blk, 1, 32), x)
+
+
+def test_q8_0_rounds_half_away_from_zero():
+    # amax = 127/128 -> d = 1/128, id = 128: x*id = +-2.5 -> +-3 (not banker's 2)
+    x = np.zeros((1, 32), np.float32)
+    x[0, 0] = 127.0 / 128.0
+    x[0, 1] = 2.5 / 128.0
+    x[0, 2] = -2.5 / 128.0
+    x[0, 3] = 3.5 / 128.0
+    x[0, 4] = 0.5 / 128.0
+    q = O.quantize(O.Q8_0, x)[0, 2:].view(np.int8)
+    assert list(q[:5]) == [127, 3, -3, 4, 1]
+
+
+def test_q8_0_error_bound():
+    w = O.randn(0, 7, 0.02, (64, 1024))
+    blk = O.quantize(O.Q8_0, w)
+    deq = O.dequantize(O.Q8_0, blk, 64, 1024)
+    amax = np.abs(w.reshape(64, 32, 32)).max(axis=2, keepdims=True)
+    d = amax / 127.0
+    err = np.abs(w.reshape(64, 32, 32) - deq.reshape(64, 32, 32))
+    # rounding to the level (d/2) plus 127 levels of the f16 rounding of d
+    assert np.all(err <= d * (0.5 + 127 * 2.0 ** -11) + 1e-12)
+
+
+# ---------------------------------------------------------------- Q4_K
+def _pack_k4(sc, mn):
+    """GGML k4 packing of eight 6-bit (scale, min) pairs into 12 bytes."""
+    s = [0] * 12
+    for j in range(8):
+        if j < 4:
+            s[j] |= sc[j] & 63
+            s[j + 4] |= mn[j] & 63
+        else:
+            s[j + 4] |= (sc[j] & 0xF) | ((mn[j] & 0xF) << 4)
+            s[j - 4] |= (sc[j] >> 4) << 6
+            s[j] |= (mn[j] >> 4) << 6
+    return np.array(s, dtype=np.uint8)
+
+
+def test_q4_k_scale_min_pack_roundtrip_all_pairs():
+    rng = np.random.default_rng(3)
+    for _ in range(2000):
+        sc = rng.integers(0, 64, 8)
+        mn = rng.integers(0, 64, 8)
+        packed = _pack_k4(sc, mn)
+        for j in range(8):
+            assert O.get_scale_min_k4(j, packed) == (sc[j], mn[j])
+    # every value in every slot
+    for v in range(64):
+        packed = _pack_k4([v] * 8, [63 - v] * 8)
+        for j in range(8):
+            assert O.get_scale_min_k4(j, packed) == (v, 63 - v)
+
+
+def _q4k_block(d, dmin, sc, mn, qs):
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([d], np.float16).view(np.uint8)
+    blk[2:4] = np.array([dmin], np.float16).view(np.uint8)
+    blk[4:16] = _pack_k4(sc, mn)
+    blk[16:] = qs
+    return blk
+
+
+def test_q4_k_dequant_known_answers():
+    # d = 0.5, dmin = 0.25; sub-block scales 1..8, mins 0,2,4,..14 (6-bit)
+    sc = [1, 2, 3, 4, 5, 6, 7, 63]
+    mn = [0, 2, 4, 6, 8, 10, 12, 63]
+    qs = np.zeros(128, np.uint8)
+    qs[0] = 0x7A    # element 0: low nibble 10 (sub-block 0); element 32: high 7 (sub-block 1)
+    qs[31] = 0xF1   # element 31: 1 (sb 0); element 63: 15 (sb 1)
+    qs[32] = 0x23   # element 64: 3 (sb 2); element 96: 2 (sb 3)
+    qs[127] = 0x9F  # element 223: 15 (sb 6); element 255: 9 (sb 7)
+    y = O.dequantize(O.Q4_K, _q4k_block(0.5, 0.25, sc, mn, qs).reshape(1, 144), 1, 256)[0]
+    assert y[0] == 0.5 * 1 * 10 - 0.25 * 0    # 5.0
+    assert y[31] == 0.5 * 1 * 1 - 0.0          # 0.5
+    assert y[32] == 0.5 * 2 * 7 - 0.25 * 2    # 6.5
+    assert y[63] == 0.5 * 2 * 15 - 0.5        # 14.5
+    assert y[64] == 0.5 * 3 * 3 - 0.25 * 4    # 3.5
+    assert y[96] == 0.5 * 4 * 2 - 0.25 * 6    # 2.5
+    assert y[223] == 0.5 * 7 * 15 - 0.25 * 12  # 49.5
+    assert y[255] == 0.5 * 63 * 9 - 0.25 * 63  # 267.75
+    assert y[1] == 0.0 and y[33] == -0.5 and y[65] == -1.0 and y[254] == -15.75
+    assert y[224] == -15.75  # sb 7, nibble 0
+
+
+def test_q4_k_dequant_is_exact_f32_formula_for_random_bytes():
+    # all byte patterns allowed: values are d*sc*q - dmin*m computed with a
+    # single rounding (d*sc*q is exact: 11 + 6 + 4 significant bits)
+    rng = np.random.default_rng(4)
+    n = 64
+    raw = rng.integers(0, 256, (n, 144), dtype=np.uint8)
+    d = np.abs(rng.standard_normal(n)).astype(np.float16) * np.float16(0.01)
+    dm = np.abs(rng.standard_normal(n)).astype(np.float16) * np.float16(0.01)
+    raw[:, 0:2] = d.reshape(n, 1).view(np.uint8)
+    raw[:, 2:4] = dm.reshape(n, 1).view(np.uint8)
+    y = O.dequantize(O.Q4_K, raw, n, 256)
+    for r in range(n):
+        for sb in range(8):
+            s, m = O.get_scale_min_k4(sb, raw[r, 4:16])
+            chunk = raw[r, 16 + 32 * (sb // 2): 16 + 32 * (sb // 2) + 32]
+            q = (chunk & 0xF) if sb % 2 == 0 else (chunk >> 4)
+            exact = float(d[r]) * s * q.astype(np.float64) - float(dm[r]) * m  # f64, then one rounding
+            assert np.array_equal(y[r, 32 * sb: 32 * sb + 32], exact.astype(np.float32))
+
+
+def test_q4_k_quantize_invariants():
+    # make_qkx1_quants bit-parity with candle is unpinned; check what any
+    # faithful Q4_K quantizer must satisfy
+    w = O.randn(0, 9, 0.02, (32, 1024))
+    blk = O.quantize(O.Q4_K, w)
+    deq = O.dequantize(O.Q4_K, blk, 32, 1024)
+    rel = np.sqrt(((w - deq) ** 2).mean()) / np.sqrt((w ** 2).mean())
+    assert rel < 0.12, rel  # 4-bit levels over a +-3 sigma range
+    # monotone within a sub-block (shared scale and min)
+    wb, db = w.reshape(-1, 32), deq.reshape(-1, 32)
+    for i in range(0, wb.shape[0], 7):
+        o = np.argsort(wb[i], kind="stable")
+        assert np.all(np.diff(db[i][o]) >= 0)
+    # constant block -> all zero (make_qkx1_quants returns (0, 0) for max == min)
+    c = O.quantize(O.Q4_K, np.full((1, 256), 0.25, np.float32))
+    assert not O.dequantize(O.Q4_K, c, 1, 256).any()
+
+
+def test_q8_k_invariants():
+    x = O.randn(0, 11, 1.0, (1024,))
+    x[5] = -7.5  # first element of largest |x|: iscale = -128/x[5], so its level is -128
+    x[6] = 7.5   # same magnitude, other sign: 128 -> clamped to 127
+    blk = O.quantize_q8_k(x).reshape(4, 292)
+    for b in range(4):
+        d = blk[b, 0:4].view(np.float32)[0]
+        qs = blk[b, 4:260].view(np.int8).astype(np.int32)
+        bs = blk[b, 260:292].view(np.int16).astype(np.int32)
+        xs = x[256 * b: 256 * (b + 1)]
+        imax = int(np.argmax(np.abs(xs)))
+        assert qs[imax] == -128
+        assert np.array_equal(bs, qs.reshape(16, 16).sum(axis=1))
+        ok = qs != 127  # a level clamped at 127 may sit one step off
+        assert np.all(np.abs(qs * np.float64(d) - xs)[ok] <= abs(d) * 0.5 + 1e-7)
+    assert blk[0, 4 + 5].view(np.int8) == -128
+    assert blk[0, 4 + 6].view(np.int8) == 127
+
+
+# ---------------------------------------------------------------- dots
+def test_vec_dot_q8_0_exact_integer_brute_force():
+    rng = np.random.default_rng(5)
+    k = 512
+    w = O.quantize(O.Q8_0, O.randn(1, 1, 0.02, (1, k)))[0]
+    xq = O.quantize_q8_0_row(O.randn(1, 2, 1.0, (k,)))
+    got = O.lib().o_vec_dot_q8_0_q8_0(k, w.ctypes.data, xq.ctypes.data)
+    want = 0.0
+    for b in range(k // 32):
+        wq = w[34 * b + 2: 34 * b + 34].view(np.int8).astype(np.int64)
+        xqq = xq[34 * b + 2: 34 * b + 34].view(np.int8).astype(np.int64)
+        dw = float(w[34 * b: 34 * b + 2].view(np.float16)[0])
+        dx = float(xq[34 * b: 34 * b + 2].view(np.float16)[0])
+        want += int((wq * xqq).sum()) * dw * dx
+    assert abs(got - want) <= 1e-5 * abs(want) + 1e-6
+    del rng
+
+
+def test_vec_dot_q4_k_equals_dequantized_dot():
+    # Q4_K . Q8_K == dequant(W) . dequant(Q8_K(x)) exactly in real arithmetic
+    k = 1024
+    w = O.quantize(O.Q4_K, O.randn(2, 1, 0.02, (1, k)))[0]
+    x = O.randn(2, 2, 1.0, (k,))
+    xq = O.quantize_q8_k(x)
+    got = O.lib().o_vec_dot_q4_k_q8_k(k, w.ctypes.data, xq.ctypes.data)
+    wd = O.dequantize(O.Q4_K, w, 1, k)[0].astype(np.float64)
+    xd = np.concatenate([
+        xq[292 * b + 4: 292 * b + 260].view(np.int8).astype(np.float64) * float(xq[292 * b: 292 * b + 4].view(np.float32)[0])
+        for b in range(k // 256)])
+    want = float(wd @ xd)
+    assert abs(got - want) <= 2e-5 * (np.abs(wd) @ np.abs(xd))
+
+
+# ---------------------------------------------------------------- matmul
+@pytest.mark.parametrize("qtype,k", [(O.Q8_0, 64), (O.Q4_K, 512)])
+def test_matmul_dequant_mode_brute_force(qtype, k):
+    n, m = 24, 3
+    w = O.quantize(qtype, O.randn(3, 1, 0.02, (n, k)))
+    x = O.randn(3, 2, 1.0, (m, k))
+    y = O.matmul(qtype, w, n, k, x, O.MODE_DEQUANT_F32)
+    wd = O.dequantize(qtype, w, n, k).astype(np.float64)
+    for i in range(m):
+        for j in range(n):
+            s = math.fsum(float(a) * float(b) for a, b in zip(x[i], wd[j]))
+            assert y[i, j] == np.float32(s)
+
+
+@pytest.mark.parametrize("qtype,k", [(O.Q8_0, 1024), (O.Q4_K, 1024)])
+def test_matmul_q8act_close_to_dequant(qtype, k):
+    n, m = 96, 2
+    w = O.quantize(qtype, O.randn(4, 1, 0.02, (n, k)))
+    x = O.randn(4, 2, 1.0, (m, k))
+    yd = O.matmul(qtype, w, n, k, x, O.MODE_DEQUANT_F32)
+    yq = O.matmul(qtype, w, n, k, x, O.MODE_Q8ACT)
+    for i in range(m):
+        nrm = np.linalg.norm(yd[i])
+        err = np.abs(yq[i] - yd[i]).max() / nrm
+        assert 1e-6 < err < 5e-3, err  # the activation rounding: not zero, not large
+
+
+@pytest.mark.parametrize("qtype,k", [(O.Q8_0, 1024), (O.Q4_K, 2048)])
+def test_baseline_avx2_matches_scalar_q8act(qtype, k):
+    n, m = 200, 3
+    w = O.quantize(qtype, O.randn(5, 1, 0.02, (n, k)))
+    x = O.randn(5, 2, 1.0, (m, k))
+    ys = O.matmul(qtype, w, n, k, x, O.MODE_Q8ACT)
+    yb = O.baseline_matmul(qtype, w, n, k, x)
+    for i in range(m):
+        assert np.abs(yb[i] - ys[i]).max() <= 1e-5 * np.linalg.norm(ys[i])
+
+
+# ---------------------------------------------------------------- epilogue + argmax
+def test_gate_up_silu_closed_form():
+    rng = np.random.default_rng(6)
+    h = 4096
+    y = (rng.standard_normal((2, 2 * h)) * 3).astype(np.float32)
+    y[0, :5] = [0.0, -100.0, 100.0, 1e-30, -0.0]
+    y[0, h:h + 5] = [3.0, 2.0, 0.5, 1.0, 7.0]
+    got = O.bf16_bits_to_f32(O.gate_up_silu(y))
+    g = O.bf16_round(y[:, :h]).astype(np.float64)
+    u = O.bf16_round(y[:, h:]).astype(np.float64)
+    want = O.bf16_round((g / (1.0 + np.exp(-g)) * u).astype(np.float32))
+    assert got[0, 0] == 0.0 and got[0, 1] == 0.0 and got[0, 2] == 50.0
+    # f32 silu vs f64 silu: equal except on a bf16 rounding boundary (<= 1 ulp)
+    diff = np.abs(got - want)
+    ulp = np.abs(want) * 2.0 ** -7 + 1e-38
+    assert np.all(diff <= ulp)
+    assert (diff == 0).mean() > 0.995
+
+
+def test_argmax_reference_tie_vectors():
+    # engine/src/engine.rs:3086-3128 n2_greedy_tie_rule_matches_argmax
+    V = 248_320
+    bf = lambda v: O.bf16_round(np.array([v], np.float32))[0]
+    data = np.full(3 * V, bf(-2.5), np.float32)
+    data[1_000] = bf(21.0)
+    data[200_000] = bf(21.0)
+    data[V + 5] = bf(21.03)
+    data[V + 7] = bf(20.97)
+    data[2 * V + 42] = bf(30.5)
+    data[2 * V + 4_242] = bf(30.5)
+    data[2 * V + 248_000] = bf(30.5)
+    assert data[V + 5] == data[V + 7]
+    assert list(O.argmax_rows(data.reshape(3, V))) == [1000, 5, 42]
+    assert O.argmax_rows(np.array([np.nan, 1.0, 1.0], np.float32))[0] == 1
+    assert O.argmax_rows(np.full(4, -np.inf, np.float32))[0] == 0
+    assert O.lib().o_argmax(None, 0) == 0
