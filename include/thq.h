@@ -1,0 +1,158 @@
+/*
+ * thq.h — C ABI of the MI355X block-quantized matmul library (libthq.so).
+ *
+ * This is the drop-in boundary for token-horizon's quantized projection path:
+ * the GGUF Q8_0 / Q4_K weight x activation GEMV/GEMM that the engine runs for
+ * every Qwen-class projection, the fused gate/up MLP projection and the LM
+ * head (including the speculative-decode verify step).
+ *
+ * Conventions
+ *  - Plain C: pointers, sizes, enums.  No torch or HIP types cross the ABI;
+ *    `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *  - Device pointers are marked *_dev.  Calls are stream-ordered and
+ *    asynchronous unless stated otherwise.
+ *  - Every function returns THQ_OK (0) or a negative error code; the message
+ *    of the last failure on the calling thread is thq_last_error().  No C++
+ *    exception ever crosses the ABI.
+ *  - Weights are immutable after creation and may be shared by any number of
+ *    concurrent calls.  Calls on distinct streams are re-entrant, except that
+ *    calls sharing one context's workspace (see thq_matmul) must be ordered
+ *    on one stream.
+ *  - W is [N, K] row-major (row n = output feature n), exactly the GGUF
+ *    tensor layout QTensor::data() returns.  y[m, n] = sum_k x[m, k] * W[n, k].
+ */
+#ifndef THQ_H
+#define THQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- enums ---- */
+
+/* GGML type ids, as stored in GGUF files.
+ * Replaces candle-core's GgmlDType (Q8_0, Q4K) that QTensor::dtype() returns
+ * on the path engine/src/model.rs:551-562 -> quantized_qwen3::ModelWeights. */
+typedef enum thq_dtype {
+    THQ_Q8_0 = 8,  /* 32 weights / 34 B: f16 d, i8 qs[32]                        */
+    THQ_Q4_K = 12  /* 256 weights / 144 B: f16 d, f16 dmin, u8 scales[12], u8 qs[128] */
+} thq_dtype;
+
+/* activation / output element types */
+typedef enum thq_act {
+    THQ_ACT_F32 = 0,
+    THQ_ACT_BF16 = 1
+} thq_act;
+
+/* thq_matmul flags */
+#define THQ_MODE_DEQUANT_F32 0u /* y = x . dequant(W)^T, f32 accumulation (default)  */
+#define THQ_MODE_EXACT_W 0x10u  /* never round dequantized weights to bf16 on MFMA   */
+
+/* error codes */
+#define THQ_OK 0
+#define THQ_EINVAL (-1)       /* null pointer, bad enum, bad flag            */
+#define THQ_ESHAPE (-2)       /* K not a multiple of the block, dims mismatch */
+#define THQ_EDTYPE (-3)       /* unsupported dtype combination                */
+#define THQ_EALIGN (-4)       /* device pointer alignment the call requires   */
+#define THQ_EHIP (-5)         /* HIP runtime error                            */
+#define THQ_ENOMEM (-6)       /* device allocation failed                     */
+
+typedef struct thq_ctx thq_ctx;
+typedef struct thq_weight thq_weight;
+
+/* ---- context ---- */
+
+/* One context per device: owns the device's workspace and kernel state.
+ * Replaces the process-global pipeline/OnceLock state of the reference's ops
+ * (engine/src/quant_kernel.rs:2980-2987, 3008-3038) and candle's Device. */
+int thq_init(int device, thq_ctx** out);
+void thq_destroy(thq_ctx* ctx);
+
+/* Message of the last failure on the calling thread ("" if none). */
+const char* thq_last_error(void);
+
+/* Library version string. */
+const char* thq_version(void);
+
+/* ---- weights ---- */
+
+/* Copy GGUF block bytes (host memory, [N][K/bs] blocks row-major, exactly
+ * QTensor::data()) to the device.  The library may repack on device; the
+ * handle owns its device memory.  Synchronous.
+ * Replaces candle's QTensor::new / QMatMul::from_arc
+ * (reached from engine/src/model.rs:551-562). */
+int thq_weight_upload(thq_ctx* ctx, thq_dtype dtype, const void* host_blocks, int64_t n, int64_t k,
+                      thq_weight** out);
+
+/* As thq_weight_upload, from GGUF block bytes already in device memory. */
+int thq_weight_from_device(thq_ctx* ctx, thq_dtype dtype, const void* dev_blocks, int64_t n, int64_t k,
+                           void* stream, thq_weight** out);
+
+/* Quantize an f32 [N, K] device matrix to `dtype` on the device, with the
+ * same rounding rules as candle's CPU quantizer (BlockQ8_0::from_float,
+ * BlockQ4K::from_float).  Replaces QTensor::quantize. */
+int thq_quantize(thq_ctx* ctx, thq_dtype dtype, const float* w_dev, int64_t n, int64_t k, void* stream,
+                 thq_weight** out);
+
+/* Row-concatenate weights of one dtype and K: QKV = [q; k; v], gate|up =
+ * [gate; up].  Replaces QLin fusion (engine/src/qwen35.rs:1581-1621 fuse_lins). */
+int thq_weight_fuse(thq_ctx* ctx, const thq_weight* const* parts, int nparts, thq_weight** out);
+
+void thq_weight_free(thq_weight* w);
+
+/* Shape / dtype / GGUF byte size of a weight. */
+int thq_weight_info(const thq_weight* w, thq_dtype* dtype, int64_t* n, int64_t* k, size_t* gguf_bytes);
+
+/* Copy the GGUF block bytes back to host memory (QTensor::data()).  Synchronous. */
+int thq_weight_download(const thq_weight* w, void* host_blocks);
+
+/* ---- compute ---- */
+
+/* Exact f32 dequantization, out_dev [N, K] (QTensor::dequantize). Bit-exact
+ * with candle's BlockQ8_0/BlockQ4K::to_float. */
+int thq_dequantize(thq_ctx* ctx, const thq_weight* w, float* out_dev, void* stream);
+
+/* y[M, N] = x[M, K] . W^T with f32 accumulation.
+ * Replaces QMatMul::forward ([ext] candle-core 0.11 quantized/mod.rs, called
+ * for every projection by quantized_qwen3) and the engine's routed projection
+ * QLin::linear_ps (engine/src/qwen35.rs:398-617).  Routes by M internally:
+ *   M == 1     decode GEMV (exact dequantized weights)
+ *   M >= 2     MFMA GEMM; weights are rounded to bf16 on the MFMA path unless
+ *              THQ_MODE_EXACT_W (or Q8_0 with M <= 64), activations bf16.
+ *   x f32 with M >= 2 runs an exact f32 path.
+ * Inputs: x_dev [M, K] of x_type, y_dev [M, N] of y_type, both contiguous.
+ * M == 0 is a no-op.  Errors: THQ_ESHAPE for K mismatch, THQ_EINVAL for
+ * null pointers. */
+int thq_matmul(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m, void* y_dev,
+               thq_act y_type, uint32_t flags, void* stream);
+
+/* Fused gate/up projection: `fused` = [gate; up] (2H rows).  y[M, H] =
+ * bf16( silu(bf16(g)) * bf16(u) ) with silu in f32, g = x.gate^T, u = x.up^T.
+ * Replaces QLin::gate_up_act_ps (engine/src/qwen35.rs:711-884) and its kernel
+ * epilogue (engine/src/quant_kernel.rs:2922-2926). y_type must be BF16 or F32
+ * (F32 holds the same bf16-rounded values). */
+int thq_gate_up_silu(thq_ctx* ctx, const thq_weight* fused, const void* x_dev, thq_act x_type, int64_t m,
+                     void* y_dev, thq_act y_type, uint32_t flags, void* stream);
+
+/* LM head + per-row greedy argmax.  logits_dev [M, N] f32 may be NULL (a
+ * context workspace is used).  idx_dev [M] u32.  Weights are never rounded
+ * (exact dequantized values), so the argmax follows the logits computed in
+ * f32.  Tie rule of engine/src/engine.rs:1891-1898: lowest index among equal
+ * maxima, NaN never selected, a row of -inf/NaN gives 0.
+ * Replaces the verify consumer `logits.argmax(D::Minus1)`
+ * (engine/src/engine.rs:1086-1087, 2438-2440) fed by the LM head
+ * (engine/src/qwen35.rs:5202-5212). */
+int thq_matmul_argmax(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m,
+                      float* logits_dev, uint32_t* idx_dev, uint32_t flags, void* stream);
+
+/* Per-row argmax of an f32 [M, N] device matrix, same tie rule
+ * (candle Tensor::argmax(D::Minus1) / engine.rs greedy_argmax). */
+int thq_argmax(thq_ctx* ctx, const float* v_dev, int64_t m, int64_t n, uint32_t* idx_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* THQ_H */

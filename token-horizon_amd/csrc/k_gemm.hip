@@ -1,0 +1,367 @@
+// k_gemm.hip — prefill / speculative-verify GEMM for gfx950:
+// y[M, N] = x[M, K] (bf16) . W[N, K]^T with W in GGUF Q4_K or Q8_0 blocks.
+//
+// Role: the m > 8 projections of the reference (AffineQpf / AffineQmppPrefill,
+// engine/src/quant_kernel.rs:3740-5095, routed by pf_route :5117) over GGUF
+// weights; fused gate/up with the silu(gate)*up epilogue
+// (engine/src/quant_kernel.rs:2922-2926).
+//
+// Tiling: block tile BM x 128 (N) x 64 (K), 4 waves as 2 (M) x 2 (N), wave
+// tile (BM/2) x 64 made of 32x32 v_mfma_f32_32x32x16_bf16 tiles.  Each K step
+// the block dequantizes a 128 x 64 W tile into LDS as bf16 (one 16-32 B
+// vector of packed weights per thread) while the MFMAs consume the previous
+// tile: two LDS buffers, one barrier per K step.
+//
+// Two weight modes:
+//   rounded  W tile = bf16(d*sc*q - dmin*m)         (Q4_K, Q8_0; large M)
+//   exact    W tile = bf16(q) (exact for |q| <= 255) and the f32 block scale
+//            is applied to each 32-wide partial in registers (Q8_0), so the
+//            result carries no weight rounding (LM head / argmax).
+// Split-K: grid.z splits write f32 partials that k_split_reduce sums in a
+// fixed order (deterministic), applying the same epilogue.
+#include "thq_dev.hpp"
+#include "thq_kernels.hpp"
+
+namespace thq {
+
+constexpr int BN = 128;
+constexpr int BK = 64;
+constexpr int LDK = BK + 8;  // padded LDS row (bf16 elements): 144 B
+
+__device__ __forceinline__ f32x16_t mfma32(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// W-tile column c (0..127) -> weight row; in gate/up mode each wave's 64
+// columns are 32 gate rows followed by the 32 up rows of the same outputs.
+template <bool GU>
+__device__ __forceinline__ int64_t tile_row(int c, int64_t bx, int64_t nout, int64_t up_off, bool& valid) {
+    if (GU) {
+        const int wn = c >> 6, tn = (c >> 5) & 1, j = c & 31;
+        const int64_t i = bx * 64 + 32 * wn + j;
+        valid = i < nout;
+        return i + (tn ? up_off : 0);
+    }
+    const int64_t r = bx * BN + c;
+    valid = r < nout;
+    return r;
+}
+
+// 8 packed nibbles (one per byte, bits 0..3) -> d1*q - m1 as 4 bf16 pairs
+__device__ __forceinline__ void deq8_q4(uint32_t w, float d1, float m1, uint32_t* out) {
+    const float f0 = ubyte_f32<0>(w), f1 = ubyte_f32<1>(w);
+    const float f2 = ubyte_f32<2>(w), f3 = ubyte_f32<3>(w);
+    out[0] = pack_bf16x2(__builtin_fmaf(d1, f0, -m1), __builtin_fmaf(d1, f1, -m1));
+    out[1] = pack_bf16x2(__builtin_fmaf(d1, f2, -m1), __builtin_fmaf(d1, f3, -m1));
+}
+
+template <int QT, bool EXACT, int BM, bool GU, typename YT, bool SPLIT>
+__global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ Wq, const uint16_t* __restrict__ Wd,
+                                             const bf16_t* __restrict__ X, void* __restrict__ Yv, int M, int K,
+                                             int64_t nout, int64_t up_off, int64_t ldy, int kiters_per_split) {
+    constexpr int TM = BM / 2;   // wave tile rows (M)
+    constexpr int MT = TM / 32;  // 32-row MFMA tiles per wave
+    constexpr int XCH = BM * 8 / 256;  // 16-B X chunks per thread per K step
+    __shared__ __attribute__((aligned(16))) bf16_t Xs[2][BM][LDK];
+    __shared__ __attribute__((aligned(16))) bf16_t Ws[2][BN][LDK];
+    __shared__ float Ds[2][BN][2];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int64_t bx = blockIdx.x;
+    const int64_t m0 = (int64_t)blockIdx.y * BM;
+    const int kit0 = blockIdx.z * kiters_per_split;
+    int kit1 = kit0 + kiters_per_split;
+    const int kiters = K / BK;
+    if (kit1 > kiters) kit1 = kiters;
+
+    // this thread's W-tile row and half
+    const int wc = tid >> 1, wh = tid & 1;
+    bool wvalid;
+    const int64_t wrow = tile_row<GU>(wc, bx, nout, up_off, wvalid);
+
+    uint4 xr[XCH];
+    uint4 wr0, wr1;     // packed weights
+    uint4 hdr;          // Q4_K superblock header
+    uint16_t dq = 0;    // Q8_0 block scale
+
+    auto gload = [&](int kit) {
+        const int k0 = kit * BK;
+#pragma unroll
+        for (int i = 0; i < XCH; ++i) {
+            const int c = tid + 256 * i;
+            const int row = c >> 3, col8 = c & 7;
+            const int64_t m = m0 + row;
+            if (m < M)
+                xr[i] = *reinterpret_cast<const uint4*>(X + m * K + k0 + 8 * col8);
+            else
+                xr[i] = make_uint4(0, 0, 0, 0);
+        }
+        if (!wvalid) {
+            wr0 = wr1 = hdr = make_uint4(0, 0, 0, 0);
+            dq = 0;
+            return;
+        }
+        if (QT == 12) {
+            const uint8_t* blk = Wq + wrow * (int64_t)(K >> 8) * THQ_Q4K_BYTES + (int64_t)(k0 >> 8) * THQ_Q4K_BYTES;
+            const int j = (k0 & 255) >> 6;
+            hdr = *reinterpret_cast<const uint4*>(blk);
+            wr0 = *reinterpret_cast<const uint4*>(blk + 16 + 32 * j + 16 * wh);
+        } else {
+            const uint4* q = reinterpret_cast<const uint4*>(Wq + wrow * K + k0 + 32 * wh);
+            wr0 = q[0];
+            wr1 = q[1];
+            dq = Wd[wrow * (K >> 5) + (k0 >> 5) + wh];
+        }
+    };
+
+    auto lstore = [&](int buf, int kit) {
+#pragma unroll
+        for (int i = 0; i < XCH; ++i) {
+            const int c = tid + 256 * i;
+            *reinterpret_cast<uint4*>(&Xs[buf][c >> 3][8 * (c & 7)]) = xr[i];
+        }
+        if (QT == 12) {
+            const int j = ((kit * BK) & 255) >> 6;
+            uint32_t sc0, mm0, sc1, mm1;
+            scale_min_k4(2 * j, hdr.y, hdr.z, hdr.w, sc0, mm0);
+            scale_min_k4(2 * j + 1, hdr.y, hdr.z, hdr.w, sc1, mm1);
+            const float d = f16_to_f32(hdr.x & 0xFFFF), dmin = f16_to_f32(hdr.x >> 16);
+            const float d1 = d * (float)sc0, m1 = dmin * (float)mm0;
+            const float d2 = d * (float)sc1, m2 = dmin * (float)mm1;
+            const uint32_t q[4] = {wr0.x, wr0.y, wr0.z, wr0.w};
+            uint32_t lo[8], hi[8];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                deq8_q4(q[t] & 0x0F0F0F0Fu, d1, m1, lo + 2 * t);
+                deq8_q4((q[t] >> 4) & 0x0F0F0F0Fu, d2, m2, hi + 2 * t);
+            }
+            uint4* dl = reinterpret_cast<uint4*>(&Ws[buf][wc][16 * wh]);
+            uint4* dh = reinterpret_cast<uint4*>(&Ws[buf][wc][32 + 16 * wh]);
+            dl[0] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+            dl[1] = make_uint4(lo[4], lo[5], lo[6], lo[7]);
+            dh[0] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+            dh[1] = make_uint4(hi[4], hi[5], hi[6], hi[7]);
+        } else {
+            const uint32_t q[8] = {wr0.x, wr0.y, wr0.z, wr0.w, wr1.x, wr1.y, wr1.z, wr1.w};
+            const float d = f16_to_f32(dq);
+            uint32_t o[16];
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const float f0 = (float)(int8_t)(q[t] & 0xFF), f1 = (float)(int8_t)((q[t] >> 8) & 0xFF);
+                const float f2 = (float)(int8_t)((q[t] >> 16) & 0xFF), f3 = (float)(int8_t)(q[t] >> 24);
+                if (EXACT) {
+                    o[2 * t] = pack_bf16x2(f0, f1);
+                    o[2 * t + 1] = pack_bf16x2(f2, f3);
+                } else {
+                    o[2 * t] = pack_bf16x2(f0 * d, f1 * d);
+                    o[2 * t + 1] = pack_bf16x2(f2 * d, f3 * d);
+                }
+            }
+            uint4* dst = reinterpret_cast<uint4*>(&Ws[buf][wc][32 * wh]);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) dst[v] = make_uint4(o[4 * v], o[4 * v + 1], o[4 * v + 2], o[4 * v + 3]);
+            if (EXACT) Ds[buf][wc][wh] = d;
+        }
+    };
+
+    f32x16_t acc[MT][2];
+    f32x16_t tot[MT][2];
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                acc[a][b][i] = 0.0f;
+                tot[a][b][i] = 0.0f;
+            }
+
+    if (kit0 < kit1) {
+        gload(kit0);
+        lstore(0, kit0);
+    }
+    __syncthreads();
+    const int lr = lane & 31, lk = 8 * (lane >> 5);
+    for (int kit = kit0; kit < kit1; ++kit) {
+        const int buf = (kit - kit0) & 1;
+        const bool more = kit + 1 < kit1;
+        if (more) gload(kit + 1);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            bf16x8_t a[MT], b[2];
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                a[t] = *reinterpret_cast<const bf16x8_t*>(&Xs[buf][wm * TM + 32 * t + lr][16 * kk + lk]);
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                b[t] = *reinterpret_cast<const bf16x8_t*>(&Ws[buf][wn * 64 + 32 * t + lr][16 * kk + lk]);
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+            if (EXACT && (kk & 1)) {
+                // end of a 32-wide block: scale the partial into the total
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float ds = Ds[buf][wn * 64 + 32 * j + lr][kk >> 1];
+#pragma unroll
+                    for (int i = 0; i < MT; ++i)
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) {
+                            tot[i][j][e] = __builtin_fmaf(ds, acc[i][j][e], tot[i][j][e]);
+                            acc[i][j][e] = 0.0f;
+                        }
+                }
+            }
+        }
+        if (more) lstore(buf ^ 1, kit + 1);
+        __syncthreads();
+    }
+    if (!EXACT) {
+#pragma unroll
+        for (int i = 0; i < MT; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) tot[i][j] = acc[i][j];
+    }
+
+    // epilogue: lane holds column lr of each 32x32 tile, rows 8*(e/4) + 4*(lane/32) + e%4
+    const int rq = 4 * (lane >> 5);
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int64_t m = m0 + wm * TM + 32 * i + 8 * (e >> 2) + rq + (e & 3);
+            if (m >= M) continue;
+            if (GU) {
+                const int64_t o = bx * 64 + 32 * wn + lr;
+                if (o >= nout) continue;
+                if (SPLIT) {
+                    float* P = static_cast<float*>(Yv) + (int64_t)blockIdx.z * M * ldy;
+                    P[m * ldy + o] = tot[i][0][e];
+                    P[m * ldy + up_off + o] = tot[i][1][e];
+                } else {
+                    store_y<YT>(static_cast<YT*>(Yv) + m * ldy + o, silu_mul(tot[i][0][e], tot[i][1][e]));
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int64_t n = bx * BN + wn * 64 + 32 * j + lr;
+                    if (n >= nout) continue;
+                    if (SPLIT)
+                        (static_cast<float*>(Yv) + (int64_t)blockIdx.z * M * ldy)[m * ldy + n] = tot[i][j][e];
+                    else
+                        store_y<YT>(static_cast<YT*>(Yv) + m * ldy + n, tot[i][j][e]);
+                }
+            }
+        }
+    }
+}
+
+// sum split partials P[s][M][ldp] in split order, then the epilogue
+template <bool GU, typename YT>
+__global__ __launch_bounds__(256) void k_split_reduce(const float* __restrict__ P, YT* __restrict__ y, int M,
+                                                     int64_t nout, int64_t up_off, int64_t ldp, int splits) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (int64_t)M * nout) return;
+    const int64_t m = t / nout, o = t - m * nout;
+    float g = 0.0f, u = 0.0f;
+    for (int s = 0; s < splits; ++s) {
+        const float* Ps = P + (int64_t)s * M * ldp + m * ldp;
+        g += Ps[o];
+        if (GU) u += Ps[up_off + o];
+    }
+    store_y<YT>(y + m * nout + o, GU ? silu_mul(g, u) : g);
+}
+
+// ------------------------------------------------------------------ launch
+static inline int env_int(const char* name, int dflt) {
+    const char* v = getenv(name);
+    return v && *v ? atoi(v) : dflt;
+}
+
+GemmPlan plan_gemm(int qtype, bool exact, int64_t M, int64_t N_rows, int64_t K, bool gu) {
+    GemmPlan p;
+    int bm = env_int("THQ_GEMM_BM", 0);
+    if (bm != 64 && bm != 128 && bm != 256) bm = M <= 64 ? 64 : (M <= 128 ? 128 : 256);
+    if (exact && bm > 64) bm = 64;  // the exact tile keeps two accumulator sets
+    p.bm = bm;
+    const int64_t nout = gu ? N_rows / 2 : N_rows;
+    p.tiles_n = gu ? (nout + 63) / 64 : (nout + BN - 1) / BN;
+    p.tiles_m = (M + bm - 1) / bm;
+    const int kiters = (int)(K / BK);
+    int splits = env_int("THQ_GEMM_SPLITS", 0);
+    if (splits <= 0) {
+        const int64_t blocks = p.tiles_n * p.tiles_m;
+        const int64_t want = 512;  // two blocks per CU
+        splits = 1;
+        if (blocks < want) {
+            splits = (int)((want + blocks - 1) / blocks);
+            const int max_split = kiters / 2 > 0 ? kiters / 2 : 1;
+            if (splits > max_split) splits = max_split;
+        }
+    }
+    if (splits > kiters) splits = kiters;
+    if (splits < 1) splits = 1;
+    p.kps = (kiters + splits - 1) / splits;
+    p.splits = (kiters + p.kps - 1) / p.kps;
+    p.workspace_bytes = p.splits > 1 ? (size_t)p.splits * (size_t)M * (size_t)N_rows * sizeof(float) : 0;
+    return p;
+}
+
+template <int QT, bool EXACT, int BM, bool GU, typename YT>
+static hipError_t gemm_t(const GemmPlan& p, const WeightView& w, const bf16_t* x, void* y, int M, float* ws,
+                         hipStream_t s) {
+    const int64_t nout = GU ? w.N / 2 : w.N;
+    const int64_t up_off = GU ? w.N / 2 : 0;
+    dim3 grid((unsigned)p.tiles_n, (unsigned)p.tiles_m, (unsigned)p.splits);
+    if (p.splits == 1) {
+        hipLaunchKernelGGL((k_gemm<QT, EXACT, BM, GU, YT, false>), grid, dim3(256), 0, s, w.q, w.d, x, y, M,
+                           (int)w.K, nout, up_off, nout, p.kps);
+        return hipGetLastError();
+    }
+    // partials in natural weight-row order: ld = N rows
+    hipLaunchKernelGGL((k_gemm<QT, EXACT, BM, GU, float, true>), grid, dim3(256), 0, s, w.q, w.d, x, (void*)ws, M,
+                       (int)w.K, nout, up_off, (int64_t)w.N, p.kps);
+    const int64_t total = (int64_t)M * nout;
+    hipLaunchKernelGGL((k_split_reduce<GU, YT>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ws,
+                       static_cast<YT*>(y), M, nout, up_off, (int64_t)w.N, p.splits);
+    return hipGetLastError();
+}
+
+template <int QT, bool EXACT, bool GU, typename YT>
+static hipError_t gemm_bm(const GemmPlan& p, const WeightView& w, const bf16_t* x, void* y, int M, float* ws,
+                          hipStream_t s) {
+    if constexpr (EXACT) {
+        return gemm_t<QT, EXACT, 64, GU, YT>(p, w, x, y, M, ws, s);
+    } else {
+        if (p.bm == 64) return gemm_t<QT, EXACT, 64, GU, YT>(p, w, x, y, M, ws, s);
+        if (p.bm == 128) return gemm_t<QT, EXACT, 128, GU, YT>(p, w, x, y, M, ws, s);
+        return gemm_t<QT, EXACT, 256, GU, YT>(p, w, x, y, M, ws, s);
+    }
+}
+
+hipError_t launch_gemm(const GemmPlan& p, const WeightView& w, const void* x, void* y, bool yf32, bool gu, bool exact,
+                       int M, float* ws, hipStream_t s) {
+    const bf16_t* xb = static_cast<const bf16_t*>(x);
+    if (w.qtype == 12) {
+        if (exact) return hipErrorInvalidValue;
+        if (gu) return yf32 ? gemm_bm<12, false, true, float>(p, w, xb, y, M, ws, s)
+                            : gemm_bm<12, false, true, bf16_t>(p, w, xb, y, M, ws, s);
+        return yf32 ? gemm_bm<12, false, false, float>(p, w, xb, y, M, ws, s)
+                    : gemm_bm<12, false, false, bf16_t>(p, w, xb, y, M, ws, s);
+    }
+    if (exact) {
+        if (gu) return yf32 ? gemm_bm<8, true, true, float>(p, w, xb, y, M, ws, s)
+                            : gemm_bm<8, true, true, bf16_t>(p, w, xb, y, M, ws, s);
+        return yf32 ? gemm_bm<8, true, false, float>(p, w, xb, y, M, ws, s)
+                    : gemm_bm<8, true, false, bf16_t>(p, w, xb, y, M, ws, s);
+    }
+    if (gu) return yf32 ? gemm_bm<8, false, true, float>(p, w, xb, y, M, ws, s)
+                        : gemm_bm<8, false, true, bf16_t>(p, w, xb, y, M, ws, s);
+    return yf32 ? gemm_bm<8, false, false, float>(p, w, xb, y, M, ws, s)
+                : gemm_bm<8, false, false, bf16_t>(p, w, xb, y, M, ws, s);
+}
+
+}  // namespace thq

@@ -1,0 +1,419 @@
+// thq_api.cpp — the extern "C" boundary (include/thq.h): device contexts,
+// weight lifetime, validation, routing by M, and error reporting.  No C++
+// exception crosses the ABI; every entry point returns a THQ_* code.
+//
+// Routing mirrors the reference's projection router QLin::linear_ps
+// (engine/src/qwen35.rs:398-617: m == 1 -> GEMV, m > 1 -> tile kernels,
+// inapplicable kernels fall back instead of failing) and candle's
+// QMatMul::forward.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/thq.h"
+#include "thq_kernels.hpp"
+
+struct thq_ctx {
+    int device = 0;
+    std::mutex mu;
+    void* ws = nullptr;  // workspace: split-K partials, argmax partials, logits
+    size_t ws_bytes = 0;
+};
+
+struct thq_weight {
+    thq_ctx* ctx = nullptr;
+    int qtype = 0;
+    int64_t N = 0, K = 0;
+    uint8_t* q = nullptr;    // Q4_K superblocks, or Q8_0 i8 plane
+    uint16_t* d = nullptr;   // Q8_0 f16 scale plane
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_err = buf;
+    return code;
+}
+
+#define HIP_TRY(expr)                                                                            \
+    do {                                                                                         \
+        hipError_t e_ = (expr);                                                                  \
+        if (e_ != hipSuccess) return fail(THQ_EHIP, "%s: %s", #expr, hipGetErrorString(e_));     \
+    } while (0)
+
+int block_of(int qtype) { return qtype == THQ_Q8_0 ? 32 : (qtype == THQ_Q4_K ? 256 : 0); }
+
+size_t gguf_bytes(int qtype, int64_t n, int64_t k) {
+    if (qtype == THQ_Q8_0) return (size_t)n * (size_t)(k / 32) * 34;
+    return (size_t)n * (size_t)(k / 256) * 144;
+}
+
+thq::WeightView view(const thq_weight* w) { return thq::WeightView{w->qtype, w->N, w->K, w->q, w->d}; }
+
+int check_dtype_shape(int dtype, int64_t n, int64_t k) {
+    const int bs = block_of(dtype);
+    if (!bs) return fail(THQ_EDTYPE, "unsupported weight dtype %d (want Q8_0=8 or Q4_K=12)", dtype);
+    if (n <= 0 || k <= 0) return fail(THQ_ESHAPE, "weight shape [%lld, %lld] must be positive", (long long)n, (long long)k);
+    if (k % bs) return fail(THQ_ESHAPE, "K=%lld is not a multiple of the block size %d", (long long)k, bs);
+    if (k > (int64_t)1 << 30 || n > (int64_t)1 << 40) return fail(THQ_ESHAPE, "weight shape too large");
+    return THQ_OK;
+}
+
+int alloc_weight(thq_ctx* ctx, int dtype, int64_t n, int64_t k, thq_weight** out) {
+    thq_weight* w = new (std::nothrow) thq_weight();
+    if (!w) return fail(THQ_ENOMEM, "host allocation failed");
+    w->ctx = ctx;
+    w->qtype = dtype;
+    w->N = n;
+    w->K = k;
+    size_t qb = dtype == THQ_Q8_0 ? (size_t)n * (size_t)k : gguf_bytes(dtype, n, k);
+    hipError_t e = hipMalloc((void**)&w->q, qb);
+    if (e != hipSuccess) {
+        delete w;
+        return fail(THQ_ENOMEM, "hipMalloc(%zu) for weight: %s", qb, hipGetErrorString(e));
+    }
+    if (dtype == THQ_Q8_0) {
+        e = hipMalloc((void**)&w->d, (size_t)n * (size_t)(k / 32) * 2);
+        if (e != hipSuccess) {
+            (void)hipFree(w->q);
+            delete w;
+            return fail(THQ_ENOMEM, "hipMalloc for Q8_0 scales: %s", hipGetErrorString(e));
+        }
+    }
+    *out = w;
+    return THQ_OK;
+}
+
+// Grow the context workspace; growing synchronizes the device first so no
+// in-flight kernel still reads the old buffer.
+int ensure_ws(thq_ctx* ctx, size_t bytes) {
+    if (bytes <= ctx->ws_bytes) return THQ_OK;
+    HIP_TRY(hipDeviceSynchronize());
+    if (ctx->ws) HIP_TRY(hipFree(ctx->ws));
+    ctx->ws = nullptr;
+    ctx->ws_bytes = 0;
+    size_t want = bytes + (bytes >> 3);
+    hipError_t e = hipMalloc(&ctx->ws, want);
+    if (e != hipSuccess) return fail(THQ_ENOMEM, "workspace hipMalloc(%zu): %s", want, hipGetErrorString(e));
+    ctx->ws_bytes = want;
+    return THQ_OK;
+}
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) != hipSuccess) prev = -1;
+        if (prev != dev) (void)hipSetDevice(dev);
+    }
+    ~DeviceGuard() {
+        int cur = -1;
+        if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev) (void)hipSetDevice(prev);
+    }
+};
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Shared body of matmul / gate_up / argmax-logits.
+int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t m, void* y, int yt, uint32_t flags,
+               bool gu, void* stream) {
+    if (!ctx || !w) return fail(THQ_EINVAL, "null context or weight");
+    if (xt != THQ_ACT_F32 && xt != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad x_type %d", xt);
+    if (yt != THQ_ACT_F32 && yt != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad y_type %d", yt);
+    if (flags & ~(THQ_MODE_EXACT_W)) return fail(THQ_EINVAL, "unknown flags 0x%x", flags);
+    if (m < 0) return fail(THQ_ESHAPE, "M=%lld must be >= 0", (long long)m);
+    if (m > (1 << 24)) return fail(THQ_ESHAPE, "M=%lld too large", (long long)m);
+    if (gu && (w->N % 2)) return fail(THQ_ESHAPE, "gate/up weight has an odd row count %lld", (long long)w->N);
+    if (m == 0) return THQ_OK;
+    if (!x || !y) return fail(THQ_EINVAL, "null x or y");
+    DeviceGuard g(ctx->device);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    const thq::WeightView v = view(w);
+    const bool xf32 = xt == THQ_ACT_F32, yf32 = yt == THQ_ACT_F32;
+    const int64_t nout = gu ? w->N / 2 : w->N;
+    const int64_t up_off = gu ? w->N / 2 : 0;
+    hipError_t e;
+    if (m == 1 && aligned16(x) && thq::gemv1_supported(w->qtype, (int)w->K)) {
+        e = thq::launch_gemv1(v, x, xf32, y, yf32, gu, nout, up_off, s);
+    } else if (!xf32 && aligned16(x) && !(w->qtype == THQ_Q4_K && (flags & THQ_MODE_EXACT_W))) {
+        const bool exact = (flags & THQ_MODE_EXACT_W) || (w->qtype == THQ_Q8_0 && m <= 64);
+        thq::GemmPlan p = thq::plan_gemm(w->qtype, exact, m, w->N, w->K, gu);
+        std::lock_guard<std::mutex> lk(ctx->mu);
+        if (p.workspace_bytes) {
+            int rc = ensure_ws(ctx, p.workspace_bytes);
+            if (rc) return rc;
+        }
+        e = thq::launch_gemm(p, v, x, y, yf32, gu, exact, (int)m, static_cast<float*>(ctx->ws), s);
+    } else {
+        e = thq::launch_generic(v, x, xf32, y, yf32, gu, (int)m, nout, up_off, s);
+    }
+    if (e != hipSuccess) return fail(THQ_EHIP, "kernel launch: %s", hipGetErrorString(e));
+    return THQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* thq_last_error(void) { return g_err.c_str(); }
+
+const char* thq_version(void) { return "thq 0.1 gfx950"; }
+
+int thq_init(int device, thq_ctx** out) {
+    if (!out) return fail(THQ_EINVAL, "null out");
+    int count = 0;
+    HIP_TRY(hipGetDeviceCount(&count));
+    if (device < 0 || device >= count) return fail(THQ_EINVAL, "device %d out of range (%d devices)", device, count);
+    thq_ctx* c = new (std::nothrow) thq_ctx();
+    if (!c) return fail(THQ_ENOMEM, "host allocation failed");
+    c->device = device;
+    *out = c;
+    return THQ_OK;
+}
+
+void thq_destroy(thq_ctx* ctx) {
+    if (!ctx) return;
+    if (ctx->ws) {
+        DeviceGuard g(ctx->device);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(ctx->ws);
+    }
+    delete ctx;
+}
+
+int thq_weight_upload(thq_ctx* ctx, thq_dtype dtype, const void* host_blocks, int64_t n, int64_t k,
+                      thq_weight** out) {
+    if (!ctx || !host_blocks || !out) return fail(THQ_EINVAL, "null argument");
+    int rc = check_dtype_shape(dtype, n, k);
+    if (rc) return rc;
+    DeviceGuard g(ctx->device);
+    const size_t bytes = gguf_bytes(dtype, n, k);
+    if (dtype == THQ_Q4_K) {
+        thq_weight* w = nullptr;
+        rc = alloc_weight(ctx, dtype, n, k, &w);
+        if (rc) return rc;
+        hipError_t e = hipMemcpy(w->q, host_blocks, bytes, hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            thq_weight_free(w);
+            return fail(THQ_EHIP, "hipMemcpy weight: %s", hipGetErrorString(e));
+        }
+        *out = w;
+        return THQ_OK;
+    }
+    void* staging = nullptr;
+    hipError_t e = hipMalloc(&staging, bytes);
+    if (e != hipSuccess) return fail(THQ_ENOMEM, "hipMalloc staging(%zu): %s", bytes, hipGetErrorString(e));
+    e = hipMemcpy(staging, host_blocks, bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(staging);
+        return fail(THQ_EHIP, "hipMemcpy weight: %s", hipGetErrorString(e));
+    }
+    rc = thq_weight_from_device(ctx, dtype, staging, n, k, nullptr, out);
+    if (rc == THQ_OK) {
+        e = hipStreamSynchronize(nullptr);
+        if (e != hipSuccess) rc = fail(THQ_EHIP, "sync after repack: %s", hipGetErrorString(e));
+    }
+    (void)hipFree(staging);
+    return rc;
+}
+
+int thq_weight_from_device(thq_ctx* ctx, thq_dtype dtype, const void* dev_blocks, int64_t n, int64_t k, void* stream,
+                           thq_weight** out) {
+    if (!ctx || !dev_blocks || !out) return fail(THQ_EINVAL, "null argument");
+    int rc = check_dtype_shape(dtype, n, k);
+    if (rc) return rc;
+    DeviceGuard g(ctx->device);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    thq_weight* w = nullptr;
+    rc = alloc_weight(ctx, dtype, n, k, &w);
+    if (rc) return rc;
+    hipError_t e;
+    if (dtype == THQ_Q4_K)
+        e = hipMemcpyAsync(w->q, dev_blocks, gguf_bytes(dtype, n, k), hipMemcpyDeviceToDevice, s);
+    else
+        e = thq::launch_repack_q8_0(static_cast<const uint8_t*>(dev_blocks), reinterpret_cast<int8_t*>(w->q), w->d,
+                                    n * (k / 32), s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        thq_weight_free(w);
+        return fail(THQ_EHIP, "weight from device: %s", hipGetErrorString(e));
+    }
+    *out = w;
+    return THQ_OK;
+}
+
+int thq_quantize(thq_ctx* ctx, thq_dtype dtype, const float* w_dev, int64_t n, int64_t k, void* stream,
+                 thq_weight** out) {
+    if (!ctx || !w_dev || !out) return fail(THQ_EINVAL, "null argument");
+    int rc = check_dtype_shape(dtype, n, k);
+    if (rc) return rc;
+    if (!aligned16(w_dev)) return fail(THQ_EALIGN, "w_dev must be 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    thq_weight* w = nullptr;
+    rc = alloc_weight(ctx, dtype, n, k, &w);
+    if (rc) return rc;
+    hipError_t e = dtype == THQ_Q8_0
+                       ? thq::launch_quantize_q8_0(w_dev, reinterpret_cast<int8_t*>(w->q), w->d, n * (k / 32), s)
+                       : thq::launch_quantize_q4k(w_dev, w->q, n * (k / 256), s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        thq_weight_free(w);
+        return fail(THQ_EHIP, "quantize: %s", hipGetErrorString(e));
+    }
+    *out = w;
+    return THQ_OK;
+}
+
+int thq_weight_fuse(thq_ctx* ctx, const thq_weight* const* parts, int nparts, thq_weight** out) {
+    if (!ctx || !parts || nparts <= 0 || !out) return fail(THQ_EINVAL, "null argument or no parts");
+    int64_t n = 0;
+    for (int i = 0; i < nparts; ++i) {
+        if (!parts[i]) return fail(THQ_EINVAL, "part %d is null", i);
+        if (parts[i]->qtype != parts[0]->qtype) return fail(THQ_EDTYPE, "part %d dtype differs", i);
+        if (parts[i]->K != parts[0]->K)
+            return fail(THQ_ESHAPE, "part %d has K=%lld, part 0 has K=%lld", i, (long long)parts[i]->K,
+                        (long long)parts[0]->K);
+        n += parts[i]->N;
+    }
+    const int dtype = parts[0]->qtype;
+    const int64_t k = parts[0]->K;
+    DeviceGuard g(ctx->device);
+    thq_weight* w = nullptr;
+    int rc = alloc_weight(ctx, dtype, n, k, &w);
+    if (rc) return rc;
+    size_t qoff = 0, doff = 0;
+    for (int i = 0; i < nparts; ++i) {
+        const size_t qb = dtype == THQ_Q8_0 ? (size_t)parts[i]->N * (size_t)k : gguf_bytes(dtype, parts[i]->N, k);
+        hipError_t e = hipMemcpy(w->q + qoff, parts[i]->q, qb, hipMemcpyDeviceToDevice);
+        if (e == hipSuccess && dtype == THQ_Q8_0) {
+            const size_t db = (size_t)parts[i]->N * (size_t)(k / 32) * 2;
+            e = hipMemcpy(reinterpret_cast<uint8_t*>(w->d) + doff, parts[i]->d, db, hipMemcpyDeviceToDevice);
+            doff += db;
+        }
+        if (e != hipSuccess) {
+            thq_weight_free(w);
+            return fail(THQ_EHIP, "fuse copy: %s", hipGetErrorString(e));
+        }
+        qoff += qb;
+    }
+    *out = w;
+    return THQ_OK;
+}
+
+void thq_weight_free(thq_weight* w) {
+    if (!w) return;
+    DeviceGuard g(w->ctx ? w->ctx->device : 0);
+    if (w->q) (void)hipFree(w->q);
+    if (w->d) (void)hipFree(w->d);
+    delete w;
+}
+
+int thq_weight_info(const thq_weight* w, thq_dtype* dtype, int64_t* n, int64_t* k, size_t* bytes) {
+    if (!w) return fail(THQ_EINVAL, "null weight");
+    if (dtype) *dtype = (thq_dtype)w->qtype;
+    if (n) *n = w->N;
+    if (k) *k = w->K;
+    if (bytes) *bytes = gguf_bytes(w->qtype, w->N, w->K);
+    return THQ_OK;
+}
+
+int thq_weight_download(const thq_weight* w, void* host_blocks) {
+    if (!w || !host_blocks) return fail(THQ_EINVAL, "null argument");
+    DeviceGuard g(w->ctx->device);
+    if (w->qtype == THQ_Q4_K) {
+        HIP_TRY(hipMemcpy(host_blocks, w->q, gguf_bytes(w->qtype, w->N, w->K), hipMemcpyDeviceToHost));
+        return THQ_OK;
+    }
+    const int64_t nb = w->N * (w->K / 32);
+    std::vector<int8_t> qs((size_t)(w->N * w->K));
+    std::vector<uint16_t> ds((size_t)nb);
+    HIP_TRY(hipMemcpy(qs.data(), w->q, qs.size(), hipMemcpyDeviceToHost));
+    HIP_TRY(hipMemcpy(ds.data(), w->d, ds.size() * 2, hipMemcpyDeviceToHost));
+    uint8_t* dst = static_cast<uint8_t*>(host_blocks);
+    for (int64_t b = 0; b < nb; ++b) {
+        std::memcpy(dst + b * 34, &ds[(size_t)b], 2);
+        std::memcpy(dst + b * 34 + 2, qs.data() + b * 32, 32);
+    }
+    return THQ_OK;
+}
+
+int thq_dequantize(thq_ctx* ctx, const thq_weight* w, float* out_dev, void* stream) {
+    if (!ctx || !w || !out_dev) return fail(THQ_EINVAL, "null argument");
+    if (!aligned16(out_dev)) return fail(THQ_EALIGN, "out_dev must be 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e = w->qtype == THQ_Q8_0
+                       ? thq::launch_dequant_q8_0(reinterpret_cast<const int8_t*>(w->q), w->d, out_dev,
+                                                  w->N * (w->K / 32), s)
+                       : thq::launch_dequant_q4k(w->q, out_dev, w->N * (w->K / 256), s);
+    if (e != hipSuccess) return fail(THQ_EHIP, "dequantize: %s", hipGetErrorString(e));
+    return THQ_OK;
+}
+
+int thq_matmul(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m, void* y_dev,
+               thq_act y_type, uint32_t flags, void* stream) {
+    return run_matmul(ctx, w, x_dev, x_type, m, y_dev, y_type, flags, false, stream);
+}
+
+int thq_gate_up_silu(thq_ctx* ctx, const thq_weight* fused, const void* x_dev, thq_act x_type, int64_t m, void* y_dev,
+                     thq_act y_type, uint32_t flags, void* stream) {
+    return run_matmul(ctx, fused, x_dev, x_type, m, y_dev, y_type, flags, true, stream);
+}
+
+int thq_argmax(thq_ctx* ctx, const float* v_dev, int64_t m, int64_t n, uint32_t* idx_dev, void* stream) {
+    if (!ctx) return fail(THQ_EINVAL, "null context");
+    if (m < 0 || n < 0) return fail(THQ_ESHAPE, "negative shape");
+    if (m == 0) return THQ_OK;
+    if (!idx_dev || (n > 0 && !v_dev)) return fail(THQ_EINVAL, "null argument");
+    if (n > 0xFFFFFFFFll) return fail(THQ_ESHAPE, "row length exceeds u32 indices");
+    DeviceGuard g(ctx->device);
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    int rc = ensure_ws(ctx, thq::argmax_workspace_bytes(m, n));
+    if (rc) return rc;
+    hipError_t e = thq::launch_argmax(v_dev, m, n, idx_dev, ctx->ws, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(THQ_EHIP, "argmax: %s", hipGetErrorString(e));
+    return THQ_OK;
+}
+
+int thq_matmul_argmax(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m,
+                      float* logits_dev, uint32_t* idx_dev, uint32_t flags, void* stream) {
+    if (!ctx || !w) return fail(THQ_EINVAL, "null context or weight");
+    if (m == 0) return THQ_OK;
+    if (!idx_dev) return fail(THQ_EINVAL, "null idx_dev");
+    DeviceGuard g(ctx->device);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    float* logits = logits_dev;
+    if (!logits) {
+        // logits live at the end of the workspace, after the GEMM / argmax scratch
+        const thq::GemmPlan p = thq::plan_gemm(w->qtype, true, m, w->N, w->K, false);
+        const size_t scratch = std::max(p.workspace_bytes, thq::argmax_workspace_bytes(m, w->N));
+        const size_t off = (scratch + 255) & ~(size_t)255;
+        const size_t need = off + (size_t)m * (size_t)w->N * sizeof(float);
+        {
+            std::lock_guard<std::mutex> lk(ctx->mu);
+            int rc = ensure_ws(ctx, need);
+            if (rc) return rc;
+        }
+        // the matmul and argmax use the workspace head; logits use its tail
+        logits = reinterpret_cast<float*>(static_cast<char*>(ctx->ws) + off);
+    }
+    int rc = run_matmul(ctx, w, x_dev, x_type, m, logits, THQ_ACT_F32, flags | THQ_MODE_EXACT_W, false, stream);
+    if (rc) return rc;
+    return thq_argmax(ctx, logits, m, w->N, idx_dev, s);
+}
+
+}  // extern "C"

@@ -1,0 +1,50 @@
+// thq_kernels.hpp — host-side launchers of the gfx950 kernels (internal).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace thq {
+
+// A weight as the kernels see it.
+//   Q4_K (qtype 12): q = GGUF superblocks [N][K/256][144 B], d = nullptr
+//   Q8_0 (qtype 8):  q = i8 plane [N][K], d = f16 scale plane [N][K/32]
+struct WeightView {
+    int qtype;
+    int64_t N, K;
+    const uint8_t* q;
+    const uint16_t* d;
+};
+
+struct GemmPlan {
+    int bm = 64;
+    int64_t tiles_n = 0, tiles_m = 0;
+    int splits = 1, kps = 0;
+    size_t workspace_bytes = 0;
+};
+
+// weights
+hipError_t launch_repack_q8_0(const uint8_t* raw, int8_t* qs, uint16_t* d, int64_t nblocks, hipStream_t s);
+hipError_t launch_quantize_q8_0(const float* w, int8_t* qs, uint16_t* d, int64_t nblocks, hipStream_t s);
+hipError_t launch_quantize_q4k(const float* w, uint8_t* out, int64_t nsuper, hipStream_t s);
+hipError_t launch_dequant_q8_0(const int8_t* qs, const uint16_t* d, float* out, int64_t nblocks, hipStream_t s);
+hipError_t launch_dequant_q4k(const uint8_t* raw, float* out, int64_t nsuper, hipStream_t s);
+
+// decode GEMV (M = 1); gu = fused gate/up over a [gate; up] weight
+bool gemv1_supported(int qtype, int K);
+hipError_t launch_gemv1(const WeightView& w, const void* x, bool xf32, void* y, bool yf32, bool gu, int64_t nout,
+                        int64_t up_off, hipStream_t s);
+// exact generic kernel, any M, scalar activation loads
+hipError_t launch_generic(const WeightView& w, const void* x, bool xf32, void* y, bool yf32, bool gu, int M,
+                          int64_t nout, int64_t up_off, hipStream_t s);
+
+// MFMA GEMM (bf16 activations)
+GemmPlan plan_gemm(int qtype, bool exact, int64_t M, int64_t N_rows, int64_t K, bool gu);
+hipError_t launch_gemm(const GemmPlan& p, const WeightView& w, const void* x, void* y, bool yf32, bool gu, bool exact,
+                       int M, float* ws, hipStream_t s);
+
+// argmax
+size_t argmax_workspace_bytes(int64_t m, int64_t n);
+hipError_t launch_argmax(const float* v, int64_t m, int64_t n, uint32_t* idx, void* ws, hipStream_t s);
+
+}  // namespace thq

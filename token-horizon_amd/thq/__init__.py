@@ -1,0 +1,250 @@
+"""ctypes front end of libthq.so (the C ABI in include/thq.h).
+
+Python here is plumbing for tests and benchmarks: torch tensors provide
+device memory and the current HIP stream; all compute runs in the gfx950
+kernels of libthq.so.  The module raises at import if the library is not
+built, so nothing ever falls back to a CPU path.
+
+The classes mirror candle's quantized API that the reference engine uses
+([ext] candle-core 0.11 quantized::{QTensor, QMatMul}, reached from
+engine/src/model.rs:551-562): QTensor.quantize / .dequantize / .data,
+QMatMul.from_qtensor(...).forward(x).
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import torch
+
+HERE = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB_PATH = os.path.join(HERE, "libthq.so")
+
+Q8_0 = 8
+Q4_K = 12
+BLOCK = {Q8_0: 32, Q4_K: 256}
+BLOCK_BYTES = {Q8_0: 34, Q4_K: 144}
+
+ACT_F32 = 0
+ACT_BF16 = 1
+MODE_DEQUANT_F32 = 0
+MODE_EXACT_W = 0x10
+
+OK = 0
+EINVAL, ESHAPE, EDTYPE, EALIGN, EHIP, ENOMEM = -1, -2, -3, -4, -5, -6
+
+# every symbol include/thq.h declares
+EXPORTS = (
+    "thq_init", "thq_destroy", "thq_last_error", "thq_version", "thq_weight_upload", "thq_weight_from_device",
+    "thq_quantize", "thq_weight_fuse", "thq_weight_free", "thq_weight_info", "thq_weight_download",
+    "thq_dequantize", "thq_matmul", "thq_gate_up_silu", "thq_matmul_argmax", "thq_argmax",
+)
+
+
+class ThqError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"thq error {code}: {msg}")
+        self.code = code
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"libthq.so is not built ({LIB_PATH}); run __graft_entry__.build()")
+    L = C.CDLL(LIB_PATH)
+    P, i64, u32, I = C.c_void_p, C.c_int64, C.c_uint32, C.c_int
+    PP = C.POINTER(C.c_void_p)
+    sig = {
+        "thq_init": ([I, PP], I),
+        "thq_destroy": ([P], None),
+        "thq_last_error": ([], C.c_char_p),
+        "thq_version": ([], C.c_char_p),
+        "thq_weight_upload": ([P, I, P, i64, i64, PP], I),
+        "thq_weight_from_device": ([P, I, P, i64, i64, P, PP], I),
+        "thq_quantize": ([P, I, P, i64, i64, P, PP], I),
+        "thq_weight_fuse": ([P, PP, I, PP], I),
+        "thq_weight_free": ([P], None),
+        "thq_weight_info": ([P, C.POINTER(C.c_int), C.POINTER(i64), C.POINTER(i64), C.POINTER(C.c_size_t)], I),
+        "thq_weight_download": ([P, P], I),
+        "thq_dequantize": ([P, P, P, P], I),
+        "thq_matmul": ([P, P, P, I, i64, P, I, u32, P], I),
+        "thq_gate_up_silu": ([P, P, P, I, i64, P, I, u32, P], I),
+        "thq_matmul_argmax": ([P, P, P, I, i64, P, P, u32, P], I),
+        "thq_argmax": ([P, P, i64, i64, P, P], I),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = res
+    return L
+
+
+lib = _load()
+
+
+def last_error() -> str:
+    return lib.thq_last_error().decode()
+
+
+def check(rc: int):
+    if rc != OK:
+        raise ThqError(rc, last_error())
+    return rc
+
+
+def _stream(stream=None):
+    if stream is None:
+        stream = torch.cuda.current_stream()
+    return C.c_void_p(stream.cuda_stream)
+
+
+def _ptr(t: torch.Tensor | None):
+    return C.c_void_p(t.data_ptr()) if t is not None else C.c_void_p(0)
+
+
+def _act(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return ACT_F32
+    if t.dtype == torch.bfloat16:
+        return ACT_BF16
+    raise TypeError(f"activations must be float32 or bfloat16, got {t.dtype}")
+
+
+class Context:
+    """One per device (thq_init)."""
+
+    _by_dev: dict[int, "Context"] = {}
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        check(lib.thq_init(device, C.byref(h)))
+        self.h = h
+        self.device = device
+
+    @classmethod
+    def get(cls, device: int = 0) -> "Context":
+        if device not in cls._by_dev:
+            cls._by_dev[device] = Context(device)
+        return cls._by_dev[device]
+
+    def __del__(self):
+        if getattr(self, "h", None) and lib is not None:
+            lib.thq_destroy(self.h)
+            self.h = None
+
+
+class QTensor:
+    """Device-resident quantized weight [N, K] (candle QTensor analogue)."""
+
+    def __init__(self, handle: C.c_void_p, ctx: Context):
+        self.h = handle
+        self.ctx = ctx
+        dt, n, k, nb = C.c_int(), C.c_int64(), C.c_int64(), C.c_size_t()
+        check(lib.thq_weight_info(self.h, C.byref(dt), C.byref(n), C.byref(k), C.byref(nb)))
+        self.dtype, self.n, self.k, self.nbytes = dt.value, n.value, k.value, nb.value
+
+    @property
+    def shape(self):
+        return (self.n, self.k)
+
+    @classmethod
+    def from_gguf_bytes(cls, dtype: int, blocks, n: int, k: int, ctx: Context | None = None) -> "QTensor":
+        """blocks: host bytes (numpy uint8 / bytes) or a device uint8 tensor."""
+        ctx = ctx or Context.get(torch.cuda.current_device())
+        h = C.c_void_p()
+        if isinstance(blocks, torch.Tensor) and blocks.is_cuda:
+            check(lib.thq_weight_from_device(ctx.h, dtype, _ptr(blocks), n, k, _stream(), C.byref(h)))
+        else:
+            import numpy as np
+            arr = np.ascontiguousarray(np.frombuffer(blocks, dtype=np.uint8) if isinstance(blocks, (bytes, bytearray))
+                                       else blocks, dtype=np.uint8)
+            check(lib.thq_weight_upload(ctx.h, dtype, arr.ctypes.data_as(C.c_void_p), n, k, C.byref(h)))
+        return cls(h, ctx)
+
+    @classmethod
+    def quantize(cls, w: torch.Tensor, dtype: int, ctx: Context | None = None) -> "QTensor":
+        """Quantize an f32 [N, K] device tensor on the GPU (QTensor::quantize)."""
+        ctx = ctx or Context.get(w.device.index or 0)
+        assert w.dtype == torch.float32 and w.is_cuda and w.dim() == 2 and w.is_contiguous()
+        h = C.c_void_p()
+        check(lib.thq_quantize(ctx.h, dtype, _ptr(w), w.shape[0], w.shape[1], _stream(), C.byref(h)))
+        return cls(h, ctx)
+
+    @classmethod
+    def fuse(cls, parts: list["QTensor"]) -> "QTensor":
+        arr = (C.c_void_p * len(parts))(*[p.h.value for p in parts])
+        h = C.c_void_p()
+        check(lib.thq_weight_fuse(parts[0].ctx.h, arr, len(parts), C.byref(h)))
+        return cls(h, parts[0].ctx)
+
+    def data(self):
+        """GGUF block bytes (numpy uint8, [N, row_bytes])."""
+        import numpy as np
+        out = np.empty(self.nbytes, dtype=np.uint8)
+        check(lib.thq_weight_download(self.h, out.ctypes.data_as(C.c_void_p)))
+        return out.reshape(self.n, -1)
+
+    def dequantize(self) -> torch.Tensor:
+        out = torch.empty((self.n, self.k), dtype=torch.float32, device="cuda")
+        check(lib.thq_dequantize(self.ctx.h, self.h, _ptr(out), _stream()))
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None) and lib is not None:
+            lib.thq_weight_free(self.h)
+            self.h = None
+
+
+def matmul(w: QTensor, x: torch.Tensor, out_dtype=torch.float32, flags: int = 0, out: torch.Tensor | None = None):
+    """y[M, N] = x[M, K] . W^T through thq_matmul."""
+    x2 = x.reshape(-1, x.shape[-1]) if x.dim() != 2 else x
+    if x2.shape[-1] != w.k:
+        raise ValueError(f"x last dim {x2.shape[-1]} != weight inp {w.k}")
+    assert x2.is_contiguous() or x2.numel() == 0
+    m = x2.shape[0]
+    if out is None:
+        out = torch.empty((m, w.n), dtype=out_dtype, device=x.device)
+    check(lib.thq_matmul(w.ctx.h, w.h, _ptr(x2), _act(x2), m, _ptr(out), _act(out), flags, _stream()))
+    return out.reshape(*x.shape[:-1], w.n)
+
+
+def gate_up_silu(w: QTensor, x: torch.Tensor, out_dtype=torch.bfloat16, flags: int = 0):
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.shape[-1] != w.k:
+        raise ValueError(f"x last dim {x2.shape[-1]} != weight inp {w.k}")
+    m = x2.shape[0]
+    out = torch.empty((m, w.n // 2), dtype=out_dtype, device=x.device)
+    check(lib.thq_gate_up_silu(w.ctx.h, w.h, _ptr(x2), _act(x2), m, _ptr(out), _act(out), flags, _stream()))
+    return out.reshape(*x.shape[:-1], w.n // 2)
+
+
+def matmul_argmax(w: QTensor, x: torch.Tensor, want_logits: bool = True, flags: int = 0):
+    x2 = x.reshape(-1, x.shape[-1])
+    m = x2.shape[0]
+    logits = torch.empty((m, w.n), dtype=torch.float32, device=x.device) if want_logits else None
+    idx = torch.empty((m,), dtype=torch.int32, device=x.device)
+    check(lib.thq_matmul_argmax(w.ctx.h, w.h, _ptr(x2), _act(x2), m, _ptr(logits), _ptr(idx), flags, _stream()))
+    return logits, idx
+
+
+def argmax(v: torch.Tensor, ctx: Context | None = None) -> torch.Tensor:
+    assert v.dtype == torch.float32 and v.is_contiguous()
+    ctx = ctx or Context.get(v.device.index or 0)
+    v2 = v if v.dim() == 2 else v.reshape(1, -1)
+    m, n = v2.shape
+    idx = torch.empty((m,), dtype=torch.int32, device=v.device)
+    check(lib.thq_argmax(ctx.h, _ptr(v2), m, n, _ptr(idx), _stream()))
+    return idx
+
+
+class QMatMul:
+    """candle QMatMul analogue: forward(x) = x . W^T."""
+
+    def __init__(self, qt: QTensor):
+        self.w = qt
+
+    @classmethod
+    def from_qtensor(cls, qt: QTensor) -> "QMatMul":
+        return cls(qt)
+
+    def forward(self, x: torch.Tensor, out_dtype=None) -> torch.Tensor:
+        return matmul(self.w, x, out_dtype or x.dtype)
