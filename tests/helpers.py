@@ -15,14 +15,22 @@ def rel_row_err(y: np.ndarray, ref: np.ndarray) -> float:
     return float((np.abs(y - ref).max(axis=1) / nrm).max())
 
 
-def assert_close_elem(tag: str, got: np.ndarray, want: np.ndarray, rel: float):
+def assert_close_elem(tag: str, got: np.ndarray, want: np.ndarray, rel: float, floor: str = "max"):
     """Per-element bound in the style of the reference's qmvt assert_close
-    (engine/src/qwen35.rs:6946-6958): |got - want| <= rel * max(|want|, 0.02 max|want|)."""
+    (engine/src/qwen35.rs:6946-6958): |got - want| <= rel * max(|want|, f), with
+    f = 0.02 max|want| (floor="max", exact weights) or f = rms of the row
+    (floor="rms", for tiles that round dequantized weights to bf16: their error
+    is ~1.1e-3 rms(y) per element independent of |y|, so 2^-7 rms is ~7 sigma)."""
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
     mag = np.abs(want).max()
     assert mag > 0, f"{tag}: degenerate reference"
-    tol = rel * np.maximum(np.abs(want), 0.02 * mag)
+    if floor == "rms":
+        w2 = want.reshape(-1, want.shape[-1])
+        f = np.sqrt((w2 ** 2).mean(axis=1, keepdims=True)).reshape(want.shape[:-1] + (1,))
+    else:
+        f = 0.02 * mag
+    tol = rel * np.maximum(np.abs(want), f)
     bad = np.abs(got - want) > tol
     if bad.any():
         i = np.argwhere(bad)[0]

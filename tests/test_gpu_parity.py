@@ -126,7 +126,10 @@ def test_q4k_decode_gemv(m, n, k):
     err = rel_row_err(y, ref)
     assert err <= 1e-2, err
     # exact weights at m = 1; bf16-rounded tile weights above
-    assert_close_elem(f"q4k gemv m={m}", y, ref, 2.0 ** -12 if m == 1 else 2.0 ** -7)
+    if m == 1:  # exact weights in registers
+        assert_close_elem(f"q4k gemv m={m}", y, ref, 2.0 ** -12)
+    else:       # MFMA tile with bf16-rounded weights
+        assert_close_elem(f"q4k gemv m={m}", y, ref, 2.0 ** -7, floor="rms")
 
 
 # ------------------------------------------------------------------ config 3
@@ -138,17 +141,21 @@ def test_q4k_prefill_gemm(m, n, k):
     y = thq.matmul(w, xb, torch.bfloat16)
     # every row: checksum of the row sums, sum_n y[m, n] = x[m] . (sum_n W[n])
     wsum = O.dequantize(O.Q4_K, b, n, k).astype(np.float64).sum(axis=0)
-    rows = y.float().sum(dim=1).double().cpu().numpy()
+    yf = y.float()
+    rows = yf.sum(dim=1).double().cpu().numpy()
+    rms = yf.pow(2).mean(dim=1).sqrt().double().cpu().numpy()
     want_rows = xf.astype(np.float64) @ wsum
-    scale = np.abs(xf).astype(np.float64) @ np.abs(wsum) + 1.0
-    assert np.all(np.abs(rows - want_rows) <= 2e-3 * scale)
+    # bf16 weight + output rounding noise sums to ~2e-3 sqrt(N) rms(y); 10x margin
+    assert np.all(np.abs(rows - want_rows) <= 0.02 * np.sqrt(n) * rms)
     # sampled rows in full against the oracle
     rng = np.random.default_rng(m)
     pick = np.unique(np.concatenate([[0, m - 1], rng.integers(0, m, 10)]))
     ref = O.matmul(O.Q4_K, b, n, k, xf[pick], O.MODE_DEQUANT_F32)
     got = tonp(y)[pick]
     assert rel_row_err(got, ref) <= 1e-2
-    assert_close_elem(f"q4k gemm m={m}", got, ref, 2.0 ** -7)
+    # bf16 output: one output rounding step (2^-8..2^-7 relative) on top of the
+    # bf16 weight-rounding noise, so 2^-6 of max(|y|, rms(y))
+    assert_close_elem(f"q4k gemm m={m}", got, ref, 2.0 ** -6, floor="rms")
 
 
 @pytest.mark.parametrize("m", [9, 33, 100])
@@ -159,7 +166,7 @@ def test_q4k_gemm_ragged_m(m):
     y = tonp(thq.matmul(w, xb, torch.float32))
     ref = O.matmul(O.Q4_K, b, n, k, xf, O.MODE_DEQUANT_F32)
     assert rel_row_err(y, ref) <= 1e-2
-    assert_close_elem(f"q4k ragged m={m}", y, ref, 2.0 ** -7)
+    assert_close_elem(f"q4k ragged m={m}", y, ref, 2.0 ** -7, floor="rms")
 
 
 @pytest.mark.parametrize("m,flags", [(16, 0), (100, 0), (100, thq.MODE_EXACT_W)])
@@ -170,7 +177,10 @@ def test_q8_0_gemm(m, flags):
     y = tonp(thq.matmul(w, xb, torch.float32, flags=flags))
     ref = O.matmul(O.Q8_0, b, n, k, xf, O.MODE_DEQUANT_F32)
     exact = flags or m <= 64
-    assert_close_elem(f"q8_0 gemm m={m}", y, ref, 2.0 ** -14 if exact else 2.0 ** -7)
+    if exact:
+        assert_close_elem(f"q8_0 gemm m={m}", y, ref, 2.0 ** -14)
+    else:
+        assert_close_elem(f"q8_0 gemm m={m}", y, ref, 2.0 ** -7, floor="rms")
 
 
 @pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K])
@@ -247,7 +257,7 @@ def test_gate_up_epilogue_matches_matmul(m):
     # bf16(silu(bf16(g)) * bf16(u)); the device exp may differ by one bf16 step
     want = O.bf16_bits_to_f32(O.gate_up_silu(gu))
     got = tonp(out)
-    assert_close_elem(f"gate_up m={m} vs own matmul", got, want, 2.0 ** -7)
+    assert_close_elem(f"gate_up m={m} vs own matmul", got, want, 2.0 ** -7)  # one bf16 step
     assert (got == want).mean() > 0.99
     # and against the oracle's f64 matmul
     ref = O.bf16_bits_to_f32(O.gate_up_silu(O.matmul(O.Q4_K, np.concatenate([bg, bu]), 2 * h, k, xf)))
@@ -265,7 +275,7 @@ def test_decoder_layer_projections(m):
         y = tonp(thq.matmul(w, xb, torch.bfloat16))
         ref = O.matmul(O.Q4_K, b, n, kk, xf[pick], O.MODE_DEQUANT_F32)
         assert rel_row_err(y[pick], ref) <= 1e-2, name
-        assert_close_elem(name, y[pick], ref, 2.0 ** -6)
+        assert_close_elem(name, y[pick], ref, 2.0 ** -6, floor="rms")
     bg, bu = weight_bytes(O.Q4_K, 12288, k, seed=31), weight_bytes(O.Q4_K, 12288, k, seed=32)
     fused = thq.QTensor.from_gguf_bytes(O.Q4_K, np.concatenate([bg, bu]), 24576, k)
     act = thq.gate_up_silu(fused, xb, torch.bfloat16)
