@@ -56,7 +56,7 @@ __device__ __forceinline__ void deq8_q4(uint32_t w, float d1, float m1, uint32_t
 }
 
 template <int QT, bool EXACT, int BM, bool GU, typename YT, bool SPLIT>
-__global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ Wq, const uint16_t* __restrict__ Wd,
+__global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Wa,
                                              const bf16_t* __restrict__ X, void* __restrict__ Yv, int M, int K,
                                              int64_t nout, int64_t up_off, int64_t ldy, int kiters_per_split) {
     constexpr int TM = BM / 2;   // wave tile rows (M)
@@ -104,15 +104,17 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ Wq, co
             return;
         }
         if (QT == 12) {
-            const uint8_t* blk = Wq + wrow * (int64_t)(K >> 8) * THQ_Q4K_BYTES + (int64_t)(k0 >> 8) * THQ_Q4K_BYTES;
-            const int j = (k0 & 255) >> 6;
-            hdr = *reinterpret_cast<const uint4*>(blk);
-            wr0 = *reinterpret_cast<const uint4*>(blk + 16 + 32 * j + 16 * wh);
+            const int nsb = K >> 8, sidx = k0 >> 8, j = (k0 & 255) >> 6;
+            hdr.x = *reinterpret_cast<const uint32_t*>(Wq + q4k_hdword(wrow, nsb, sidx, 0));
+            hdr.y = *reinterpret_cast<const uint32_t*>(Wq + q4k_hdword(wrow, nsb, sidx, 1));
+            hdr.z = *reinterpret_cast<const uint32_t*>(Wq + q4k_hdword(wrow, nsb, sidx, 2));
+            hdr.w = *reinterpret_cast<const uint32_t*>(Wq + q4k_hdword(wrow, nsb, sidx, 3));
+            wr0 = *reinterpret_cast<const uint4*>(Wq + q4k_piece(wrow, nsb, sidx, wh, j));
         } else {
             const uint4* q = reinterpret_cast<const uint4*>(Wq + wrow * K + k0 + 32 * wh);
             wr0 = q[0];
             wr1 = q[1];
-            dq = Wd[wrow * (K >> 5) + (k0 >> 5) + wh];
+            dq = reinterpret_cast<const uint16_t*>(Wa)[wrow * (K >> 5) + (k0 >> 5) + wh];
         }
     };
 
@@ -125,9 +127,9 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ Wq, co
         if (QT == 12) {
             const int j = ((kit * BK) & 255) >> 6;
             uint32_t sc0, mm0, sc1, mm1;
-            scale_min_k4(2 * j, hdr.y, hdr.z, hdr.w, sc0, mm0);
-            scale_min_k4(2 * j + 1, hdr.y, hdr.z, hdr.w, sc1, mm1);
-            const float d = f16_to_f32(hdr.x & 0xFFFF), dmin = f16_to_f32(hdr.x >> 16);
+            q4k_hdr_sm(hdr, 2 * j, sc0, mm0);
+            q4k_hdr_sm(hdr, 2 * j + 1, sc1, mm1);
+            const float d = q4k_hdr_d(hdr), dmin = q4k_hdr_dmin(hdr);
             const float d1 = d * (float)sc0, m1 = dmin * (float)mm0;
             const float d2 = d * (float)sc1, m2 = dmin * (float)mm1;
             const uint32_t q[4] = {wr0.x, wr0.y, wr0.z, wr0.w};
@@ -317,12 +319,12 @@ static hipError_t gemm_t(const GemmPlan& p, const WeightView& w, const bf16_t* x
     const int64_t up_off = GU ? w.N / 2 : 0;
     dim3 grid((unsigned)p.tiles_n, (unsigned)p.tiles_m, (unsigned)p.splits);
     if (p.splits == 1) {
-        hipLaunchKernelGGL((k_gemm<QT, EXACT, BM, GU, YT, false>), grid, dim3(256), 0, s, w.q, w.d, x, y, M,
+        hipLaunchKernelGGL((k_gemm<QT, EXACT, BM, GU, YT, false>), grid, dim3(256), 0, s, w.q, w.aux, x, y, M,
                            (int)w.K, nout, up_off, nout, p.kps);
         return hipGetLastError();
     }
     // partials in natural weight-row order: ld = N rows
-    hipLaunchKernelGGL((k_gemm<QT, EXACT, BM, GU, float, true>), grid, dim3(256), 0, s, w.q, w.d, x, (void*)ws, M,
+    hipLaunchKernelGGL((k_gemm<QT, EXACT, BM, GU, float, true>), grid, dim3(256), 0, s, w.q, w.aux, x, (void*)ws, M,
                        (int)w.K, nout, up_off, (int64_t)w.N, p.kps);
     const int64_t total = (int64_t)M * nout;
     hipLaunchKernelGGL((k_split_reduce<GU, YT>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ws,

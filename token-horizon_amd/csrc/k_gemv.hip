@@ -46,101 +46,295 @@ __device__ __forceinline__ void write_rows(YT* __restrict__ y, int64_t base, int
     }
 }
 
-// ------------------------------------------------------------------ Q4_K M=1, bf16 x
-// KC = number of 4096-wide K chunks (K <= 4096*KC).  R rows per wave.
-template <int KC, int R, bool GU, typename YT>
-__global__ __launch_bounds__(256) void k_gemv1_q4k_bf16(const uint8_t* __restrict__ W, const bf16_t* __restrict__ x,
-                                                       YT* __restrict__ y, int64_t nout, int K, int64_t up_off) {
-    const int lane = threadIdx.x & 63;
-    const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int64_t base = wave * (GU ? R / 2 : R);
-    if (base >= nout) return;
-    const int nsb = K >> 8;
-    const int64_t rb = (int64_t)nsb * THQ_Q4K_BYTES;
-    const int sl = lane >> 2, part = lane & 3;
+// ------------------------------------------------------------------ wave helpers
+// value of lane P of each quad, in every lane of the quad (DPP quad_perm)
+template <int P>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, P | (P << 2) | (P << 4) | (P << 6), 0xF, 0xF, false);
+}
 
-    // activations for this lane: pairs (x[2i], x[2i+1]) of both sub-blocks
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// sum over the 16 lanes of each DPP row; every lane of the row gets it
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_f<0x141>(v);  // row_half_mirror
+    v += dpp_f<0x140>(v);  // row_mirror
+    return v;
+}
+
+// Transposed reduction of R per-lane partials over the 64 lanes: each step
+// halves the values a lane carries, so R rows cost about as much as one.
+// Afterwards every lane holds the total of slot slot_of_lane<R>(lane): R=1
+// slot 0 everywhere; R=2 slot lane/32; R=4 slot 2*(lane/32) + (lane/16)%2.
+template <int R>
+__device__ __forceinline__ float reduce_slots(const float (&v)[R], int lane) {
+    const bool up = lane & 32, b4 = lane & 16;
+    float k;
+    if constexpr (R == 4) {
+        const float s0 = up ? v[0] : v[2], s1 = up ? v[1] : v[3];
+        const float k0 = (up ? v[2] : v[0]) + __shfl_xor(s0, 32, 64);
+        const float k1 = (up ? v[3] : v[1]) + __shfl_xor(s1, 32, 64);
+        k = (b4 ? k1 : k0) + __shfl_xor(b4 ? k0 : k1, 16, 64);
+    } else if constexpr (R == 2) {
+        k = (up ? v[1] : v[0]) + __shfl_xor(up ? v[0] : v[1], 32, 64);
+        k += __shfl_xor(k, 16, 64);
+    } else {
+        k = v[0] + __shfl_xor(v[0], 32, 64);
+        k += __shfl_xor(k, 16, 64);
+    }
+    return row16_sum(k);
+}
+
+template <int R>
+__device__ __forceinline__ int slot_of_lane(int lane) {
+    if constexpr (R == 4) return 2 * (lane >> 5) + ((lane >> 4) & 1);
+    if constexpr (R == 2) return lane >> 5;
+    return 0;
+}
+
+// ------------------------------------------------------------------ Q4_K M=1, bf16 x
+// Persistent: a fixed grid of waves walks "units" = (row quad, 4096-wide K
+// chunk); each wave owns quads w, w + W, ... and all their chunks, and issues
+// the loads of its next unit before computing the current one, so HBM
+// streaming overlaps the VALU work.  With the row-quad layout a unit is nine
+// contiguous 1-KB wave loads: eight nibble pieces (row r, half h) and the
+// quad's transposed header dwords.  Gate/up: a unit holds the gate quad and
+// the matching up quad (8 slots).  x and its per-lane sub-block sums come
+// from LDS, staged once per block.
+//
+// Per 8 weights: 2 masks, 4 v_perm against a constant 0x43 byte (bf16 0x43nn
+// = 128 + q), 4 v_dot2_f32_bf16; the 128 offset is removed with the lane's
+// sum of x; d and dmin are assembled from the quad's header dwords with DPP.
+template <bool GU>
+struct Q4Unit {
+    static constexpr int NQ = GU ? 2 : 1;
+    uint4 nib[NQ][4][2];
+    uint4 hdr[NQ];
+};
+
+// lane's 16-B offsets inside a row quad for chunk c (clamped to a real
+// superblock: lanes past K multiply by zero activations)
+template <bool GU>
+__device__ __forceinline__ void q4k_unit_load(Q4Unit<GU>& U, const uint8_t* __restrict__ W, int64_t gq, int c,
+                                              int64_t up_off, int nsb, int lane) {
+    int s = 16 * c + (lane >> 2);
+    const int li = s < nsb ? 16 * c * 4 + lane : (lane & 3);
+    const int64_t qb = (int64_t)nsb * 576;
+#pragma unroll
+    for (int qi = 0; qi < Q4Unit<GU>::NQ; ++qi) {
+        const uint8_t* g = W + (qi ? (gq + (up_off >> 2)) : gq) * qb + (int64_t)li * 16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+                U.nib[qi][r][h] = *reinterpret_cast<const uint4*>(g + (int64_t)r * nsb * 128 + (int64_t)h * nsb * 64);
+        U.hdr[qi] = *reinterpret_cast<const uint4*>(g + (int64_t)nsb * 512);
+    }
+}
+
+template <bool GU>
+__device__ __forceinline__ void q4k_unit_compute(float (&acc)[GU ? 8 : 4], const Q4Unit<GU>& U,
+                                                 const uint32_t (&xlo)[16], const uint32_t (&xhi)[16], float sxlo,
+                                                 float sxhi) {
+    const uint32_t C43 = 0x43434343u;
+#pragma unroll
+    for (int qi = 0; qi < Q4Unit<GU>::NQ; ++qi) {
+        const uint32_t hq[4] = {U.hdr[qi].x, U.hdr[qi].y, U.hdr[qi].z, U.hdr[qi].w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint4 v0 = U.nib[qi][r][0], v1 = U.nib[qi][r][1];
+            const uint32_t qw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            float alo = 0.0f, ahi = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const uint32_t lo = qw[t] & 0x0F0F0F0Fu, hi = (qw[t] >> 4) & 0x0F0F0F0Fu;
+                // perm(C43, v, sel): bytes [v.b_i, 0x43, v.b_i+1, 0x43] = bf16 pair (128+q_i, 128+q_i+1)
+                alo = dot2_bf16(__builtin_amdgcn_perm(C43, lo, 0x04010400u), xlo[2 * t], alo);
+                alo = dot2_bf16(__builtin_amdgcn_perm(C43, lo, 0x04030402u), xlo[2 * t + 1], alo);
+                ahi = dot2_bf16(__builtin_amdgcn_perm(C43, hi, 0x04010400u), xhi[2 * t], ahi);
+                ahi = dot2_bf16(__builtin_amdgcn_perm(C43, hi, 0x04030402u), xhi[2 * t + 1], ahi);
+            }
+            const uint32_t h = hq[r];
+            const uint32_t t0 = quad_bcast<0>(h), t1 = quad_bcast<1>(h);
+            const uint32_t t2 = quad_bcast<2>(h), t3 = quad_bcast<3>(h);
+            const float d = f16_to_f32((uint16_t)__builtin_amdgcn_perm(t1, t0, 0x0c0c0703u));
+            const float dmin = f16_to_f32((uint16_t)__builtin_amdgcn_perm(t3, t2, 0x0c0c0703u));
+            const float sc0 = (float)(h & 63u), m0 = (float)((h >> 6) & 63u);
+            const float sc1 = (float)((h >> 12) & 63u), m1 = (float)((h >> 18) & 63u);
+            // sum x*q = a - 128 * sum x, per sub-block; then d*sc and dmin*m
+            const float dot = __builtin_fmaf(sc1, ahi, sc0 * alo);
+            const float ssc = __builtin_fmaf(sc1, sxhi, sc0 * sxlo);
+            const float smn = __builtin_fmaf(m1, sxhi, m0 * sxlo);
+            float a = __builtin_fmaf(d, __builtin_fmaf(-128.0f, ssc, dot), acc[4 * qi + r]);
+            acc[4 * qi + r] = __builtin_fmaf(-dmin, smn, a);
+        }
+    }
+}
+
+// 8-slot transposed reduction: lanes with (lane & 7) == 0 end with slot
+// 4*(lane/32) + 2*((lane/16)%2) + (lane/8)%2
+__device__ __forceinline__ float reduce_slots8(const float (&v)[8], int lane) {
+    const bool b5 = lane & 32, b4 = lane & 16, b3 = lane & 8;
+    float k[4], k2[2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) k[i] = (b5 ? v[4 + i] : v[i]) + __shfl_xor(b5 ? v[i] : v[4 + i], 32, 64);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) k2[i] = (b4 ? k[2 + i] : k[i]) + __shfl_xor(b4 ? k[i] : k[2 + i], 16, 64);
+    float t = (b3 ? k2[1] : k2[0]) + __shfl_xor(b3 ? k2[0] : k2[1], 8, 64);
+    t += dpp_f<0xB1>(t);   // quad_perm [1,0,3,2]
+    t += dpp_f<0x4E>(t);   // quad_perm [2,3,0,1]
+    t += dpp_f<0x141>(t);  // row_half_mirror
+    return t;
+}
+
+template <bool GU, typename YT>
+__device__ __forceinline__ void q4k_unit_store(YT* __restrict__ y, int64_t gq, int64_t nout, int lane,
+                                               const float (&acc)[GU ? 8 : 4]) {
+    if constexpr (GU) {
+        const float tot = reduce_slots8(acc, lane);
+        const float u = __shfl_xor(tot, 32, 64);  // up slot = gate slot + 4
+        if ((lane & 7) || (lane & 32)) return;
+        const int64_t o = 4 * gq + ((lane >> 3) & 3);
+        if (o < nout) store_y<YT>(y + o, silu_mul(tot, u));
+    } else {
+        const float tot = reduce_slots<4>(acc, lane);
+        if (lane & 15) return;
+        const int64_t o = 4 * gq + slot_of_lane<4>(lane);
+        if (o < nout) store_y<YT>(y + o, tot);
+    }
+}
+
+template <int KC, bool GU, typename YT>
+__global__ __launch_bounds__(256) void k_gemv1_q4k_bf16(const uint8_t* __restrict__ W, const bf16_t* __restrict__ x,
+                                                       YT* __restrict__ y, int64_t nout, int K, int64_t up_off,
+                                                       int64_t nquads) {
+    extern __shared__ uint4 lds[];  // x (K bf16)
+    const int lane = threadIdx.x & 63;
+    const int64_t nwaves = (int64_t)gridDim.x * (blockDim.x >> 6);
+    const int64_t w = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int nsb = K >> 8;
+    // units of this wave: quads w, w + nwaves, ... times KC chunks
+    const int64_t nunits = (w < nquads ? (nquads - 1 - w) / nwaves + 1 : 0) * KC;
+
+    Q4Unit<GU> A, B;
+    if (nunits) q4k_unit_load<GU>(A, W, w, 0, up_off, nsb, lane);
+    for (int i = threadIdx.x; i < (K >> 3); i += blockDim.x) lds[i] = reinterpret_cast<const uint4*>(x)[i];
+    __syncthreads();
+    if (!nunits) return;
+
+    // this lane's activations for every chunk (bf16 pairs) and their sums
     uint32_t xlo[KC][16], xhi[KC][16];
     float sxlo[KC], sxhi[KC];
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
-        const int s = 16 * c + sl;
-        sxlo[c] = 0.0f;
-        sxhi[c] = 0.0f;
+        const int s = 16 * c + (lane >> 2);
+        float a0 = 0.0f, b0 = 0.0f;
         if (s < nsb) {
-            const uint4* xp = reinterpret_cast<const uint4*>(x + (int64_t)s * 256 + 64 * part);
+            const uint4* xp = lds + s * 32 + 8 * (lane & 3);
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const uint4 a = xp[v], b = xp[4 + v];
-                xlo[c][4 * v] = a.x; xlo[c][4 * v + 1] = a.y; xlo[c][4 * v + 2] = a.z; xlo[c][4 * v + 3] = a.w;
-                xhi[c][4 * v] = b.x; xhi[c][4 * v + 1] = b.y; xhi[c][4 * v + 2] = b.z; xhi[c][4 * v + 3] = b.w;
+                const uint4 p = xp[v], q = xp[4 + v];
+                xlo[c][4 * v] = p.x; xlo[c][4 * v + 1] = p.y; xlo[c][4 * v + 2] = p.z; xlo[c][4 * v + 3] = p.w;
+                xhi[c][4 * v] = q.x; xhi[c][4 * v + 1] = q.y; xhi[c][4 * v + 2] = q.z; xhi[c][4 * v + 3] = q.w;
             }
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                sxlo[c] += bf16_to_f32(xlo[c][i] & 0xFFFF) + bf16_to_f32(xlo[c][i] >> 16);
-                sxhi[c] += bf16_to_f32(xhi[c][i] & 0xFFFF) + bf16_to_f32(xhi[c][i] >> 16);
+                a0 = dot2_bf16(xlo[c][i], 0x3F803F80u, a0);  // bf16 (1, 1)
+                b0 = dot2_bf16(xhi[c][i], 0x3F803F80u, b0);
             }
         } else {
 #pragma unroll
             for (int i = 0; i < 16; ++i) { xlo[c][i] = 0; xhi[c][i] = 0; }
         }
+        sxlo[c] = a0;
+        sxhi[c] = b0;
     }
 
-    // issue every weight load of the wave before any math
-    uint4 hdr[R][KC], q0[R][KC], q1[R][KC];
+    float acc[GU ? 8 : 4];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        int64_t row = slot_row<R, GU>(base, r, up_off);
-        const bool ok = GU ? (base + (r >> 1) < nout) : (row < nout);
-        if (!ok) row = GU ? up_off * (r & 1) : 0;
+    for (int i = 0; i < (GU ? 8 : 4); ++i) acc[i] = 0.0f;
+    // unit i = (quad w + (i / KC) * nwaves, chunk i % KC); walk it incrementally
+    int64_t gq = w;
+    int c = 0;
+    auto advance = [&](int64_t& q, int& ch) {
+        if (++ch == KC) { ch = 0; q += nwaves; }
+    };
+    auto finish = [&](const Q4Unit<GU>& U, int64_t q, int ch) {
+        // KC is small: select the chunk's activations with a static switch
 #pragma unroll
-        for (int c = 0; c < KC; ++c) {
-            const int s = 16 * c + sl;
-            if (s < nsb) {
-                const uint8_t* blk = W + row * rb + (int64_t)s * THQ_Q4K_BYTES;
-                hdr[r][c] = *reinterpret_cast<const uint4*>(blk);
-                q0[r][c] = *reinterpret_cast<const uint4*>(blk + 16 + 32 * part);
-                q1[r][c] = *reinterpret_cast<const uint4*>(blk + 32 + 32 * part);
-            } else {
-                hdr[r][c] = make_uint4(0, 0, 0, 0);
-                q0[r][c] = hdr[r][c];
-                q1[r][c] = hdr[r][c];
-            }
+        for (int cc = 0; cc < KC; ++cc)
+            if (cc == ch) q4k_unit_compute<GU>(acc, U, xlo[cc], xhi[cc], sxlo[cc], sxhi[cc]);
+        if (ch == KC - 1) {
+            q4k_unit_store<GU, YT>(y, q, nout, lane, acc);
+#pragma unroll
+            for (int j = 0; j < (GU ? 8 : 4); ++j) acc[j] = 0.0f;
         }
+    };
+    // two units per trip so the A/B register sets never need copying
+    for (int64_t i = 0;; i += 2) {
+        int64_t q1 = gq;
+        int c1 = c;
+        advance(q1, c1);
+        if (i + 1 < nunits) q4k_unit_load<GU>(B, W, q1, c1, up_off, nsb, lane);
+        finish(A, gq, c);
+        if (i + 1 >= nunits) break;
+        int64_t q2 = q1;
+        int c2 = c1;
+        advance(q2, c2);
+        if (i + 2 < nunits) q4k_unit_load<GU>(A, W, q2, c2, up_off, nsb, lane);
+        finish(B, q1, c1);
+        if (i + 2 >= nunits) break;
+        gq = q2;
+        c = c2;
     }
+}
 
-    float acc[R];
+// One-shot variant for K <= 4096: one wave per row quad, every load issued at
+// entry, no second register set (so enough waves stay resident to keep the
+// HBM queues full).
+template <bool GU, typename YT>
+__global__ __launch_bounds__(256) void k_gemv1_q4k_bf16_1s(const uint8_t* __restrict__ W,
+                                                          const bf16_t* __restrict__ x, YT* __restrict__ y,
+                                                          int64_t nout, int K, int64_t up_off, int64_t nquads) {
+    extern __shared__ uint4 lds[];  // x (K bf16)
+    const int lane = threadIdx.x & 63;
+    const int64_t gq = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int nsb = K >> 8;
+    Q4Unit<GU> A;
+    if (gq < nquads) q4k_unit_load<GU>(A, W, gq, 0, up_off, nsb, lane);
+    for (int i = threadIdx.x; i < (K >> 3); i += blockDim.x) lds[i] = reinterpret_cast<const uint4*>(x)[i];
+    __syncthreads();
+    if (gq >= nquads) return;
+    const int s = lane >> 2;
+    uint32_t xlo[16], xhi[16];
+    float sxlo = 0.0f, sxhi = 0.0f;
+    if (s < nsb) {
+        const uint4* xp = lds + s * 32 + 8 * (lane & 3);
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        float a = 0.0f;
-#pragma unroll
-        for (int c = 0; c < KC; ++c) {
-            const uint32_t qw[8] = {q0[r][c].x, q0[r][c].y, q0[r][c].z, q0[r][c].w,
-                                    q1[r][c].x, q1[r][c].y, q1[r][c].z, q1[r][c].w};
-            float alo = 0.0f, ahi = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 8; ++t) {
-                const uint32_t p0 = __builtin_amdgcn_perm(0u, qw[t], 0x0c010c00u);  // bytes 4t, 4t+1
-                const uint32_t p1 = __builtin_amdgcn_perm(0u, qw[t], 0x0c030c02u);  // bytes 4t+2, 4t+3
-                // (q | 0x4300) is the bf16 of 128 + q
-                alo = dot2_bf16((p0 & 0x000F000Fu) | 0x43004300u, xlo[c][2 * t], alo);
-                alo = dot2_bf16((p1 & 0x000F000Fu) | 0x43004300u, xlo[c][2 * t + 1], alo);
-                ahi = dot2_bf16(((p0 >> 4) & 0x000F000Fu) | 0x43004300u, xhi[c][2 * t], ahi);
-                ahi = dot2_bf16(((p1 >> 4) & 0x000F000Fu) | 0x43004300u, xhi[c][2 * t + 1], ahi);
-            }
-            const float dlo = alo - 128.0f * sxlo[c];  // sum x*q over sub-block 2p
-            const float dhi = ahi - 128.0f * sxhi[c];  // sum x*q over sub-block 2p+1
-            const uint4 h = hdr[r][c];
-            uint32_t sc0, m0, sc1, m1;
-            scale_min_k4(2 * part, h.y, h.z, h.w, sc0, m0);
-            scale_min_k4(2 * part + 1, h.y, h.z, h.w, sc1, m1);
-            const float d = f16_to_f32(h.x & 0xFFFF), dmin = f16_to_f32(h.x >> 16);
-            a = __builtin_fmaf(d, (float)sc0 * dlo + (float)sc1 * dhi, a);
-            a = __builtin_fmaf(-dmin, (float)m0 * sxlo[c] + (float)m1 * sxhi[c], a);
+        for (int v = 0; v < 4; ++v) {
+            const uint4 p = xp[v], q = xp[4 + v];
+            xlo[4 * v] = p.x; xlo[4 * v + 1] = p.y; xlo[4 * v + 2] = p.z; xlo[4 * v + 3] = p.w;
+            xhi[4 * v] = q.x; xhi[4 * v + 1] = q.y; xhi[4 * v + 2] = q.z; xhi[4 * v + 3] = q.w;
         }
-        acc[r] = wave_sum(a);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            sxlo = dot2_bf16(xlo[i], 0x3F803F80u, sxlo);  // bf16 (1, 1)
+            sxhi = dot2_bf16(xhi[i], 0x3F803F80u, sxhi);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) { xlo[i] = 0; xhi[i] = 0; }
     }
-    write_rows<R, GU, YT>(y, base, nout, acc);
+    float acc[GU ? 8 : 4];
+#pragma unroll
+    for (int i = 0; i < (GU ? 8 : 4); ++i) acc[i] = 0.0f;
+    q4k_unit_compute<GU>(acc, A, xlo, xhi, sxlo, sxhi);
+    q4k_unit_store<GU, YT>(y, gq, nout, lane, acc);
 }
 
 // ------------------------------------------------------------------ Q4_K M=1, f32 x
@@ -152,7 +346,6 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_f32(const uint8_t* __restrict
     const int64_t base = wave * (GU ? R / 2 : R);
     if (base >= nout) return;
     const int nsb = K >> 8;
-    const int64_t rb = (int64_t)nsb * THQ_Q4K_BYTES;
     const int sl = lane >> 2, part = lane & 3;
 
     float acc[R];
@@ -178,10 +371,13 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_f32(const uint8_t* __restrict
             int64_t row = slot_row<R, GU>(base, r, up_off);
             const bool ok = GU ? (base + (r >> 1) < nout) : (row < nout);
             if (!ok) row = GU ? up_off * (r & 1) : 0;
-            const uint8_t* blk = W + row * rb + (int64_t)s * THQ_Q4K_BYTES;
-            const uint4 h = *reinterpret_cast<const uint4*>(blk);
-            const uint4 a4 = *reinterpret_cast<const uint4*>(blk + 16 + 32 * part);
-            const uint4 b4 = *reinterpret_cast<const uint4*>(blk + 32 + 32 * part);
+            uint4 h;
+            h.x = *reinterpret_cast<const uint32_t*>(W + q4k_hdword(row, nsb, s, 0));
+            h.y = *reinterpret_cast<const uint32_t*>(W + q4k_hdword(row, nsb, s, 1));
+            h.z = *reinterpret_cast<const uint32_t*>(W + q4k_hdword(row, nsb, s, 2));
+            h.w = *reinterpret_cast<const uint32_t*>(W + q4k_hdword(row, nsb, s, 3));
+            const uint4 a4 = *reinterpret_cast<const uint4*>(W + q4k_piece(row, nsb, s, 0, part));
+            const uint4 b4 = *reinterpret_cast<const uint4*>(W + q4k_piece(row, nsb, s, 1, part));
             const uint32_t qw[8] = {a4.x, a4.y, a4.z, a4.w, b4.x, b4.y, b4.z, b4.w};
             float dl = 0.0f, dh = 0.0f;
 #pragma unroll
@@ -193,9 +389,9 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_f32(const uint8_t* __restrict
                 }
             }
             uint32_t sc0, m0, sc1, m1;
-            scale_min_k4(2 * part, h.y, h.z, h.w, sc0, m0);
-            scale_min_k4(2 * part + 1, h.y, h.z, h.w, sc1, m1);
-            const float d = f16_to_f32(h.x & 0xFFFF), dmin = f16_to_f32(h.x >> 16);
+            q4k_hdr_sm(h, 2 * part, sc0, m0);
+            q4k_hdr_sm(h, 2 * part + 1, sc1, m1);
+            const float d = q4k_hdr_d(h), dmin = q4k_hdr_dmin(h);
             acc[r] = __builtin_fmaf(d, (float)sc0 * dl + (float)sc1 * dh, acc[r]);
             acc[r] = __builtin_fmaf(-dmin, (float)m0 * sxl + (float)m1 * sxh, acc[r]);
         }
@@ -282,7 +478,7 @@ __global__ __launch_bounds__(256) void k_gemv1_q8(const int8_t* __restrict__ Q, 
 // sub-blocks, dequantize them exactly to f32 and dot with up to 8
 // activation rows read with scalar loads (any alignment).
 template <int QT, bool GU, typename XT, typename YT>
-__global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict__ Wq, const uint16_t* __restrict__ Wd,
+__global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Wa,
                                                      const XT* __restrict__ x, YT* __restrict__ y, int M,
                                                      int64_t nout, int K, int64_t up_off, int64_t ldy) {
     const int lane = threadIdx.x & 63;
@@ -301,19 +497,25 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict_
             const int64_t row = o + (r ? up_off : 0);
             float wv[32];
             if (QT == 12) {
-                const uint8_t* blk = Wq + row * (int64_t)(K >> 8) * THQ_Q4K_BYTES + (int64_t)(sbi >> 3) * THQ_Q4K_BYTES;
-                const int j = sbi & 7;
-                const uint4 h = *reinterpret_cast<const uint4*>(blk);
+                const int nsb = K >> 8, s = sbi >> 3, j = sbi & 7;
+                uint4 h;
+                h.x = *reinterpret_cast<const uint32_t*>(Wq + q4k_hdword(row, nsb, s, 0));
+                h.y = *reinterpret_cast<const uint32_t*>(Wq + q4k_hdword(row, nsb, s, 1));
+                h.z = *reinterpret_cast<const uint32_t*>(Wq + q4k_hdword(row, nsb, s, 2));
+                h.w = *reinterpret_cast<const uint32_t*>(Wq + q4k_hdword(row, nsb, s, 3));
                 uint32_t sc, mm;
-                scale_min_k4(j, h.y, h.z, h.w, sc, mm);
-                const float d1 = f16_to_f32(h.x & 0xFFFF) * (float)sc, m1 = f16_to_f32(h.x >> 16) * (float)mm;
-                const uint8_t* q = blk + 16 + 32 * (j >> 1);
+                q4k_hdr_sm(h, j, sc, mm);
+                const float d1 = q4k_hdr_d(h) * (float)sc, m1 = q4k_hdr_dmin(h) * (float)mm;
                 const int sh = (j & 1) * 4;
 #pragma unroll
-                for (int i = 0; i < 32; ++i) wv[i] = d1 * (float)((q[i] >> sh) & 0xF) - m1;
+                for (int hh = 0; hh < 2; ++hh) {
+                    const uint8_t* q = Wq + q4k_piece(row, nsb, s, hh, j >> 1);
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) wv[16 * hh + i] = d1 * (float)((q[i] >> sh) & 0xF) - m1;
+                }
             } else {
                 const int8_t* q = reinterpret_cast<const int8_t*>(Wq) + row * K + 32 * sbi;
-                const float d = f16_to_f32(Wd[row * nsub + sbi]);
+                const float d = f16_to_f32(reinterpret_cast<const uint16_t*>(Wa)[row * nsub + sbi]);
 #pragma unroll
                 for (int i = 0; i < 32; ++i) wv[i] = (float)q[i] * d;
             }
@@ -344,62 +546,49 @@ static inline int env_int(const char* name, int dflt) {
     return v && *v ? atoi(v) : dflt;
 }
 
-template <int KC, int R, bool GU, typename YT>
+// resident waves per CU (tunable: THQ_GEMV_WPC)
+template <bool GU, typename YT>
 static void launch_q4k_bf16_t(const uint8_t* W, const bf16_t* x, YT* y, int64_t nout, int K, int64_t up_off,
                               hipStream_t s) {
-    const int64_t per_wave = GU ? R / 2 : R;
-    const int64_t waves = (nout + per_wave - 1) / per_wave;
-    hipLaunchKernelGGL((k_gemv1_q4k_bf16<KC, R, GU, YT>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, W, x,
-                       y, nout, K, up_off);
-}
-
-template <int KC, bool GU, typename YT>
-static void pick_r_q4k_bf16(int R, const uint8_t* W, const bf16_t* x, YT* y, int64_t nout, int K, int64_t up_off,
-                            hipStream_t s) {
-    if constexpr (GU) {
-        if (R >= 4) launch_q4k_bf16_t<KC, 4, GU, YT>(W, x, y, nout, K, up_off, s);
-        else launch_q4k_bf16_t<KC, 2, GU, YT>(W, x, y, nout, K, up_off, s);
-    } else {
-        if (R >= 4) launch_q4k_bf16_t<KC, 4, GU, YT>(W, x, y, nout, K, up_off, s);
-        else if (R == 2) launch_q4k_bf16_t<KC, 2, GU, YT>(W, x, y, nout, K, up_off, s);
-        else launch_q4k_bf16_t<KC, 1, GU, YT>(W, x, y, nout, K, up_off, s);
+    const int64_t nquads = (nout + 3) / 4;
+    const int wpc = env_int("THQ_GEMV_WPC", 8);
+    int64_t waves = (int64_t)256 * (wpc > 0 ? wpc : 8);
+    if (waves > nquads) waves = nquads;
+    const size_t lds = (size_t)K * 2;
+    if (K <= 4096 && env_int("THQ_GEMV_ONESHOT", 1)) {
+        hipLaunchKernelGGL((k_gemv1_q4k_bf16_1s<GU, YT>), dim3((unsigned)((nquads + 3) / 4)), dim3(256), lds, s, W, x,
+                           y, nout, K, up_off, nquads);
+        return;
+    }
+    const unsigned grid = (unsigned)((waves + 3) / 4);
+    switch ((K / 256 + 15) / 16) {
+        case 1: hipLaunchKernelGGL((k_gemv1_q4k_bf16<1, GU, YT>), dim3(grid), dim3(256), lds, s, W, x, y, nout, K, up_off, nquads); break;
+        case 2: hipLaunchKernelGGL((k_gemv1_q4k_bf16<2, GU, YT>), dim3(grid), dim3(256), lds, s, W, x, y, nout, K, up_off, nquads); break;
+        case 3: hipLaunchKernelGGL((k_gemv1_q4k_bf16<3, GU, YT>), dim3(grid), dim3(256), lds, s, W, x, y, nout, K, up_off, nquads); break;
+        default: hipLaunchKernelGGL((k_gemv1_q4k_bf16<4, GU, YT>), dim3(grid), dim3(256), lds, s, W, x, y, nout, K, up_off, nquads); break;
     }
 }
 
-// default rows per wave: enough waves to fill 256 CUs several times over
-static int default_r(int64_t nrows, int kc) {
-    const int r = env_int("THQ_GEMV_R", 0);
-    if (r > 0) return r;
-    if (kc >= 2) return 1;
-    return nrows >= 8192 ? 2 : 1;
-}
-
 template <bool GU, typename YT>
-static hipError_t gemv1_q4k_t(const uint8_t* W, const void* x, bool xf32, YT* y, int64_t nout, int K,
-                              int64_t up_off, hipStream_t s) {
+static hipError_t gemv1_q4k_t(const uint8_t* W, const void* x, bool xf32, YT* y, int64_t nout, int K, int64_t up_off,
+                              hipStream_t s) {
     const int kc = (K + 4095) / 4096;
-    const int R = default_r(GU ? 2 * nout : nout, kc) * (GU ? 2 : 1);
     if (!xf32) {
-        const bf16_t* xb = static_cast<const bf16_t*>(x);
-        switch (kc) {
-            case 1: pick_r_q4k_bf16<1, GU, YT>(R, W, xb, y, nout, K, up_off, s); break;
-            case 2: pick_r_q4k_bf16<2, GU, YT>(R, W, xb, y, nout, K, up_off, s); break;
-            case 3: pick_r_q4k_bf16<3, GU, YT>(R, W, xb, y, nout, K, up_off, s); break;
-            case 4: pick_r_q4k_bf16<4, GU, YT>(R, W, xb, y, nout, K, up_off, s); break;
-            default: return hipErrorInvalidValue;
-        }
+        launch_q4k_bf16_t<GU, YT>(W, static_cast<const bf16_t*>(x), y, nout, K, up_off, s);
     } else {
         const float* xf = static_cast<const float*>(x);
         constexpr int RR = GU ? 2 : 1;
-        const int64_t waves = nout;
-        const unsigned grid = (unsigned)((waves + 3) / 4);
+        const unsigned grid = (unsigned)((nout + 3) / 4);
+#define THQ_F32(KC_) \
+    hipLaunchKernelGGL((k_gemv1_q4k_f32<KC_, RR, GU, YT>), dim3(grid), dim3(256), 0, s, W, xf, y, nout, K, up_off)
         switch (kc) {
-            case 1: hipLaunchKernelGGL((k_gemv1_q4k_f32<1, RR, GU, YT>), dim3(grid), dim3(256), 0, s, W, xf, y, nout, K, up_off); break;
-            case 2: hipLaunchKernelGGL((k_gemv1_q4k_f32<2, RR, GU, YT>), dim3(grid), dim3(256), 0, s, W, xf, y, nout, K, up_off); break;
-            case 3: hipLaunchKernelGGL((k_gemv1_q4k_f32<3, RR, GU, YT>), dim3(grid), dim3(256), 0, s, W, xf, y, nout, K, up_off); break;
-            case 4: hipLaunchKernelGGL((k_gemv1_q4k_f32<4, RR, GU, YT>), dim3(grid), dim3(256), 0, s, W, xf, y, nout, K, up_off); break;
+            case 1: THQ_F32(1); break;
+            case 2: THQ_F32(2); break;
+            case 3: THQ_F32(3); break;
+            case 4: THQ_F32(4); break;
             default: return hipErrorInvalidValue;
         }
+#undef THQ_F32
     }
     return hipGetLastError();
 }
@@ -431,8 +620,8 @@ static hipError_t gemv1_q8_t(const int8_t* Q, const uint16_t* D, const XT* x, YT
     return hipGetLastError();
 }
 
-bool gemv1_supported(int qtype, int K) {
-    if (qtype == 12) return K % 256 == 0 && K <= 4 * 4096;
+bool gemv1_supported(int qtype, int K, bool gu, int64_t n_rows) {
+    if (qtype == 12) return K % 256 == 0 && K <= 4 * 4096 && (!gu || (n_rows / 2) % 4 == 0);
     return K % 32 == 0 && K <= 8 * 1024;
 }
 
@@ -448,7 +637,8 @@ hipError_t launch_gemv1(const WeightView& w, const void* x, bool xf32, void* y, 
                     : gemv1_q4k_t<false, bf16_t>(w.q, x, xf32, (bf16_t*)y, nout, K, up_off, s);
     }
     const int8_t* Q = reinterpret_cast<const int8_t*>(w.q);
-#define THQ_Q8(GU_, XT_, YT_) gemv1_q8_t<GU_, XT_, YT_>(Q, w.d, (const XT_*)x, (YT_*)y, nout, K, up_off, s)
+    const uint16_t* D = reinterpret_cast<const uint16_t*>(w.aux);
+#define THQ_Q8(GU_, XT_, YT_) gemv1_q8_t<GU_, XT_, YT_>(Q, D, (const XT_*)x, (YT_*)y, nout, K, up_off, s)
     if (gu) {
         if (xf32) return yf32 ? THQ_Q8(true, float, float) : THQ_Q8(true, float, bf16_t);
         return yf32 ? THQ_Q8(true, bf16_t, float) : THQ_Q8(true, bf16_t, bf16_t);
@@ -464,7 +654,7 @@ static hipError_t generic_t(const WeightView& w, const XT* x, YT* y, int M, int6
     for (int m0 = 0; m0 < M; m0 += 8) {
         const int mm = M - m0 < 8 ? M - m0 : 8;
         hipLaunchKernelGGL((k_gemv_generic<QT, GU, XT, YT>), dim3((unsigned)((nout + 3) / 4)), dim3(256), 0, s, w.q,
-                           w.d, x + (int64_t)m0 * w.K, y + (int64_t)m0 * ldy, mm, nout, (int)w.K, up_off, ldy);
+                           w.aux, x + (int64_t)m0 * w.K, y + (int64_t)m0 * ldy, mm, nout, (int)w.K, up_off, ldy);
     }
     return hipGetLastError();
 }

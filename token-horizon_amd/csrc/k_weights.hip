@@ -1,6 +1,7 @@
 // k_weights.hip — weight preparation kernels for gfx950:
 //   * repack GGUF Q8_0 blocks (34 B, 2-byte aligned) into an aligned i8 plane
-//     [N][K] plus an f16 scale plane [N][K/32]
+//     [N][K] plus an f16 scale plane [N][K/32]; GGUF Q4_K blocks into the
+//     row-quad layout (thq_dev.hpp, q4k_group)
 //   * quantize f32 weights on the device with candle's CPU rounding rules
 //     ([ext] candle-core 0.11.0 k_quants.rs BlockQ8_0/BlockQ4K::from_float,
 //     utils.rs make_qkx1_quants), bit-identical to the CPU quantizer
@@ -124,11 +125,12 @@ __device__ void make_qkx1_quants_32(const float* x, float& scale_out, float& min
     min_out = -min;
 }
 
-// 8 lanes per superblock: lane j runs make_qkx1_quants on sub-block j, lane 0
-// of the group packs the 6-bit scales, every lane requantizes its sub-block
-// and the even lane of each pair writes the 32 shared bytes.
-__global__ __launch_bounds__(256) void k_quantize_q4k(const float* __restrict__ w, uint8_t* __restrict__ out,
-                                                      int64_t nsuper) {
+// 8 lanes per superblock: lane j runs make_qkx1_quants on sub-block j, the
+// group OR-reduces the 6-bit scales into the on-device header (lanes 0..3
+// write its four dwords), every lane requantizes its sub-block and the even
+// lane of each pair writes the 32 shared nibble bytes as two 16-B pieces.
+__global__ __launch_bounds__(256) void k_quantize_q4k(const float* __restrict__ w, uint8_t* __restrict__ dst,
+                                                      int64_t nsuper, int nsb) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t sb = t >> 3;
     const int j = (int)(t & 7);
@@ -155,34 +157,32 @@ __global__ __launch_bounds__(256) void k_quantize_q4k(const float* __restrict__ 
     const int lmi = nearest_int(inv_min * minv);
     const uint32_t ls = (uint32_t)(uint8_t)(lsi < 63 ? lsi : 63);
     const uint32_t lm = (uint32_t)(uint8_t)(lmi < 63 ? lmi : 63);
-    // pack the 12 scale bytes: every lane builds its contribution, OR-reduce
-    uint32_t s0 = 0, s1 = 0, s2 = 0;  // bytes 0..3, 4..7, 8..11
-    if (j < 4) {
-        s0 |= ls << (8 * j);
-        s1 |= lm << (8 * j);
-    } else {
-        const int i = j - 4;
-        s2 |= ((ls & 0xFu) | ((lm & 0xFu) << 4)) << (8 * i);
-        s0 |= ((ls >> 4) << 6) << (8 * i);
-        s1 |= ((lm >> 4) << 6) << (8 * i);
+    // on-device header: lane j owns 12 bits of H[j/2]; OR-reduce over the group
+    uint32_t h0 = 0, h1 = 0, h2 = 0, h3 = 0;
+    {
+        const uint32_t f = (ls | (lm << 6)) << (12 * (j & 1));
+        h0 = (j >> 1) == 0 ? f : 0u;
+        h1 = (j >> 1) == 1 ? f : 0u;
+        h2 = (j >> 1) == 2 ? f : 0u;
+        h3 = (j >> 1) == 3 ? f : 0u;
     }
 #pragma unroll
     for (int off = 1; off < 8; off <<= 1) {
-        s0 |= __shfl_xor(s0, off, 64);
-        s1 |= __shfl_xor(s1, off, 64);
-        s2 |= __shfl_xor(s2, off, 64);
+        h0 |= __shfl_xor(h0, off, 64);
+        h1 |= __shfl_xor(h1, off, 64);
+        h2 |= __shfl_xor(h2, off, 64);
+        h3 |= __shfl_xor(h3, off, 64);
     }
     const _Float16 dh = (_Float16)(max_scale / 63.0f);
     const _Float16 mh = (_Float16)(max_min / 63.0f);
-    // requantize this sub-block against the stored scale/min
-    uint32_t sc, m;
-    scale_min_k4(j, s0, s1, s2, sc, m);
-    const float d = (float)dh * (float)sc;
+    // requantize this sub-block against the stored scale/min (ls, lm are what
+    // get_scale_min_k4 returns for this sub-block: the packing is lossless)
+    const float d = (float)dh * (float)ls;
     uint32_t L[8];  // 32 nibble values, one per byte
 #pragma unroll
     for (int i = 0; i < 8; ++i) L[i] = 0;
     if (d != 0.0f) {
-        const float dm = (float)mh * (float)m;
+        const float dm = (float)mh * (float)lm;
 #pragma unroll
         for (int i = 0; i < 32; ++i) {
             int lv = nearest_int((x[i] + dm) / d);
@@ -198,17 +198,20 @@ __global__ __launch_bounds__(256) void k_quantize_q4k(const float* __restrict__ 
         P[i] = (j & 1) ? 0u : (L[i] | (other << 4));
     }
     if (!live) return;
-    uint8_t* blk = out + sb * THQ_Q4K_BYTES;
-    if (j == 0) {
+    const int64_t n = sb / nsb;
+    const int sidx = (int)(sb - n * nsb);
+    if (j < 4) {  // header dword j of this row
         uint16_t dbits, mbits;
         __builtin_memcpy(&dbits, &dh, 2);
         __builtin_memcpy(&mbits, &mh, 2);
-        *reinterpret_cast<uint4*>(blk) = make_uint4((uint32_t)dbits | ((uint32_t)mbits << 16), s0, s1, s2);
+        const uint32_t dd = (uint32_t)dbits | ((uint32_t)mbits << 16);
+        const uint32_t hw = j == 0 ? h0 : (j == 1 ? h1 : (j == 2 ? h2 : h3));
+        *reinterpret_cast<uint32_t*>(dst + q4k_hdword(n, nsb, sidx, j)) = hw | (((dd >> (8 * j)) & 0xFFu) << 24);
     }
     if ((j & 1) == 0) {
-        uint4* dst = reinterpret_cast<uint4*>(blk + 16 + 32 * (j >> 1));
-        dst[0] = make_uint4(P[0], P[1], P[2], P[3]);
-        dst[1] = make_uint4(P[4], P[5], P[6], P[7]);
+        const int part = j >> 1;
+        *reinterpret_cast<uint4*>(dst + q4k_piece(n, nsb, sidx, 0, part)) = make_uint4(P[0], P[1], P[2], P[3]);
+        *reinterpret_cast<uint4*>(dst + q4k_piece(n, nsb, sidx, 1, part)) = make_uint4(P[4], P[5], P[6], P[7]);
     }
 }
 
@@ -239,24 +242,28 @@ __global__ __launch_bounds__(256) void k_dequant_q8_0(const int8_t* __restrict__
 }
 
 // one thread per (superblock, sub-block j): y = d*sc*q - dmin*m
-__global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__ raw, float* __restrict__ out,
-                                                     int64_t nsuper) {
+__global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__ src, float* __restrict__ out,
+                                                     int64_t nsuper, int nsb) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t sb = t >> 3;
     const int j = (int)(t & 7);
     if (sb >= nsuper) return;
-    const uint8_t* blk = raw + sb * THQ_Q4K_BYTES;
-    const uint4 h = *reinterpret_cast<const uint4*>(blk);
-    const float d = f16_to_f32(h.x & 0xFFFF), dmin = f16_to_f32(h.x >> 16);
+    const int64_t n = sb / nsb;
+    const int sidx = (int)(sb - n * nsb);
+    uint4 h;
+    h.x = *reinterpret_cast<const uint32_t*>(src + q4k_hdword(n, nsb, sidx, 0));
+    h.y = *reinterpret_cast<const uint32_t*>(src + q4k_hdword(n, nsb, sidx, 1));
+    h.z = *reinterpret_cast<const uint32_t*>(src + q4k_hdword(n, nsb, sidx, 2));
+    h.w = *reinterpret_cast<const uint32_t*>(src + q4k_hdword(n, nsb, sidx, 3));
+    const float d = q4k_hdr_d(h), dmin = q4k_hdr_dmin(h);
     uint32_t sc, m;
-    scale_min_k4(j, h.y, h.z, h.w, sc, m);
+    q4k_hdr_sm(h, j, sc, m);
     const float d1 = d * (float)sc, m1 = dmin * (float)m;
-    const uint4* q = reinterpret_cast<const uint4*>(blk + 16 + 32 * (j >> 1));
     const int shift = (j & 1) * 4;
     float4* dst = reinterpret_cast<float4*>(out + sb * THQ_QK_K + 32 * j);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
-        const uint4 v = q[hh];
+        const uint4 v = *reinterpret_cast<const uint4*>(src + q4k_piece(n, nsb, sidx, hh, j >> 1));
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -268,6 +275,42 @@ __global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__
             dst[4 * hh + i] = o;
         }
     }
+}
+
+// ---------------------------------------------------------------- Q4_K repack
+// one thread per superblock: GGUF 144-B block -> row-quad layout
+__global__ __launch_bounds__(256) void k_repack_q4k(const uint8_t* __restrict__ gguf, uint8_t* __restrict__ dst,
+                                                    int64_t nsuper, int nsb) {
+    const int64_t sb = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (sb >= nsuper) return;
+    const int64_t n = sb / nsb;
+    const int sidx = (int)(sb - n * nsb);
+    const uint4* src = reinterpret_cast<const uint4*>(gguf + sb * THQ_Q4K_BYTES);
+    const uint4 h = q4k_hdr_from_gguf(src[0]);
+    const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+    for (int p = 0; p < 4; ++p) *reinterpret_cast<uint32_t*>(dst + q4k_hdword(n, nsb, sidx, p)) = hw[p];
+#pragma unroll
+    for (int c = 0; c < 8; ++c)  // 16-B chunk c of the nibbles = part c/2, half c%2
+        *reinterpret_cast<uint4*>(dst + q4k_piece(n, nsb, sidx, c & 1, c >> 1)) = src[1 + c];
+}
+
+// one thread per (source row, superblock): copy between row-quad planes
+__global__ __launch_bounds__(256) void k_q4k_copy_rows(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                       int64_t nsuper, int64_t dst_row0, int nsb) {
+    const int64_t sb = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (sb >= nsuper) return;
+    const int64_t n = sb / nsb;
+    const int sidx = (int)(sb - n * nsb);
+    const int64_t m = dst_row0 + n;
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+        *reinterpret_cast<uint32_t*>(dst + q4k_hdword(m, nsb, sidx, p)) =
+            *reinterpret_cast<const uint32_t*>(src + q4k_hdword(n, nsb, sidx, p));
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+        *reinterpret_cast<uint4*>(dst + q4k_piece(m, nsb, sidx, c & 1, c >> 1)) =
+            *reinterpret_cast<const uint4*>(src + q4k_piece(n, nsb, sidx, c & 1, c >> 1));
 }
 
 // ---------------------------------------------------------------- launchers
@@ -285,9 +328,26 @@ hipError_t launch_quantize_q8_0(const float* w, int8_t* qs, uint16_t* d, int64_t
     return hipGetLastError();
 }
 
-hipError_t launch_quantize_q4k(const float* w, uint8_t* out, int64_t nsuper, hipStream_t s) {
+hipError_t launch_quantize_q4k(const float* w, uint8_t* dst, int64_t n, int nsb, hipStream_t s) {
+    const int64_t nsuper = n * nsb;
     if (nsuper == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_quantize_q4k, dim3(grid_for(nsuper * 8, 256)), dim3(256), 0, s, w, out, nsuper);
+    hipLaunchKernelGGL(k_quantize_q4k, dim3(grid_for(nsuper * 8, 256)), dim3(256), 0, s, w, dst, nsuper, nsb);
+    return hipGetLastError();
+}
+
+hipError_t launch_repack_q4k(const uint8_t* gguf, uint8_t* dst, int64_t n, int nsb, hipStream_t s) {
+    const int64_t nsuper = n * nsb;
+    if (nsuper == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_repack_q4k, dim3(grid_for(nsuper, 256)), dim3(256), 0, s, gguf, dst, nsuper, nsb);
+    return hipGetLastError();
+}
+
+hipError_t launch_q4k_copy_rows(const uint8_t* src, int64_t n, uint8_t* dst, int64_t dst_row0, int nsb,
+                                hipStream_t s) {
+    const int64_t nsuper = n * nsb;
+    if (nsuper == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_q4k_copy_rows, dim3(grid_for(nsuper, 256)), dim3(256), 0, s, src, dst, nsuper, dst_row0,
+                       nsb);
     return hipGetLastError();
 }
 
@@ -297,9 +357,10 @@ hipError_t launch_dequant_q8_0(const int8_t* qs, const uint16_t* d, float* out, 
     return hipGetLastError();
 }
 
-hipError_t launch_dequant_q4k(const uint8_t* raw, float* out, int64_t nsuper, hipStream_t s) {
+hipError_t launch_dequant_q4k(const uint8_t* src, float* out, int64_t n, int nsb, hipStream_t s) {
+    const int64_t nsuper = n * nsb;
     if (nsuper == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_dequant_q4k, dim3(grid_for(nsuper * 8, 256)), dim3(256), 0, s, raw, out, nsuper);
+    hipLaunchKernelGGL(k_dequant_q4k, dim3(grid_for(nsuper * 8, 256)), dim3(256), 0, s, src, out, nsuper, nsb);
     return hipGetLastError();
 }
 

@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "../../include/thq.h"
+#include "thq_dev.hpp"
 #include "thq_kernels.hpp"
 
 struct thq_ctx {
@@ -31,8 +32,8 @@ struct thq_weight {
     thq_ctx* ctx = nullptr;
     int qtype = 0;
     int64_t N = 0, K = 0;
-    uint8_t* q = nullptr;    // Q4_K superblocks, or Q8_0 i8 plane
-    uint16_t* d = nullptr;   // Q8_0 f16 scale plane
+    uint8_t* q = nullptr;    // Q8_0 i8 plane / Q4_K nibble plane
+    uint8_t* aux = nullptr;  // Q8_0 f16 scale plane / Q4_K header plane
 };
 
 namespace {
@@ -62,7 +63,17 @@ size_t gguf_bytes(int qtype, int64_t n, int64_t k) {
     return (size_t)n * (size_t)(k / 256) * 144;
 }
 
-thq::WeightView view(const thq_weight* w) { return thq::WeightView{w->qtype, w->N, w->K, w->q, w->d}; }
+thq::WeightView view(const thq_weight* w) { return thq::WeightView{w->qtype, w->N, w->K, w->q, w->aux}; }
+
+// device plane sizes: Q8_0 = i8 plane + f16 scale plane; Q4_K = one row-quad
+// plane (rows padded to a multiple of 4, padding zero)
+size_t q_plane_bytes(int qtype, int64_t n, int64_t k) {
+    if (qtype == THQ_Q8_0) return (size_t)n * (size_t)k;
+    return (size_t)((n + 3) / 4) * (size_t)(k / 256) * 576;
+}
+size_t aux_plane_bytes(int qtype, int64_t n, int64_t k) {
+    return qtype == THQ_Q8_0 ? (size_t)n * (size_t)(k / 32) * 2 : 0;
+}
 
 int check_dtype_shape(int dtype, int64_t n, int64_t k) {
     const int bs = block_of(dtype);
@@ -80,19 +91,16 @@ int alloc_weight(thq_ctx* ctx, int dtype, int64_t n, int64_t k, thq_weight** out
     w->qtype = dtype;
     w->N = n;
     w->K = k;
-    size_t qb = dtype == THQ_Q8_0 ? (size_t)n * (size_t)k : gguf_bytes(dtype, n, k);
+    const size_t qb = q_plane_bytes(dtype, n, k), ab = aux_plane_bytes(dtype, n, k);
     hipError_t e = hipMalloc((void**)&w->q, qb);
+    if (e == hipSuccess && dtype == THQ_Q4_K && (n & 3)) e = hipMemset(w->q, 0, qb);  // zero padding rows
+    if (e == hipSuccess && ab) {
+        e = hipMalloc((void**)&w->aux, ab);
+        if (e != hipSuccess) (void)hipFree(w->q);
+    }
     if (e != hipSuccess) {
         delete w;
-        return fail(THQ_ENOMEM, "hipMalloc(%zu) for weight: %s", qb, hipGetErrorString(e));
-    }
-    if (dtype == THQ_Q8_0) {
-        e = hipMalloc((void**)&w->d, (size_t)n * (size_t)(k / 32) * 2);
-        if (e != hipSuccess) {
-            (void)hipFree(w->q);
-            delete w;
-            return fail(THQ_ENOMEM, "hipMalloc for Q8_0 scales: %s", hipGetErrorString(e));
-        }
+        return fail(THQ_ENOMEM, "hipMalloc(%zu + %zu) for weight: %s", qb, ab, hipGetErrorString(e));
     }
     *out = w;
     return THQ_OK;
@@ -146,7 +154,7 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
     const int64_t nout = gu ? w->N / 2 : w->N;
     const int64_t up_off = gu ? w->N / 2 : 0;
     hipError_t e;
-    if (m == 1 && aligned16(x) && thq::gemv1_supported(w->qtype, (int)w->K)) {
+    if (m == 1 && aligned16(x) && thq::gemv1_supported(w->qtype, (int)w->K, gu, w->N)) {
         e = thq::launch_gemv1(v, x, xf32, y, yf32, gu, nout, up_off, s);
     } else if (!xf32 && aligned16(x) && !(w->qtype == THQ_Q4_K && (flags & THQ_MODE_EXACT_W))) {
         const bool exact = (flags & THQ_MODE_EXACT_W) || (w->qtype == THQ_Q8_0 && m <= 64);
@@ -201,18 +209,6 @@ int thq_weight_upload(thq_ctx* ctx, thq_dtype dtype, const void* host_blocks, in
     if (rc) return rc;
     DeviceGuard g(ctx->device);
     const size_t bytes = gguf_bytes(dtype, n, k);
-    if (dtype == THQ_Q4_K) {
-        thq_weight* w = nullptr;
-        rc = alloc_weight(ctx, dtype, n, k, &w);
-        if (rc) return rc;
-        hipError_t e = hipMemcpy(w->q, host_blocks, bytes, hipMemcpyHostToDevice);
-        if (e != hipSuccess) {
-            thq_weight_free(w);
-            return fail(THQ_EHIP, "hipMemcpy weight: %s", hipGetErrorString(e));
-        }
-        *out = w;
-        return THQ_OK;
-    }
     void* staging = nullptr;
     hipError_t e = hipMalloc(&staging, bytes);
     if (e != hipSuccess) return fail(THQ_ENOMEM, "hipMalloc staging(%zu): %s", bytes, hipGetErrorString(e));
@@ -221,11 +217,7 @@ int thq_weight_upload(thq_ctx* ctx, thq_dtype dtype, const void* host_blocks, in
         (void)hipFree(staging);
         return fail(THQ_EHIP, "hipMemcpy weight: %s", hipGetErrorString(e));
     }
-    rc = thq_weight_from_device(ctx, dtype, staging, n, k, nullptr, out);
-    if (rc == THQ_OK) {
-        e = hipStreamSynchronize(nullptr);
-        if (e != hipSuccess) rc = fail(THQ_EHIP, "sync after repack: %s", hipGetErrorString(e));
-    }
+    rc = thq_weight_from_device(ctx, dtype, staging, n, k, nullptr, out);  // synchronizes
     (void)hipFree(staging);
     return rc;
 }
@@ -240,16 +232,15 @@ int thq_weight_from_device(thq_ctx* ctx, thq_dtype dtype, const void* dev_blocks
     thq_weight* w = nullptr;
     rc = alloc_weight(ctx, dtype, n, k, &w);
     if (rc) return rc;
-    hipError_t e;
-    if (dtype == THQ_Q4_K)
-        e = hipMemcpyAsync(w->q, dev_blocks, gguf_bytes(dtype, n, k), hipMemcpyDeviceToDevice, s);
-    else
-        e = thq::launch_repack_q8_0(static_cast<const uint8_t*>(dev_blocks), reinterpret_cast<int8_t*>(w->q), w->d,
-                                    n * (k / 32), s);
+    const uint8_t* src = static_cast<const uint8_t*>(dev_blocks);
+    hipError_t e = dtype == THQ_Q4_K
+                       ? thq::launch_repack_q4k(src, w->q, n, (int)(k / 256), s)
+                       : thq::launch_repack_q8_0(src, reinterpret_cast<int8_t*>(w->q),
+                                                 reinterpret_cast<uint16_t*>(w->aux), n * (k / 32), s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
         thq_weight_free(w);
-        return fail(THQ_EHIP, "weight from device: %s", hipGetErrorString(e));
+        return fail(THQ_EHIP, "weight repack: %s", hipGetErrorString(e));
     }
     *out = w;
     return THQ_OK;
@@ -267,8 +258,9 @@ int thq_quantize(thq_ctx* ctx, thq_dtype dtype, const float* w_dev, int64_t n, i
     rc = alloc_weight(ctx, dtype, n, k, &w);
     if (rc) return rc;
     hipError_t e = dtype == THQ_Q8_0
-                       ? thq::launch_quantize_q8_0(w_dev, reinterpret_cast<int8_t*>(w->q), w->d, n * (k / 32), s)
-                       : thq::launch_quantize_q4k(w_dev, w->q, n * (k / 256), s);
+                       ? thq::launch_quantize_q8_0(w_dev, reinterpret_cast<int8_t*>(w->q),
+                                                   reinterpret_cast<uint16_t*>(w->aux), n * (k / 32), s)
+                       : thq::launch_quantize_q4k(w_dev, w->q, n, (int)(k / 256), s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
         thq_weight_free(w);
@@ -295,20 +287,29 @@ int thq_weight_fuse(thq_ctx* ctx, const thq_weight* const* parts, int nparts, th
     thq_weight* w = nullptr;
     int rc = alloc_weight(ctx, dtype, n, k, &w);
     if (rc) return rc;
-    size_t qoff = 0, doff = 0;
+    size_t qoff = 0, aoff = 0;
+    int64_t row0 = 0;
     for (int i = 0; i < nparts; ++i) {
-        const size_t qb = dtype == THQ_Q8_0 ? (size_t)parts[i]->N * (size_t)k : gguf_bytes(dtype, parts[i]->N, k);
-        hipError_t e = hipMemcpy(w->q + qoff, parts[i]->q, qb, hipMemcpyDeviceToDevice);
-        if (e == hipSuccess && dtype == THQ_Q8_0) {
-            const size_t db = (size_t)parts[i]->N * (size_t)(k / 32) * 2;
-            e = hipMemcpy(reinterpret_cast<uint8_t*>(w->d) + doff, parts[i]->d, db, hipMemcpyDeviceToDevice);
-            doff += db;
+        hipError_t e;
+        if (dtype == THQ_Q4_K) {
+            e = thq::launch_q4k_copy_rows(parts[i]->q, parts[i]->N, w->q, row0, (int)(k / 256), nullptr);
+        } else {
+            const size_t qb = q_plane_bytes(dtype, parts[i]->N, k), ab = aux_plane_bytes(dtype, parts[i]->N, k);
+            e = hipMemcpy(w->q + qoff, parts[i]->q, qb, hipMemcpyDeviceToDevice);
+            if (e == hipSuccess) e = hipMemcpy(w->aux + aoff, parts[i]->aux, ab, hipMemcpyDeviceToDevice);
+            qoff += qb;
+            aoff += ab;
         }
+        row0 += parts[i]->N;
         if (e != hipSuccess) {
             thq_weight_free(w);
             return fail(THQ_EHIP, "fuse copy: %s", hipGetErrorString(e));
         }
-        qoff += qb;
+    }
+    hipError_t e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) {
+        thq_weight_free(w);
+        return fail(THQ_EHIP, "fuse: %s", hipGetErrorString(e));
     }
     *out = w;
     return THQ_OK;
@@ -318,7 +319,7 @@ void thq_weight_free(thq_weight* w) {
     if (!w) return;
     DeviceGuard g(w->ctx ? w->ctx->device : 0);
     if (w->q) (void)hipFree(w->q);
-    if (w->d) (void)hipFree(w->d);
+    if (w->aux) (void)hipFree(w->aux);
     delete w;
 }
 
@@ -334,18 +335,29 @@ int thq_weight_info(const thq_weight* w, thq_dtype* dtype, int64_t* n, int64_t* 
 int thq_weight_download(const thq_weight* w, void* host_blocks) {
     if (!w || !host_blocks) return fail(THQ_EINVAL, "null argument");
     DeviceGuard g(w->ctx->device);
+    std::vector<uint8_t> qs(q_plane_bytes(w->qtype, w->N, w->K));
+    std::vector<uint8_t> aux(aux_plane_bytes(w->qtype, w->N, w->K));
+    HIP_TRY(hipMemcpy(qs.data(), w->q, qs.size(), hipMemcpyDeviceToHost));
+    if (!aux.empty()) HIP_TRY(hipMemcpy(aux.data(), w->aux, aux.size(), hipMemcpyDeviceToHost));
+    uint8_t* dst = static_cast<uint8_t*>(host_blocks);
     if (w->qtype == THQ_Q4_K) {
-        HIP_TRY(hipMemcpy(host_blocks, w->q, gguf_bytes(w->qtype, w->N, w->K), hipMemcpyDeviceToHost));
+        const int nsb = (int)(w->K / 256);
+        for (int64_t n = 0; n < w->N; ++n) {
+            for (int s = 0; s < nsb; ++s) {
+                uint8_t* blk = dst + (n * nsb + s) * 144;
+                uint32_t hw[4];
+                for (int p = 0; p < 4; ++p) std::memcpy(&hw[p], qs.data() + thq::q4k_hdword(n, nsb, s, p), 4);
+                const uint4 h = thq::q4k_hdr_to_gguf(make_uint4(hw[0], hw[1], hw[2], hw[3]));
+                std::memcpy(blk, &h, 16);
+                for (int c = 0; c < 8; ++c)
+                    std::memcpy(blk + 16 + 16 * c, qs.data() + thq::q4k_piece(n, nsb, s, c & 1, c >> 1), 16);
+            }
+        }
         return THQ_OK;
     }
     const int64_t nb = w->N * (w->K / 32);
-    std::vector<int8_t> qs((size_t)(w->N * w->K));
-    std::vector<uint16_t> ds((size_t)nb);
-    HIP_TRY(hipMemcpy(qs.data(), w->q, qs.size(), hipMemcpyDeviceToHost));
-    HIP_TRY(hipMemcpy(ds.data(), w->d, ds.size() * 2, hipMemcpyDeviceToHost));
-    uint8_t* dst = static_cast<uint8_t*>(host_blocks);
     for (int64_t b = 0; b < nb; ++b) {
-        std::memcpy(dst + b * 34, &ds[(size_t)b], 2);
+        std::memcpy(dst + b * 34, aux.data() + 2 * b, 2);
         std::memcpy(dst + b * 34 + 2, qs.data() + b * 32, 32);
     }
     return THQ_OK;
@@ -357,9 +369,10 @@ int thq_dequantize(thq_ctx* ctx, const thq_weight* w, float* out_dev, void* stre
     DeviceGuard g(ctx->device);
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e = w->qtype == THQ_Q8_0
-                       ? thq::launch_dequant_q8_0(reinterpret_cast<const int8_t*>(w->q), w->d, out_dev,
+                       ? thq::launch_dequant_q8_0(reinterpret_cast<const int8_t*>(w->q),
+                                                  reinterpret_cast<const uint16_t*>(w->aux), out_dev,
                                                   w->N * (w->K / 32), s)
-                       : thq::launch_dequant_q4k(w->q, out_dev, w->N * (w->K / 256), s);
+                       : thq::launch_dequant_q4k(w->q, out_dev, w->N, (int)(w->K / 256), s);
     if (e != hipSuccess) return fail(THQ_EHIP, "dequantize: %s", hipGetErrorString(e));
     return THQ_OK;
 }

@@ -4,7 +4,8 @@
 //   Q8_0: 32 weights / 34 B  = f16 d, i8 qs[32]            (repacked on device
 //         into an i8 plane [N][K] and an f16 scale plane [N][K/32])
 //   Q4_K: 256 weights / 144 B = f16 d, f16 dmin, u8 scales[12], u8 qs[128]
-//         (kept in GGUF order: one 144-B superblock is nine 16-B vectors)
+//         (re-laid on device in row quads, headers re-encoded: see
+//         q4k_hdr_from_gguf and q4k_group below)
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -46,7 +47,7 @@ __device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to
 
 // GGML get_scale_min_k4 on the 12 scale bytes held as three dwords
 // s0 = scales[0..3], s1 = scales[4..7], s2 = scales[8..11].
-__device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc,
+__host__ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc,
                                              uint32_t& m) {
     if (j < 4) {
         sc = (s0 >> (8 * j)) & 63u;
@@ -57,6 +58,83 @@ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, ui
         sc = (b8 & 0xFu) | (((s0 >> (8 * i + 6)) & 3u) << 4);
         m = (b8 >> 4) | (((s1 >> (8 * i + 6)) & 3u) << 4);
     }
+}
+
+// ---------------------------------------------------------------------------
+// On-device Q4_K header.  The 16 header bytes of a GGUF superblock (f16 d,
+// f16 dmin, 12 bytes of k4-packed 6-bit scales/mins) are re-encoded at upload
+// as four dwords H[p], one per 64-weight part p (sub-blocks 2p and 2p+1):
+//   bits  0..5  sc(2p)    bits  6..11 m(2p)
+//   bits 12..17 sc(2p+1)  bits 18..23 m(2p+1)
+//   bits 24..31 byte p of (d_bits | dmin_bits << 16)
+// A lane working on part p decodes its scales from one dword.  Download
+// converts back to GGUF bytes.
+__host__ __device__ __forceinline__ uint4 q4k_hdr_from_gguf(uint4 g) {
+    uint32_t h[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        uint32_t sc0, m0, sc1, m1;
+        scale_min_k4(2 * p, g.y, g.z, g.w, sc0, m0);
+        scale_min_k4(2 * p + 1, g.y, g.z, g.w, sc1, m1);
+        h[p] = sc0 | (m0 << 6) | (sc1 << 12) | (m1 << 18) | (((g.x >> (8 * p)) & 0xFFu) << 24);
+    }
+    return make_uint4(h[0], h[1], h[2], h[3]);
+}
+
+__host__ __device__ __forceinline__ uint4 q4k_hdr_to_gguf(uint4 h) {
+    const uint32_t hp[4] = {h.x, h.y, h.z, h.w};
+    uint32_t s[3] = {0, 0, 0};
+    uint32_t dd = 0;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        dd |= (hp[p] >> 24) << (8 * p);
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            const int j = 2 * p + half;
+            const uint32_t sc = (hp[p] >> (12 * half)) & 63u, m = (hp[p] >> (12 * half + 6)) & 63u;
+            if (j < 4) {
+                s[0] |= sc << (8 * j);
+                s[1] |= m << (8 * j);
+            } else {
+                const int i = j - 4;
+                s[2] |= ((sc & 0xFu) | ((m & 0xFu) << 4)) << (8 * i);
+                s[0] |= (sc >> 4) << (8 * i + 6);
+                s[1] |= (m >> 4) << (8 * i + 6);
+            }
+        }
+    }
+    return make_uint4(dd, s[0], s[1], s[2]);
+}
+
+// d and dmin of an on-device header
+__device__ __forceinline__ float q4k_hdr_d(uint4 h) {
+    return f16_to_f32((uint16_t)__builtin_amdgcn_perm(h.y, h.x, 0x0c0c0703u));
+}
+__device__ __forceinline__ float q4k_hdr_dmin(uint4 h) {
+    return f16_to_f32((uint16_t)__builtin_amdgcn_perm(h.w, h.z, 0x0c0c0703u));
+}
+// (sc, m) of sub-block j
+__device__ __forceinline__ void q4k_hdr_sm(uint4 h, int j, uint32_t& sc, uint32_t& m) {
+    const uint32_t hp[4] = {h.x, h.y, h.z, h.w};
+    const uint32_t w = hp[j >> 1] >> (12 * (j & 1));
+    sc = w & 63u;
+    m = (w >> 6) & 63u;
+}
+
+// Q4_K device layout ("row quads").  Rows are grouped by four; group
+// g = n/4 occupies nsb*576 bytes (= 4 rows x nsb x 144) at g*nsb*576:
+//   nibbles  [r = n%4][h][s][p][16 B]  piece (h, s, p) = bytes 32p+16h .. +15
+//                                       of superblock s's 128 nibble bytes
+//   headers  [s][p][r][4 B] at +nsb*512 dword p of row r's re-encoded header
+// For a K chunk of 16 superblocks, lane 4s+p of a wave reads piece (h, s, p)
+// of row r with one 16-B load (the wave reads a contiguous 1 KB) and the four
+// rows' header dword p with one more 16-B load.
+__host__ __device__ __forceinline__ int64_t q4k_group(int64_t n, int nsb) { return (n >> 2) * (int64_t)nsb * 576; }
+__host__ __device__ __forceinline__ int64_t q4k_piece(int64_t n, int nsb, int s, int h, int p) {
+    return q4k_group(n, nsb) + (int64_t)(n & 3) * nsb * 128 + (int64_t)h * nsb * 64 + (int64_t)(4 * s + p) * 16;
+}
+__host__ __device__ __forceinline__ int64_t q4k_hdword(int64_t n, int nsb, int s, int p) {
+    return q4k_group(n, nsb) + (int64_t)nsb * 512 + (int64_t)(4 * s + p) * 16 + 4 * (n & 3);
 }
 
 // byte I of w as f32 (selected to v_cvt_f32_ubyteI)

@@ -6,14 +6,18 @@
 
 namespace thq {
 
-// A weight as the kernels see it.
-//   Q4_K (qtype 12): q = GGUF superblocks [N][K/256][144 B], d = nullptr
-//   Q8_0 (qtype 8):  q = i8 plane [N][K], d = f16 scale plane [N][K/32]
+// A weight as the kernels see it (device layouts; download restores GGUF bytes).
+//   Q8_0 (qtype 8):  q   = i8 plane [N][K]
+//                    aux = f16 scale plane [N][K/32]
+//   Q4_K (qtype 12): q   = row-quad plane, ceil(N/4) groups of 4 x K/256 x
+//                          144 B (layout in thq_dev.hpp, q4k_group); padding
+//                          rows are zero
+//                    aux = unused
 struct WeightView {
     int qtype;
     int64_t N, K;
     const uint8_t* q;
-    const uint16_t* d;
+    const uint8_t* aux;
 };
 
 struct GemmPlan {
@@ -26,12 +30,16 @@ struct GemmPlan {
 // weights
 hipError_t launch_repack_q8_0(const uint8_t* raw, int8_t* qs, uint16_t* d, int64_t nblocks, hipStream_t s);
 hipError_t launch_quantize_q8_0(const float* w, int8_t* qs, uint16_t* d, int64_t nblocks, hipStream_t s);
-hipError_t launch_quantize_q4k(const float* w, uint8_t* out, int64_t nsuper, hipStream_t s);
+hipError_t launch_quantize_q4k(const float* w, uint8_t* dst, int64_t n, int nsb, hipStream_t s);
+// GGUF Q4_K blocks -> row-quad plane (rows dst_row0 ..)
+hipError_t launch_repack_q4k(const uint8_t* gguf, uint8_t* dst, int64_t n, int nsb, hipStream_t s);
+// copy rows between row-quad planes (weight fusion)
+hipError_t launch_q4k_copy_rows(const uint8_t* src, int64_t n, uint8_t* dst, int64_t dst_row0, int nsb, hipStream_t s);
 hipError_t launch_dequant_q8_0(const int8_t* qs, const uint16_t* d, float* out, int64_t nblocks, hipStream_t s);
-hipError_t launch_dequant_q4k(const uint8_t* raw, float* out, int64_t nsuper, hipStream_t s);
+hipError_t launch_dequant_q4k(const uint8_t* src, float* out, int64_t n, int nsb, hipStream_t s);
 
 // decode GEMV (M = 1); gu = fused gate/up over a [gate; up] weight
-bool gemv1_supported(int qtype, int K);
+bool gemv1_supported(int qtype, int K, bool gu, int64_t n_rows);
 hipError_t launch_gemv1(const WeightView& w, const void* x, bool xf32, void* y, bool yf32, bool gu, int64_t nout,
                         int64_t up_off, hipStream_t s);
 // exact generic kernel, any M, scalar activation loads
