@@ -261,6 +261,326 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ Wq, co
     }
 }
 
+// ------------------------------------------------------------------ streamed GEMM (rounded weights)
+// The production kernel for bf16 activations with rounded weight tiles.
+// Every global read is a direct-to-LDS copy (global_load_lds_dword[x4]),
+// issued two K steps ahead of its use, so no register holds in-flight data
+// and each wave waits on its own copies with one explicit s_waitcnt per
+// K step, followed by the block barrier:
+//   X ring      3 slots of BM x 64 bf16, rows of 128 B with 16-B chunk c of
+//               row r at chunk slot c ^ (r & 7) (conflict-free MFMA operand
+//               reads); rows past M copy row M-1 and are never stored
+//   raw W ring  3 slots of the packed 128 x 64 weight tile as stored in HBM
+//               (Q4_K: 32 B of nibbles + the 16-B header per row; Q8_0: 64 B
+//               of int8 + one dword of two f16 scales per row)
+//   W tiles     2 bf16 buffers, swizzled like X; while the MFMAs of step t
+//               read one, step t+1's raw tile is dequantized into the other,
+//               a quarter after each 16-wide MFMA round
+// The copies are written as inline asm because the compiler's own wait
+// insertion treats any LDS access after a direct-to-LDS load as dependent on
+// it (a vmcnt(0) before every LDS read), which would serialize the ring.
+// Block order: blocks are dealt round-robin to the 8 XCDs; the grid is
+// renumbered so that each XCD runs a contiguous range of tiles (tiles along N
+// fastest), keeping its X rows in its own L2.
+// Offsets are 32-bit: the host routes X or weight planes of 4 GiB and more to
+// k_gemm.
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(size_t)(__attribute__((address_space(3))) const void*)p;
+}
+// 16 (x4) or 4 bytes per lane from base + voff to LDS at m0 + 16*lane (4*lane)
+__device__ __forceinline__ void dma16(uint32_t lds, const void* base, uint32_t voff) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"{m0}"(lds), "v"(voff), "s"(base) : "memory");
+}
+__device__ __forceinline__ void dma4(uint32_t lds, const void* base, uint32_t voff) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dword %1, %2" ::"{m0}"(lds), "v"(voff), "s"(base) : "memory");
+}
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 3); }
+
+// linear block -> (x, y, z) tile, contiguous ranges per XCD
+__device__ __forceinline__ void xcd_tile(int tiles_n, int tiles_m, int& x, int& y, int& z) {
+    const int nb = gridDim.x, b = blockIdx.x;
+    const int q = (nb + 7) >> 3, tall = (nb & 7) ? (nb & 7) : 8;
+    const int xcd = b & 7, local = b >> 3;
+    const int L = xcd < tall ? xcd * q + local : tall * q + (xcd - tall) * (q - 1) + local;
+    x = L % tiles_n;
+    y = (L / tiles_n) % tiles_m;
+    z = L / (tiles_n * tiles_m);
+}
+
+template <int QT, int BM, bool GU, typename YT, bool SPLIT>
+__global__ __launch_bounds__(256) void k_gemm_dma(const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Wa,
+                                                 const bf16_t* __restrict__ X, void* __restrict__ Yv, int M, int K,
+                                                 int64_t nout, int64_t up_off, int64_t ldy, int kiters_per_split,
+                                                 int tiles_n, int tiles_m) {
+    constexpr int TM = BM / 2;
+    constexpr int MT = TM / 32;
+    constexpr int XI = BM / 32;                          // X copies per wave per K step (8 rows each)
+    constexpr int WI = 3;                                // raw W copies per wave per K step
+    constexpr int NIB = QT == 12 ? BN * 32 : BN * 64;    // packed weight bytes per raw slot
+    constexpr int AUX = QT == 12 ? BN * 16 : 4 * 64 * 4;  // header / scale bytes per raw slot
+    constexpr int RAW = NIB + AUX;
+    __shared__ __attribute__((aligned(16))) bf16_t Xs[3][BM * BK];
+    __shared__ __attribute__((aligned(16))) bf16_t Ws[2][BN * BK];
+    __shared__ __attribute__((aligned(16))) uint8_t Wr[3][RAW];
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    int bxi, byi, bzi;
+    xcd_tile(tiles_n, tiles_m, bxi, byi, bzi);
+    const int64_t bx = bxi;
+    const int64_t m0 = (int64_t)byi * BM;
+    const int kit0 = bzi * kiters_per_split;
+    const int kiters = K / BK;
+    const int kit1 = kit0 + kiters_per_split < kiters ? kit0 + kiters_per_split : kiters;
+    const int T = kit1 > kit0 ? kit1 - kit0 : 0;
+    const int nsb = K >> 8;
+
+    // ---- copy descriptors (per-lane 32-bit offsets, per-wave LDS bases)
+    uint32_t xoff[XI];
+    {
+        const int c = (lane & 7) ^ (lane >> 3);  // row & 7 == lane >> 3 (BM/4 and 8i are multiples of 8)
+#pragma unroll
+        for (int i = 0; i < XI; ++i) {
+            const int r = wave * (BM / 4) + 8 * i + (lane >> 3);
+            int64_t m = m0 + r;
+            if (m >= M) m = M - 1;
+            xoff[i] = (uint32_t)((m * K + 8 * c) * 2);
+        }
+    }
+    const uint32_t xlds = lds_addr(&Xs[0][0]) + wave * (BM / 4) * 128;
+    const uint32_t wlds = lds_addr(&Wr[0][0]);
+    uint32_t woff[WI];
+    auto clamp_row = [&](int c) {
+        bool v;
+        const int64_t r = tile_row<GU>(c, bx, nout, up_off, v);
+        return v ? r : (int64_t)0;
+    };
+    if (QT == 12) {
+        woff[0] = (uint32_t)q4k_piece(clamp_row(32 * wave + (lane >> 1)), nsb, 0, lane & 1, 0);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            woff[1 + i] = (uint32_t)q4k_hdword(clamp_row(32 * wave + 16 * i + (lane >> 2)), nsb, 0, lane & 3);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            woff[i] = (uint32_t)(clamp_row(32 * wave + 16 * i + (lane >> 2)) * K + 16 * (lane & 3));
+        woff[2] = (uint32_t)(clamp_row(32 * wave + (lane & 31)) * (K >> 5) * 2);
+    }
+    auto xcopy = [&](int kit, int slot) {
+        const bf16_t* base = X + kit * BK;
+#pragma unroll
+        for (int i = 0; i < XI; ++i) dma16(xlds + slot * (BM * BK * 2) + i * 1024, base, xoff[i]);
+    };
+    auto wcopy = [&](int kit, int slot) {
+        const uint32_t l = wlds + slot * RAW;
+        if (QT == 12) {
+            dma16(l + wave * 1024, Wq + kit * 16, woff[0]);
+            dma4(l + NIB + (32 * wave) * 16, Wq + (kit >> 2) * 64, woff[1]);
+            dma4(l + NIB + (32 * wave + 16) * 16, Wq + (kit >> 2) * 64, woff[2]);
+        } else {
+            dma16(l + (32 * wave) * 64, Wq + kit * 64, woff[0]);
+            dma16(l + (32 * wave + 16) * 64, Wq + kit * 64, woff[1]);
+            dma4(l + NIB + wave * 256, Wa + kit * 4, woff[2]);
+        }
+    };
+
+    // ---- dequantization: thread -> tile row wc, half wh (wave-uniform)
+    const int wc = tid & (BN - 1), wh = tid >> 7;
+    bool wvalid;
+    (void)tile_row<GU>(wc, bx, nout, up_off, wvalid);
+    // Per K step each thread converts 32 weights.  Byte -> f32 goes through
+    // v_perm_b32 with an exponent byte (no int->float conversion):
+    //   Q4_K nibble q:   bytes [0, 0, q, 0x43]        = 128 + q
+    //                    w = fma(d1, 128 + q, -(128*d1 + m1))
+    //   Q8_0 int8 q:     u = q ^ 0x80 (0..255); bytes [0, u, 0, 0x47]
+    //                    = 2^15 + u;  w = fma(d, that, -(2^15 + 128)*d) = d*q
+    // (the high byte keeps the exponent's low bit clear, so the value byte
+    // sits in mantissa bits only; (2^15 + 128)*d = 257*128*d is exact in f32,
+    // so the Q8_0 result is exact; Q4_K differs from d1*q - m1 by far less
+    // than the bf16 rounding that follows).
+    struct Raw {
+        uint4 q0, q1;
+        float s0, c0, s1, c1;  // scale and offset of the tile row's two 32-weight halves
+    };
+    auto rload = [&](int slot, int kit) {
+        Raw R;
+        const uint8_t* w = &Wr[slot][0];
+        if (QT == 12) {
+            R.q0 = *reinterpret_cast<const uint4*>(w + wc * 32 + wh * 16);
+            R.q1 = R.q0;
+            const uint4 h = *reinterpret_cast<const uint4*>(w + NIB + wc * 16);
+            const uint32_t hw = *reinterpret_cast<const uint32_t*>(w + NIB + wc * 16 + (kit & 3) * 4);
+            float d = q4k_hdr_d(h), dm = q4k_hdr_dmin(h);
+            if (!wvalid) d = dm = 0.0f;
+            R.s0 = d * (float)(hw & 63u);
+            R.c0 = __builtin_fmaf(128.0f, R.s0, dm * (float)((hw >> 6) & 63u));
+            R.s1 = d * (float)((hw >> 12) & 63u);
+            R.c1 = __builtin_fmaf(128.0f, R.s1, dm * (float)((hw >> 18) & 63u));
+        } else {
+            R.q0 = *reinterpret_cast<const uint4*>(w + wc * 64 + wh * 32);
+            R.q1 = *reinterpret_cast<const uint4*>(w + wc * 64 + wh * 32 + 16);
+            const uint32_t sc = *reinterpret_cast<const uint32_t*>(w + NIB + (wc >> 5) * 256 + (wc & 31) * 4);
+            float d = f16_to_f32((uint16_t)(wh ? sc >> 16 : sc));
+            if (!wvalid) d = 0.0f;
+            R.s0 = R.s1 = d;
+            R.c0 = R.c1 = 32896.0f * d;
+        }
+        return R;
+    };
+    // quarter qtr (0..3) of the tile row: 8 weights -> one 16-B chunk
+    auto dequant = [&](const Raw& R, int buf, int qtr) {
+        bf16_t* wt = &Ws[buf][0];
+        uint32_t a, b;
+        float sc, c;
+        int ch;
+        uint32_t E;
+        if (QT == 12) {
+            const bool hi = qtr >= 2;  // quarters 0,1: low nibbles (first half); 2,3: high (second)
+            const uint32_t qa = (qtr & 1) ? R.q0.z : R.q0.x, qb = (qtr & 1) ? R.q0.w : R.q0.y;
+            a = hi ? (qa >> 4) & 0x0F0F0F0Fu : qa & 0x0F0F0F0Fu;
+            b = hi ? (qb >> 4) & 0x0F0F0F0Fu : qb & 0x0F0F0F0Fu;
+            sc = hi ? R.s1 : R.s0;
+            c = hi ? R.c1 : R.c0;
+            ch = (hi ? 4 : 0) + 2 * wh + (qtr & 1);
+            E = 0x43434343u;
+        } else {
+            a = (qtr == 0 ? R.q0.x : qtr == 1 ? R.q0.z : qtr == 2 ? R.q1.x : R.q1.z) ^ 0x80808080u;
+            b = (qtr == 0 ? R.q0.y : qtr == 1 ? R.q0.w : qtr == 2 ? R.q1.y : R.q1.w) ^ 0x80808080u;
+            sc = R.s0;
+            c = R.c0;
+            ch = 4 * wh + qtr;
+            E = 0x47474747u;
+        }
+        // byte i of v into byte 2 (Q4_K) or byte 1 (Q8_0), exponent byte from E
+        auto f = [&](uint32_t v, int i) {
+            const uint32_t sel = QT == 12 ? 0x04000c0cu | ((uint32_t)i << 16) : 0x040c000cu | ((uint32_t)i << 8);
+            return __builtin_fmaf(sc, __uint_as_float(__builtin_amdgcn_perm(E, v, sel)), -c);
+        };
+        const uint32_t o0 = pack_bf16x2(f(a, 0), f(a, 1));
+        const uint32_t o1 = pack_bf16x2(f(a, 2), f(a, 3));
+        const uint32_t o2 = pack_bf16x2(f(b, 0), f(b, 1));
+        const uint32_t o3 = pack_bf16x2(f(b, 2), f(b, 3));
+        *reinterpret_cast<uint4*>(wt + swz(wc, ch)) = make_uint4(o0, o1, o2, o3);
+    };
+
+    f32x16_t acc[MT][2];
+#pragma unroll
+    for (int a = 0; a < MT; ++a)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) acc[a][b][i] = 0.0f;
+
+    const int lr = lane & 31, lhalf = lane >> 5;
+    // MFMAs of one K step on X slot xs / W buffer wb; with has_next, the raw
+    // tile in slot rs (step kn) is dequantized into W buffer wb ^ 1
+    auto step = [&](int xs, int wb, bool has_next, int rs, int kn) {
+        Raw R;
+        if (has_next) R = rload(rs, kn);
+        const bf16_t* xt = &Xs[xs][0];
+        const bf16_t* wt = &Ws[wb][0];
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const int ch = 2 * kk + lhalf;
+            bf16x8_t a[MT], b[2];
+#pragma unroll
+            for (int t = 0; t < MT; ++t) a[t] = *reinterpret_cast<const bf16x8_t*>(xt + swz(wm * TM + 32 * t + lr, ch));
+#pragma unroll
+            for (int t = 0; t < 2; ++t) b[t] = *reinterpret_cast<const bf16x8_t*>(wt + swz(wn * 64 + 32 * t + lr, ch));
+#pragma unroll
+            for (int i = 0; i < MT; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+            if (has_next) dequant(R, wb ^ 1, kk);
+        }
+    };
+
+    if (T > 0) {
+        // prologue: X(0), raw(0), raw(1), X(1), raw(2).  Step 0 reads X(0)
+        // and dequantizes raw(1), so everything up to raw(1) must land here;
+        // X(1) and raw(2) stay in flight
+        xcopy(kit0, 0);
+        wcopy(kit0, 0);
+        if (T > 1) {
+            wcopy(kit0 + 1, 1);
+            xcopy(kit0 + 1, 1);
+        }
+        if (T > 2) wcopy(kit0 + 2, 2);
+        if (T > 2) wait_vm<XI + WI>();
+        else if (T > 1) wait_vm<XI>();
+        else wait_vm<0>();
+        __syncthreads();
+        {
+            const Raw R = rload(0, kit0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) dequant(R, 0, q);
+        }
+        __syncthreads();
+    }
+    int xs = 0, rs = 1;  // X slot of step t, raw slot of step t + 1
+    int t = 0;
+    // steady state: X two steps ahead into slot (t + 2) % 3, raw W three
+    // steps ahead into slot (t + 3) % 3 == t % 3
+    for (; t + 3 < T; ++t) {
+        xcopy(kit0 + t + 2, xs == 0 ? 2 : xs - 1);
+        wcopy(kit0 + t + 3, xs);
+        step(xs, t & 1, true, rs, kit0 + t + 1);
+        wait_vm<XI + WI>();
+        __syncthreads();
+        xs = xs == 2 ? 0 : xs + 1;
+        rs = rs == 2 ? 0 : rs + 1;
+    }
+    // last (up to) three steps
+    for (; t < T; ++t) {
+        const bool px = t + 2 < T;
+        if (px) xcopy(kit0 + t + 2, xs == 0 ? 2 : xs - 1);
+        step(xs, t & 1, t + 1 < T, rs, kit0 + t + 1);
+        if (px) wait_vm<XI>();
+        else wait_vm<0>();
+        __syncthreads();
+        xs = xs == 2 ? 0 : xs + 1;
+        rs = rs == 2 ? 0 : rs + 1;
+    }
+
+    // epilogue: lane holds column lr of each 32x32 tile, rows 8*(e/4) + 4*(lane/32) + e%4
+    const int rq = 4 * lhalf;
+#pragma unroll
+    for (int i = 0; i < MT; ++i) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int64_t m = m0 + wm * TM + 32 * i + 8 * (e >> 2) + rq + (e & 3);
+            if (m >= M) continue;
+            if (GU) {
+                const int64_t o = bx * 64 + 32 * wn + lr;
+                if (o >= nout) continue;
+                if (SPLIT) {
+                    float* P = static_cast<float*>(Yv) + (int64_t)bzi * M * ldy;
+                    P[m * ldy + o] = acc[i][0][e];
+                    P[m * ldy + up_off + o] = acc[i][1][e];
+                } else {
+                    store_y<YT>(static_cast<YT*>(Yv) + m * ldy + o, silu_mul(acc[i][0][e], acc[i][1][e]));
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int64_t n = bx * BN + wn * 64 + 32 * j + lr;
+                    if (n >= nout) continue;
+                    if (SPLIT)
+                        (static_cast<float*>(Yv) + (int64_t)bzi * M * ldy)[m * ldy + n] = acc[i][j][e];
+                    else
+                        store_y<YT>(static_cast<YT*>(Yv) + m * ldy + n, acc[i][j][e]);
+                }
+            }
+        }
+    }
+}
+
 // sum split partials P[s][M][ldp] in split order, then the epilogue
 template <bool GU, typename YT>
 __global__ __launch_bounds__(256) void k_split_reduce(const float* __restrict__ P, YT* __restrict__ y, int M,
@@ -318,6 +638,24 @@ static hipError_t gemm_t(const GemmPlan& p, const WeightView& w, const bf16_t* x
     const int64_t nout = GU ? w.N / 2 : w.N;
     const int64_t up_off = GU ? w.N / 2 : 0;
     dim3 grid((unsigned)p.tiles_n, (unsigned)p.tiles_m, (unsigned)p.splits);
+    const uint64_t xbytes = (uint64_t)M * (uint64_t)w.K * 2;
+    const uint64_t wbytes = QT == 12 ? (uint64_t)((w.N + 3) / 4) * (uint64_t)(w.K / 256) * 576
+                                     : (uint64_t)w.N * (uint64_t)w.K;
+    if (!EXACT && xbytes < (1ull << 32) && wbytes < (1ull << 32) && !env_int("THQ_GEMM_V1", 0)) {
+        const unsigned nb = (unsigned)(p.tiles_n * p.tiles_m * p.splits);
+        if (p.splits == 1) {
+            hipLaunchKernelGGL((k_gemm_dma<QT, BM, GU, YT, false>), dim3(nb), dim3(256), 0, s, w.q, w.aux, x, y, M,
+                               (int)w.K, nout, up_off, nout, p.kps, (int)p.tiles_n, (int)p.tiles_m);
+            return hipGetLastError();
+        }
+        hipLaunchKernelGGL((k_gemm_dma<QT, BM, GU, float, true>), dim3(nb), dim3(256), 0, s, w.q, w.aux, x,
+                           (void*)ws, M, (int)w.K, nout, up_off, (int64_t)w.N, p.kps, (int)p.tiles_n,
+                           (int)p.tiles_m);
+        const int64_t total = (int64_t)M * nout;
+        hipLaunchKernelGGL((k_split_reduce<GU, YT>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ws,
+                           static_cast<YT*>(y), M, nout, up_off, (int64_t)w.N, p.splits);
+        return hipGetLastError();
+    }
     if (p.splits == 1) {
         hipLaunchKernelGGL((k_gemm<QT, EXACT, BM, GU, YT, false>), grid, dim3(256), 0, s, w.q, w.aux, x, y, M,
                            (int)w.K, nout, up_off, nout, p.kps);

@@ -39,8 +39,14 @@ __device__ __forceinline__ bf16_t f32_to_bf16(float f) {
     return r;
 }
 
+// one v_cvt_pk_bf16_f32 (round to nearest even, like f32_to_bf16)
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+    typedef float f32x2_v __attribute__((ext_vector_type(2)));
+    const f32x2_v f = {lo, hi};
+    const bf16x2_t b = __builtin_convertvector(f, bf16x2_t);
+    uint32_t r;
+    __builtin_memcpy(&r, &b, 4);
+    return r;
 }
 
 __device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
