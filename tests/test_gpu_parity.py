@@ -125,11 +125,27 @@ def test_q4k_decode_gemv(m, n, k):
     ref = O.matmul(O.Q4_K, b, n, k, xf, O.MODE_DEQUANT_F32)
     err = rel_row_err(y, ref)
     assert err <= 1e-2, err
-    # exact weights at m = 1; bf16-rounded tile weights above
-    if m == 1:  # exact weights in registers
-        assert_close_elem(f"q4k gemv m={m}", y, ref, 2.0 ** -12)
-    else:       # MFMA tile with bf16-rounded weights
-        assert_close_elem(f"q4k gemv m={m}", y, ref, 2.0 ** -7, floor="rms")
+    # decode paths (m <= 8) keep exact dequantized weights: only f32 summation order differs
+    assert_close_elem(f"q4k gemv m={m}", y, ref, 2.0 ** -12)
+
+
+@pytest.mark.parametrize("qtype", [O.Q4_K, O.Q8_0])
+@pytest.mark.parametrize("n,k", [(100, 256), (777, 1024), (300, 2816)])
+@pytest.mark.parametrize("m", [2, 3, 8])
+def test_skinny_gemv_shapes(qtype, n, k, m):
+    """Decode GEMV on the matrix cores for 2 <= M <= 8 at small / odd K: one wave
+    per block, K split across blocks, ragged row tiles; exact weights."""
+    b, w = upload(qtype, n, k)
+    xf, xb = bf16_x(m, k, seed=3)
+    y = tonp(thq.matmul(w, xb, torch.float32))
+    ref = O.matmul(qtype, b, n, k, xf, O.MODE_DEQUANT_F32)
+    assert rel_row_err(y, ref) <= 1e-2
+    assert_close_elem(f"skinny gemv qtype={qtype} {n}x{k} m={m}", y, ref, 2.0 ** -12)
+    # the fused gate/up epilogue on the same shapes (rows split in two halves)
+    if n % 2 == 0:
+        act = tonp(thq.gate_up_silu(w, xb, torch.float32))
+        want = O.bf16_bits_to_f32(O.gate_up_silu(y))
+        assert_close_elem(f"skinny gate/up {n}x{k} m={m}", act, want, 2.0 ** -7)
 
 
 # ------------------------------------------------------------------ config 3

@@ -597,6 +597,20 @@ __global__ __launch_bounds__(256) void k_split_reduce(const float* __restrict__ 
     store_y<YT>(y + m * nout + o, GU ? silu_mul(g, u) : g);
 }
 
+hipError_t launch_split_reduce(const float* P, void* y, bool yf32, bool gu, int M, int64_t nout, int64_t up_off,
+                               int64_t ldp, int splits, hipStream_t s) {
+    const int64_t total = (int64_t)M * nout;
+    const dim3 grid((unsigned)((total + 255) / 256));
+    if (gu) {
+        if (yf32) hipLaunchKernelGGL((k_split_reduce<true, float>), grid, dim3(256), 0, s, P, (float*)y, M, nout, up_off, ldp, splits);
+        else hipLaunchKernelGGL((k_split_reduce<true, bf16_t>), grid, dim3(256), 0, s, P, (bf16_t*)y, M, nout, up_off, ldp, splits);
+    } else {
+        if (yf32) hipLaunchKernelGGL((k_split_reduce<false, float>), grid, dim3(256), 0, s, P, (float*)y, M, nout, up_off, ldp, splits);
+        else hipLaunchKernelGGL((k_split_reduce<false, bf16_t>), grid, dim3(256), 0, s, P, (bf16_t*)y, M, nout, up_off, ldp, splits);
+    }
+    return hipGetLastError();
+}
+
 // ------------------------------------------------------------------ launch
 static inline int env_int(const char* name, int dflt) {
     const char* v = getenv(name);

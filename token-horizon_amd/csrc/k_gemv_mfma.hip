@@ -1,0 +1,400 @@
+// k_gemv_mfma.hip — decode GEMV for 1 <= M <= 8 bf16 activation rows on the
+// matrix cores, with exact (unrounded) dequantized weights.
+//
+// Role: the m = 1..8 projections of the reference (AffineQmvT / AffineQmpp,
+// engine/src/quant_kernel.rs:2964-3140, 3188-3738, routed by rows in
+// QLin::linear_ps, engine/src/qwen35.rs:398-617) over GGUF Q4_K / Q8_0
+// weights.  HBM-bound: every weight byte is read once with 16-B loads.
+//
+// Why MFMA for a GEMV: with M rows of x, a VALU dot product costs ~M/2
+// instructions per weight; here the products run on v_mfma_f32_32x32x16_bf16
+// and the VALU only converts packed weights to bf16 (one v_perm per two Q4_K
+// weights) and applies the per-32-weight scales, independent of M.
+//
+// Exactness.  Q4_K weight = d1*q - m1 per 32-weight sub-block.  The B operand
+// holds bf16(128 + q) (exact: bytes [q, 0x43]), so the MFMA gives
+// A = sum x*(128 + q) over a sub-block, and
+//     sum x*w = d1*A - (128*d1 + m1) * S,   S = sum x over the sub-block,
+// with S computed once per block while the activations are staged in LDS.
+// Q8_0: B = bf16(q) (exact for |q| <= 128), sum = d*A.
+//
+// Tiling.  A block owns 32 weight rows (gate/up: 16 gate + 16 up rows of the
+// same outputs) over a K range (all of K, or one of `splits` ranges when the
+// tiles alone cannot fill the GPU; split partials are summed in a fixed order
+// by k_split_reduce).  The block stages its activation rows x[0..M) of that
+// range in LDS (with the 32-wide sums S), while the first weight chunks are
+// already in flight; its (up to 8) waves then split the range into slices of
+// whole 256-wide chunks, loading the chunk after next while computing.
+// Units are 64 weights.  Lane l: weight row n = l % 32, half g = l / 32:
+//   Q4_K  lane loads piece g (bytes 16g..16g+15) of the unit's 32 nibble
+//         bytes; low nibbles of bytes 16g+0..7 / 16g+8..15 feed two MFMAs of
+//         the first sub-block (k = k0 + 16g + 0..7 / 8..15), high nibbles the
+//         second sub-block (k0 + 32 + ...).
+//   Q8_0  lane loads bytes 16g..16g+15 of each of the unit's two blocks, same
+//         k mapping (first block = k0..k0+31, second = k0+32..k0+63).
+// The MFMA output lane holds column n and rows 8*(e/4) + 4*g + e%4; with
+// M <= 8 only e = 0..3 (rows 4g + e) are live.  Each wave accumulates its
+// slice in registers; the block sums the slices in LDS in wave order
+// (deterministic) and applies the epilogue.
+#include "thq_dev.hpp"
+#include "thq_kernels.hpp"
+
+#include <type_traits>
+
+namespace thq {
+
+namespace {
+
+__device__ __forceinline__ f32x16_t mfma32x16(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
+    bf16x8_t r;
+    __builtin_memcpy(&r, &v, 16);
+    return r;
+}
+// low nibbles of the bytes of a, b (already masked to 4 bits) -> bf16(128 + q) x 8
+__device__ __forceinline__ bf16x8_t nib_bf16x8(uint32_t a, uint32_t b) {
+    const uint32_t C = 0x43434343u;
+    return as_bf16x8(make_uint4(__builtin_amdgcn_perm(C, a, 0x04010400u), __builtin_amdgcn_perm(C, a, 0x04030402u),
+                                __builtin_amdgcn_perm(C, b, 0x04010400u), __builtin_amdgcn_perm(C, b, 0x04030402u)));
+}
+// int8 bytes of a, b -> bf16(q) x 8 (exact)
+__device__ __forceinline__ bf16x8_t i8_bf16x8(uint32_t a, uint32_t b) {
+    auto cv = [](uint32_t w, int i) { return (float)(int8_t)(w >> (8 * i)); };
+    return as_bf16x8(make_uint4(pack_bf16x2(cv(a, 0), cv(a, 1)), pack_bf16x2(cv(a, 2), cv(a, 3)),
+                                pack_bf16x2(cv(b, 0), cv(b, 1)), pack_bf16x2(cv(b, 2), cv(b, 3))));
+}
+
+constexpr int MAXW = 8;          // waves per block
+constexpr int XS_ELEMS = 32768;  // staged activations (bf16) per block: M * Kb <= 32768
+constexpr int KB_MAX = 8192;     // K range of one block
+constexpr int XCH = 8;           // staged 16-B activation chunks per thread: M * cpw / 2 <= XCH
+
+// Packed weights and scales of one chunk (4 units = one Q4_K superblock) of a
+// wave's K slice.
+template <int QT>
+struct Chunk {
+    uint4 w[QT == 12 ? 4 : 8];
+    uint32_t s[4];
+};
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// X is not __restrict__: its loads must stay ordered before the weight loads
+// by the compiler barrier in the staging step.
+// Grid: tiles x splits blocks; block (tile, split) owns the tile's 32 weight
+// rows over K range [split*Kb, (split+1)*Kb), Kb = waves * cpw * 256.
+template <int QT, int E, int NX, bool GU, bool SPLIT, typename YT>
+__global__ __launch_bounds__(512, QT == 12 ? 4 : 2) void k_gemv_mfma(const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Wa,
+                                                  const bf16_t* X, void* __restrict__ Yv, int M, int K,
+                                                  int64_t nout, int64_t up_off, int64_t nrows, int cpw, int splits) {
+    // staged activation rows (row stride Kb + 8: rows start 16 B apart in bank
+    // order), sub-block sums S[sb][8] and the cross-wave reduction buffer
+    __shared__ __attribute__((aligned(16))) bf16_t xs[XS_ELEMS + 8 * 8];
+    __shared__ __attribute__((aligned(16))) float Ss[QT == 12 ? KB_MAX / 32 : 1][8];
+    // the cross-wave reduction reuses the staging buffer once all waves are done with it
+    float(*red)[8][32] = reinterpret_cast<float(*)[8][32]>(&xs[0]);
+    static_assert(MAXW * 8 * 32 * 4 <= XS_ELEMS * 2, "reduction buffer exceeds the staging buffer");
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nw = blockDim.x >> 6;
+    const int n = lane & 31, g = lane >> 5;
+    const int tile = blockIdx.x / splits, split = blockIdx.x - tile * splits;
+    const int Kb = nw * cpw * 256;
+    const int kb0 = split * Kb;
+    const int XR = Kb + 8;
+
+    int64_t row;
+    bool valid;
+    if (GU) {
+        const int64_t o = (int64_t)tile * 16 + (n & 15);
+        valid = o < nout;
+        row = o + (n >= 16 ? up_off : 0);
+    } else {
+        row = (int64_t)tile * 32 + n;
+        valid = row < nout;
+    }
+    if (!valid) row = 0;  // in-bounds reads; its scales are zeroed below
+    const int c0 = kb0 / 256 + wave * cpw;  // first 256-wide chunk of this wave
+
+    const uint8_t* pw;
+    const uint8_t* ps;
+    if (QT == 12) {
+        const int nsb = K >> 8;
+        pw = Wq + q4k_piece(row, nsb, 0, g, 0);
+        ps = Wq + q4k_hdword(row, nsb, 0, 0);
+    } else {
+        pw = Wq + row * K + 16 * g;
+        ps = Wa + row * (K >> 5) * 2;
+    }
+    auto load = [&](Chunk<QT>& C, int c) {
+        if (QT == 12) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                C.w[u] = *reinterpret_cast<const uint4*>(pw + (int64_t)c * 64 + u * 16);
+                C.s[u] = *reinterpret_cast<const uint32_t*>(ps + (int64_t)c * 64 + u * 16);
+            }
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                C.w[2 * u] = *reinterpret_cast<const uint4*>(pw + (int64_t)c * 256 + u * 64);
+                C.w[2 * u + 1] = *reinterpret_cast<const uint4*>(pw + (int64_t)c * 256 + u * 64 + 32);
+                C.s[u] = *reinterpret_cast<const uint32_t*>(ps + (int64_t)c * 16 + u * 4);
+            }
+        }
+    };
+    // ---- stage x[0..M)[kb0 .. kb0+Kb) and the 32-wide sums S (Q4_K).  The
+    // activation loads are issued first, then the first two weight chunks, so
+    // that the (in-order) wait before the LDS writes covers only the x loads
+    // and the weight reads overlap the staging and the first chunk's math.
+    const int cpr = Kb >> 3;  // 16-B chunks per row (a multiple of 4)
+    const int total = M * cpr;  // <= NX * blockDim.x
+    // straight-line loads (clamped indices, both chunks always loaded) keep the
+    // compiler's wait counts exact
+    uint4 xv[NX];
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+        int ch = threadIdx.x + i * blockDim.x;
+        ch = ch < total ? ch : total - 1;
+        const int m = ch / cpr, c = ch - m * cpr;
+        xv[i] = *reinterpret_cast<const uint4*>(X + (int64_t)m * K + kb0 + 8 * c);
+    }
+    // keep the x loads ahead of the weight loads (IR and machine scheduling)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    Chunk<QT> B0, B1;
+    load(B0, c0);
+    load(B1, cpw > 1 ? c0 + 1 : c0);
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+        const int ch = threadIdx.x + i * blockDim.x;
+        if (ch < total) {
+            const int m = ch / cpr, c = ch - m * cpr;
+            const uint4 v = xv[i];
+            *reinterpret_cast<uint4*>(&xs[m * XR + 8 * c]) = v;
+            if (QT == 12) {
+                // lanes 4j..4j+3 hold the 4 chunks of one sub-block (quads stay whole)
+                const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+                bf16x2_t p[4];
+                __builtin_memcpy(p, &v, 16);
+                float t = __builtin_amdgcn_fdot2_f32_bf16(p[0], one, 0.0f, false);
+                t = __builtin_amdgcn_fdot2_f32_bf16(p[1], one, t, false);
+                t = __builtin_amdgcn_fdot2_f32_bf16(p[2], one, t, false);
+                t = __builtin_amdgcn_fdot2_f32_bf16(p[3], one, t, false);
+                t = dpp_add<0xB1>(t);  // quad_perm [1,0,3,2]
+                t = dpp_add<0x4E>(t);  // quad_perm [2,3,0,1]
+                if ((c & 3) == 0) Ss[c >> 2][m] = t;
+            }
+        }
+    }
+    __syncthreads();
+
+    // 32x32 A operand row n (clamped to M-1)
+    const bf16_t* xa = &xs[(n < M ? n : M - 1) * XR + 16 * g];
+    const f32x16_t z16 = {};
+    float tot[E];
+#pragma unroll
+    for (int e = 0; e < E; ++e) tot[e] = 0.0f;
+
+    auto compute = [&](const Chunk<QT>& C, int c) {
+        float d = 0.0f, dm = 0.0f;
+        if (QT == 12) {
+            d = f16_to_f32((uint16_t)__builtin_amdgcn_perm(C.s[1], C.s[0], 0x0c0c0703u));
+            dm = f16_to_f32((uint16_t)__builtin_amdgcn_perm(C.s[3], C.s[2], 0x0c0c0703u));
+            if (!valid) d = dm = 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int kl = (c * 4 + u) * 64 - kb0;  // offset inside the staged range
+            const uint4 a0 = *reinterpret_cast<const uint4*>(xa + kl);
+            const uint4 a1 = *reinterpret_cast<const uint4*>(xa + kl + 8);
+            const uint4 a2 = *reinterpret_cast<const uint4*>(xa + kl + 32);
+            const uint4 a3 = *reinterpret_cast<const uint4*>(xa + kl + 40);
+            if (QT == 12) {
+                const f32x4_t S1 = *reinterpret_cast<const f32x4_t*>(&Ss[kl >> 5][4 * g]);
+                const f32x4_t S2 = *reinterpret_cast<const f32x4_t*>(&Ss[(kl >> 5) + 1][4 * g]);
+                const uint32_t h = C.s[u];
+                const float d1 = d * (float)(h & 63u), d2 = d * (float)((h >> 12) & 63u);
+                const float c1 = __builtin_fmaf(128.0f, d1, dm * (float)((h >> 6) & 63u));
+                const float c2 = __builtin_fmaf(128.0f, d2, dm * (float)((h >> 18) & 63u));
+                const uint4 q = C.w[u];
+                const uint32_t M4 = 0x0F0F0F0Fu;
+                // one sub-block at a time keeps a single 16-register accumulator live
+                f32x16_t A = mfma32x16(as_bf16x8(a0), nib_bf16x8(q.x & M4, q.y & M4), z16);
+                A = mfma32x16(as_bf16x8(a1), nib_bf16x8(q.z & M4, q.w & M4), A);
+#pragma unroll
+                for (int e = 0; e < E; ++e) tot[e] = __builtin_fmaf(-c1, S1[e], __builtin_fmaf(d1, A[e], tot[e]));
+                A = mfma32x16(as_bf16x8(a2), nib_bf16x8((q.x >> 4) & M4, (q.y >> 4) & M4), z16);
+                A = mfma32x16(as_bf16x8(a3), nib_bf16x8((q.z >> 4) & M4, (q.w >> 4) & M4), A);
+#pragma unroll
+                for (int e = 0; e < E; ++e) tot[e] = __builtin_fmaf(-c2, S2[e], __builtin_fmaf(d2, A[e], tot[e]));
+            } else {
+                float da = f16_to_f32((uint16_t)C.s[u]), db = f16_to_f32((uint16_t)(C.s[u] >> 16));
+                if (!valid) da = db = 0.0f;
+                const uint4 q0 = C.w[2 * u], q1 = C.w[2 * u + 1];
+                f32x16_t A = mfma32x16(as_bf16x8(a0), i8_bf16x8(q0.x, q0.y), z16);
+                A = mfma32x16(as_bf16x8(a1), i8_bf16x8(q0.z, q0.w), A);
+#pragma unroll
+                for (int e = 0; e < E; ++e) tot[e] = __builtin_fmaf(da, A[e], tot[e]);
+                A = mfma32x16(as_bf16x8(a2), i8_bf16x8(q1.x, q1.y), z16);
+                A = mfma32x16(as_bf16x8(a3), i8_bf16x8(q1.z, q1.w), A);
+#pragma unroll
+                for (int e = 0; e < E; ++e) tot[e] = __builtin_fmaf(db, A[e], tot[e]);
+            }
+        }
+    };
+
+    // two chunk buffers; the chunk after next loads while a chunk computes
+    for (int c = 0; c < cpw; c += 2) {
+        compute(B0, c0 + c);
+        if (c + 2 < cpw) load(B0, c0 + c + 2);
+        if (c + 1 >= cpw) break;
+        compute(B1, c0 + c + 1);
+        if (c + 3 < cpw) load(B1, c0 + c + 3);
+    }
+
+    // ---- block reduction over the waves' K slices, in wave order
+    __syncthreads();  // every wave is done reading xs
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+        const int m = 4 * g + e;
+        if (m < M) red[wave][m][n] = tot[e];
+    }
+    __syncthreads();
+    // outputs are strided over the block: a block may have fewer threads than 32*M
+    if (SPLIT) {
+        // f32 partial in natural weight-row order: P[split][m][row]
+        for (int t = threadIdx.x; t < 32 * M; t += blockDim.x) {
+            const int c = t & 31, m = t >> 5;
+            float sum = 0.0f;
+            for (int w = 0; w < nw; ++w) sum += red[w][m][c];
+            int64_t r;
+            bool ok;
+            if (GU) {
+                const int64_t o = (int64_t)tile * 16 + (c & 15);
+                ok = o < nout;
+                r = o + (c >= 16 ? up_off : 0);
+            } else {
+                r = (int64_t)tile * 32 + c;
+                ok = r < nout;
+            }
+            if (ok) static_cast<float*>(Yv)[((int64_t)split * M + m) * nrows + r] = sum;
+        }
+    } else if (GU) {
+        for (int t = threadIdx.x; t < 16 * M; t += blockDim.x) {
+            const int c = t & 15, m = t >> 4;
+            float gs = 0.0f, us = 0.0f;
+            for (int w = 0; w < nw; ++w) {
+                gs += red[w][m][c];
+                us += red[w][m][c + 16];
+            }
+            const int64_t o = (int64_t)tile * 16 + c;
+            if (o < nout) store_y<YT>(static_cast<YT*>(Yv) + (int64_t)m * nout + o, silu_mul(gs, us));
+        }
+    } else {
+        for (int t = threadIdx.x; t < 32 * M; t += blockDim.x) {
+            const int c = t & 31, m = t >> 5;
+            float sum = 0.0f;
+            for (int w = 0; w < nw; ++w) sum += red[w][m][c];
+            const int64_t o = (int64_t)tile * 32 + c;
+            if (o < nout) store_y<YT>(static_cast<YT*>(Yv) + (int64_t)m * nout + o, sum);
+        }
+    }
+}
+
+int env_int(const char* name) {
+    const char* v = getenv(name);
+    return v && *v ? atoi(v) : 0;
+}
+
+template <int QT, int E, int NX, bool GU, typename YT>
+hipError_t run(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* y, int M, int64_t nout, int64_t up_off,
+               float* ws, hipStream_t s) {
+    const int64_t tiles = GU ? (nout + 15) / 16 : (nout + 31) / 32;
+    const dim3 grid((unsigned)(tiles * p.splits)), block(64 * p.waves);
+    if (p.splits == 1) {
+        hipLaunchKernelGGL((k_gemv_mfma<QT, E, NX, GU, false, YT>), grid, block, 0, s, w.q, w.aux, x, y, M,
+                           (int)w.K, nout, up_off, w.N, p.cpw, 1);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL((k_gemv_mfma<QT, E, NX, GU, true, float>), grid, block, 0, s, w.q, w.aux, x, (void*)ws, M,
+                       (int)w.K, nout, up_off, w.N, p.cpw, p.splits);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_split_reduce(ws, y, std::is_same<YT, float>::value, GU, M, nout, up_off, w.N, p.splits, s);
+}
+
+// staged activation chunks per thread: M * cpw * 256 / 8 / (64 * waves) = M * cpw / 2, rounded up to 1, 2, 4, 8
+template <int QT, int E, bool GU, typename YT>
+hipError_t run_nx(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* y, int M, int64_t nout,
+                  int64_t up_off, float* ws, hipStream_t s) {
+    const int need = (M * p.cpw + 1) / 2;
+    if (need <= 1) return run<QT, E, 1, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
+    if (need <= 2) return run<QT, E, 2, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
+    if (need <= 4) return run<QT, E, 4, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
+    return run<QT, E, 8, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
+}
+
+template <int QT, bool GU, typename YT>
+hipError_t run_e(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* y, int M, int64_t nout,
+                 int64_t up_off, float* ws, hipStream_t s) {
+    if (M == 1) return run_nx<QT, 1, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
+    return run_nx<QT, 4, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
+}
+
+}  // namespace
+
+GemvPlan plan_gemv_mfma(int qtype, int64_t M, int64_t N_rows, int64_t K, bool gu) {
+    GemvPlan p;
+    if (M < 1 || M > 8 || K < 256 || K % 256 || K > (1 << 20)) return p;
+    if (qtype != 8 && qtype != 12) return p;
+    const int64_t nout = gu ? N_rows / 2 : N_rows;
+    const int64_t tiles = gu ? (nout + 15) / 16 : (nout + 31) / 32;
+    const int chunks = (int)(K / 256);
+    const int fs = env_int("THQ_GEMV_SPLITS"), fw = env_int("THQ_GEMV_WAVES");
+    // fewest K splits that fit the staged activations and give >= 256 blocks
+    // (else the most splits, up to 16, that fit); waves: the most (<= 8) that
+    // divide the block's chunks with M * (chunks per wave) <= 2 * XCH
+    for (int s = 1; s <= chunks && s <= 16; ++s) {
+        if (chunks % s || (fs && s != fs)) continue;
+        const int64_t kb = K / s;
+        if (kb > KB_MAX || M * kb > XS_ELEMS) continue;
+        const int cps = chunks / s;
+        int w = 0;
+        for (int c = MAXW; c >= 1; --c)
+            if (cps % c == 0 && (!fw || c == fw) && M * (cps / c) <= 2 * XCH) {
+                w = c;
+                break;
+            }
+        if (!w) continue;
+        p.splits = s;
+        p.waves = w;
+        p.cpw = cps / w;
+        p.workspace_bytes = s > 1 ? (size_t)s * (size_t)M * (size_t)N_rows * sizeof(float) : 0;
+        if (fs || tiles * s >= 256) break;
+    }
+    return p;
+}
+
+hipError_t launch_gemv_mfma(const GemvPlan& p, const WeightView& w, const void* x, void* y, bool yf32, bool gu, int M,
+                            int64_t nout, int64_t up_off, float* ws, hipStream_t s) {
+    if (!p.waves) return hipErrorInvalidValue;
+    const bf16_t* xb = static_cast<const bf16_t*>(x);
+    if (w.qtype == 12) {
+        if (gu) return yf32 ? run_e<12, true, float>(p, w, xb, y, M, nout, up_off, ws, s)
+                            : run_e<12, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
+        return yf32 ? run_e<12, false, float>(p, w, xb, y, M, nout, up_off, ws, s)
+                    : run_e<12, false, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
+    }
+    if (gu) return yf32 ? run_e<8, true, float>(p, w, xb, y, M, nout, up_off, ws, s)
+                        : run_e<8, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
+    return yf32 ? run_e<8, false, float>(p, w, xb, y, M, nout, up_off, ws, s)
+                : run_e<8, false, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
+}
+
+}  // namespace thq

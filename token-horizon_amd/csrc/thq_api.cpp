@@ -154,8 +154,23 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
     const int64_t nout = gu ? w->N / 2 : w->N;
     const int64_t up_off = gu ? w->N / 2 : 0;
     hipError_t e;
-    if (m == 1 && aligned16(x) && thq::gemv1_supported(w->qtype, (int)w->K, gu, w->N)) {
+    // M = 1 keeps the VALU GEMV unless THQ_GEMV_M1=mfma; 2..8 bf16 rows go to the MFMA GEMV
+    static const bool m1_mfma = [] {
+        const char* v = getenv("THQ_GEMV_M1");
+        return v && !strcmp(v, "mfma");
+    }();
+    const thq::GemvPlan gp = (!xf32 && aligned16(x) && m <= 8) ? thq::plan_gemv_mfma(w->qtype, m, w->N, w->K, gu)
+                                                                 : thq::GemvPlan{};
+    const bool skinny = gp.waves > 0;
+    if (m == 1 && !(m1_mfma && skinny) && aligned16(x) && thq::gemv1_supported(w->qtype, (int)w->K, gu, w->N)) {
         e = thq::launch_gemv1(v, x, xf32, y, yf32, gu, nout, up_off, s);
+    } else if (skinny) {
+        std::lock_guard<std::mutex> lk(ctx->mu);
+        if (gp.workspace_bytes) {
+            int rc = ensure_ws(ctx, gp.workspace_bytes);
+            if (rc) return rc;
+        }
+        e = thq::launch_gemv_mfma(gp, v, x, y, yf32, gu, (int)m, nout, up_off, static_cast<float*>(ctx->ws), s);
     } else if (!xf32 && aligned16(x) && !(w->qtype == THQ_Q4_K && (flags & THQ_MODE_EXACT_W))) {
         const bool exact = (flags & THQ_MODE_EXACT_W) || (w->qtype == THQ_Q8_0 && m <= 64);
         thq::GemmPlan p = thq::plan_gemm(w->qtype, exact, m, w->N, w->K, gu);

@@ -42,6 +42,17 @@ hipError_t launch_dequant_q4k(const uint8_t* src, float* out, int64_t n, int nsb
 bool gemv1_supported(int qtype, int K, bool gu, int64_t n_rows);
 hipError_t launch_gemv1(const WeightView& w, const void* x, bool xf32, void* y, bool yf32, bool gu, int64_t nout,
                         int64_t up_off, hipStream_t s);
+// decode GEMV on MFMA: 1 <= M <= 8 bf16 activation rows, exact weights
+struct GemvPlan {
+    int waves = 0, cpw = 0, splits = 0;  // waves per block, 256-wide chunks per wave, K splits
+    size_t workspace_bytes = 0;          // split partials (f32 [splits][M][N])
+};
+GemvPlan plan_gemv_mfma(int qtype, int64_t M, int64_t N_rows, int64_t K, bool gu);  // waves == 0: unsupported
+hipError_t launch_gemv_mfma(const GemvPlan& p, const WeightView& w, const void* x, void* y, bool yf32, bool gu, int M,
+                            int64_t nout, int64_t up_off, float* ws, hipStream_t s);
+// sum split partials P[s][M][ldp] in split order, then the epilogue
+hipError_t launch_split_reduce(const float* P, void* y, bool yf32, bool gu, int M, int64_t nout, int64_t up_off,
+                               int64_t ldp, int splits, hipStream_t s);
 // exact generic kernel, any M, scalar activation loads
 hipError_t launch_generic(const WeightView& w, const void* x, bool xf32, void* y, bool yf32, bool gu, int M,
                           int64_t nout, int64_t up_off, hipStream_t s);

@@ -207,21 +207,28 @@ def matmul(w: QTensor, x: torch.Tensor, out_dtype=torch.float32, flags: int = 0,
     return out.reshape(*x.shape[:-1], w.n)
 
 
-def gate_up_silu(w: QTensor, x: torch.Tensor, out_dtype=torch.bfloat16, flags: int = 0):
+def gate_up_silu(w: QTensor, x: torch.Tensor, out_dtype=torch.bfloat16, flags: int = 0,
+                 out: torch.Tensor | None = None):
+    """y[M, N/2] = bf16(silu(bf16(g)) * bf16(u)) over a fused [gate; up] weight."""
     x2 = x.reshape(-1, x.shape[-1])
     if x2.shape[-1] != w.k:
         raise ValueError(f"x last dim {x2.shape[-1]} != weight inp {w.k}")
     m = x2.shape[0]
-    out = torch.empty((m, w.n // 2), dtype=out_dtype, device=x.device)
+    if out is None:
+        out = torch.empty((m, w.n // 2), dtype=out_dtype, device=x.device)
     check(lib.thq_gate_up_silu(w.ctx.h, w.h, _ptr(x2), _act(x2), m, _ptr(out), _act(out), flags, _stream()))
     return out.reshape(*x.shape[:-1], w.n // 2)
 
 
-def matmul_argmax(w: QTensor, x: torch.Tensor, want_logits: bool = True, flags: int = 0):
+def matmul_argmax(w: QTensor, x: torch.Tensor, want_logits: bool = True, flags: int = 0,
+                  logits: torch.Tensor | None = None, idx: torch.Tensor | None = None):
+    """LM head + per-row greedy argmax; returns (logits or None, idx int32)."""
     x2 = x.reshape(-1, x.shape[-1])
     m = x2.shape[0]
-    logits = torch.empty((m, w.n), dtype=torch.float32, device=x.device) if want_logits else None
-    idx = torch.empty((m,), dtype=torch.int32, device=x.device)
+    if logits is None and want_logits:
+        logits = torch.empty((m, w.n), dtype=torch.float32, device=x.device)
+    if idx is None:
+        idx = torch.empty((m,), dtype=torch.int32, device=x.device)
     check(lib.thq_matmul_argmax(w.ctx.h, w.h, _ptr(x2), _act(x2), m, _ptr(logits), _ptr(idx), flags, _stream()))
     return logits, idx
 
