@@ -299,7 +299,11 @@ template <int N>
 __device__ __forceinline__ void wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + ((chunk ^ (row & 7)) << 3); }
+// LDS has 64 banks of 4 B: 16 lanes of a b128 access share a cycle, i.e. two
+// 128-B rows per bank row.  Chunk c of row r sits at slot c ^ ((r >> 1) & 7),
+// so any 16 consecutive rows at one chunk hit 16 distinct 16-B bank groups.
+__device__ __forceinline__ int swz_slot(int row, int chunk) { return chunk ^ ((row >> 1) & 7); }
+__device__ __forceinline__ int swz(int row, int chunk) { return row * BK + (swz_slot(row, chunk) << 3); }
 
 // linear block -> (x, y, z) tile, contiguous ranges per XCD
 __device__ __forceinline__ void xcd_tile(int tiles_n, int tiles_m, int& x, int& y, int& z) {
@@ -312,18 +316,32 @@ __device__ __forceinline__ void xcd_tile(int tiles_n, int tiles_m, int& x, int& 
     z = L / (tiles_n * tiles_m);
 }
 
-template <int QT, int BM, bool GU, typename YT, bool SPLIT>
-__global__ __launch_bounds__(256) void k_gemm_dma(const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Wa,
-                                                 const bf16_t* __restrict__ X, void* __restrict__ Yv, int M, int K,
-                                                 int64_t nout, int64_t up_off, int64_t ldy, int kiters_per_split,
-                                                 int tiles_n, int tiles_m) {
-    constexpr int TM = BM / 2;
+template <int QT, int BM, int WM, bool GU, typename YT, bool SPLIT>
+__global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Wa,
+                                                      const bf16_t* __restrict__ X, void* __restrict__ Yv, int M, int K,
+                                                      int64_t nout, int64_t up_off, int64_t ldy, int kiters_per_split,
+                                                      int tiles_n, int tiles_m) {
+    // waves: WM (along M) x 2 (along N); wave tile TM x 64
+    constexpr int NW = 2 * WM;
+    constexpr int TM = BM / WM;
     constexpr int MT = TM / 32;
-    constexpr int XI = BM / 32;                          // X copies per wave per K step (8 rows each)
-    constexpr int WI = 3;                                // raw W copies per wave per K step
-    constexpr int NIB = QT == 12 ? BN * 32 : BN * 64;    // packed weight bytes per raw slot
-    constexpr int AUX = QT == 12 ? BN * 16 : 4 * 64 * 4;  // header / scale bytes per raw slot
+    static_assert(MT >= 1 && (NW == 4 || NW == 8), "tile configuration");
+    // copies per wave per K step: X = 8*BM 16-B slots over NW waves; packed
+    // weights: Q4_K 256 slots of nibbles + 512 header dwords, Q8_0 512 slots
+    // of int8 + 128 scale dwords, spread so that every wave issues the same
+    // number of copies (some with part of the wave active)
+    constexpr int XI = BM / (8 * NW);
+    constexpr int NIB = QT == 12 ? BN * 32 : BN * 64;   // packed weight bytes per raw slot
+    constexpr int AUX = QT == 12 ? BN * 16 : BN * 4;     // header / scale bytes per raw slot
     constexpr int RAW = NIB + AUX;
+    constexpr int NSLOT = QT == 12 ? 256 / NW : 512 / NW;      // 16-B weight slots per wave
+    constexpr int NI = NSLOT >= 64 ? NSLOT / 64 : 1;           // their copies
+    constexpr int NL = NSLOT >= 64 ? 64 : NSLOT;               // active lanes per copy
+    constexpr int HSLOT = QT == 12 ? 512 / NW : 128 / NW;      // header / scale dwords per wave
+    constexpr int HI = HSLOT >= 64 ? HSLOT / 64 : 1;
+    constexpr int HL = HSLOT >= 64 ? 64 : HSLOT;
+    constexpr int WI = NI + HI;
+    static_assert(XI >= 1 && NI * NL == NSLOT && HI * HL == HSLOT, "copy split");
     __shared__ __attribute__((aligned(16))) bf16_t Xs[3][BM * BK];
     __shared__ __attribute__((aligned(16))) bf16_t Ws[2][BN * BK];
     __shared__ __attribute__((aligned(16))) uint8_t Wr[3][RAW];
@@ -343,34 +361,38 @@ __global__ __launch_bounds__(256) void k_gemm_dma(const uint8_t* __restrict__ Wq
 
     // ---- copy descriptors (per-lane 32-bit offsets, per-wave LDS bases)
     uint32_t xoff[XI];
-    {
-        const int c = (lane & 7) ^ (lane >> 3);  // row & 7 == lane >> 3 (BM/4 and 8i are multiples of 8)
 #pragma unroll
-        for (int i = 0; i < XI; ++i) {
-            const int r = wave * (BM / 4) + 8 * i + (lane >> 3);
-            int64_t m = m0 + r;
-            if (m >= M) m = M - 1;
-            xoff[i] = (uint32_t)((m * K + 8 * c) * 2);
-        }
+    for (int i = 0; i < XI; ++i) {
+        // lane -> row r, LDS slot lane & 7, which holds chunk swz_slot(r, lane & 7)
+        const int r = wave * (BM / NW) + 8 * i + (lane >> 3);
+        const int c = swz_slot(r, lane & 7);
+        int64_t m = m0 + r;
+        if (m >= M) m = M - 1;
+        xoff[i] = (uint32_t)((m * K + 8 * c) * 2);
     }
-    const uint32_t xlds = lds_addr(&Xs[0][0]) + wave * (BM / 4) * 128;
+    const uint32_t xlds = lds_addr(&Xs[0][0]) + wave * (BM / NW) * 128;
     const uint32_t wlds = lds_addr(&Wr[0][0]);
-    uint32_t woff[WI];
     auto clamp_row = [&](int c) {
         bool v;
         const int64_t r = tile_row<GU>(c, bx, nout, up_off, v);
         return v ? r : (int64_t)0;
     };
-    if (QT == 12) {
-        woff[0] = (uint32_t)q4k_piece(clamp_row(32 * wave + (lane >> 1)), nsb, 0, lane & 1, 0);
+    // packed weights: Q4_K slot j = h*128 + row (piece h of the row),
+    // Q8_0 slot j = (half*2 + c)*128 + row (bytes 32*half + 16*c .. +15);
+    // headers: Q4_K dword j = row*4 + p, Q8_0 dword j = row (two f16 scales)
+    uint32_t noff[NI], hoff[HI];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            woff[1 + i] = (uint32_t)q4k_hdword(clamp_row(32 * wave + 16 * i + (lane >> 2)), nsb, 0, lane & 3);
-    } else {
+    for (int i = 0; i < NI; ++i) {
+        const int j = wave * NSLOT + 64 * i + (lane < NL ? lane : 0);
+        const int row = j & 127, hc = j >> 7;
+        if (QT == 12) noff[i] = (uint32_t)q4k_piece(clamp_row(row), nsb, 0, hc, 0);
+        else noff[i] = (uint32_t)(clamp_row(row) * K + 32 * (hc >> 1) + 16 * (hc & 1));
+    }
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            woff[i] = (uint32_t)(clamp_row(32 * wave + 16 * i + (lane >> 2)) * K + 16 * (lane & 3));
-        woff[2] = (uint32_t)(clamp_row(32 * wave + (lane & 31)) * (K >> 5) * 2);
+    for (int i = 0; i < HI; ++i) {
+        const int j = wave * HSLOT + 64 * i + (lane < HL ? lane : 0);
+        if (QT == 12) hoff[i] = (uint32_t)q4k_hdword(clamp_row(j >> 2), nsb, 0, j & 3);
+        else hoff[i] = (uint32_t)(clamp_row(j) * (K >> 5) * 2);
     }
     auto xcopy = [&](int kit, int slot) {
         const bf16_t* base = X + kit * BK;
@@ -379,19 +401,25 @@ __global__ __launch_bounds__(256) void k_gemm_dma(const uint8_t* __restrict__ Wq
     };
     auto wcopy = [&](int kit, int slot) {
         const uint32_t l = wlds + slot * RAW;
-        if (QT == 12) {
-            dma16(l + wave * 1024, Wq + kit * 16, woff[0]);
-            dma4(l + NIB + (32 * wave) * 16, Wq + (kit >> 2) * 64, woff[1]);
-            dma4(l + NIB + (32 * wave + 16) * 16, Wq + (kit >> 2) * 64, woff[2]);
-        } else {
-            dma16(l + (32 * wave) * 64, Wq + kit * 64, woff[0]);
-            dma16(l + (32 * wave + 16) * 64, Wq + kit * 64, woff[1]);
-            dma4(l + NIB + wave * 256, Wa + kit * 4, woff[2]);
+        const uint8_t* nb = QT == 12 ? Wq + kit * 16 : Wq + kit * 64;
+        const uint8_t* hb = QT == 12 ? Wq + (kit >> 2) * 64 : Wa + kit * 4;
+#pragma unroll
+        for (int i = 0; i < NI; ++i) {
+            if (NL == 64 || lane < NL) dma16(l + (wave * NSLOT + 64 * i) * 16, nb, noff[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < HI; ++i) {
+            if (HL == 64 || lane < HL) dma4(l + NIB + (wave * HSLOT + 64 * i) * 4, hb, hoff[i]);
         }
     };
 
-    // ---- dequantization: thread -> tile row wc, half wh (wave-uniform)
-    const int wc = tid & (BN - 1), wh = tid >> 7;
+    // ---- dequantization: thread -> tile row wc and (wave-uniform) part q:
+    // 4 waves: q = piece / half wh, quarters 0..3; 8 waves: piece / half
+    // wh = q >> 1, quarters 2*(q & 1) + {0, 1}
+    constexpr int QPT = 16 / NW;  // quarters (8 weights) per thread per K step
+    const int wc = tid & (BN - 1), q = tid >> 7;
+    const int wh = NW == 4 ? q : q >> 1;
+    const int qbase = NW == 4 ? 0 : 2 * (q & 1);
     bool wvalid;
     (void)tile_row<GU>(wc, bx, nout, up_off, wvalid);
     // Per K step each thread converts 32 weights.  Byte -> f32 goes through
@@ -412,7 +440,7 @@ __global__ __launch_bounds__(256) void k_gemm_dma(const uint8_t* __restrict__ Wq
         Raw R;
         const uint8_t* w = &Wr[slot][0];
         if (QT == 12) {
-            R.q0 = *reinterpret_cast<const uint4*>(w + wc * 32 + wh * 16);
+            R.q0 = *reinterpret_cast<const uint4*>(w + (wh * BN + wc) * 16);
             R.q1 = R.q0;
             const uint4 h = *reinterpret_cast<const uint4*>(w + NIB + wc * 16);
             const uint32_t hw = *reinterpret_cast<const uint32_t*>(w + NIB + wc * 16 + (kit & 3) * 4);
@@ -423,9 +451,10 @@ __global__ __launch_bounds__(256) void k_gemm_dma(const uint8_t* __restrict__ Wq
             R.s1 = d * (float)((hw >> 12) & 63u);
             R.c1 = __builtin_fmaf(128.0f, R.s1, dm * (float)((hw >> 18) & 63u));
         } else {
-            R.q0 = *reinterpret_cast<const uint4*>(w + wc * 64 + wh * 32);
-            R.q1 = *reinterpret_cast<const uint4*>(w + wc * 64 + wh * 32 + 16);
-            const uint32_t sc = *reinterpret_cast<const uint32_t*>(w + NIB + (wc >> 5) * 256 + (wc & 31) * 4);
+            // 4 waves: both 16-B pieces of the half; 8 waves: only piece q & 1
+            R.q0 = *reinterpret_cast<const uint4*>(w + ((wh * 2 + (NW == 4 ? 0 : (q & 1))) * BN + wc) * 16);
+            R.q1 = NW == 4 ? *reinterpret_cast<const uint4*>(w + ((wh * 2 + 1) * BN + wc) * 16) : R.q0;
+            const uint32_t sc = *reinterpret_cast<const uint32_t*>(w + NIB + wc * 4);
             float d = f16_to_f32((uint16_t)(wh ? sc >> 16 : sc));
             if (!wvalid) d = 0.0f;
             R.s0 = R.s1 = d;
@@ -433,28 +462,34 @@ __global__ __launch_bounds__(256) void k_gemm_dma(const uint8_t* __restrict__ Wq
         }
         return R;
     };
-    // quarter qtr (0..3) of the tile row: 8 weights -> one 16-B chunk
-    auto dequant = [&](const Raw& R, int buf, int qtr) {
+    // the thread's quarter k (0 .. QPT-1, compile-time): 8 weights -> one 16-B chunk
+    auto dequant = [&](const Raw& R, int buf, int k) {
         bf16_t* wt = &Ws[buf][0];
         uint32_t a, b;
         float sc, c;
         int ch;
         uint32_t E;
         if (QT == 12) {
-            const bool hi = qtr >= 2;  // quarters 0,1: low nibbles (first half); 2,3: high (second)
-            const uint32_t qa = (qtr & 1) ? R.q0.z : R.q0.x, qb = (qtr & 1) ? R.q0.w : R.q0.y;
-            a = hi ? (qa >> 4) & 0x0F0F0F0Fu : qa & 0x0F0F0F0Fu;
-            b = hi ? (qb >> 4) & 0x0F0F0F0Fu : qb & 0x0F0F0F0Fu;
+            // low nibbles = first 32 weights of the step, high = second 32; 4 waves:
+            // quarters 0,1 low and 2,3 high; 8 waves: the half is q & 1
+            const int hi = NW == 4 ? (k >> 1) : (q & 1);
+            const int sel = NW == 4 ? (k & 1) : k;
+            const uint32_t qa = sel ? R.q0.z : R.q0.x, qb = sel ? R.q0.w : R.q0.y;
+            a = (qa >> (4 * hi)) & 0x0F0F0F0Fu;
+            b = (qb >> (4 * hi)) & 0x0F0F0F0Fu;
             sc = hi ? R.s1 : R.s0;
             c = hi ? R.c1 : R.c0;
-            ch = (hi ? 4 : 0) + 2 * wh + (qtr & 1);
+            ch = 4 * hi + 2 * wh + sel;
             E = 0x43434343u;
         } else {
-            a = (qtr == 0 ? R.q0.x : qtr == 1 ? R.q0.z : qtr == 2 ? R.q1.x : R.q1.z) ^ 0x80808080u;
-            b = (qtr == 0 ? R.q0.y : qtr == 1 ? R.q0.w : qtr == 2 ? R.q1.y : R.q1.w) ^ 0x80808080u;
+            // 4 waves: quarters 0,1 from q0 and 2,3 from q1; 8 waves: both from q0
+            const uint4 src = (NW == 4 && k >= 2) ? R.q1 : R.q0;
+            const int sel = NW == 4 ? (k & 1) : k;
+            a = (sel ? src.z : src.x) ^ 0x80808080u;
+            b = (sel ? src.w : src.y) ^ 0x80808080u;
             sc = R.s0;
             c = R.c0;
-            ch = 4 * wh + qtr;
+            ch = 4 * wh + qbase + k;
             E = 0x47474747u;
         }
         // byte i of v into byte 2 (Q4_K) or byte 1 (Q8_0), exponent byte from E
@@ -481,23 +516,29 @@ __global__ __launch_bounds__(256) void k_gemm_dma(const uint8_t* __restrict__ Wq
     // MFMAs of one K step on X slot xs / W buffer wb; with has_next, the raw
     // tile in slot rs (step kn) is dequantized into W buffer wb ^ 1
     auto step = [&](int xs, int wb, bool has_next, int rs, int kn) {
-        Raw R;
-        if (has_next) R = rload(rs, kn);
         const bf16_t* xt = &Xs[xs][0];
         const bf16_t* wt = &Ws[wb][0];
+        // every operand fragment of the step is requested up front so the LDS
+        // latency overlaps the first MFMAs
+        bf16x8_t a[4][MT], b[4][2];
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
             const int ch = 2 * kk + lhalf;
-            bf16x8_t a[MT], b[2];
 #pragma unroll
-            for (int t = 0; t < MT; ++t) a[t] = *reinterpret_cast<const bf16x8_t*>(xt + swz(wm * TM + 32 * t + lr, ch));
+            for (int t = 0; t < MT; ++t)
+                a[kk][t] = *reinterpret_cast<const bf16x8_t*>(xt + swz(wm * TM + 32 * t + lr, ch));
 #pragma unroll
-            for (int t = 0; t < 2; ++t) b[t] = *reinterpret_cast<const bf16x8_t*>(wt + swz(wn * 64 + 32 * t + lr, ch));
+            for (int t = 0; t < 2; ++t) b[kk][t] = *reinterpret_cast<const bf16x8_t*>(wt + swz(wn * 64 + 32 * t + lr, ch));
+        }
+        Raw R;
+        if (has_next) R = rload(rs, kn);
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
 #pragma unroll
             for (int i = 0; i < MT; ++i)
 #pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
-            if (has_next) dequant(R, wb ^ 1, kk);
+                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(a[kk][i], b[kk][j], acc[i][j]);
+            if (has_next && (kk % (4 / QPT)) == (4 / QPT) - 1) dequant(R, wb ^ 1, kk / (4 / QPT));
         }
     };
 
@@ -519,7 +560,7 @@ __global__ __launch_bounds__(256) void k_gemm_dma(const uint8_t* __restrict__ Wq
         {
             const Raw R = rload(0, kit0);
 #pragma unroll
-            for (int q = 0; q < 4; ++q) dequant(R, 0, q);
+            for (int k = 0; k < QPT; ++k) dequant(R, 0, k);
         }
         __syncthreads();
     }
@@ -657,12 +698,13 @@ static hipError_t gemm_t(const GemmPlan& p, const WeightView& w, const bf16_t* x
                                      : (uint64_t)w.N * (uint64_t)w.K;
     if (!EXACT && xbytes < (1ull << 32) && wbytes < (1ull << 32) && !env_int("THQ_GEMM_V1", 0)) {
         const unsigned nb = (unsigned)(p.tiles_n * p.tiles_m * p.splits);
+        constexpr int WM = BM == 64 ? 2 : 4;  // 8 waves (2 per SIMD) for the large tiles
         if (p.splits == 1) {
-            hipLaunchKernelGGL((k_gemm_dma<QT, BM, GU, YT, false>), dim3(nb), dim3(256), 0, s, w.q, w.aux, x, y, M,
-                               (int)w.K, nout, up_off, nout, p.kps, (int)p.tiles_n, (int)p.tiles_m);
+            hipLaunchKernelGGL((k_gemm_dma<QT, BM, WM, GU, YT, false>), dim3(nb), dim3(128 * WM), 0, s, w.q, w.aux,
+                               x, y, M, (int)w.K, nout, up_off, nout, p.kps, (int)p.tiles_n, (int)p.tiles_m);
             return hipGetLastError();
         }
-        hipLaunchKernelGGL((k_gemm_dma<QT, BM, GU, float, true>), dim3(nb), dim3(256), 0, s, w.q, w.aux, x,
+        hipLaunchKernelGGL((k_gemm_dma<QT, BM, WM, GU, float, true>), dim3(nb), dim3(128 * WM), 0, s, w.q, w.aux, x,
                            (void*)ws, M, (int)w.K, nout, up_off, (int64_t)w.N, p.kps, (int)p.tiles_n,
                            (int)p.tiles_m);
         const int64_t total = (int64_t)M * nout;

@@ -343,7 +343,9 @@ hipError_t run_nx(const GemvPlan& p, const WeightView& w, const bf16_t* x, void*
 template <int QT, bool GU, typename YT>
 hipError_t run_e(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* y, int M, int64_t nout,
                  int64_t up_off, float* ws, hipStream_t s) {
+    // live accumulator rows per lane: rows 4g + e < M, e < E
     if (M == 1) return run_nx<QT, 1, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
+    if (M == 2) return run_nx<QT, 2, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
     return run_nx<QT, 4, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
 }
 
