@@ -120,7 +120,7 @@ struct Q4Unit {
 // lane's 16-B offsets inside a row quad for chunk c (clamped to a real
 // superblock: lanes past K multiply by zero activations)
 template <bool GU>
-__device__ __forceinline__ void q4k_unit_load(Q4Unit<GU>& U, const uint8_t* __restrict__ W, int64_t gq, int c,
+__device__ __forceinline__ void q4k_unit_load(Q4Unit<GU>& U, const uint8_t* W, int64_t gq, int c,
                                               int64_t up_off, int nsb, int lane) {
     int s = 16 * c + (lane >> 2);
     const int li = s < nsb ? 16 * c * 4 + lane : (lane & 3);
@@ -296,18 +296,30 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_bf16(const uint8_t* __restric
 
 // One-shot variant for K <= 4096: one wave per row quad, every load issued at
 // entry, no second register set (so enough waves stay resident to keep the
-// HBM queues full).
+// HBM queues full).  The block's x loads are issued before the weight loads:
+// the wait before x goes to LDS then covers only x (vector-memory counters
+// drain in order), so the block barrier does not hold the math back until
+// every weight byte has landed, and each row's math starts as its data
+// arrives.  W and x are not __restrict__ so that the compiler barrier keeps
+// that order.
 template <bool GU, typename YT>
-__global__ __launch_bounds__(256) void k_gemv1_q4k_bf16_1s(const uint8_t* __restrict__ W,
-                                                          const bf16_t* __restrict__ x, YT* __restrict__ y,
+__global__ __launch_bounds__(256) void k_gemv1_q4k_bf16_1s(const uint8_t* W, const bf16_t* x, YT* __restrict__ y,
                                                           int64_t nout, int K, int64_t up_off, int64_t nquads) {
     extern __shared__ uint4 lds[];  // x (K bf16)
     const int lane = threadIdx.x & 63;
     const int64_t gq = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const int nsb = K >> 8;
-    Q4Unit<GU> A;
-    if (gq < nquads) q4k_unit_load<GU>(A, W, gq, 0, up_off, nsb, lane);
-    for (int i = threadIdx.x; i < (K >> 3); i += blockDim.x) lds[i] = reinterpret_cast<const uint4*>(x)[i];
+    // 16-B chunks of x: two per thread (K / 8 <= 512)
+    const int nx = K >> 3;
+    const int c0 = threadIdx.x, c1 = threadIdx.x + 256;
+    const uint4 xv0 = reinterpret_cast<const uint4*>(x)[c0 < nx ? c0 : nx - 1];
+    const uint4 xv1 = reinterpret_cast<const uint4*>(x)[c1 < nx ? c1 : nx - 1];
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    Q4Unit<GU> A;  // unconditional (clamped quad) so the wait counts stay exact
+    q4k_unit_load<GU>(A, W, gq < nquads ? gq : nquads - 1, 0, up_off, nsb, lane);
+    if (c0 < nx) lds[c0] = xv0;
+    if (c1 < nx) lds[c1] = xv1;
     __syncthreads();
     if (gq >= nquads) return;
     const int s = lane >> 2;
