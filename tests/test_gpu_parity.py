@@ -129,6 +129,21 @@ def test_q4k_decode_gemv(m, n, k):
     assert_close_elem(f"q4k gemv m={m}", y, ref, 2.0 ** -12)
 
 
+@pytest.mark.parametrize("n,k", [(202, 8192), (130, 16384)])
+def test_q4k_gemv_m1_k_split(n, k):
+    """M = 1 decode GEMV with K split over 2 / 4 chunks per block (ragged row
+    quads); also the fused gate/up form on the same weight."""
+    b, w = upload(O.Q4_K, n, k, seed=4)
+    xf, xb = bf16_x(1, k, seed=6)
+    y = tonp(thq.matmul(w, xb, torch.float32))
+    ref = O.matmul(O.Q4_K, b, n, k, xf, O.MODE_DEQUANT_F32)
+    assert rel_row_err(y, ref) <= 1e-2
+    assert_close_elem(f"q4k gemv m=1 {n}x{k}", y, ref, 2.0 ** -12)
+    act = tonp(thq.gate_up_silu(w, xb, torch.float32))
+    want = O.bf16_bits_to_f32(O.gate_up_silu(y))
+    assert_close_elem(f"q4k gate/up m=1 {n}x{k}", act, want, 2.0 ** -7)
+
+
 @pytest.mark.parametrize("qtype", [O.Q4_K, O.Q8_0])
 @pytest.mark.parametrize("n,k", [(100, 256), (777, 1024), (300, 2816)])
 @pytest.mark.parametrize("m", [2, 3, 8])

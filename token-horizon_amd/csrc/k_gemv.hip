@@ -294,6 +294,78 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_bf16(const uint8_t* __restric
     }
 }
 
+// K-split one-shot variant for 4096 < K <= KC * 4096: a block holds 4 row
+// quads x KC waves, wave (quad, chunk) loads its 4096-wide chunk of the quad
+// at entry (after the block's x loads, as in the one-shot kernel) and the
+// chunks' row totals are summed in LDS in chunk order before the epilogue.
+template <int KC, bool GU, typename YT>
+__global__ __launch_bounds__(256 * KC) void k_gemv1_q4k_bf16_ks(const uint8_t* W, const bf16_t* x,
+                                                               YT* __restrict__ y, int64_t nout, int K,
+                                                               int64_t up_off, int64_t nquads) {
+    extern __shared__ uint4 lds[];  // x (K bf16)
+    __shared__ float red[4][KC][8];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int c = wv % KC, qb = wv / KC;
+    const int64_t gq = (int64_t)blockIdx.x * 4 + qb;
+    const int nsb = K >> 8;
+    // x: two 16-B chunks per thread (K / 8 <= 512 * KC = 2 * blockDim)
+    const int nx = K >> 3, nt = 256 * KC;
+    const int x0 = threadIdx.x, x1 = threadIdx.x + nt;
+    const uint4 xv0 = reinterpret_cast<const uint4*>(x)[x0 < nx ? x0 : nx - 1];
+    const uint4 xv1 = reinterpret_cast<const uint4*>(x)[x1 < nx ? x1 : nx - 1];
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    Q4Unit<GU> A;
+    q4k_unit_load<GU>(A, W, gq < nquads ? gq : nquads - 1, c, up_off, nsb, lane);
+    if (x0 < nx) lds[x0] = xv0;
+    if (x1 < nx) lds[x1] = xv1;
+    __syncthreads();
+    const int s = 16 * c + (lane >> 2);
+    uint32_t xlo[16], xhi[16];
+    float sxlo = 0.0f, sxhi = 0.0f;
+    if (s < nsb) {
+        const uint4* xp = lds + s * 32 + 8 * (lane & 3);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint4 p = xp[v], q = xp[4 + v];
+            xlo[4 * v] = p.x; xlo[4 * v + 1] = p.y; xlo[4 * v + 2] = p.z; xlo[4 * v + 3] = p.w;
+            xhi[4 * v] = q.x; xhi[4 * v + 1] = q.y; xhi[4 * v + 2] = q.z; xhi[4 * v + 3] = q.w;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            sxlo = dot2_bf16(xlo[i], 0x3F803F80u, sxlo);  // bf16 (1, 1)
+            sxhi = dot2_bf16(xhi[i], 0x3F803F80u, sxhi);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) { xlo[i] = 0; xhi[i] = 0; }
+    }
+    float acc[GU ? 8 : 4];
+#pragma unroll
+    for (int i = 0; i < (GU ? 8 : 4); ++i) acc[i] = 0.0f;
+    q4k_unit_compute<GU>(acc, A, xlo, xhi, sxlo, sxhi);
+    // per-chunk row totals: slots 0..3 (gate rows for GU), 4..7 (up rows)
+    if constexpr (GU) {
+        const float tot = reduce_slots8(acc, lane);
+        if (!(lane & 7)) red[qb][c][4 * (lane >> 5) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1)] = tot;
+    } else {
+        const float tot = reduce_slots<4>(acc, lane);
+        if (!(lane & 15)) red[qb][c][slot_of_lane<4>(lane)] = tot;
+    }
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        const int q2 = threadIdx.x >> 2, r = threadIdx.x & 3;
+        float g = 0.0f, u = 0.0f;
+#pragma unroll
+        for (int cc = 0; cc < KC; ++cc) {
+            g += red[q2][cc][r];
+            if (GU) u += red[q2][cc][r + 4];
+        }
+        const int64_t o = 4 * ((int64_t)blockIdx.x * 4 + q2) + r;
+        if (o < nout) store_y<YT>(y + o, GU ? silu_mul(g, u) : g);
+    }
+}
+
 // One-shot variant for K <= 4096: one wave per row quad, every load issued at
 // entry, no second register set (so enough waves stay resident to keep the
 // HBM queues full).  The block's x loads are issued before the weight loads:
@@ -571,6 +643,14 @@ static void launch_q4k_bf16_t(const uint8_t* W, const bf16_t* x, YT* y, int64_t 
         hipLaunchKernelGGL((k_gemv1_q4k_bf16_1s<GU, YT>), dim3((unsigned)((nquads + 3) / 4)), dim3(256), lds, s, W, x,
                            y, nout, K, up_off, nquads);
         return;
+    }
+    if (K <= 4 * 4096 && env_int("THQ_GEMV_ONESHOT", 1)) {
+        const dim3 grid((unsigned)((nquads + 3) / 4));
+        switch ((K + 4095) / 4096) {
+            case 2: hipLaunchKernelGGL((k_gemv1_q4k_bf16_ks<2, GU, YT>), grid, dim3(512), lds, s, W, x, y, nout, K, up_off, nquads); return;
+            case 3: hipLaunchKernelGGL((k_gemv1_q4k_bf16_ks<3, GU, YT>), grid, dim3(768), lds, s, W, x, y, nout, K, up_off, nquads); return;
+            default: hipLaunchKernelGGL((k_gemv1_q4k_bf16_ks<4, GU, YT>), grid, dim3(1024), lds, s, W, x, y, nout, K, up_off, nquads); return;
+        }
     }
     const unsigned grid = (unsigned)((waves + 3) / 4);
     switch ((K / 256 + 15) / 16) {
