@@ -38,7 +38,9 @@ extern "C" {
  * on the path engine/src/model.rs:551-562 -> quantized_qwen3::ModelWeights. */
 typedef enum thq_dtype {
     THQ_Q8_0 = 8,  /* 32 weights / 34 B: f16 d, i8 qs[32]                        */
-    THQ_Q4_K = 12  /* 256 weights / 144 B: f16 d, f16 dmin, u8 scales[12], u8 qs[128] */
+    THQ_Q4_K = 12, /* 256 weights / 144 B: f16 d, f16 dmin, u8 scales[12], u8 qs[128] */
+    THQ_Q8_K = 15  /* 256 activations / 292 B: f32 d, i8 qs[256], i16 bsums[16]
+                      (dot type of Q4_K; thq_quantize_act only)                   */
 } thq_dtype;
 
 /* activation / output element types */
@@ -49,6 +51,9 @@ typedef enum thq_act {
 
 /* thq_matmul flags */
 #define THQ_MODE_DEQUANT_F32 0u /* y = x . dequant(W)^T, f32 accumulation (default)  */
+#define THQ_MODE_Q8ACT 0x1u     /* candle's default CPU semantics: x rows quantized to
+                                   Q8_0 (Q8_0 W) or Q8_K (Q4_K W), exact integer
+                                   block dots, f32 block scaling                     */
 #define THQ_MODE_EXACT_W 0x10u  /* never round dequantized weights to bf16 on MFMA   */
 
 /* error codes */
@@ -115,6 +120,16 @@ int thq_weight_download(const thq_weight* w, void* host_blocks);
  * with candle's BlockQ8_0/BlockQ4K::to_float. */
 int thq_dequantize(thq_ctx* ctx, const thq_weight* w, float* out_dev, void* stream);
 
+/* Quantize activation rows x[M, K] (f32 or bf16, 16-byte aligned) to GGML
+ * blocks of `dot_type`: THQ_Q8_0 (34-B blocks, 2-byte aligned blocks_dev) or
+ * THQ_Q8_K (292-B blocks, 4-byte aligned), M * K/bs blocks row-major.
+ * Bit-identical to [ext] candle-core 0.11 BlockQ8_0::from_float /
+ * BlockQ8K::from_float, the first step of k_quants::matmul that candle's
+ * QMatMul::forward runs for quantized weights (and the step THQ_MODE_Q8ACT
+ * runs inside thq_matmul).  bf16 x is widened to f32 exactly first. */
+int thq_quantize_act(thq_ctx* ctx, thq_dtype dot_type, const void* x_dev, thq_act x_type, int64_t m, int64_t k,
+                     void* blocks_dev, void* stream);
+
 /* y[M, N] = x[M, K] . W^T with f32 accumulation.
  * Replaces QMatMul::forward ([ext] candle-core 0.11 quantized/mod.rs, called
  * for every projection by quantized_qwen3) and the engine's routed projection
@@ -123,6 +138,11 @@ int thq_dequantize(thq_ctx* ctx, const thq_weight* w, float* out_dev, void* stre
  *   M >= 2     MFMA GEMM; weights are rounded to bf16 on the MFMA path unless
  *              THQ_MODE_EXACT_W (or Q8_0 with M <= 64), activations bf16.
  *   x f32 with M >= 2 runs an exact f32 path.
+ * THQ_MODE_Q8ACT instead reproduces candle's default CPU k_quants::matmul:
+ * x rows are quantized as thq_quantize_act does (into the context
+ * workspace), every block dot is exact in integers and scaled in f32; only
+ * the f32 summation order over blocks differs from candle's.  Any M; x must
+ * be 16-byte aligned (THQ_EALIGN otherwise).
  * Inputs: x_dev [M, K] of x_type, y_dev [M, N] of y_type, both contiguous.
  * M == 0 is a no-op.  Errors: THQ_ESHAPE for K mismatch, THQ_EINVAL for
  * null pointers. */

@@ -1,0 +1,177 @@
+"""GPU parity of THQ_MODE_Q8ACT (candle's default CPU matmul semantics).
+
+[ext] candle-core 0.11 k_quants::matmul quantizes each activation row to the
+weight's dot type (BlockQ8_0::from_float for Q8_0 weights, BlockQ8K::from_float
+for Q4_K weights), then takes exact integer block dots scaled in f32.
+
+The bars are as follows:
+  - thq_quantize_act is bit-exact against the oracle's restatement of both
+    quantizers (GGML block bytes compared), including zero blocks, NaNs,
+    opposite-sign ties and half-way rounding.
+  - thq_matmul(THQ_MODE_Q8ACT) matches the oracle's Q8ACT matmul to 1e-5 of
+    the row norm. The integer parts are exact, so only the f32 order of the
+    block sums differs: ten times tighter than the f32 bar of 1e-4.
+  - It stays within the f32 / bf16 bars of the exact (DEQUANT_F32) result
+    only loosely. Q8 activations cost accuracy, which is candle's behaviour,
+    so that check is 1e-2.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import activations, assert_close_elem, rel_row_err, weight_bytes
+
+pytestmark = pytest.mark.gpu
+
+thq = pytest.importorskip("thq")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    torch.cuda.init()
+    yield
+    torch.cuda.synchronize()
+
+
+def tonp(t):
+    return t.float().cpu().numpy()
+
+
+def edge_rows(k: int) -> np.ndarray:
+    """Rows that exercise the quantizers' special cases (k >= 512)."""
+    rows = np.zeros((4, k), np.float32)
+    # row 0 stays zero: d = 0, all quants 0
+    # row 1: amax = 127 in the first 32-block (d = 1: x.5 rounds away from zero)
+    #        and max = -128 in the first 256-block (iscale = 1 for Q8_K)
+    rows[1, :32] = np.arange(32, dtype=np.float32) - 15.5
+    rows[1, 31] = 127.0
+    rows[1, 40] = -128.0
+    rows[1, 41:64] = np.arange(23, dtype=np.float32) + 0.5
+    # row 2: opposite-sign ties (the first of equal magnitudes is the Q8_K max)
+    rows[2, 3] = 2.0
+    rows[2, 7] = -2.0
+    rows[2, 300] = -3.0
+    rows[2, 301] = 3.0
+    rows[2, 256:300] = 0.25
+    # row 3: NaNs (never the max; Q8_0 quantizes NaN to 0, Q8_K to 127)
+    rows[3] = O.randn(9, 3, 1.0, (k,))
+    rows[3, 5] = np.nan
+    rows[3, 260] = np.nan
+    rows[3, 480:512] = np.nan  # a Q8_0 block of NaNs only
+    return rows
+
+
+def oracle_q8(dot_type: int, x: np.ndarray) -> np.ndarray:
+    rows = [O.quantize_q8_0_row(r) if dot_type == thq.Q8_0 else O.quantize_q8_k(r) for r in x]
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("dot_type", [thq.Q8_0, thq.Q8_K])
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+def test_quantize_act_bit_exact(dot_type, act):
+    k = 4096
+    x = np.concatenate([edge_rows(k), activations(5, k, seed=21)])
+    if act == "bf16":
+        x = O.bf16_round(x)
+        xt = torch.from_numpy(x).cuda().to(torch.bfloat16)
+    else:
+        xt = torch.from_numpy(x).cuda()
+    got = thq.quantize_act(xt, dot_type).cpu().numpy()
+    want = oracle_q8(dot_type, x)
+    assert got.shape == want.shape
+    bad = np.argwhere(got != want)
+    assert bad.size == 0, f"{len(bad)} bytes differ; first (row, byte) {tuple(bad[0])}"
+
+
+def q8act_ref(qtype, b, n, k, x):
+    return O.matmul(qtype, b, n, k, x, O.MODE_Q8ACT)
+
+
+CASES = [
+    (O.Q8_0, 3072, 1024, 1),   # the Q8_0 single-matmul shape
+    (O.Q8_0, 3072, 1024, 5),
+    (O.Q8_0, 100, 1056, 3),    # K chunk of 1024 + one block
+    (O.Q8_0, 257, 2048, 17),   # two row tiles of 8 plus one row
+    (O.Q4_K, 1024, 4096, 1),
+    (O.Q4_K, 1024, 4096, 3),
+    (O.Q4_K, 1024, 4096, 8),
+    (O.Q4_K, 1024, 4096, 13),
+    (O.Q4_K, 130, 2816, 2),    # 11 superblocks: a partial 4096 chunk
+    (O.Q4_K, 301, 12288, 4),   # row tiles limited by LDS (4 rows of 12288)
+    (O.Q4_K, 66, 16384, 9),
+]
+
+
+@pytest.mark.parametrize("qtype,n,k,m", CASES)
+@pytest.mark.parametrize("act", ["f32", "bf16"])
+def test_q8act_matmul_matches_oracle(qtype, n, k, m, act):
+    b = weight_bytes(qtype, n, k, seed=2)
+    w = thq.QTensor.from_gguf_bytes(qtype, b, n, k)
+    x = activations(m, k, seed=8)
+    if act == "bf16":
+        x = O.bf16_round(x)
+        xt = torch.from_numpy(x).cuda().to(torch.bfloat16)
+    else:
+        xt = torch.from_numpy(x).cuda()
+    y = tonp(thq.matmul(w, xt, torch.float32, flags=thq.MODE_Q8ACT))
+    ref = q8act_ref(qtype, b, n, k, x)
+    err = rel_row_err(y, ref)
+    assert err <= 1e-5, err
+    assert_close_elem(f"q8act {qtype} {n}x{k} m={m}", y, ref, 2.0 ** -14)
+    # Q8 activations stay close to the exact product (candle's accuracy)
+    assert rel_row_err(y, O.matmul(qtype, b, n, k, x, O.MODE_DEQUANT_F32)) <= 1e-2
+
+
+@pytest.mark.parametrize("qtype,n,k,m", [(O.Q4_K, 1000, 1024, 1), (O.Q4_K, 1000, 1024, 6), (O.Q8_0, 1000, 1024, 3)])
+def test_q8act_gate_up(qtype, n, k, m):
+    """Fused gate/up in Q8ACT mode: the epilogue over the same integer dots.
+    h = 1000 outputs is not a multiple of 4 x 4-output waves (ragged)."""
+    bg = weight_bytes(qtype, n, k, seed=31)
+    bu = weight_bytes(qtype, n, k, seed=32)
+    both = np.concatenate([bg, bu])
+    fused = thq.QTensor.from_gguf_bytes(qtype, both, 2 * n, k)
+    xf = O.bf16_round(activations(m, k, seed=33))
+    xb = torch.from_numpy(xf).cuda().to(torch.bfloat16)
+    gu = tonp(thq.matmul(fused, xb, torch.float32, flags=thq.MODE_Q8ACT))
+    assert rel_row_err(gu, q8act_ref(qtype, both, 2 * n, k, xf)) <= 1e-5
+    got = tonp(thq.gate_up_silu(fused, xb, torch.bfloat16, flags=thq.MODE_Q8ACT))
+    # same integer dots and summation tree as the plain matmul: only the
+    # device exp can move a value by one bf16 step
+    want = O.bf16_bits_to_f32(O.gate_up_silu(gu))
+    assert_close_elem(f"q8act gate/up m={m}", got, want, 2.0 ** -7)
+    assert (got == want).mean() > 0.99
+
+
+def test_q8act_argmax_and_bf16_out():
+    n, k, m = 5000, 1024, 3
+    b = weight_bytes(O.Q8_0, n, k, seed=41)
+    w = thq.QTensor.from_gguf_bytes(O.Q8_0, b, n, k)
+    x = activations(m, k, seed=42)
+    xt = torch.from_numpy(x).cuda()
+    logits, idx = thq.matmul_argmax(w, xt, flags=thq.MODE_Q8ACT)
+    ref = q8act_ref(O.Q8_0, b, n, k, x)
+    assert rel_row_err(tonp(logits), ref) <= 1e-5
+    assert np.array_equal(idx.cpu().numpy().astype(np.uint32), O.argmax_rows(tonp(logits)))
+    # internal logits (NULL): the workspace holds both the quantized rows and the logits
+    _, idx2 = thq.matmul_argmax(w, xt, want_logits=False, flags=thq.MODE_Q8ACT)
+    assert torch.equal(idx, idx2)
+    yb = tonp(thq.matmul(w, xt, torch.bfloat16, flags=thq.MODE_Q8ACT))
+    assert np.array_equal(yb, O.bf16_round(tonp(logits)))
+
+
+def test_q8act_errors():
+    b = weight_bytes(O.Q8_0, 64, 1024, seed=1)
+    w = thq.QTensor.from_gguf_bytes(O.Q8_0, b, 64, 1024)
+    buf = torch.zeros(1025, device="cuda")
+    with pytest.raises(thq.ThqError) as e:  # x starts 4 bytes past a 16-byte boundary
+        thq.matmul(w, buf[1:].view(1, 1024), flags=thq.MODE_Q8ACT)
+    assert e.value.code == thq.EALIGN
+    with pytest.raises(thq.ThqError) as e:
+        thq.quantize_act(torch.zeros((1, 1000), device="cuda"), thq.Q8_K)
+    assert e.value.code == thq.ESHAPE
+    with pytest.raises(thq.ThqError) as e:
+        thq.quantize_act(torch.zeros((1, 1024), device="cuda"), thq.Q4_K)
+    assert e.value.code == thq.EDTYPE

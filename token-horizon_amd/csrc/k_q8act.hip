@@ -1,0 +1,529 @@
+// k_q8act.hip — THQ_MODE_Q8ACT: candle's default CPU matmul semantics on gfx950.
+//
+// [ext] candle-core 0.11 k_quants::matmul((m, k, n), lhs, rhs_t, dst) first
+// quantizes every activation row to the weight's VecDotType
+// (BlockQ8_0::from_float for Q8_0 weights, BlockQ8K::from_float for Q4_K
+// weights), then computes each output as T::vec_dot(k, w_row, x_row_q): an
+// integer dot per block, scaled in f32.  Here the quantizers are
+// bit-identical to candle's, and the integer block dots are exact
+// (v_dot4_i32_i8).  Only the f32 order in which the block terms are summed
+// differs from candle's.
+//
+// Quantized activations on the device (split planes, internal):
+//   xq [M][K] i8
+//   Q8_0: xd [M][K/32] f32 = f32(f16(d)), the value vec_dot multiplies by
+//   Q8_K: xd [M][K/256] f32 d, xb [M][K/32] i16 sums of 32 quants
+//         (pairs of GGML's 16-wide bsums)
+// thq_quantize_act writes GGML blocks instead (34-B Q8_0, 292-B Q8_K).
+//
+// The quantizers are compiled with -ffp-contract=off: every product and
+// quotient rounds as written, like the Rust code they follow.
+#include "thq_dev.hpp"
+#include "thq_kernels.hpp"
+
+namespace thq {
+namespace {
+
+// ------------------------------------------------------------------ helpers
+__device__ __forceinline__ void load4(const float* p, float (&v)[4]) {
+    const float4 t = *reinterpret_cast<const float4*>(p);
+    v[0] = t.x;
+    v[1] = t.y;
+    v[2] = t.z;
+    v[3] = t.w;
+}
+__device__ __forceinline__ void load4(const bf16_t* p, float (&v)[4]) {
+    const uint2 t = *reinterpret_cast<const uint2*>(p);
+    v[0] = bf16_to_f32(t.x & 0xFFFFu);
+    v[1] = bf16_to_f32(t.x >> 16);
+    v[2] = bf16_to_f32(t.y & 0xFFFFu);
+    v[3] = bf16_to_f32(t.y >> 16);
+}
+
+// Rust `f as i8`: saturating, NaN -> 0; returned as the byte's bits
+__device__ __forceinline__ uint32_t as_i8_bits(float v) {
+    if (v != v) return 0u;
+    v = fminf(fmaxf(v, -128.0f), 127.0f);
+    return (uint32_t)(uint8_t)(int8_t)v;
+}
+
+__device__ __forceinline__ uint16_t f16_bits(float f) {
+    const _Float16 h = (_Float16)f;  // round to nearest even, like half::f16::from_f32
+    uint16_t b;
+    __builtin_memcpy(&b, &h, 2);
+    return b;
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+template <int P>
+__device__ __forceinline__ uint32_t quad_lane(uint32_t v) {  // lane P of each quad, to all four
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, P | (P << 2) | (P << 4) | (P << 6), 0xF, 0xF, false);
+}
+__device__ __forceinline__ int pair_sum(int v) {  // lanes 2i, 2i+1
+    return v + __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
+}
+__device__ __forceinline__ int quad_sum(int v) {
+    v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+    return v + __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+}
+
+// Transposed wave reduction of N per-lane values (N a power of two <= 64):
+// each step with a value count above one hands half of them to the partner
+// lane, so N values cost about N shuffles.  Afterwards a[0] of lane L is the
+// wave total of value tred_slot<N>(L).
+template <int N, int OFF>
+struct TRed {
+    static __device__ __forceinline__ void run(float* a, int lane) {
+        if constexpr (OFF == 0) {
+            return;
+        } else if constexpr (N > 1) {
+            const bool up = lane & OFF;
+#pragma unroll
+            for (int i = 0; i < N / 2; ++i) {
+                const float keep = up ? a[i + N / 2] : a[i];
+                const float give = up ? a[i] : a[i + N / 2];
+                a[i] = keep + __shfl_xor(give, OFF, 64);
+            }
+            TRed<N / 2, OFF / 2>::run(a, lane);
+        } else {
+            a[0] += __shfl_xor(a[0], OFF, 64);
+            TRed<1, OFF / 2>::run(a, lane);
+        }
+    }
+};
+
+template <int N>
+__device__ __forceinline__ int tred_slot(int lane) {
+    int s = 0, n = N;
+    for (int off = 32; off >= 1 && n > 1; off >>= 1, n >>= 1)
+        if (lane & off) s += n / 2;
+    return s;
+}
+
+// ------------------------------------------------------------------ activation quantizers
+// Q8_0 ([ext] BlockQ8_0::from_float): 8 lanes per 32-wide block, 4 values
+// per lane.  amax = max |x| from 0 (NaN never wins), d = amax / 127,
+// id = d != 0 ? 1 / d : 0, q = round(x * id) as i8, stored d = f16(d).
+template <typename XT, bool GGUF>
+__global__ __launch_bounds__(256) void k_quant_act_q8_0(const XT* __restrict__ x, int64_t nq, int8_t* __restrict__ xq,
+                                                        float* __restrict__ xd, uint8_t* __restrict__ blk) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const bool live = t < nq;  // nq is a multiple of 8: a block's lanes are all live or all not
+    float v[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (live) load4(x + 4 * t, v);
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t q = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) q |= as_i8_bits(roundf(v[i] * id)) << (8 * i);
+    if (!live) return;
+    const int64_t b = t >> 3;
+    const int j = (int)(t & 7);
+    const uint16_t dh = f16_bits(d);
+    if constexpr (GGUF) {
+        uint16_t* p = reinterpret_cast<uint16_t*>(blk + b * 34);  // 2-B aligned blocks
+        if (j == 0) p[0] = dh;
+        p[1 + 2 * j] = (uint16_t)(q & 0xFFFFu);
+        p[2 + 2 * j] = (uint16_t)(q >> 16);
+    } else {
+        reinterpret_cast<uint32_t*>(xq)[t] = q;
+        if (j == 0) xd[b] = f16_to_f32(dh);
+    }
+}
+
+// Q8_K ([ext] BlockQ8K::from_float): one wave per 256-wide block, 4 values
+// per lane.  max = the signed element of largest magnitude, the first one
+// on equal magnitudes (NaN never wins); amax == 0 gives d = 0 and zero
+// quants; else iscale = -128 / max, q = min(round(iscale * x), 127) as i8,
+// d = 1 / iscale, bsums = sums of 16 quants.
+template <typename XT, bool GGUF>
+__global__ __launch_bounds__(256) void k_quant_act_q8k(const XT* __restrict__ x, int64_t nblk, int8_t* __restrict__ xq,
+                                                       float* __restrict__ xd, int16_t* __restrict__ xb,
+                                                       uint8_t* __restrict__ blk) {
+    const int lane = threadIdx.x & 63;
+    const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= nblk) return;  // the whole wave
+    float v[4];
+    load4(x + b * 256 + 4 * lane, v);
+    float key = -1.0f, val = 0.0f;
+    int idx = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float a = fabsf(v[i]);
+        if (a > key) {
+            key = a;
+            idx = 4 * lane + i;
+            val = v[i];
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ok = __shfl_xor(key, off, 64), ov = __shfl_xor(val, off, 64);
+        const int oi = __shfl_xor(idx, off, 64);
+        if (ok > key || (ok == key && oi < idx)) {
+            key = ok;
+            idx = oi;
+            val = ov;
+        }
+    }
+    uint32_t q = 0;
+    float d = 0.0f;
+    if (key > 0.0f) {
+        const float iscale = -128.0f / val;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q |= as_i8_bits(fminf(roundf(iscale * v[i]), 127.0f)) << (8 * i);
+        d = 1.0f / iscale;
+    }
+    int s = (int)(int8_t)(q & 0xFFu) + (int)(int8_t)((q >> 8) & 0xFFu) + (int)(int8_t)((q >> 16) & 0xFFu) +
+            (int)(int8_t)(q >> 24);
+    s = quad_sum(s);  // 16 quants: lanes 4j .. 4j+3
+    const int s32 = s + __shfl_xor(s, 4, 64);
+    if constexpr (GGUF) {
+        uint8_t* p = blk + b * 292;  // 4-B aligned blocks
+        if (lane == 0) *reinterpret_cast<float*>(p) = d;
+        reinterpret_cast<uint32_t*>(p + 4)[lane] = q;
+        if ((lane & 3) == 0) reinterpret_cast<int16_t*>(p + 260)[lane >> 2] = (int16_t)s;
+    } else {
+        reinterpret_cast<uint32_t*>(xq + b * 256)[lane] = q;
+        if (lane == 0) xd[b] = d;
+        if ((lane & 7) == 0) xb[b * 8 + (lane >> 3)] = (int16_t)s32;
+    }
+}
+
+// ------------------------------------------------------------------ dot kernels
+// A wave owns four outputs (gate/up: four gate rows and the four matching up
+// rows) and walks K; a block of four waves shares MT activation rows staged
+// in LDS.  Lanes accumulate f32 block terms; the NR x MT totals are reduced
+// across the wave at the end with the transposed reduction.
+template <bool GU>
+__device__ __forceinline__ void wave_rows(int64_t (&rows)[GU ? 8 : 4], int64_t o0, int64_t nout, int64_t up_off) {
+#pragma unroll
+    for (int r = 0; r < (GU ? 8 : 4); ++r) {
+        int64_t o = o0 + (r & 3);
+        if (o >= nout) o = nout - 1;  // loads stay in bounds; the store is skipped
+        rows[r] = (GU && r >= 4) ? o + up_off : o;
+    }
+}
+
+template <int MT, bool GU, typename YT>
+__device__ __forceinline__ void q8act_store(float (&acc)[(GU ? 8 : 4) * MT], int lane, YT* __restrict__ y, int64_t o0,
+                                            int64_t nout, int m0, int mrows, int64_t ldy) {
+    constexpr int NV = (GU ? 8 : 4) * MT;
+    constexpr int SPAN = 64 / NV;
+    TRed<NV, 32>::run(acc, lane);
+    const float tot = acc[0];
+    const int slot = tred_slot<NV>(lane);
+    const int r = slot / MT, m = slot - (slot / MT) * MT;
+    if constexpr (GU) {
+        const float u = __shfl_xor(tot, 32, 64);  // up slot = gate slot + NV/2
+        if ((lane & (SPAN - 1)) || (lane & 32)) return;
+        if (m < mrows && o0 + r < nout) store_y<YT>(y + (int64_t)(m0 + m) * ldy + o0 + r, silu_mul(tot, u));
+    } else {
+        if (lane & (SPAN - 1)) return;
+        if (m < mrows && o0 + r < nout) store_y<YT>(y + (int64_t)(m0 + m) * ldy + o0 + r, tot);
+    }
+}
+
+// Q4_K weights x Q8_K activations ([ext] BlockQ4K::vec_dot).  Lane 4s'+p of
+// a 4096-wide chunk takes part p (sub-blocks 2p, 2p+1) of superblock s: the
+// two 16-B nibble pieces of each row and the row's header dword p.  Per
+// superblock and row the quad forms the exact integers
+//   aux = sum_j sc_j * (q4 . q8)_j,   mins = sum_j m_j * bsum32_j
+// and adds (d_w * d_x) * aux - (dmin_w * d_x) * mins.
+// LDS: x [MT][K/16] 16-B pieces (piece 4u + t of lane unit u at slot
+// 4u + ((t + u/4) & 3), so a lane's four reads hit distinct banks), the
+// 32-sum pairs [MT][K/64] u32 and d [MT][K/256] f32.
+template <int MT, bool GU, typename YT>
+__global__ __launch_bounds__(256) void k_q8act_q4k(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
+                                                   const float* __restrict__ xd, const int16_t* __restrict__ xb,
+                                                   YT* __restrict__ y, int M, int64_t nout, int K, int64_t up_off,
+                                                   int64_t ldy) {
+    constexpr int NR = GU ? 8 : 4;
+    extern __shared__ uint4 lds4[];
+    const int nsb = K >> 8, nu = K >> 6, npc = K >> 4;
+    const int m0 = blockIdx.y * MT;
+    const int mrows = M - m0 < MT ? M - m0 : MT;
+    uint4* xs = lds4;
+    uint32_t* bsl = reinterpret_cast<uint32_t*>(lds4 + MT * npc);
+    float* dxl = reinterpret_cast<float*>(bsl + MT * nu);
+    for (int i = threadIdx.x; i < MT * npc; i += 256) {
+        const int m = i / npc, P = i - m * npc;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (m < mrows) v = reinterpret_cast<const uint4*>(xq + (int64_t)(m0 + m) * K)[P];
+        const int u = P >> 2, t = P & 3;
+        xs[m * npc + 4 * u + ((t + (u >> 2)) & 3)] = v;
+    }
+    for (int i = threadIdx.x; i < MT * nu; i += 256) {
+        const int m = i / nu, u = i - m * nu;
+        bsl[i] = m < mrows ? reinterpret_cast<const uint32_t*>(xb + (int64_t)(m0 + m) * (K >> 5))[u] : 0u;
+    }
+    for (int i = threadIdx.x; i < MT * nsb; i += 256) {
+        const int m = i / nsb, s = i - m * nsb;
+        dxl[i] = m < mrows ? xd[(int64_t)(m0 + m) * nsb + s] : 0.0f;
+    }
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63, p = lane & 3;
+    const int64_t o0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;
+    int64_t rows[NR];
+    wave_rows<GU>(rows, o0, nout, up_off);
+    float acc[NR * MT];
+#pragma unroll
+    for (int i = 0; i < NR * MT; ++i) acc[i] = 0.0f;
+    const int nch = (nsb + 15) >> 4;
+    for (int c = 0; c < nch; ++c) {
+        const int s = 16 * c + (lane >> 2);
+        const bool live = s < nsb;
+        const int sl = live ? s : nsb - 1;
+        uint4 w0[NR], w1[NR];
+        uint32_t hw[NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            w0[r] = *reinterpret_cast<const uint4*>(W + q4k_piece(rows[r], nsb, sl, 0, p));
+            w1[r] = *reinterpret_cast<const uint4*>(W + q4k_piece(rows[r], nsb, sl, 1, p));
+            hw[r] = *reinterpret_cast<const uint32_t*>(W + q4k_hdword(rows[r], nsb, sl, p));
+        }
+        float dw[NR], dmw[NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            const uint32_t t0 = quad_lane<0>(hw[r]), t1 = quad_lane<1>(hw[r]);
+            const uint32_t t2 = quad_lane<2>(hw[r]), t3 = quad_lane<3>(hw[r]);
+            dw[r] = f16_to_f32((uint16_t)__builtin_amdgcn_perm(t1, t0, 0x0c0c0703u));
+            dmw[r] = f16_to_f32((uint16_t)__builtin_amdgcn_perm(t3, t2, 0x0c0c0703u));
+        }
+        const int u = 4 * sl + p;  // lane unit in the row
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            uint4 xv[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) xv[t] = xs[m * npc + 4 * u + ((t + (u >> 2)) & 3)];
+            const uint32_t bs = bsl[m * nu + u];
+            const int bs0 = (int)(int16_t)(bs & 0xFFFFu), bs1 = (int)(int16_t)(bs >> 16);
+            const float dx = dxl[m * nsb + sl];
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                const uint32_t M4 = 0x0F0F0F0Fu;
+                int dlo = sdot4(w0[r].x & M4, xv[0].x, 0);
+                dlo = sdot4(w0[r].y & M4, xv[0].y, dlo);
+                dlo = sdot4(w0[r].z & M4, xv[0].z, dlo);
+                dlo = sdot4(w0[r].w & M4, xv[0].w, dlo);
+                dlo = sdot4(w1[r].x & M4, xv[1].x, dlo);
+                dlo = sdot4(w1[r].y & M4, xv[1].y, dlo);
+                dlo = sdot4(w1[r].z & M4, xv[1].z, dlo);
+                dlo = sdot4(w1[r].w & M4, xv[1].w, dlo);
+                int dhi = sdot4((w0[r].x >> 4) & M4, xv[2].x, 0);
+                dhi = sdot4((w0[r].y >> 4) & M4, xv[2].y, dhi);
+                dhi = sdot4((w0[r].z >> 4) & M4, xv[2].z, dhi);
+                dhi = sdot4((w0[r].w >> 4) & M4, xv[2].w, dhi);
+                dhi = sdot4((w1[r].x >> 4) & M4, xv[3].x, dhi);
+                dhi = sdot4((w1[r].y >> 4) & M4, xv[3].y, dhi);
+                dhi = sdot4((w1[r].z >> 4) & M4, xv[3].z, dhi);
+                dhi = sdot4((w1[r].w >> 4) & M4, xv[3].w, dhi);
+                const uint32_t h = hw[r];
+                const int sc0 = (int)(h & 63u), mn0 = (int)((h >> 6) & 63u);
+                const int sc1 = (int)((h >> 12) & 63u), mn1 = (int)((h >> 18) & 63u);
+                const int aux = quad_sum(sc0 * dlo + sc1 * dhi);
+                const int mins = quad_sum(mn0 * bs0 + mn1 * bs1);
+                const float dd = dw[r] * dx, dm = dmw[r] * dx;
+                const float a = __builtin_fmaf(-dm, (float)mins, __builtin_fmaf(dd, (float)aux, acc[r * MT + m]));
+                acc[r * MT + m] = live ? a : acc[r * MT + m];
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NR * MT; ++i) acc[i] = p == 0 ? acc[i] : 0.0f;  // one lane per quad
+    q8act_store<MT, GU, YT>(acc, lane, y, o0, nout, m0, mrows, ldy);
+}
+
+// Q8_0 weights x Q8_0 activations ([ext] BlockQ8_0::vec_dot: per block
+// (sum q_w q_x) * (d_w * d_x)).  Lane l of a 1024-wide chunk takes 16 bytes
+// (half a block) of each row; the lane pair forms the block's integer dot.
+// LDS: x [MT][K] i8, d [MT][K/32] f32.
+template <int MT, bool GU, typename YT>
+__global__ __launch_bounds__(256) void k_q8act_q8_0(const int8_t* __restrict__ Q, const uint16_t* __restrict__ D,
+                                                    const int8_t* __restrict__ xq, const float* __restrict__ xd,
+                                                    YT* __restrict__ y, int M, int64_t nout, int K, int64_t up_off,
+                                                    int64_t ldy) {
+    constexpr int NR = GU ? 8 : 4;
+    extern __shared__ uint4 lds4[];
+    const int nb = K >> 5, npc = K >> 4;
+    const int m0 = blockIdx.y * MT;
+    const int mrows = M - m0 < MT ? M - m0 : MT;
+    uint4* xs = lds4;
+    float* dxl = reinterpret_cast<float*>(lds4 + MT * npc);
+    for (int i = threadIdx.x; i < MT * npc; i += 256) {
+        const int m = i / npc, P = i - m * npc;
+        xs[i] = m < mrows ? reinterpret_cast<const uint4*>(xq + (int64_t)(m0 + m) * K)[P] : make_uint4(0u, 0u, 0u, 0u);
+    }
+    for (int i = threadIdx.x; i < MT * nb; i += 256) {
+        const int m = i / nb, b = i - m * nb;
+        dxl[i] = m < mrows ? xd[(int64_t)(m0 + m) * nb + b] : 0.0f;
+    }
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63;
+    const int64_t o0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;
+    int64_t rows[NR];
+    wave_rows<GU>(rows, o0, nout, up_off);
+    float acc[NR * MT];
+#pragma unroll
+    for (int i = 0; i < NR * MT; ++i) acc[i] = 0.0f;
+    const int nch = (K + 1023) >> 10;
+    for (int c = 0; c < nch; ++c) {
+        const int k0 = 1024 * c + 16 * lane;
+        const bool live = k0 < K;  // K is a multiple of 32: a lane pair is live together
+        const int kk = live ? k0 : K - 16;
+        const int b = kk >> 5;
+        uint4 wq[NR];
+        float dw[NR];
+#pragma unroll
+        for (int r = 0; r < NR; ++r) {
+            wq[r] = *reinterpret_cast<const uint4*>(Q + rows[r] * K + kk);
+            dw[r] = f16_to_f32(D[rows[r] * nb + b]);
+        }
+#pragma unroll
+        for (int m = 0; m < MT; ++m) {
+            const uint4 xv = xs[m * npc + (kk >> 4)];
+            const float dx = dxl[m * nb + b];
+#pragma unroll
+            for (int r = 0; r < NR; ++r) {
+                int sacc = sdot4(wq[r].x, xv.x, 0);
+                sacc = sdot4(wq[r].y, xv.y, sacc);
+                sacc = sdot4(wq[r].z, xv.z, sacc);
+                sacc = sdot4(wq[r].w, xv.w, sacc);
+                sacc = pair_sum(sacc);
+                const float a = __builtin_fmaf(dw[r] * dx, (float)sacc, acc[r * MT + m]);
+                acc[r * MT + m] = live ? a : acc[r * MT + m];
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NR * MT; ++i) acc[i] = (lane & 1) ? 0.0f : acc[i];  // one lane per block
+    q8act_store<MT, GU, YT>(acc, lane, y, o0, nout, m0, mrows, ldy);
+}
+
+// ------------------------------------------------------------------ host side
+constexpr size_t kLdsCap = 64 * 1024;
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+size_t lds_bytes(int qtype, int mt, int K) {
+    const size_t x = (size_t)mt * K;
+    return qtype == 12 ? x + (size_t)mt * (K / 64) * 4 + (size_t)mt * (K / 256) * 4 : x + (size_t)mt * (K / 32) * 4;
+}
+
+int pick_mt(int qtype, int64_t M, int K) {
+    int mt = 8;
+    while (mt > 1 && mt / 2 >= M) mt /= 2;
+    while (mt > 1 && lds_bytes(qtype, mt, K) > kLdsCap) mt /= 2;
+    return mt;
+}
+
+struct ActPlanes {
+    int8_t* xq;
+    float* xd;
+    int16_t* xb;
+};
+
+ActPlanes act_planes(int qtype, void* ws, int64_t M, int64_t K) {
+    char* p = static_cast<char*>(ws);
+    ActPlanes a;
+    a.xq = reinterpret_cast<int8_t*>(p);
+    p += align256((size_t)M * K);
+    a.xd = reinterpret_cast<float*>(p);
+    p += align256((size_t)M * (K / (qtype == 12 ? 256 : 32)) * 4);
+    a.xb = reinterpret_cast<int16_t*>(p);
+    return a;
+}
+
+template <typename XT>
+hipError_t quant_act_t(int qtype, const XT* x, int64_t M, int64_t K, const ActPlanes* pl, uint8_t* blocks,
+                       hipStream_t s) {
+    if (qtype == 8) {
+        const int64_t nq = M * K / 4;
+        const dim3 grid((unsigned)((nq + 255) / 256));
+        if (blocks)
+            hipLaunchKernelGGL((k_quant_act_q8_0<XT, true>), grid, dim3(256), 0, s, x, nq, nullptr, nullptr, blocks);
+        else
+            hipLaunchKernelGGL((k_quant_act_q8_0<XT, false>), grid, dim3(256), 0, s, x, nq, pl->xq, pl->xd, nullptr);
+    } else {
+        const int64_t nblk = M * K / 256;
+        const dim3 grid((unsigned)((nblk + 3) / 4));
+        if (blocks)
+            hipLaunchKernelGGL((k_quant_act_q8k<XT, true>), grid, dim3(256), 0, s, x, nblk, nullptr, nullptr, nullptr,
+                               blocks);
+        else
+            hipLaunchKernelGGL((k_quant_act_q8k<XT, false>), grid, dim3(256), 0, s, x, nblk, pl->xq, pl->xd, pl->xb,
+                               nullptr);
+    }
+    return hipGetLastError();
+}
+
+template <int MT, bool GU, typename YT>
+void launch_dot(const WeightView& w, const ActPlanes& a, YT* y, int M, int64_t nout, int64_t up_off, hipStream_t s) {
+    const int K = (int)w.K;
+    const int64_t waves = (nout + 3) / 4;
+    const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)((M + MT - 1) / MT));
+    const size_t lds = lds_bytes(w.qtype, MT, K);
+    if (w.qtype == 12)
+        hipLaunchKernelGGL((k_q8act_q4k<MT, GU, YT>), grid, dim3(256), lds, s, w.q, a.xq, a.xd, a.xb, y, M, nout, K,
+                           up_off, nout);
+    else
+        hipLaunchKernelGGL((k_q8act_q8_0<MT, GU, YT>), grid, dim3(256), lds, s, reinterpret_cast<const int8_t*>(w.q),
+                           reinterpret_cast<const uint16_t*>(w.aux), a.xq, a.xd, y, M, nout, K, up_off, nout);
+}
+
+template <bool GU, typename YT>
+void launch_dot_mt(int mt, const WeightView& w, const ActPlanes& a, YT* y, int M, int64_t nout, int64_t up_off,
+                   hipStream_t s) {
+    switch (mt) {
+        case 8: launch_dot<8, GU, YT>(w, a, y, M, nout, up_off, s); break;
+        case 4: launch_dot<4, GU, YT>(w, a, y, M, nout, up_off, s); break;
+        case 2: launch_dot<2, GU, YT>(w, a, y, M, nout, up_off, s); break;
+        default: launch_dot<1, GU, YT>(w, a, y, M, nout, up_off, s); break;
+    }
+}
+
+}  // namespace
+
+bool q8act_supported(int qtype, int64_t K) { return lds_bytes(qtype, 1, (int)K) <= kLdsCap; }
+
+size_t q8act_workspace_bytes(int qtype, int64_t M, int64_t K) {
+    return align256((size_t)M * K) + align256((size_t)M * (K / (qtype == 12 ? 256 : 32)) * 4) +
+           (qtype == 12 ? align256((size_t)M * (K / 32) * 2) : 0);
+}
+
+hipError_t launch_quantize_act(int qtype, const void* x, bool xf32, int64_t M, int64_t K, void* blocks,
+                               hipStream_t s) {
+    uint8_t* b = static_cast<uint8_t*>(blocks);
+    return xf32 ? quant_act_t<float>(qtype, static_cast<const float*>(x), M, K, nullptr, b, s)
+                : quant_act_t<bf16_t>(qtype, static_cast<const bf16_t*>(x), M, K, nullptr, b, s);
+}
+
+hipError_t launch_q8act(const WeightView& w, const void* x, bool xf32, void* y, bool yf32, bool gu, int M,
+                        int64_t nout, int64_t up_off, void* ws, hipStream_t s) {
+    const ActPlanes a = act_planes(w.qtype, ws, M, w.K);
+    hipError_t e = xf32 ? quant_act_t<float>(w.qtype, static_cast<const float*>(x), M, w.K, &a, nullptr, s)
+                        : quant_act_t<bf16_t>(w.qtype, static_cast<const bf16_t*>(x), M, w.K, &a, nullptr, s);
+    if (e != hipSuccess) return e;
+    const int mt = pick_mt(w.qtype, M, (int)w.K);
+    if (gu) {
+        if (yf32) launch_dot_mt<true, float>(mt, w, a, static_cast<float*>(y), M, nout, up_off, s);
+        else launch_dot_mt<true, bf16_t>(mt, w, a, static_cast<bf16_t*>(y), M, nout, up_off, s);
+    } else {
+        if (yf32) launch_dot_mt<false, float>(mt, w, a, static_cast<float*>(y), M, nout, up_off, s);
+        else launch_dot_mt<false, bf16_t>(mt, w, a, static_cast<bf16_t*>(y), M, nout, up_off, s);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace thq

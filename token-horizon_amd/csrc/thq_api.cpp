@@ -141,7 +141,7 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
     if (!ctx || !w) return fail(THQ_EINVAL, "null context or weight");
     if (xt != THQ_ACT_F32 && xt != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad x_type %d", xt);
     if (yt != THQ_ACT_F32 && yt != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad y_type %d", yt);
-    if (flags & ~(THQ_MODE_EXACT_W)) return fail(THQ_EINVAL, "unknown flags 0x%x", flags);
+    if (flags & ~(THQ_MODE_EXACT_W | THQ_MODE_Q8ACT)) return fail(THQ_EINVAL, "unknown flags 0x%x", flags);
     if (m < 0) return fail(THQ_ESHAPE, "M=%lld must be >= 0", (long long)m);
     if (m > (1 << 24)) return fail(THQ_ESHAPE, "M=%lld too large", (long long)m);
     if (gu && (w->N % 2)) return fail(THQ_ESHAPE, "gate/up weight has an odd row count %lld", (long long)w->N);
@@ -154,6 +154,17 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
     const int64_t nout = gu ? w->N / 2 : w->N;
     const int64_t up_off = gu ? w->N / 2 : 0;
     hipError_t e;
+    if (flags & THQ_MODE_Q8ACT) {
+        if (!thq::q8act_supported(w->qtype, w->K))
+            return fail(THQ_ESHAPE, "K=%lld too large for THQ_MODE_Q8ACT", (long long)w->K);
+        if (!aligned16(x)) return fail(THQ_EALIGN, "THQ_MODE_Q8ACT needs 16-byte aligned x");
+        std::lock_guard<std::mutex> lk(ctx->mu);
+        int rc = ensure_ws(ctx, thq::q8act_workspace_bytes(w->qtype, m, w->K));
+        if (rc) return rc;
+        e = thq::launch_q8act(v, x, xf32, y, yf32, gu, (int)m, nout, up_off, ctx->ws, s);
+        if (e != hipSuccess) return fail(THQ_EHIP, "kernel launch: %s", hipGetErrorString(e));
+        return THQ_OK;
+    }
     // M = 1 keeps the VALU GEMV unless THQ_GEMV_M1=mfma; 2..8 bf16 rows go to the MFMA GEMV
     static const bool m1_mfma = [] {
         const char* v = getenv("THQ_GEMV_M1");
@@ -392,6 +403,27 @@ int thq_dequantize(thq_ctx* ctx, const thq_weight* w, float* out_dev, void* stre
     return THQ_OK;
 }
 
+int thq_quantize_act(thq_ctx* ctx, thq_dtype dot_type, const void* x_dev, thq_act x_type, int64_t m, int64_t k,
+                     void* blocks_dev, void* stream) {
+    if (!ctx) return fail(THQ_EINVAL, "null context");
+    if (dot_type != THQ_Q8_0 && dot_type != THQ_Q8_K)
+        return fail(THQ_EDTYPE, "dot type %d is not Q8_0 (8) or Q8_K (15)", (int)dot_type);
+    if (x_type != THQ_ACT_F32 && x_type != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad x_type %d", (int)x_type);
+    const int bs = dot_type == THQ_Q8_0 ? 32 : 256;
+    if (m < 0 || k <= 0 || k % bs) return fail(THQ_ESHAPE, "shape [%lld, %lld] (K must be a positive multiple of %d)",
+                                                (long long)m, (long long)k, bs);
+    if (m == 0) return THQ_OK;
+    if (!x_dev || !blocks_dev) return fail(THQ_EINVAL, "null argument");
+    if (!aligned16(x_dev)) return fail(THQ_EALIGN, "x_dev must be 16-byte aligned");
+    if ((uintptr_t)blocks_dev & (dot_type == THQ_Q8_0 ? 1u : 3u))
+        return fail(THQ_EALIGN, "blocks_dev must be %d-byte aligned", dot_type == THQ_Q8_0 ? 2 : 4);
+    DeviceGuard g(ctx->device);
+    hipError_t e = thq::launch_quantize_act(dot_type == THQ_Q8_0 ? 8 : 12, x_dev, x_type == THQ_ACT_F32, m, k,
+                                            blocks_dev, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(THQ_EHIP, "quantize_act: %s", hipGetErrorString(e));
+    return THQ_OK;
+}
+
 int thq_matmul(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m, void* y_dev,
                thq_act y_type, uint32_t flags, void* stream) {
     return run_matmul(ctx, w, x_dev, x_type, m, y_dev, y_type, flags, false, stream);
@@ -428,7 +460,8 @@ int thq_matmul_argmax(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_
     if (!logits) {
         // logits live at the end of the workspace, after the GEMM / argmax scratch
         const thq::GemmPlan p = thq::plan_gemm(w->qtype, true, m, w->N, w->K, false);
-        const size_t scratch = std::max(p.workspace_bytes, thq::argmax_workspace_bytes(m, w->N));
+        size_t scratch = std::max(p.workspace_bytes, thq::argmax_workspace_bytes(m, w->N));
+        if (flags & THQ_MODE_Q8ACT) scratch = std::max(scratch, thq::q8act_workspace_bytes(w->qtype, m, w->K));
         const size_t off = (scratch + 255) & ~(size_t)255;
         const size_t need = off + (size_t)m * (size_t)w->N * sizeof(float);
         {

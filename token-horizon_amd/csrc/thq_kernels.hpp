@@ -62,6 +62,15 @@ GemmPlan plan_gemm(int qtype, bool exact, int64_t M, int64_t N_rows, int64_t K, 
 hipError_t launch_gemm(const GemmPlan& p, const WeightView& w, const void* x, void* y, bool yf32, bool gu, bool exact,
                        int M, float* ws, hipStream_t s);
 
+// THQ_MODE_Q8ACT: activation quantization + exact integer block dots
+bool q8act_supported(int qtype, int64_t K);
+size_t q8act_workspace_bytes(int qtype, int64_t M, int64_t K);
+hipError_t launch_q8act(const WeightView& w, const void* x, bool xf32, void* y, bool yf32, bool gu, int M,
+                        int64_t nout, int64_t up_off, void* ws, hipStream_t s);
+// GGML blocks of the dot type (qtype 8 -> Q8_0 blocks, 12 -> Q8_K blocks)
+hipError_t launch_quantize_act(int qtype, const void* x, bool xf32, int64_t M, int64_t K, void* blocks,
+                               hipStream_t s);
+
 // argmax
 size_t argmax_workspace_bytes(int64_t m, int64_t n);
 hipError_t launch_argmax(const float* v, int64_t m, int64_t n, uint32_t* idx, void* ws, hipStream_t s);

@@ -22,12 +22,14 @@ LIB_PATH = os.path.join(HERE, "libthq.so")
 
 Q8_0 = 8
 Q4_K = 12
-BLOCK = {Q8_0: 32, Q4_K: 256}
-BLOCK_BYTES = {Q8_0: 34, Q4_K: 144}
+Q8_K = 15  # activation dot type of Q4_K (thq_quantize_act)
+BLOCK = {Q8_0: 32, Q4_K: 256, Q8_K: 256}
+BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q8_K: 292}
 
 ACT_F32 = 0
 ACT_BF16 = 1
 MODE_DEQUANT_F32 = 0
+MODE_Q8ACT = 0x1
 MODE_EXACT_W = 0x10
 
 OK = 0
@@ -37,7 +39,7 @@ EINVAL, ESHAPE, EDTYPE, EALIGN, EHIP, ENOMEM = -1, -2, -3, -4, -5, -6
 EXPORTS = (
     "thq_init", "thq_destroy", "thq_last_error", "thq_version", "thq_weight_upload", "thq_weight_from_device",
     "thq_quantize", "thq_weight_fuse", "thq_weight_free", "thq_weight_info", "thq_weight_download",
-    "thq_dequantize", "thq_matmul", "thq_gate_up_silu", "thq_matmul_argmax", "thq_argmax",
+    "thq_dequantize", "thq_quantize_act", "thq_matmul", "thq_gate_up_silu", "thq_matmul_argmax", "thq_argmax",
 )
 
 
@@ -66,6 +68,7 @@ def _load():
         "thq_weight_info": ([P, C.POINTER(C.c_int), C.POINTER(i64), C.POINTER(i64), C.POINTER(C.c_size_t)], I),
         "thq_weight_download": ([P, P], I),
         "thq_dequantize": ([P, P, P, P], I),
+        "thq_quantize_act": ([P, I, P, I, i64, i64, P, P], I),
         "thq_matmul": ([P, P, P, I, i64, P, I, u32, P], I),
         "thq_gate_up_silu": ([P, P, P, I, i64, P, I, u32, P], I),
         "thq_matmul_argmax": ([P, P, P, I, i64, P, P, u32, P], I),
@@ -192,6 +195,18 @@ class QTensor:
         if getattr(self, "h", None) and lib is not None:
             lib.thq_weight_free(self.h)
             self.h = None
+
+
+def quantize_act(x: torch.Tensor, dot_type: int, ctx: Context | None = None) -> torch.Tensor:
+    """GGML blocks of x[M, K] rows (candle's BlockQ8_0 / BlockQ8K::from_float) as a
+    uint8 device tensor [M, K/bs * block bytes] (thq_quantize_act)."""
+    x2 = x.reshape(-1, x.shape[-1])
+    assert x2.is_contiguous()
+    ctx = ctx or Context.get(x.device.index or 0)
+    m, k = x2.shape
+    out = torch.empty((m, (k // BLOCK[dot_type]) * BLOCK_BYTES[dot_type]), dtype=torch.uint8, device=x.device)
+    check(lib.thq_quantize_act(ctx.h, dot_type, _ptr(x2), _act(x2), m, k, _ptr(out), _stream()))
+    return out
 
 
 def matmul(w: QTensor, x: torch.Tensor, out_dtype=torch.float32, flags: int = 0, out: torch.Tensor | None = None):
