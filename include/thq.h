@@ -39,8 +39,12 @@ extern "C" {
 typedef enum thq_dtype {
     THQ_Q8_0 = 8,  /* 32 weights / 34 B: f16 d, i8 qs[32]                        */
     THQ_Q4_K = 12, /* 256 weights / 144 B: f16 d, f16 dmin, u8 scales[12], u8 qs[128] */
-    THQ_Q8_K = 15  /* 256 activations / 292 B: f32 d, i8 qs[256], i16 bsums[16]
+    THQ_Q8_K = 15, /* 256 activations / 292 B: f32 d, i8 qs[256], i16 bsums[16]
                       (dot type of Q4_K; thq_quantize_act only)                   */
+    THQ_MLX_Q4 = 100 /* MLX affine 4-bit, the engine's own QLin format (not a GGML id):
+                        u32 wq [N][K/8], 8 nibbles per word LSB first; bf16 sb
+                        [N][2*K/gs], each row's K/gs scales then its K/gs biases;
+                        w[n][k] = q * scale[n][k/gs] + bias[n][k/gs]             */
 } thq_dtype;
 
 /* activation / output element types */
@@ -114,11 +118,35 @@ int thq_weight_info(const thq_weight* w, thq_dtype* dtype, int64_t* n, int64_t* 
 /* Copy the GGUF block bytes back to host memory (QTensor::data()).  Synchronous. */
 int thq_weight_download(const thq_weight* w, void* host_blocks);
 
+/* MLX affine 4-bit weights (THQ_MLX_Q4), the engine's QLin
+ * (engine/src/qwen35.rs:311-319: wq U32 [out, in/8], sb BF16 [out, 2*ng]).
+ * `tiled` = 0: row-major arrays as QLin::new takes them; `tiled` = 1: the
+ * QLin::tiled layout (qwen35.rs:629-697; word / scale addresses q4woff / q4sb,
+ * engine/src/quant_kernel.rs:1085-1101): wq [ceil(N/256)][K/64][256][8],
+ * scales [(tile*ng + g)*256 + col] and biases after all ceil(N/256)*ng*256
+ * scales, rows padded to 256.  K must be a multiple of 64, gs a multiple of
+ * 64 dividing K (64 for tiled).  Synchronous.  Replaces the QLin constructors
+ * (Weights::get_lin, qwen35.rs:249-300) and QLin::tiled. */
+int thq_affine_upload(thq_ctx* ctx, const uint32_t* wq_host, const uint16_t* sb_host, int64_t n, int64_t k, int gs,
+                      int tiled, thq_weight** out);
+int thq_affine_from_device(thq_ctx* ctx, const uint32_t* wq_dev, const uint16_t* sb_dev, int64_t n, int64_t k, int gs,
+                           int tiled, void* stream, thq_weight** out);
+/* The row-major QLin arrays back (wq [N][K/8], sb [N][2*K/gs]).  Synchronous. */
+int thq_affine_download(const thq_weight* w, uint32_t* wq_host, uint16_t* sb_host);
+
 /* ---- compute ---- */
 
 /* Exact f32 dequantization, out_dev [N, K] (QTensor::dequantize). Bit-exact
- * with candle's BlockQ8_0/BlockQ4K::to_float. */
+ * with candle's BlockQ8_0/BlockQ4K::to_float.  MLX affine: q*scale + bias
+ * rounded once to f32. */
 int thq_dequantize(thq_ctx* ctx, const thq_weight* w, float* out_dev, void* stream);
+
+/* bf16 dequantization, out_dev [N, K] bf16 bits, 16-byte aligned.  MLX
+ * affine: bit-exact with dequant_affine (engine/src/qwen35.rs:110-134:
+ * bf16::from_f64(q * scale + bias)) and AffineDequant's W -> bf16 scratch
+ * (engine/src/quant_kernel.rs:1035-1040); GGUF types: the f32 values of
+ * thq_dequantize rounded to nearest even. */
+int thq_dequantize_bf16(thq_ctx* ctx, const thq_weight* w, uint16_t* out_dev, void* stream);
 
 /* Quantize activation rows x[M, K] (f32 or bf16, 16-byte aligned) to GGML
  * blocks of `dot_type`: THQ_Q8_0 (34-B blocks, 2-byte aligned blocks_dev) or

@@ -60,6 +60,12 @@ def lib():
         L.o_argmax.argtypes = [P, i64]
         L.o_argmax.restype = C.c_uint32
         L.o_argmax_rows.argtypes = [P, i64, i64, P]
+        L.o_bf16_from_f64_half.argtypes = [C.c_double]
+        L.o_bf16_from_f64_half.restype = C.c_uint16
+        L.o_affine_dequant_bf16.argtypes = [P, P, i64, i64, C.c_int, P]
+        L.o_affine_dequant_f32.argtypes = [P, P, i64, i64, C.c_int, P]
+        L.o_affine_matmul.argtypes = [P, P, i64, i64, C.c_int, P, i64, P]
+        L.o_affine_tile.argtypes = [P, P, i64, i64, P, P]
         L.o_baseline_has_avx2.restype = C.c_int
         L.o_max_threads.restype = C.c_int
         _lib = L
@@ -191,3 +197,50 @@ def max_threads() -> int:
 
 def has_avx2() -> bool:
     return bool(lib().o_baseline_has_avx2())
+
+
+# ------------------------------------------------------------------ MLX affine 4-bit
+def bf16_from_f64_half(v: float) -> int:
+    """[ext] half 2.7.1 bf16::from_f64 (dequant_affine's rounding)."""
+    return int(lib().o_bf16_from_f64_half(float(v)))
+
+
+def _affine_args(wq, sb, n, k):
+    wq = np.ascontiguousarray(wq, dtype=np.uint32)
+    sb = np.ascontiguousarray(sb, dtype=np.uint16)
+    assert wq.size == n * k // 8 and sb.size % n == 0
+    return wq, sb
+
+
+def affine_dequant_bf16(wq, sb, n: int, k: int, gs: int = 64) -> np.ndarray:
+    """dequant_affine (engine/src/qwen35.rs:110-134): bf16 bits [n, k]."""
+    wq, sb = _affine_args(wq, sb, n, k)
+    out = np.empty((n, k), dtype=np.uint16)
+    lib().o_affine_dequant_bf16(_p(wq), _p(sb), n, k, gs, _p(out))
+    return out
+
+
+def affine_dequant_f32(wq, sb, n: int, k: int, gs: int = 64) -> np.ndarray:
+    wq, sb = _affine_args(wq, sb, n, k)
+    out = np.empty((n, k), dtype=np.float32)
+    lib().o_affine_dequant_f32(_p(wq), _p(sb), n, k, gs, _p(out))
+    return out
+
+
+def affine_matmul(wq, sb, n: int, k: int, x: np.ndarray, gs: int = 64) -> np.ndarray:
+    """y = x . W^T with exact affine weights and f64 sums."""
+    wq, sb = _affine_args(wq, sb, n, k)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, k)
+    y = np.empty((x.shape[0], n), dtype=np.float32)
+    lib().o_affine_matmul(_p(wq), _p(sb), n, k, gs, _p(x), x.shape[0], _p(y))
+    return y
+
+
+def affine_tile(wq, sb, n: int, k: int):
+    """QLin::tiled (engine/src/qwen35.rs:629-697) of row-major arrays (gs = 64)."""
+    wq, sb = _affine_args(wq, sb, n, k)
+    tiles, ng = (n + 255) // 256, k // 64
+    wt = np.zeros(tiles * 256 * ng * 8, dtype=np.uint32)
+    st = np.zeros(2 * tiles * 256 * ng, dtype=np.uint16)
+    lib().o_affine_tile(_p(wq), _p(sb), n, k, _p(wt), _p(st))
+    return wt, st

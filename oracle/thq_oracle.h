@@ -29,6 +29,12 @@
  *   matmul DEQUANT_F32          brute force f64 on tiny shapes
  *   argmax                      the reference's own tie vectors
  *   gate/up SiLU epilogue       the reference test's closed form
+ *   MLX affine dequant          an independent numpy formula with correct
+ *                               rounding (equal wherever half's truncation of
+ *                               the low f64 bits cannot matter); the half
+ *                               truncation rule itself by KATs of its
+ *                               published algorithm
+ *   QLin::tiled                 the q4woff / q4sb address formulas
  */
 #ifndef THQ_ORACLE_H
 #define THQ_ORACLE_H
@@ -94,6 +100,14 @@ void o_gate_up_silu(const float* y_gu, int64_t m, int64_t h, uint16_t* out_bf16)
 /* strict '>' scan from (0, -inf): lowest index among equal maxima, NaN never wins */
 uint32_t o_argmax(const float* v, int64_t n);
 void o_argmax_rows(const float* v, int64_t m, int64_t n, uint32_t* idx);
+
+/* ---- MLX affine 4-bit (affine_oracle.c) ---- */
+uint16_t o_bf16_from_f64_half(double v); /* [ext] half 2.7.1 bf16::from_f64 */
+void o_affine_dequant_bf16(const uint32_t* wq, const uint16_t* sb, int64_t n, int64_t k, int gs, uint16_t* out);
+void o_affine_dequant_f32(const uint32_t* wq, const uint16_t* sb, int64_t n, int64_t k, int gs, float* out);
+void o_affine_matmul(const uint32_t* wq, const uint16_t* sb, int64_t n, int64_t k, int gs, const float* x, int64_t m,
+                     float* y);
+void o_affine_tile(const uint32_t* wq, const uint16_t* sb, int64_t n, int64_t k, uint32_t* wq_t, uint16_t* sb_t);
 
 /* ---- CPU baseline: AVX2 + OpenMP Q8ACT matmul (falls back to scalar) ---- */
 int o_baseline_matmul(int type, const uint8_t* w, int64_t n, int64_t k, const float* x, int64_t m,

@@ -53,3 +53,58 @@ def weight_bytes(qtype: int, n: int, k: int, seed: int = 0, sigma: float = 0.02)
 def activations(m: int, k: int, seed: int = 0) -> np.ndarray:
     """X ~ N(0, 1) [m, k] f32 from the oracle generator (stream 2)."""
     return O.randn(seed, 2_000_000 + 13 * m + k, 1.0, (m, k))
+
+
+# ------------------------------------------------------------------ MLX affine inputs
+# The reference's affine kernel tests (engine/src/qwen35.rs:6893-6930,
+# qmvt_tests) draw weights and activations from one 64-bit LCG; rand_qlin /
+# rand_x below produce the same values from the same seeds.
+_A, _C, _MASK = 6364136223846793005, 1442695040888963407, (1 << 64) - 1
+
+
+def lcg_values(seed: int, count: int) -> np.ndarray:
+    """`count` successive outputs (state >> 33) of the reference's lcg()."""
+    out = np.empty(count, dtype=np.uint64)
+    s = seed
+    for i in range(count):
+        s = (s * _A + _C) & _MASK
+        out[i] = s >> 33
+    return out
+
+
+def rand_qlin(out: int, inp: int, seed: int):
+    """rand_qlin (qwen35.rs:6900-6918): words (lcg ^ lcg << 16) [out, inp/8],
+    then per (row, group of 64) a scale 0.002 + (lcg % 1000) * 2e-5 and a bias
+    ((lcg % 2001) - 1000) * 1e-4 in f32, stored as bf16.  Returns (wq u32
+    [out, inp/8], sb bf16 bits [out, 2*ng])."""
+    ng = inp // 64
+    nw = out * inp // 8
+    v = lcg_values(seed, 2 * nw + 2 * out * ng)
+    lo, hi = v[0:2 * nw:2], v[1:2 * nw:2]
+    wq = ((lo.astype(np.uint32)) ^ ((hi.astype(np.uint64) << np.uint64(16)) & np.uint64(0xFFFFFFFF)).astype(np.uint32))
+    rest = v[2 * nw:].reshape(out, ng, 2)
+    sc = np.float32(0.002) + (rest[:, :, 0] % 1000).astype(np.float32) * np.float32(2e-5)
+    bi = ((rest[:, :, 1] % 2001).astype(np.float32) - np.float32(1000.0)) * np.float32(1e-4)
+    sb = np.concatenate([O.f32_to_bf16_bits(sc.astype(np.float32)), O.f32_to_bf16_bits(bi.astype(np.float32))],
+                        axis=1)
+    return wq.reshape(out, inp // 8), np.ascontiguousarray(sb, dtype=np.uint16)
+
+
+def rand_x(inp: int, seed: int, rows: int = 1) -> np.ndarray:
+    """rand_x (qwen35.rs:6920-6926): ((lcg % 4001) - 2000) / 1000 in f32,
+    rounded to bf16; returned as f32 values [rows, inp]."""
+    v = lcg_values(seed, rows * inp)
+    x = ((v % 4001).astype(np.float32) - np.float32(2000.0)) / np.float32(1000.0)
+    return O.bf16_round(x.astype(np.float32)).reshape(rows, inp)
+
+
+def rand_qlin_fast(out: int, inp: int, seed: int, gs: int = 64):
+    """Large shapes: the same distributions from numpy's generator."""
+    rng = np.random.default_rng(seed)
+    ng = inp // gs
+    wq = rng.integers(0, 1 << 32, (out, inp // 8), dtype=np.uint64).astype(np.uint32)
+    sc = np.float32(0.002) + rng.integers(0, 1000, (out, ng)).astype(np.float32) * np.float32(2e-5)
+    bi = (rng.integers(0, 2001, (out, ng)).astype(np.float32) - np.float32(1000.0)) * np.float32(1e-4)
+    sb = np.concatenate([O.f32_to_bf16_bits(sc.astype(np.float32)), O.f32_to_bf16_bits(bi.astype(np.float32))],
+                        axis=1)
+    return wq, np.ascontiguousarray(sb, dtype=np.uint16)

@@ -103,7 +103,7 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ Wq, co
             dq = 0;
             return;
         }
-        if (QT == 12) {
+        if (QT != 8) {
             const int nsb = K >> 8, sidx = k0 >> 8, j = (k0 & 255) >> 6;
             hdr.x = *reinterpret_cast<const uint32_t*>(Wq + q4k_hdword(wrow, nsb, sidx, 0));
             hdr.y = *reinterpret_cast<const uint32_t*>(Wq + q4k_hdword(wrow, nsb, sidx, 1));
@@ -124,14 +124,23 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ Wq, co
             const int c = tid + 256 * i;
             *reinterpret_cast<uint4*>(&Xs[buf][c >> 3][8 * (c & 7)]) = xr[i];
         }
-        if (QT == 12) {
+        if (QT != 8) {
             const int j = ((kit * BK) & 255) >> 6;
-            uint32_t sc0, mm0, sc1, mm1;
-            q4k_hdr_sm(hdr, 2 * j, sc0, mm0);
-            q4k_hdr_sm(hdr, 2 * j + 1, sc1, mm1);
-            const float d = q4k_hdr_d(hdr), dmin = q4k_hdr_dmin(hdr);
-            const float d1 = d * (float)sc0, m1 = dmin * (float)mm0;
-            const float d2 = d * (float)sc1, m2 = dmin * (float)mm1;
+            float d1, m1, d2, m2;
+            if constexpr (QT == 13) {  // affine group: w = scale * q + bias
+                const uint32_t hw = j == 0 ? hdr.x : (j == 1 ? hdr.y : (j == 2 ? hdr.z : hdr.w));
+                d1 = d2 = aff_scale(hw);
+                m1 = m2 = -aff_bias(hw);
+            } else {
+                uint32_t sc0, mm0, sc1, mm1;
+                q4k_hdr_sm(hdr, 2 * j, sc0, mm0);
+                q4k_hdr_sm(hdr, 2 * j + 1, sc1, mm1);
+                const float d = q4k_hdr_d(hdr), dmin = q4k_hdr_dmin(hdr);
+                d1 = d * (float)sc0;
+                m1 = dmin * (float)mm0;
+                d2 = d * (float)sc1;
+                m2 = dmin * (float)mm1;
+            }
             const uint32_t q[4] = {wr0.x, wr0.y, wr0.z, wr0.w};
             uint32_t lo[8], hi[8];
 #pragma unroll
@@ -331,13 +340,13 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict
     // of int8 + 128 scale dwords, spread so that every wave issues the same
     // number of copies (some with part of the wave active)
     constexpr int XI = BM / (8 * NW);
-    constexpr int NIB = QT == 12 ? BN * 32 : BN * 64;   // packed weight bytes per raw slot
-    constexpr int AUX = QT == 12 ? BN * 16 : BN * 4;     // header / scale bytes per raw slot
+    constexpr int NIB = QT != 8 ? BN * 32 : BN * 64;   // packed weight bytes per raw slot
+    constexpr int AUX = QT != 8 ? BN * 16 : BN * 4;     // header / scale bytes per raw slot
     constexpr int RAW = NIB + AUX;
-    constexpr int NSLOT = QT == 12 ? 256 / NW : 512 / NW;      // 16-B weight slots per wave
+    constexpr int NSLOT = QT != 8 ? 256 / NW : 512 / NW;      // 16-B weight slots per wave
     constexpr int NI = NSLOT >= 64 ? NSLOT / 64 : 1;           // their copies
     constexpr int NL = NSLOT >= 64 ? 64 : NSLOT;               // active lanes per copy
-    constexpr int HSLOT = QT == 12 ? 512 / NW : 128 / NW;      // header / scale dwords per wave
+    constexpr int HSLOT = QT != 8 ? 512 / NW : 128 / NW;      // header / scale dwords per wave
     constexpr int HI = HSLOT >= 64 ? HSLOT / 64 : 1;
     constexpr int HL = HSLOT >= 64 ? 64 : HSLOT;
     constexpr int WI = NI + HI;
@@ -385,13 +394,13 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict
     for (int i = 0; i < NI; ++i) {
         const int j = wave * NSLOT + 64 * i + (lane < NL ? lane : 0);
         const int row = j & 127, hc = j >> 7;
-        if (QT == 12) noff[i] = (uint32_t)q4k_piece(clamp_row(row), nsb, 0, hc, 0);
+        if (QT != 8) noff[i] = (uint32_t)q4k_piece(clamp_row(row), nsb, 0, hc, 0);
         else noff[i] = (uint32_t)(clamp_row(row) * K + 32 * (hc >> 1) + 16 * (hc & 1));
     }
 #pragma unroll
     for (int i = 0; i < HI; ++i) {
         const int j = wave * HSLOT + 64 * i + (lane < HL ? lane : 0);
-        if (QT == 12) hoff[i] = (uint32_t)q4k_hdword(clamp_row(j >> 2), nsb, 0, j & 3);
+        if (QT != 8) hoff[i] = (uint32_t)q4k_hdword(clamp_row(j >> 2), nsb, 0, j & 3);
         else hoff[i] = (uint32_t)(clamp_row(j) * (K >> 5) * 2);
     }
     auto xcopy = [&](int kit, int slot) {
@@ -401,8 +410,8 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict
     };
     auto wcopy = [&](int kit, int slot) {
         const uint32_t l = wlds + slot * RAW;
-        const uint8_t* nb = QT == 12 ? Wq + kit * 16 : Wq + kit * 64;
-        const uint8_t* hb = QT == 12 ? Wq + (kit >> 2) * 64 : Wa + kit * 4;
+        const uint8_t* nb = QT != 8 ? Wq + kit * 16 : Wq + kit * 64;
+        const uint8_t* hb = QT != 8 ? Wq + (kit >> 2) * 64 : Wa + kit * 4;
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             if (NL == 64 || lane < NL) dma16(l + (wave * NSLOT + 64 * i) * 16, nb, noff[i]);
@@ -439,17 +448,23 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict
     auto rload = [&](int slot, int kit) {
         Raw R;
         const uint8_t* w = &Wr[slot][0];
-        if (QT == 12) {
+        if (QT != 8) {
             R.q0 = *reinterpret_cast<const uint4*>(w + (wh * BN + wc) * 16);
             R.q1 = R.q0;
-            const uint4 h = *reinterpret_cast<const uint4*>(w + NIB + wc * 16);
             const uint32_t hw = *reinterpret_cast<const uint32_t*>(w + NIB + wc * 16 + (kit & 3) * 4);
-            float d = q4k_hdr_d(h), dm = q4k_hdr_dmin(h);
-            if (!wvalid) d = dm = 0.0f;
-            R.s0 = d * (float)(hw & 63u);
-            R.c0 = __builtin_fmaf(128.0f, R.s0, dm * (float)((hw >> 6) & 63u));
-            R.s1 = d * (float)((hw >> 12) & 63u);
-            R.c1 = __builtin_fmaf(128.0f, R.s1, dm * (float)((hw >> 18) & 63u));
+            if constexpr (QT == 13) {  // affine group: w = scale * (128 + q) - (128 * scale - bias)
+                const float sc = wvalid ? aff_scale(hw) : 0.0f, bi = wvalid ? aff_bias(hw) : 0.0f;
+                R.s0 = R.s1 = sc;
+                R.c0 = R.c1 = __builtin_fmaf(128.0f, sc, -bi);
+            } else {
+                const uint4 h = *reinterpret_cast<const uint4*>(w + NIB + wc * 16);
+                float d = q4k_hdr_d(h), dm = q4k_hdr_dmin(h);
+                if (!wvalid) d = dm = 0.0f;
+                R.s0 = d * (float)(hw & 63u);
+                R.c0 = __builtin_fmaf(128.0f, R.s0, dm * (float)((hw >> 6) & 63u));
+                R.s1 = d * (float)((hw >> 12) & 63u);
+                R.c1 = __builtin_fmaf(128.0f, R.s1, dm * (float)((hw >> 18) & 63u));
+            }
         } else {
             // 4 waves: both 16-B pieces of the half; 8 waves: only piece q & 1
             R.q0 = *reinterpret_cast<const uint4*>(w + ((wh * 2 + (NW == 4 ? 0 : (q & 1))) * BN + wc) * 16);
@@ -469,7 +484,7 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict
         float sc, c;
         int ch;
         uint32_t E;
-        if (QT == 12) {
+        if (QT != 8) {
             // low nibbles = first 32 weights of the step, high = second 32; 4 waves:
             // quarters 0,1 low and 2,3 high; 8 waves: the half is q & 1
             const int hi = NW == 4 ? (k >> 1) : (q & 1);
@@ -494,7 +509,7 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict
         }
         // byte i of v into byte 2 (Q4_K) or byte 1 (Q8_0), exponent byte from E
         auto f = [&](uint32_t v, int i) {
-            const uint32_t sel = QT == 12 ? 0x04000c0cu | ((uint32_t)i << 16) : 0x040c000cu | ((uint32_t)i << 8);
+            const uint32_t sel = QT != 8 ? 0x04000c0cu | ((uint32_t)i << 16) : 0x040c000cu | ((uint32_t)i << 8);
             return __builtin_fmaf(sc, __uint_as_float(__builtin_amdgcn_perm(E, v, sel)), -c);
         };
         const uint32_t o0 = pack_bf16x2(f(a, 0), f(a, 1));
@@ -694,7 +709,7 @@ static hipError_t gemm_t(const GemmPlan& p, const WeightView& w, const bf16_t* x
     const int64_t up_off = GU ? w.N / 2 : 0;
     dim3 grid((unsigned)p.tiles_n, (unsigned)p.tiles_m, (unsigned)p.splits);
     const uint64_t xbytes = (uint64_t)M * (uint64_t)w.K * 2;
-    const uint64_t wbytes = QT == 12 ? (uint64_t)((w.N + 3) / 4) * (uint64_t)(w.K / 256) * 576
+    const uint64_t wbytes = QT != 8 ? (uint64_t)((w.N + 3) / 4) * (uint64_t)(w.K / 256) * 576
                                      : (uint64_t)w.N * (uint64_t)w.K;
     if (!EXACT && xbytes < (1ull << 32) && wbytes < (1ull << 32) && !env_int("THQ_GEMM_V1", 0)) {
         const unsigned nb = (unsigned)(p.tiles_n * p.tiles_m * p.splits);
@@ -747,6 +762,13 @@ hipError_t launch_gemm(const GemmPlan& p, const WeightView& w, const void* x, vo
                             : gemm_bm<12, false, true, bf16_t>(p, w, xb, y, M, ws, s);
         return yf32 ? gemm_bm<12, false, false, float>(p, w, xb, y, M, ws, s)
                     : gemm_bm<12, false, false, bf16_t>(p, w, xb, y, M, ws, s);
+    }
+    if (w.qtype == 13) {
+        if (exact) return hipErrorInvalidValue;
+        if (gu) return yf32 ? gemm_bm<13, false, true, float>(p, w, xb, y, M, ws, s)
+                            : gemm_bm<13, false, true, bf16_t>(p, w, xb, y, M, ws, s);
+        return yf32 ? gemm_bm<13, false, false, float>(p, w, xb, y, M, ws, s)
+                    : gemm_bm<13, false, false, bf16_t>(p, w, xb, y, M, ws, s);
     }
     if (exact) {
         if (gu) return yf32 ? gemm_bm<8, true, true, float>(p, w, xb, y, M, ws, s)

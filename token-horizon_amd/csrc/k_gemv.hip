@@ -137,7 +137,7 @@ __device__ __forceinline__ void q4k_unit_load(Q4Unit<GU>& U, const uint8_t* W, i
     }
 }
 
-template <bool GU>
+template <bool GU, bool AFF>
 __device__ __forceinline__ void q4k_unit_compute(float (&acc)[GU ? 8 : 4], const Q4Unit<GU>& U,
                                                  const uint32_t (&xlo)[16], const uint32_t (&xhi)[16], float sxlo,
                                                  float sxhi) {
@@ -160,6 +160,13 @@ __device__ __forceinline__ void q4k_unit_compute(float (&acc)[GU ? 8 : 4], const
                 ahi = dot2_bf16(__builtin_amdgcn_perm(C43, hi, 0x04030402u), xhi[2 * t + 1], ahi);
             }
             const uint32_t h = hq[r];
+            if constexpr (AFF) {
+                // affine group: sum x*w = scale * (a - 128 * sum x) + bias * sum x
+                const float sc = aff_scale(h), bi = aff_bias(h), sx = sxlo + sxhi;
+                const float a = __builtin_fmaf(sc, __builtin_fmaf(-128.0f, sx, alo + ahi), acc[4 * qi + r]);
+                acc[4 * qi + r] = __builtin_fmaf(bi, sx, a);
+                continue;
+            }
             const uint32_t t0 = quad_bcast<0>(h), t1 = quad_bcast<1>(h);
             const uint32_t t2 = quad_bcast<2>(h), t3 = quad_bcast<3>(h);
             const float d = f16_to_f32((uint16_t)__builtin_amdgcn_perm(t1, t0, 0x0c0c0703u));
@@ -209,7 +216,7 @@ __device__ __forceinline__ void q4k_unit_store(YT* __restrict__ y, int64_t gq, i
     }
 }
 
-template <int KC, bool GU, typename YT>
+template <int KC, bool GU, bool AFF, typename YT>
 __global__ __launch_bounds__(256) void k_gemv1_q4k_bf16(const uint8_t* __restrict__ W, const bf16_t* __restrict__ x,
                                                        YT* __restrict__ y, int64_t nout, int K, int64_t up_off,
                                                        int64_t nquads) {
@@ -268,7 +275,7 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_bf16(const uint8_t* __restric
         // KC is small: select the chunk's activations with a static switch
 #pragma unroll
         for (int cc = 0; cc < KC; ++cc)
-            if (cc == ch) q4k_unit_compute<GU>(acc, U, xlo[cc], xhi[cc], sxlo[cc], sxhi[cc]);
+            if (cc == ch) q4k_unit_compute<GU, AFF>(acc, U, xlo[cc], xhi[cc], sxlo[cc], sxhi[cc]);
         if (ch == KC - 1) {
             q4k_unit_store<GU, YT>(y, q, nout, lane, acc);
 #pragma unroll
@@ -298,7 +305,7 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_bf16(const uint8_t* __restric
 // quads x KC waves, wave (quad, chunk) loads its 4096-wide chunk of the quad
 // at entry (after the block's x loads, as in the one-shot kernel) and the
 // chunks' row totals are summed in LDS in chunk order before the epilogue.
-template <int KC, bool GU, typename YT>
+template <int KC, bool GU, bool AFF, typename YT>
 __global__ __launch_bounds__(256 * KC) void k_gemv1_q4k_bf16_ks(const uint8_t* W, const bf16_t* x,
                                                                YT* __restrict__ y, int64_t nout, int K,
                                                                int64_t up_off, int64_t nquads) {
@@ -343,7 +350,7 @@ __global__ __launch_bounds__(256 * KC) void k_gemv1_q4k_bf16_ks(const uint8_t* W
     float acc[GU ? 8 : 4];
 #pragma unroll
     for (int i = 0; i < (GU ? 8 : 4); ++i) acc[i] = 0.0f;
-    q4k_unit_compute<GU>(acc, A, xlo, xhi, sxlo, sxhi);
+    q4k_unit_compute<GU, AFF>(acc, A, xlo, xhi, sxlo, sxhi);
     // per-chunk row totals: slots 0..3 (gate rows for GU), 4..7 (up rows)
     if constexpr (GU) {
         const float tot = reduce_slots8(acc, lane);
@@ -374,7 +381,7 @@ __global__ __launch_bounds__(256 * KC) void k_gemv1_q4k_bf16_ks(const uint8_t* W
 // every weight byte has landed, and each row's math starts as its data
 // arrives.  W and x are not __restrict__ so that the compiler barrier keeps
 // that order.
-template <bool GU, typename YT>
+template <bool GU, bool AFF, typename YT>
 __global__ __launch_bounds__(256) void k_gemv1_q4k_bf16_1s(const uint8_t* W, const bf16_t* x, YT* __restrict__ y,
                                                           int64_t nout, int K, int64_t up_off, int64_t nquads) {
     extern __shared__ uint4 lds[];  // x (K bf16)
@@ -417,12 +424,12 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_bf16_1s(const uint8_t* W, con
     float acc[GU ? 8 : 4];
 #pragma unroll
     for (int i = 0; i < (GU ? 8 : 4); ++i) acc[i] = 0.0f;
-    q4k_unit_compute<GU>(acc, A, xlo, xhi, sxlo, sxhi);
+    q4k_unit_compute<GU, AFF>(acc, A, xlo, xhi, sxlo, sxhi);
     q4k_unit_store<GU, YT>(y, gq, nout, lane, acc);
 }
 
 // ------------------------------------------------------------------ Q4_K M=1, f32 x
-template <int KC, int R, bool GU, typename YT>
+template <int KC, int R, bool GU, bool AFF, typename YT>
 __global__ __launch_bounds__(256) void k_gemv1_q4k_f32(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                                       YT* __restrict__ y, int64_t nout, int K, int64_t up_off) {
     const int lane = threadIdx.x & 63;
@@ -472,12 +479,18 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_f32(const uint8_t* __restrict
                     dh = __builtin_fmaf((float)((qw[t] >> (8 * b + 4)) & 0xF), xh[4 * t + b], dh);
                 }
             }
-            uint32_t sc0, m0, sc1, m1;
-            q4k_hdr_sm(h, 2 * part, sc0, m0);
-            q4k_hdr_sm(h, 2 * part + 1, sc1, m1);
-            const float d = q4k_hdr_d(h), dmin = q4k_hdr_dmin(h);
-            acc[r] = __builtin_fmaf(d, (float)sc0 * dl + (float)sc1 * dh, acc[r]);
-            acc[r] = __builtin_fmaf(-dmin, (float)m0 * sxl + (float)m1 * sxh, acc[r]);
+            if constexpr (AFF) {
+                const uint32_t hw = part == 0 ? h.x : (part == 1 ? h.y : (part == 2 ? h.z : h.w));
+                acc[r] = __builtin_fmaf(aff_scale(hw), dl + dh, acc[r]);
+                acc[r] = __builtin_fmaf(aff_bias(hw), sxl + sxh, acc[r]);
+            } else {
+                uint32_t sc0, m0, sc1, m1;
+                q4k_hdr_sm(h, 2 * part, sc0, m0);
+                q4k_hdr_sm(h, 2 * part + 1, sc1, m1);
+                const float d = q4k_hdr_d(h), dmin = q4k_hdr_dmin(h);
+                acc[r] = __builtin_fmaf(d, (float)sc0 * dl + (float)sc1 * dh, acc[r]);
+                acc[r] = __builtin_fmaf(-dmin, (float)m0 * sxl + (float)m1 * sxh, acc[r]);
+            }
         }
     }
 #pragma unroll
@@ -580,16 +593,25 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict_
         for (int r = 0; r < NR; ++r) {
             const int64_t row = o + (r ? up_off : 0);
             float wv[32];
-            if (QT == 12) {
-                const int nsb = K >> 8, s = sbi >> 3, j = sbi & 7;
+            if (QT != 8) {
+                // affine weights may pad K to whole superblocks: address with the padded count
+                const int nsb = (K + 255) >> 8, s = sbi >> 3, j = sbi & 7;
                 uint4 h;
                 h.x = *reinterpret_cast<const uint32_t*>(Wq + q4k_hdword(row, nsb, s, 0));
                 h.y = *reinterpret_cast<const uint32_t*>(Wq + q4k_hdword(row, nsb, s, 1));
                 h.z = *reinterpret_cast<const uint32_t*>(Wq + q4k_hdword(row, nsb, s, 2));
                 h.w = *reinterpret_cast<const uint32_t*>(Wq + q4k_hdword(row, nsb, s, 3));
-                uint32_t sc, mm;
-                q4k_hdr_sm(h, j, sc, mm);
-                const float d1 = q4k_hdr_d(h) * (float)sc, m1 = q4k_hdr_dmin(h) * (float)mm;
+                float d1, m1;
+                if (QT == 13) {
+                    const uint32_t hw = (j >> 1) == 0 ? h.x : ((j >> 1) == 1 ? h.y : ((j >> 1) == 2 ? h.z : h.w));
+                    d1 = aff_scale(hw);
+                    m1 = -aff_bias(hw);  // w = scale * q - (-bias)
+                } else {
+                    uint32_t sc, mm;
+                    q4k_hdr_sm(h, j, sc, mm);
+                    d1 = q4k_hdr_d(h) * (float)sc;
+                    m1 = q4k_hdr_dmin(h) * (float)mm;
+                }
                 const int sh = (j & 1) * 4;
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
@@ -631,7 +653,7 @@ static inline int env_int(const char* name, int dflt) {
 }
 
 // resident waves per CU (tunable: THQ_GEMV_WPC)
-template <bool GU, typename YT>
+template <bool GU, bool AFF, typename YT>
 static void launch_q4k_bf16_t(const uint8_t* W, const bf16_t* x, YT* y, int64_t nout, int K, int64_t up_off,
                               hipStream_t s) {
     const int64_t nquads = (nout + 3) / 4;
@@ -640,39 +662,39 @@ static void launch_q4k_bf16_t(const uint8_t* W, const bf16_t* x, YT* y, int64_t 
     if (waves > nquads) waves = nquads;
     const size_t lds = (size_t)K * 2;
     if (K <= 4096 && env_int("THQ_GEMV_ONESHOT", 1)) {
-        hipLaunchKernelGGL((k_gemv1_q4k_bf16_1s<GU, YT>), dim3((unsigned)((nquads + 3) / 4)), dim3(256), lds, s, W, x,
+        hipLaunchKernelGGL((k_gemv1_q4k_bf16_1s<GU, AFF, YT>), dim3((unsigned)((nquads + 3) / 4)), dim3(256), lds, s, W, x,
                            y, nout, K, up_off, nquads);
         return;
     }
     if (K <= 4 * 4096 && env_int("THQ_GEMV_ONESHOT", 1)) {
         const dim3 grid((unsigned)((nquads + 3) / 4));
         switch ((K + 4095) / 4096) {
-            case 2: hipLaunchKernelGGL((k_gemv1_q4k_bf16_ks<2, GU, YT>), grid, dim3(512), lds, s, W, x, y, nout, K, up_off, nquads); return;
-            case 3: hipLaunchKernelGGL((k_gemv1_q4k_bf16_ks<3, GU, YT>), grid, dim3(768), lds, s, W, x, y, nout, K, up_off, nquads); return;
-            default: hipLaunchKernelGGL((k_gemv1_q4k_bf16_ks<4, GU, YT>), grid, dim3(1024), lds, s, W, x, y, nout, K, up_off, nquads); return;
+            case 2: hipLaunchKernelGGL((k_gemv1_q4k_bf16_ks<2, GU, AFF, YT>), grid, dim3(512), lds, s, W, x, y, nout, K, up_off, nquads); return;
+            case 3: hipLaunchKernelGGL((k_gemv1_q4k_bf16_ks<3, GU, AFF, YT>), grid, dim3(768), lds, s, W, x, y, nout, K, up_off, nquads); return;
+            default: hipLaunchKernelGGL((k_gemv1_q4k_bf16_ks<4, GU, AFF, YT>), grid, dim3(1024), lds, s, W, x, y, nout, K, up_off, nquads); return;
         }
     }
     const unsigned grid = (unsigned)((waves + 3) / 4);
     switch ((K / 256 + 15) / 16) {
-        case 1: hipLaunchKernelGGL((k_gemv1_q4k_bf16<1, GU, YT>), dim3(grid), dim3(256), lds, s, W, x, y, nout, K, up_off, nquads); break;
-        case 2: hipLaunchKernelGGL((k_gemv1_q4k_bf16<2, GU, YT>), dim3(grid), dim3(256), lds, s, W, x, y, nout, K, up_off, nquads); break;
-        case 3: hipLaunchKernelGGL((k_gemv1_q4k_bf16<3, GU, YT>), dim3(grid), dim3(256), lds, s, W, x, y, nout, K, up_off, nquads); break;
-        default: hipLaunchKernelGGL((k_gemv1_q4k_bf16<4, GU, YT>), dim3(grid), dim3(256), lds, s, W, x, y, nout, K, up_off, nquads); break;
+        case 1: hipLaunchKernelGGL((k_gemv1_q4k_bf16<1, GU, AFF, YT>), dim3(grid), dim3(256), lds, s, W, x, y, nout, K, up_off, nquads); break;
+        case 2: hipLaunchKernelGGL((k_gemv1_q4k_bf16<2, GU, AFF, YT>), dim3(grid), dim3(256), lds, s, W, x, y, nout, K, up_off, nquads); break;
+        case 3: hipLaunchKernelGGL((k_gemv1_q4k_bf16<3, GU, AFF, YT>), dim3(grid), dim3(256), lds, s, W, x, y, nout, K, up_off, nquads); break;
+        default: hipLaunchKernelGGL((k_gemv1_q4k_bf16<4, GU, AFF, YT>), dim3(grid), dim3(256), lds, s, W, x, y, nout, K, up_off, nquads); break;
     }
 }
 
-template <bool GU, typename YT>
+template <bool GU, bool AFF, typename YT>
 static hipError_t gemv1_q4k_t(const uint8_t* W, const void* x, bool xf32, YT* y, int64_t nout, int K, int64_t up_off,
                               hipStream_t s) {
     const int kc = (K + 4095) / 4096;
     if (!xf32) {
-        launch_q4k_bf16_t<GU, YT>(W, static_cast<const bf16_t*>(x), y, nout, K, up_off, s);
+        launch_q4k_bf16_t<GU, AFF, YT>(W, static_cast<const bf16_t*>(x), y, nout, K, up_off, s);
     } else {
         const float* xf = static_cast<const float*>(x);
         constexpr int RR = GU ? 2 : 1;
         const unsigned grid = (unsigned)((nout + 3) / 4);
 #define THQ_F32(KC_) \
-    hipLaunchKernelGGL((k_gemv1_q4k_f32<KC_, RR, GU, YT>), dim3(grid), dim3(256), 0, s, W, xf, y, nout, K, up_off)
+    hipLaunchKernelGGL((k_gemv1_q4k_f32<KC_, RR, GU, AFF, YT>), dim3(grid), dim3(256), 0, s, W, xf, y, nout, K, up_off)
         switch (kc) {
             case 1: THQ_F32(1); break;
             case 2: THQ_F32(2); break;
@@ -713,7 +735,7 @@ static hipError_t gemv1_q8_t(const int8_t* Q, const uint16_t* D, const XT* x, YT
 }
 
 bool gemv1_supported(int qtype, int K, bool gu, int64_t n_rows) {
-    if (qtype == 12) return K % 256 == 0 && K <= 4 * 4096 && (!gu || (n_rows / 2) % 4 == 0);
+    if (qtype != 8) return K % 256 == 0 && K <= 4 * 4096 && (!gu || (n_rows / 2) % 4 == 0);
     return K % 32 == 0 && K <= 8 * 1024;
 }
 
@@ -722,11 +744,19 @@ hipError_t launch_gemv1(const WeightView& w, const void* x, bool xf32, void* y, 
     const int K = (int)w.K;
     if (w.qtype == 12) {
         if (gu) {
-            return yf32 ? gemv1_q4k_t<true, float>(w.q, x, xf32, (float*)y, nout, K, up_off, s)
-                        : gemv1_q4k_t<true, bf16_t>(w.q, x, xf32, (bf16_t*)y, nout, K, up_off, s);
+            return yf32 ? gemv1_q4k_t<true, false, float>(w.q, x, xf32, (float*)y, nout, K, up_off, s)
+                        : gemv1_q4k_t<true, false, bf16_t>(w.q, x, xf32, (bf16_t*)y, nout, K, up_off, s);
         }
-        return yf32 ? gemv1_q4k_t<false, float>(w.q, x, xf32, (float*)y, nout, K, up_off, s)
-                    : gemv1_q4k_t<false, bf16_t>(w.q, x, xf32, (bf16_t*)y, nout, K, up_off, s);
+        return yf32 ? gemv1_q4k_t<false, false, float>(w.q, x, xf32, (float*)y, nout, K, up_off, s)
+                    : gemv1_q4k_t<false, false, bf16_t>(w.q, x, xf32, (bf16_t*)y, nout, K, up_off, s);
+    }
+    if (w.qtype == 13) {
+        if (gu) {
+            return yf32 ? gemv1_q4k_t<true, true, float>(w.q, x, xf32, (float*)y, nout, K, up_off, s)
+                        : gemv1_q4k_t<true, true, bf16_t>(w.q, x, xf32, (bf16_t*)y, nout, K, up_off, s);
+        }
+        return yf32 ? gemv1_q4k_t<false, true, float>(w.q, x, xf32, (float*)y, nout, K, up_off, s)
+                    : gemv1_q4k_t<false, true, bf16_t>(w.q, x, xf32, (bf16_t*)y, nout, K, up_off, s);
     }
     const int8_t* Q = reinterpret_cast<const int8_t*>(w.q);
     const uint16_t* D = reinterpret_cast<const uint16_t*>(w.aux);
@@ -759,6 +789,7 @@ hipError_t launch_generic(const WeightView& w, const void* x, bool xf32, void* y
     (xf32 ? (yf32 ? THQ_G(QT_, GU_, float, float) : THQ_G(QT_, GU_, float, bf16_t))   \
           : (yf32 ? THQ_G(QT_, GU_, bf16_t, float) : THQ_G(QT_, GU_, bf16_t, bf16_t)))
     if (w.qtype == 12) return gu ? THQ_G2(12, true) : THQ_G2(12, false);
+    if (w.qtype == 13) return gu ? THQ_G2(13, true) : THQ_G2(13, false);
     return gu ? THQ_G2(8, true) : THQ_G2(8, false);
 #undef THQ_G2
 #undef THQ_G

@@ -75,7 +75,7 @@ constexpr int XCH = 8;           // staged 16-B activation chunks per thread: M 
 // wave's K slice.
 template <int QT>
 struct Chunk {
-    uint4 w[QT == 12 ? 4 : 8];
+    uint4 w[QT != 8 ? 4 : 8];
     uint32_t s[4];
 };
 
@@ -89,13 +89,13 @@ __device__ __forceinline__ float dpp_add(float v) {
 // Grid: tiles x splits blocks; block (tile, split) owns the tile's 32 weight
 // rows over K range [split*Kb, (split+1)*Kb), Kb = waves * cpw * 256.
 template <int QT, int E, int NX, bool GU, bool SPLIT, typename YT>
-__global__ __launch_bounds__(512, QT == 12 ? 4 : 2) void k_gemv_mfma(const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Wa,
+__global__ __launch_bounds__(512, QT != 8 ? 4 : 2) void k_gemv_mfma(const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Wa,
                                                   const bf16_t* X, void* __restrict__ Yv, int M, int K,
                                                   int64_t nout, int64_t up_off, int64_t nrows, int cpw, int splits) {
     // staged activation rows (row stride Kb + 8: rows start 16 B apart in bank
     // order), sub-block sums S[sb][8] and the cross-wave reduction buffer
     __shared__ __attribute__((aligned(16))) bf16_t xs[XS_ELEMS + 8 * 8];
-    __shared__ __attribute__((aligned(16))) float Ss[QT == 12 ? KB_MAX / 32 : 1][8];
+    __shared__ __attribute__((aligned(16))) float Ss[QT != 8 ? KB_MAX / 32 : 1][8];
     // the cross-wave reduction reuses the staging buffer once all waves are done with it
     float(*red)[8][32] = reinterpret_cast<float(*)[8][32]>(&xs[0]);
     static_assert(MAXW * 8 * 32 * 4 <= XS_ELEMS * 2, "reduction buffer exceeds the staging buffer");
@@ -124,7 +124,7 @@ __global__ __launch_bounds__(512, QT == 12 ? 4 : 2) void k_gemv_mfma(const uint8
 
     const uint8_t* pw;
     const uint8_t* ps;
-    if (QT == 12) {
+    if (QT != 8) {
         const int nsb = K >> 8;
         pw = Wq + q4k_piece(row, nsb, 0, g, 0);
         ps = Wq + q4k_hdword(row, nsb, 0, 0);
@@ -133,7 +133,7 @@ __global__ __launch_bounds__(512, QT == 12 ? 4 : 2) void k_gemv_mfma(const uint8
         ps = Wa + row * (K >> 5) * 2;
     }
     auto load = [&](Chunk<QT>& C, int c) {
-        if (QT == 12) {
+        if (QT != 8) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 C.w[u] = *reinterpret_cast<const uint4*>(pw + (int64_t)c * 64 + u * 16);
@@ -177,7 +177,7 @@ __global__ __launch_bounds__(512, QT == 12 ? 4 : 2) void k_gemv_mfma(const uint8
             const int m = ch / cpr, c = ch - m * cpr;
             const uint4 v = xv[i];
             *reinterpret_cast<uint4*>(&xs[m * XR + 8 * c]) = v;
-            if (QT == 12) {
+            if (QT != 8) {
                 // lanes 4j..4j+3 hold the 4 chunks of one sub-block (quads stay whole)
                 const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
                 bf16x2_t p[4];
@@ -215,13 +215,21 @@ __global__ __launch_bounds__(512, QT == 12 ? 4 : 2) void k_gemv_mfma(const uint8
             const uint4 a1 = *reinterpret_cast<const uint4*>(xa + kl + 8);
             const uint4 a2 = *reinterpret_cast<const uint4*>(xa + kl + 32);
             const uint4 a3 = *reinterpret_cast<const uint4*>(xa + kl + 40);
-            if (QT == 12) {
+            if (QT != 8) {
                 const f32x4_t S1 = *reinterpret_cast<const f32x4_t*>(&Ss[kl >> 5][4 * g]);
                 const f32x4_t S2 = *reinterpret_cast<const f32x4_t*>(&Ss[(kl >> 5) + 1][4 * g]);
                 const uint32_t h = C.s[u];
-                const float d1 = d * (float)(h & 63u), d2 = d * (float)((h >> 12) & 63u);
-                const float c1 = __builtin_fmaf(128.0f, d1, dm * (float)((h >> 6) & 63u));
-                const float c2 = __builtin_fmaf(128.0f, d2, dm * (float)((h >> 18) & 63u));
+                float d1, d2, c1, c2;
+                if constexpr (QT == 13) {  // affine group: w = scale * q + bias
+                    const float sc = valid ? aff_scale(h) : 0.0f, bi = valid ? aff_bias(h) : 0.0f;
+                    d1 = d2 = sc;
+                    c1 = c2 = __builtin_fmaf(128.0f, sc, -bi);
+                } else {
+                    d1 = d * (float)(h & 63u);
+                    d2 = d * (float)((h >> 12) & 63u);
+                    c1 = __builtin_fmaf(128.0f, d1, dm * (float)((h >> 6) & 63u));
+                    c2 = __builtin_fmaf(128.0f, d2, dm * (float)((h >> 18) & 63u));
+                }
                 const uint4 q = C.w[u];
                 const uint32_t M4 = 0x0F0F0F0Fu;
                 // one sub-block at a time keeps a single 16-register accumulator live
@@ -354,7 +362,7 @@ hipError_t run_e(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* 
 GemvPlan plan_gemv_mfma(int qtype, int64_t M, int64_t N_rows, int64_t K, bool gu) {
     GemvPlan p;
     if (M < 1 || M > 8 || K < 256 || K % 256 || K > (1 << 20)) return p;
-    if (qtype != 8 && qtype != 12) return p;
+    if (qtype != 8 && qtype != 12 && qtype != 13) return p;
     const int64_t nout = gu ? N_rows / 2 : N_rows;
     const int64_t tiles = gu ? (nout + 15) / 16 : (nout + 31) / 32;
     const int chunks = (int)(K / 256);
@@ -392,6 +400,12 @@ hipError_t launch_gemv_mfma(const GemvPlan& p, const WeightView& w, const void* 
                             : run_e<12, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
         return yf32 ? run_e<12, false, float>(p, w, xb, y, M, nout, up_off, ws, s)
                     : run_e<12, false, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
+    }
+    if (w.qtype == 13) {
+        if (gu) return yf32 ? run_e<13, true, float>(p, w, xb, y, M, nout, up_off, ws, s)
+                            : run_e<13, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
+        return yf32 ? run_e<13, false, float>(p, w, xb, y, M, nout, up_off, ws, s)
+                    : run_e<13, false, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
     }
     if (gu) return yf32 ? run_e<8, true, float>(p, w, xb, y, M, nout, up_off, ws, s)
                         : run_e<8, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);

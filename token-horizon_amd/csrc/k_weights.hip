@@ -216,33 +216,38 @@ __global__ __launch_bounds__(256) void k_quantize_q4k(const float* __restrict__ 
 }
 
 // ---------------------------------------------------------------- dequantize
+// four outputs: f32, or bf16 rounded to nearest even from the f32 values
+__device__ __forceinline__ void put4(float* p, float a, float b, float c, float d) {
+    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+}
+__device__ __forceinline__ void put4(bf16_t* p, float a, float b, float c, float d) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(pack_bf16x2(a, b), pack_bf16x2(c, d));
+}
+
 // one thread per 32-weight block: y = q * d
+template <typename OT>
 __global__ __launch_bounds__(256) void k_dequant_q8_0(const int8_t* __restrict__ qs,
-                                                      const uint16_t* __restrict__ dpl, float* __restrict__ out,
+                                                      const uint16_t* __restrict__ dpl, OT* __restrict__ out,
                                                       int64_t nblocks) {
     const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
     const float d = f16_to_f32(dpl[b]);
     const uint4* src = reinterpret_cast<const uint4*>(qs + b * THQ_QK8_0);
-    float4* dst = reinterpret_cast<float4*>(out + b * THQ_QK8_0);
+    OT* dst = out + b * THQ_QK8_0;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const uint4 v = src[h];
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float4 o;
-            o.x = (float)(int8_t)(w[i] & 0xFF) * d;
-            o.y = (float)(int8_t)((w[i] >> 8) & 0xFF) * d;
-            o.z = (float)(int8_t)((w[i] >> 16) & 0xFF) * d;
-            o.w = (float)(int8_t)(w[i] >> 24) * d;
-            dst[4 * h + i] = o;
-        }
+        for (int i = 0; i < 4; ++i)
+            put4(dst + 16 * h + 4 * i, (float)(int8_t)(w[i] & 0xFF) * d, (float)(int8_t)((w[i] >> 8) & 0xFF) * d,
+                 (float)(int8_t)((w[i] >> 16) & 0xFF) * d, (float)(int8_t)(w[i] >> 24) * d);
     }
 }
 
 // one thread per (superblock, sub-block j): y = d*sc*q - dmin*m
-__global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__ src, float* __restrict__ out,
+template <typename OT>
+__global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__ src, OT* __restrict__ out,
                                                      int64_t nsuper, int nsb) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int64_t sb = t >> 3;
@@ -260,19 +265,144 @@ __global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__
     q4k_hdr_sm(h, j, sc, m);
     const float d1 = d * (float)sc, m1 = dmin * (float)m;
     const int shift = (j & 1) * 4;
-    float4* dst = reinterpret_cast<float4*>(out + sb * THQ_QK_K + 32 * j);
+    OT* dst = out + sb * THQ_QK_K + 32 * j;
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
         const uint4 v = *reinterpret_cast<const uint4*>(src + q4k_piece(n, nsb, sidx, hh, j >> 1));
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            float4 o;
-            o.x = d1 * (float)((w[i] >> shift) & 0xF) - m1;
-            o.y = d1 * (float)((w[i] >> (shift + 8)) & 0xF) - m1;
-            o.z = d1 * (float)((w[i] >> (shift + 16)) & 0xF) - m1;
-            o.w = d1 * (float)((w[i] >> (shift + 24)) & 0xF) - m1;
-            dst[4 * hh + i] = o;
+        for (int i = 0; i < 4; ++i)
+            put4(dst + 16 * hh + 4 * i, d1 * (float)((w[i] >> shift) & 0xF) - m1,
+                 d1 * (float)((w[i] >> (shift + 8)) & 0xF) - m1, d1 * (float)((w[i] >> (shift + 16)) & 0xF) - m1,
+                 d1 * (float)((w[i] >> (shift + 24)) & 0xF) - m1);
+    }
+}
+
+// ---------------------------------------------------------------- MLX affine 4-bit
+// half 2.7.1 bf16::from_f64 (its f64_to_bf16, the rounding dequant_affine
+// uses, engine/src/qwen35.rs:110-134): the low 32 bits of the f64 mantissa
+// are dropped first, then the top 20 mantissa bits round to nearest even
+// (the round bit decides, the remaining kept bits and the result's last bit
+// break ties), with half's overflow, subnormal and NaN rules.
+__device__ __forceinline__ uint16_t bf16_from_f64_half(double v) {
+    const uint32_t x = (uint32_t)((uint64_t)__double_as_longlong(v) >> 32);
+    const uint32_t sign = x & 0x80000000u, exp = x & 0x7FF00000u;
+    uint32_t man = x & 0x000FFFFFu;
+    const uint32_t hs = sign >> 16;
+    if (exp == 0x7FF00000u) {  // inf / NaN (NaN keeps the top mantissa bits, quiet bit set)
+        const uint32_t nan_bit = (man == 0 && (uint32_t)__double_as_longlong(v) == 0) ? 0u : 0x0040u;
+        return (uint16_t)(hs | 0x7F80u | nan_bit | (man >> 13));
+    }
+    const int he = (int)(exp >> 20) - 1023 + 127;
+    if (he >= 0xFF) return (uint16_t)(hs | 0x7F80u);
+    if (he <= 0) {
+        if (14 - he > 21) return (uint16_t)hs;  // the round bit lies above the hidden bit
+        man |= 0x00100000u;
+        uint32_t hm = man >> (14 - he);
+        const uint32_t rb = 1u << (13 - he);
+        if ((man & rb) && (man & (3u * rb - 1u))) hm += 1;
+        return (uint16_t)(hs | hm);
+    }
+    const uint32_t r = hs | ((uint32_t)he << 7) | (man >> 13);
+    return (uint16_t)(((man & 0x1000u) && (man & 0x2FFFu)) ? r + 1 : r);
+}
+
+// MLX affine -> row-quad plane.  One thread per (row, 64-weight part of the
+// padded K): the part's eight words (element e = nibble e%8 of word e/8,
+// LSB first) become the two 16-B pieces (byte i: low = element i, high =
+// element 32 + i, i = 16h + j) and the header dword (bf16 scale | bf16 bias
+// << 16) of the group the part belongs to; parts past K are zero.
+// Source layouts (the engine's QLin, engine/src/qwen35.rs:311-319):
+//   row-major  wq [n][K/8], sb [n][2*ng]: the row's ng = K/gs scales, then
+//              its ng biases
+//   tiled      QLin::tiled (qwen35.rs:629-697), addresses q4woff / q4sb of
+//              engine/src/quant_kernel.rs:1085-1101: wq [row/256][g][row%256][8],
+//              scales [(tile*ng + g)*256 + row%256], biases after all
+//              tiles*ng*256 scales (gs = 64)
+__global__ __launch_bounds__(256) void k_repack_affine(const uint32_t* __restrict__ wq,
+                                                       const uint16_t* __restrict__ sb, uint8_t* __restrict__ dst,
+                                                       int64_t n, int K, int gs, int tiled, int nsb) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int nparts = nsb * 4;
+    if (t >= n * nparts) return;
+    const int64_t row = t / nparts;
+    const int gp = (int)(t - row * nparts);
+    const int s = gp >> 2, p = gp & 3;
+    uint32_t pc[2][4] = {{0u, 0u, 0u, 0u}, {0u, 0u, 0u, 0u}};
+    uint32_t hw = 0;
+    const int ng64 = K >> 6;
+    if (gp < ng64) {
+        const int64_t base = tiled ? (row >> 8) * (int64_t)ng64 * 2048 + (int64_t)gp * 2048 + (row & 255) * 8
+                                   : row * (int64_t)(K >> 3) + (int64_t)gp * 8;
+        uint32_t wd[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) wd[i] = wq[base + i];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) {
+                const uint32_t lo = (wd[2 * h + (j >> 3)] >> (4 * (j & 7))) & 0xFu;
+                const uint32_t hi = (wd[4 + 2 * h + (j >> 3)] >> (4 * (j & 7))) & 0xFu;
+                pc[h][j >> 2] |= (lo | (hi << 4)) << (8 * (j & 3));
+            }
+        uint32_t sc, bi;
+        if (tiled) {
+            const int64_t tiles = (n + 255) >> 8;
+            const int64_t prm = ((row >> 8) * ng64 + gp) * 256 + (row & 255);
+            sc = sb[prm];
+            bi = sb[prm + tiles * ng64 * 256];
+        } else {
+            const int ng = K / gs, g = gp * 64 / gs;
+            sc = sb[row * 2 * ng + g];
+            bi = sb[row * 2 * ng + ng + g];
+        }
+        hw = sc | (bi << 16);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        *reinterpret_cast<uint4*>(dst + q4k_piece(row, nsb, s, h, p)) = make_uint4(pc[h][0], pc[h][1], pc[h][2], pc[h][3]);
+    *reinterpret_cast<uint32_t*>(dst + q4k_hdword(row, nsb, s, p)) = hw;
+}
+
+// One thread per (row, 64-weight group): f32 out = fmaf(q, scale, bias) (the
+// product is exact, so one rounding of q*scale + bias); bf16 out = half's
+// f64 -> bf16 of q*scale + bias evaluated in f64, as dequant_affine does.
+template <bool BF16>
+__global__ __launch_bounds__(256) void k_dequant_affine(const uint8_t* __restrict__ src, void* __restrict__ out,
+                                                        int64_t n, int K, int nsb) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int ng64 = K >> 6;
+    if (t >= n * ng64) return;
+    const int64_t row = t / ng64;
+    const int gp = (int)(t - row * ng64);
+    const int s = gp >> 2, p = gp & 3;
+    const uint32_t hw = *reinterpret_cast<const uint32_t*>(src + q4k_hdword(row, nsb, s, p));
+    const float sc = aff_scale(hw), bi = aff_bias(hw);
+    float* of = static_cast<float*>(out) + row * (int64_t)K + 64 * gp;
+    bf16_t* ob = static_cast<bf16_t*>(out) + row * (int64_t)K + 64 * gp;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint4 v = *reinterpret_cast<const uint4*>(src + q4k_piece(row, nsb, s, h, p));
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {  // low nibbles: elements 16h + j; high: 32 + 16h + j
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                float q[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) q[b] = (float)((w[i] >> (8 * b + 4 * half)) & 0xFu);
+                const int e = 32 * half + 16 * h + 4 * i;
+                if constexpr (BF16) {
+                    uint16_t r[4];
+#pragma unroll
+                    for (int b = 0; b < 4; ++b) r[b] = bf16_from_f64_half((double)q[b] * (double)sc + (double)bi);
+                    *reinterpret_cast<uint2*>(ob + e) =
+                        make_uint2((uint32_t)r[0] | ((uint32_t)r[1] << 16), (uint32_t)r[2] | ((uint32_t)r[3] << 16));
+                } else {
+                    put4(of + e, __builtin_fmaf(q[0], sc, bi), __builtin_fmaf(q[1], sc, bi),
+                         __builtin_fmaf(q[2], sc, bi), __builtin_fmaf(q[3], sc, bi));
+                }
+            }
         }
     }
 }
@@ -351,16 +481,49 @@ hipError_t launch_q4k_copy_rows(const uint8_t* src, int64_t n, uint8_t* dst, int
     return hipGetLastError();
 }
 
-hipError_t launch_dequant_q8_0(const int8_t* qs, const uint16_t* d, float* out, int64_t nblocks, hipStream_t s) {
+hipError_t launch_dequant_q8_0(const int8_t* qs, const uint16_t* d, void* out, bool bf16, int64_t nblocks,
+                               hipStream_t s) {
     if (nblocks == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_dequant_q8_0, dim3(grid_for(nblocks, 256)), dim3(256), 0, s, qs, d, out, nblocks);
+    if (bf16)
+        hipLaunchKernelGGL(k_dequant_q8_0<bf16_t>, dim3(grid_for(nblocks, 256)), dim3(256), 0, s, qs, d,
+                           static_cast<bf16_t*>(out), nblocks);
+    else
+        hipLaunchKernelGGL(k_dequant_q8_0<float>, dim3(grid_for(nblocks, 256)), dim3(256), 0, s, qs, d,
+                           static_cast<float*>(out), nblocks);
     return hipGetLastError();
 }
 
-hipError_t launch_dequant_q4k(const uint8_t* src, float* out, int64_t n, int nsb, hipStream_t s) {
+hipError_t launch_dequant_q4k(const uint8_t* src, void* out, bool bf16, int64_t n, int nsb, hipStream_t s) {
     const int64_t nsuper = n * nsb;
     if (nsuper == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_dequant_q4k, dim3(grid_for(nsuper * 8, 256)), dim3(256), 0, s, src, out, nsuper, nsb);
+    if (bf16)
+        hipLaunchKernelGGL(k_dequant_q4k<bf16_t>, dim3(grid_for(nsuper * 8, 256)), dim3(256), 0, s, src,
+                           static_cast<bf16_t*>(out), nsuper, nsb);
+    else
+        hipLaunchKernelGGL(k_dequant_q4k<float>, dim3(grid_for(nsuper * 8, 256)), dim3(256), 0, s, src,
+                           static_cast<float*>(out), nsuper, nsb);
+    return hipGetLastError();
+}
+
+hipError_t launch_repack_affine(const uint32_t* wq, const uint16_t* sb, uint8_t* dst, int64_t n, int K, int gs,
+                                bool tiled, hipStream_t s) {
+    const int nsb = (K + 255) / 256;
+    const int64_t threads = n * nsb * 4;
+    if (threads == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_repack_affine, dim3(grid_for(threads, 256)), dim3(256), 0, s, wq, sb, dst, n, K, gs,
+                       tiled ? 1 : 0, nsb);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_affine(const uint8_t* src, void* out, bool bf16, int64_t n, int K, hipStream_t s) {
+    const int nsb = (K + 255) / 256;
+    const int64_t threads = n * (K / 64);
+    if (threads == 0) return hipSuccess;
+    if (bf16)
+        hipLaunchKernelGGL(k_dequant_affine<true>, dim3(grid_for(threads, 256)), dim3(256), 0, s, src, out, n, K, nsb);
+    else
+        hipLaunchKernelGGL(k_dequant_affine<false>, dim3(grid_for(threads, 256)), dim3(256), 0, s, src, out, n, K,
+                           nsb);
     return hipGetLastError();
 }
 

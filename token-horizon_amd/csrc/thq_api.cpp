@@ -30,10 +30,11 @@ struct thq_ctx {
 
 struct thq_weight {
     thq_ctx* ctx = nullptr;
-    int qtype = 0;
+    int qtype = 0;           // thq_dtype
     int64_t N = 0, K = 0;
-    uint8_t* q = nullptr;    // Q8_0 i8 plane / Q4_K nibble plane
-    uint8_t* aux = nullptr;  // Q8_0 f16 scale plane / Q4_K header plane
+    int gs = 0;              // MLX affine group size
+    uint8_t* q = nullptr;    // Q8_0 i8 plane / Q4_K and MLX affine row-quad plane
+    uint8_t* aux = nullptr;  // Q8_0 f16 scale plane
 };
 
 namespace {
@@ -56,20 +57,28 @@ int fail(int code, const char* fmt, ...) {
         if (e_ != hipSuccess) return fail(THQ_EHIP, "%s: %s", #expr, hipGetErrorString(e_));     \
     } while (0)
 
-int block_of(int qtype) { return qtype == THQ_Q8_0 ? 32 : (qtype == THQ_Q4_K ? 256 : 0); }
+int block_of(int qtype) {
+    return qtype == THQ_Q8_0 ? 32 : (qtype == THQ_Q4_K ? 256 : (qtype == THQ_MLX_Q4 ? 64 : 0));
+}
 
-size_t gguf_bytes(int qtype, int64_t n, int64_t k) {
+// GGUF block bytes; for MLX affine weights the QLin arrays (wq + sb)
+size_t gguf_bytes(int qtype, int64_t n, int64_t k, int gs = 64) {
     if (qtype == THQ_Q8_0) return (size_t)n * (size_t)(k / 32) * 34;
+    if (qtype == THQ_MLX_Q4) return (size_t)n * (size_t)k / 2 + (size_t)n * 2 * (size_t)(k / gs) * 2;
     return (size_t)n * (size_t)(k / 256) * 144;
 }
 
-thq::WeightView view(const thq_weight* w) { return thq::WeightView{w->qtype, w->N, w->K, w->q, w->aux}; }
+// the kernels' type ids: 8 Q8_0, 12 Q4_K, 13 MLX affine on the Q4_K layout
+thq::WeightView view(const thq_weight* w) {
+    return thq::WeightView{w->qtype == THQ_MLX_Q4 ? 13 : w->qtype, w->N, w->K, w->q, w->aux};
+}
 
-// device plane sizes: Q8_0 = i8 plane + f16 scale plane; Q4_K = one row-quad
-// plane (rows padded to a multiple of 4, padding zero)
+// device plane sizes: Q8_0 = i8 plane + f16 scale plane; Q4_K / MLX affine =
+// one row-quad plane (rows padded to a multiple of 4 and, for MLX affine, K
+// to whole superblocks; padding zero)
 size_t q_plane_bytes(int qtype, int64_t n, int64_t k) {
     if (qtype == THQ_Q8_0) return (size_t)n * (size_t)k;
-    return (size_t)((n + 3) / 4) * (size_t)(k / 256) * 576;
+    return (size_t)((n + 3) / 4) * (size_t)((k + 255) / 256) * 576;
 }
 size_t aux_plane_bytes(int qtype, int64_t n, int64_t k) {
     return qtype == THQ_Q8_0 ? (size_t)n * (size_t)(k / 32) * 2 : 0;
@@ -77,7 +86,7 @@ size_t aux_plane_bytes(int qtype, int64_t n, int64_t k) {
 
 int check_dtype_shape(int dtype, int64_t n, int64_t k) {
     const int bs = block_of(dtype);
-    if (!bs) return fail(THQ_EDTYPE, "unsupported weight dtype %d (want Q8_0=8 or Q4_K=12)", dtype);
+    if (!bs) return fail(THQ_EDTYPE, "unsupported weight dtype %d (want Q8_0=8, Q4_K=12 or MLX_Q4=100)", dtype);
     if (n <= 0 || k <= 0) return fail(THQ_ESHAPE, "weight shape [%lld, %lld] must be positive", (long long)n, (long long)k);
     if (k % bs) return fail(THQ_ESHAPE, "K=%lld is not a multiple of the block size %d", (long long)k, bs);
     if (k > (int64_t)1 << 30 || n > (int64_t)1 << 40) return fail(THQ_ESHAPE, "weight shape too large");
@@ -93,7 +102,7 @@ int alloc_weight(thq_ctx* ctx, int dtype, int64_t n, int64_t k, thq_weight** out
     w->K = k;
     const size_t qb = q_plane_bytes(dtype, n, k), ab = aux_plane_bytes(dtype, n, k);
     hipError_t e = hipMalloc((void**)&w->q, qb);
-    if (e == hipSuccess && dtype == THQ_Q4_K && (n & 3)) e = hipMemset(w->q, 0, qb);  // zero padding rows
+    if (e == hipSuccess && dtype != THQ_Q8_0 && (n & 3)) e = hipMemset(w->q, 0, qb);  // zero padding rows
     if (e == hipSuccess && ab) {
         e = hipMalloc((void**)&w->aux, ab);
         if (e != hipSuccess) (void)hipFree(w->q);
@@ -135,6 +144,33 @@ struct DeviceGuard {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// MLX affine weights: K a multiple of 64 and of the group size; groups of
+// 64 or any multiple of 64; the tiled QLin form exists for gs = 64 only
+int check_affine(int64_t n, int64_t k, int gs, int tiled) {
+    int rc = check_dtype_shape(THQ_MLX_Q4, n, k);
+    if (rc) return rc;
+    if (gs <= 0 || gs % 64 || k % gs)
+        return fail(THQ_EDTYPE, "MLX affine group size %d unsupported (a multiple of 64 dividing K=%lld)", gs,
+                    (long long)k);
+    if (tiled && gs != 64) return fail(THQ_EDTYPE, "the tiled QLin layout has groups of 64");
+    return THQ_OK;
+}
+
+// bytes of the QLin arrays: row-major or tiled (rows padded to 256)
+void affine_src_bytes(int64_t n, int64_t k, int gs, int tiled, size_t& wq_bytes, size_t& sb_bytes) {
+    const int64_t rows = tiled ? (n + 255) / 256 * 256 : n;
+    wq_bytes = (size_t)rows * (size_t)(k / 8) * 4;
+    sb_bytes = (size_t)rows * 2 * (size_t)(k / gs) * 2;
+}
+
+hipError_t dequant_any(const thq_weight* w, void* out, bool bf16, hipStream_t s) {
+    if (w->qtype == THQ_Q8_0)
+        return thq::launch_dequant_q8_0(reinterpret_cast<const int8_t*>(w->q), reinterpret_cast<const uint16_t*>(w->aux),
+                                        out, bf16, w->N * (w->K / 32), s);
+    if (w->qtype == THQ_MLX_Q4) return thq::launch_dequant_affine(w->q, out, bf16, w->N, (int)w->K, s);
+    return thq::launch_dequant_q4k(w->q, out, bf16, w->N, (int)(w->K / 256), s);
+}
+
 // Shared body of matmul / gate_up / argmax-logits.
 int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t m, void* y, int yt, uint32_t flags,
                bool gu, void* stream) {
@@ -155,6 +191,7 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
     const int64_t up_off = gu ? w->N / 2 : 0;
     hipError_t e;
     if (flags & THQ_MODE_Q8ACT) {
+        if (w->qtype == THQ_MLX_Q4) return fail(THQ_EDTYPE, "THQ_MODE_Q8ACT applies to GGUF weights only");
         if (!thq::q8act_supported(w->qtype, w->K))
             return fail(THQ_ESHAPE, "K=%lld too large for THQ_MODE_Q8ACT", (long long)w->K);
         if (!aligned16(x)) return fail(THQ_EALIGN, "THQ_MODE_Q8ACT needs 16-byte aligned x");
@@ -170,10 +207,12 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
         const char* v = getenv("THQ_GEMV_M1");
         return v && !strcmp(v, "mfma");
     }();
-    const thq::GemvPlan gp = (!xf32 && aligned16(x) && m <= 8) ? thq::plan_gemv_mfma(w->qtype, m, w->N, w->K, gu)
+    const thq::GemvPlan gp = (!xf32 && aligned16(x) && m <= 8) ? thq::plan_gemv_mfma(v.qtype, m, w->N, w->K, gu)
                                                                  : thq::GemvPlan{};
     const bool skinny = gp.waves > 0;
-    if (m == 1 && !(m1_mfma && skinny) && aligned16(x) && thq::gemv1_supported(w->qtype, (int)w->K, gu, w->N)) {
+    // the 4-bit tile kernels need whole superblocks (MLX affine K % 256 != 0 runs the generic kernel)
+    const bool q4 = w->qtype != THQ_Q8_0;
+    if (m == 1 && !(m1_mfma && skinny) && aligned16(x) && thq::gemv1_supported(v.qtype, (int)w->K, gu, w->N)) {
         e = thq::launch_gemv1(v, x, xf32, y, yf32, gu, nout, up_off, s);
     } else if (skinny) {
         std::lock_guard<std::mutex> lk(ctx->mu);
@@ -182,9 +221,9 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
             if (rc) return rc;
         }
         e = thq::launch_gemv_mfma(gp, v, x, y, yf32, gu, (int)m, nout, up_off, static_cast<float*>(ctx->ws), s);
-    } else if (!xf32 && aligned16(x) && !(w->qtype == THQ_Q4_K && (flags & THQ_MODE_EXACT_W))) {
+    } else if (!xf32 && aligned16(x) && !(q4 && ((flags & THQ_MODE_EXACT_W) || w->K % 256))) {
         const bool exact = (flags & THQ_MODE_EXACT_W) || (w->qtype == THQ_Q8_0 && m <= 64);
-        thq::GemmPlan p = thq::plan_gemm(w->qtype, exact, m, w->N, w->K, gu);
+        thq::GemmPlan p = thq::plan_gemm(v.qtype, exact, m, w->N, w->K, gu);
         std::lock_guard<std::mutex> lk(ctx->mu);
         if (p.workspace_bytes) {
             int rc = ensure_ws(ctx, p.workspace_bytes);
@@ -231,6 +270,7 @@ void thq_destroy(thq_ctx* ctx) {
 int thq_weight_upload(thq_ctx* ctx, thq_dtype dtype, const void* host_blocks, int64_t n, int64_t k,
                       thq_weight** out) {
     if (!ctx || !host_blocks || !out) return fail(THQ_EINVAL, "null argument");
+    if (dtype == THQ_MLX_Q4) return fail(THQ_EDTYPE, "MLX affine weights load with thq_affine_upload");
     int rc = check_dtype_shape(dtype, n, k);
     if (rc) return rc;
     DeviceGuard g(ctx->device);
@@ -251,6 +291,7 @@ int thq_weight_upload(thq_ctx* ctx, thq_dtype dtype, const void* host_blocks, in
 int thq_weight_from_device(thq_ctx* ctx, thq_dtype dtype, const void* dev_blocks, int64_t n, int64_t k, void* stream,
                            thq_weight** out) {
     if (!ctx || !dev_blocks || !out) return fail(THQ_EINVAL, "null argument");
+    if (dtype == THQ_MLX_Q4) return fail(THQ_EDTYPE, "MLX affine weights load with thq_affine_from_device");
     int rc = check_dtype_shape(dtype, n, k);
     if (rc) return rc;
     DeviceGuard g(ctx->device);
@@ -275,6 +316,7 @@ int thq_weight_from_device(thq_ctx* ctx, thq_dtype dtype, const void* dev_blocks
 int thq_quantize(thq_ctx* ctx, thq_dtype dtype, const float* w_dev, int64_t n, int64_t k, void* stream,
                  thq_weight** out) {
     if (!ctx || !w_dev || !out) return fail(THQ_EINVAL, "null argument");
+    if (dtype == THQ_MLX_Q4) return fail(THQ_EDTYPE, "no MLX affine quantizer (the engine loads MLX checkpoints)");
     int rc = check_dtype_shape(dtype, n, k);
     if (rc) return rc;
     if (!aligned16(w_dev)) return fail(THQ_EALIGN, "w_dev must be 16-byte aligned");
@@ -302,6 +344,7 @@ int thq_weight_fuse(thq_ctx* ctx, const thq_weight* const* parts, int nparts, th
     for (int i = 0; i < nparts; ++i) {
         if (!parts[i]) return fail(THQ_EINVAL, "part %d is null", i);
         if (parts[i]->qtype != parts[0]->qtype) return fail(THQ_EDTYPE, "part %d dtype differs", i);
+        if (parts[i]->gs != parts[0]->gs) return fail(THQ_EDTYPE, "part %d group size differs", i);
         if (parts[i]->K != parts[0]->K)
             return fail(THQ_ESHAPE, "part %d has K=%lld, part 0 has K=%lld", i, (long long)parts[i]->K,
                         (long long)parts[0]->K);
@@ -313,12 +356,13 @@ int thq_weight_fuse(thq_ctx* ctx, const thq_weight* const* parts, int nparts, th
     thq_weight* w = nullptr;
     int rc = alloc_weight(ctx, dtype, n, k, &w);
     if (rc) return rc;
+    w->gs = parts[0]->gs;
     size_t qoff = 0, aoff = 0;
     int64_t row0 = 0;
     for (int i = 0; i < nparts; ++i) {
         hipError_t e;
-        if (dtype == THQ_Q4_K) {
-            e = thq::launch_q4k_copy_rows(parts[i]->q, parts[i]->N, w->q, row0, (int)(k / 256), nullptr);
+        if (dtype != THQ_Q8_0) {
+            e = thq::launch_q4k_copy_rows(parts[i]->q, parts[i]->N, w->q, row0, (int)((k + 255) / 256), nullptr);
         } else {
             const size_t qb = q_plane_bytes(dtype, parts[i]->N, k), ab = aux_plane_bytes(dtype, parts[i]->N, k);
             e = hipMemcpy(w->q + qoff, parts[i]->q, qb, hipMemcpyDeviceToDevice);
@@ -354,12 +398,13 @@ int thq_weight_info(const thq_weight* w, thq_dtype* dtype, int64_t* n, int64_t* 
     if (dtype) *dtype = (thq_dtype)w->qtype;
     if (n) *n = w->N;
     if (k) *k = w->K;
-    if (bytes) *bytes = gguf_bytes(w->qtype, w->N, w->K);
+    if (bytes) *bytes = gguf_bytes(w->qtype, w->N, w->K, w->gs);
     return THQ_OK;
 }
 
 int thq_weight_download(const thq_weight* w, void* host_blocks) {
     if (!w || !host_blocks) return fail(THQ_EINVAL, "null argument");
+    if (w->qtype == THQ_MLX_Q4) return fail(THQ_EDTYPE, "MLX affine weights download with thq_affine_download");
     DeviceGuard g(w->ctx->device);
     std::vector<uint8_t> qs(q_plane_bytes(w->qtype, w->N, w->K));
     std::vector<uint8_t> aux(aux_plane_bytes(w->qtype, w->N, w->K));
@@ -394,12 +439,95 @@ int thq_dequantize(thq_ctx* ctx, const thq_weight* w, float* out_dev, void* stre
     if (!aligned16(out_dev)) return fail(THQ_EALIGN, "out_dev must be 16-byte aligned");
     DeviceGuard g(ctx->device);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    hipError_t e = w->qtype == THQ_Q8_0
-                       ? thq::launch_dequant_q8_0(reinterpret_cast<const int8_t*>(w->q),
-                                                  reinterpret_cast<const uint16_t*>(w->aux), out_dev,
-                                                  w->N * (w->K / 32), s)
-                       : thq::launch_dequant_q4k(w->q, out_dev, w->N, (int)(w->K / 256), s);
+    hipError_t e = dequant_any(w, out_dev, false, s);
     if (e != hipSuccess) return fail(THQ_EHIP, "dequantize: %s", hipGetErrorString(e));
+    return THQ_OK;
+}
+
+int thq_dequantize_bf16(thq_ctx* ctx, const thq_weight* w, uint16_t* out_dev, void* stream) {
+    if (!ctx || !w || !out_dev) return fail(THQ_EINVAL, "null argument");
+    if (!aligned16(out_dev)) return fail(THQ_EALIGN, "out_dev must be 16-byte aligned");
+    DeviceGuard g(ctx->device);
+    hipError_t e = dequant_any(w, out_dev, true, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(THQ_EHIP, "dequantize_bf16: %s", hipGetErrorString(e));
+    return THQ_OK;
+}
+
+int thq_affine_from_device(thq_ctx* ctx, const uint32_t* wq_dev, const uint16_t* sb_dev, int64_t n, int64_t k, int gs,
+                           int tiled, void* stream, thq_weight** out) {
+    if (!ctx || !wq_dev || !sb_dev || !out) return fail(THQ_EINVAL, "null argument");
+    int rc = check_affine(n, k, gs, tiled);
+    if (rc) return rc;
+    if (((uintptr_t)wq_dev & 3u) || ((uintptr_t)sb_dev & 1u)) return fail(THQ_EALIGN, "wq/sb misaligned");
+    DeviceGuard g(ctx->device);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    thq_weight* w = nullptr;
+    rc = alloc_weight(ctx, THQ_MLX_Q4, n, k, &w);
+    if (rc) return rc;
+    w->gs = gs;
+    hipError_t e = thq::launch_repack_affine(wq_dev, sb_dev, w->q, n, (int)k, gs, tiled != 0, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        thq_weight_free(w);
+        return fail(THQ_EHIP, "affine repack: %s", hipGetErrorString(e));
+    }
+    *out = w;
+    return THQ_OK;
+}
+
+int thq_affine_upload(thq_ctx* ctx, const uint32_t* wq_host, const uint16_t* sb_host, int64_t n, int64_t k, int gs,
+                      int tiled, thq_weight** out) {
+    if (!ctx || !wq_host || !sb_host || !out) return fail(THQ_EINVAL, "null argument");
+    int rc = check_affine(n, k, gs, tiled);
+    if (rc) return rc;
+    DeviceGuard g(ctx->device);
+    size_t wb, sbb;
+    affine_src_bytes(n, k, gs, tiled, wb, sbb);
+    void* staging = nullptr;
+    hipError_t e = hipMalloc(&staging, wb + sbb);
+    if (e != hipSuccess) return fail(THQ_ENOMEM, "hipMalloc staging(%zu): %s", wb + sbb, hipGetErrorString(e));
+    e = hipMemcpy(staging, wq_host, wb, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(static_cast<char*>(staging) + wb, sb_host, sbb, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(staging);
+        return fail(THQ_EHIP, "hipMemcpy affine weight: %s", hipGetErrorString(e));
+    }
+    rc = thq_affine_from_device(ctx, static_cast<const uint32_t*>(staging),
+                                reinterpret_cast<const uint16_t*>(static_cast<char*>(staging) + wb), n, k, gs, tiled,
+                                nullptr, out);  // synchronizes
+    (void)hipFree(staging);
+    return rc;
+}
+
+int thq_affine_download(const thq_weight* w, uint32_t* wq_host, uint16_t* sb_host) {
+    if (!w || !wq_host || !sb_host) return fail(THQ_EINVAL, "null argument");
+    if (w->qtype != THQ_MLX_Q4) return fail(THQ_EDTYPE, "not an MLX affine weight");
+    DeviceGuard g(w->ctx->device);
+    std::vector<uint8_t> qs(q_plane_bytes(w->qtype, w->N, w->K));
+    HIP_TRY(hipMemcpy(qs.data(), w->q, qs.size(), hipMemcpyDeviceToHost));
+    const int nsb = (int)((w->K + 255) / 256), ng = (int)(w->K / w->gs), per = w->gs / 64;
+    const int64_t words = w->K / 8;
+    for (int64_t n = 0; n < w->N; ++n) {
+        for (int64_t gp = 0; gp < w->K / 64; ++gp) {
+            const int s = (int)(gp >> 2), p = (int)(gp & 3);
+            uint8_t pc[2][16];
+            for (int h = 0; h < 2; ++h) std::memcpy(pc[h], qs.data() + thq::q4k_piece(n, nsb, s, h, p), 16);
+            uint32_t* wd = wq_host + n * words + gp * 8;
+            for (int i = 0; i < 8; ++i) wd[i] = 0;
+            for (int h = 0; h < 2; ++h)
+                for (int j = 0; j < 16; ++j) {
+                    const uint32_t lo = pc[h][j] & 0xFu, hi = pc[h][j] >> 4;
+                    wd[2 * h + (j >> 3)] |= lo << (4 * (j & 7));
+                    wd[4 + 2 * h + (j >> 3)] |= hi << (4 * (j & 7));
+                }
+            if (gp % per == 0) {
+                uint32_t hw;
+                std::memcpy(&hw, qs.data() + thq::q4k_hdword(n, nsb, s, p), 4);
+                sb_host[n * 2 * ng + gp / per] = (uint16_t)(hw & 0xFFFFu);
+                sb_host[n * 2 * ng + ng + gp / per] = (uint16_t)(hw >> 16);
+            }
+        }
+    }
     return THQ_OK;
 }
 
@@ -459,7 +587,7 @@ int thq_matmul_argmax(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_
     float* logits = logits_dev;
     if (!logits) {
         // logits live at the end of the workspace, after the GEMM / argmax scratch
-        const thq::GemmPlan p = thq::plan_gemm(w->qtype, true, m, w->N, w->K, false);
+        const thq::GemmPlan p = thq::plan_gemm(view(w).qtype, true, m, w->N, w->K, false);
         size_t scratch = std::max(p.workspace_bytes, thq::argmax_workspace_bytes(m, w->N));
         if (flags & THQ_MODE_Q8ACT) scratch = std::max(scratch, thq::q8act_workspace_bytes(w->qtype, m, w->K));
         const size_t off = (scratch + 255) & ~(size_t)255;

@@ -127,6 +127,21 @@ __device__ __forceinline__ void q4k_hdr_sm(uint4 h, int j, uint32_t& sc, uint32_
     m = (w >> 6) & 63u;
 }
 
+// MLX affine 4-bit weights (qtype 13 inside the library) share the Q4_K
+// row-quad layout below: a 64-weight group is one part p of a 256-weight
+// superblock (nibble byte i of the part: low = element i, high = element
+// 32 + i), and header dword p holds the group's bf16 scale (low half) and
+// bf16 bias (high half); w = scale * q + bias.  Groups of 128 store their
+// pair in both 64-halves.
+__host__ __device__ __forceinline__ float aff_scale(uint32_t hw) {
+    union { uint32_t u; float f; } v = {hw << 16};
+    return v.f;
+}
+__host__ __device__ __forceinline__ float aff_bias(uint32_t hw) {
+    union { uint32_t u; float f; } v = {hw & 0xFFFF0000u};
+    return v.f;
+}
+
 // Q4_K device layout ("row quads").  Rows are grouped by four; group
 // g = n/4 occupies nsb*576 bytes (= 4 rows x nsb x 144) at g*nsb*576:
 //   nibbles  [r = n%4][h][s][p][16 B]  piece (h, s, p) = bytes 32p+16h .. +15

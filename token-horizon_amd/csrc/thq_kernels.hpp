@@ -9,6 +9,9 @@ namespace thq {
 // A weight as the kernels see it (device layouts; download restores GGUF bytes).
 //   Q8_0 (qtype 8):  q   = i8 plane [N][K]
 //                    aux = f16 scale plane [N][K/32]
+//   MLX affine 4-bit (qtype 13): q = the same row-quad plane with affine
+//                    headers (thq_dev.hpp, aff_scale); K may be padded to
+//                    whole superblocks (zero groups)
 //   Q4_K (qtype 12): q   = row-quad plane, ceil(N/4) groups of 4 x K/256 x
 //                          144 B (layout in thq_dev.hpp, q4k_group); padding
 //                          rows are zero
@@ -35,8 +38,15 @@ hipError_t launch_quantize_q4k(const float* w, uint8_t* dst, int64_t n, int nsb,
 hipError_t launch_repack_q4k(const uint8_t* gguf, uint8_t* dst, int64_t n, int nsb, hipStream_t s);
 // copy rows between row-quad planes (weight fusion)
 hipError_t launch_q4k_copy_rows(const uint8_t* src, int64_t n, uint8_t* dst, int64_t dst_row0, int nsb, hipStream_t s);
-hipError_t launch_dequant_q8_0(const int8_t* qs, const uint16_t* d, float* out, int64_t nblocks, hipStream_t s);
-hipError_t launch_dequant_q4k(const uint8_t* src, float* out, int64_t n, int nsb, hipStream_t s);
+// dequantization to f32 (bf16 = false) or bf16
+hipError_t launch_dequant_q8_0(const int8_t* qs, const uint16_t* d, void* out, bool bf16, int64_t nblocks,
+                               hipStream_t s);
+hipError_t launch_dequant_q4k(const uint8_t* src, void* out, bool bf16, int64_t n, int nsb, hipStream_t s);
+// MLX affine 4-bit (qtype 13): QLin arrays -> row-quad plane (K padded to whole
+// superblocks), and its dequantization (bf16: the reference's f64 rounding)
+hipError_t launch_repack_affine(const uint32_t* wq, const uint16_t* sb, uint8_t* dst, int64_t n, int K, int gs,
+                                bool tiled, hipStream_t s);
+hipError_t launch_dequant_affine(const uint8_t* src, void* out, bool bf16, int64_t n, int K, hipStream_t s);
 
 // decode GEMV (M = 1); gu = fused gate/up over a [gate; up] weight
 bool gemv1_supported(int qtype, int K, bool gu, int64_t n_rows);

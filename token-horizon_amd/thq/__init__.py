@@ -23,6 +23,7 @@ LIB_PATH = os.path.join(HERE, "libthq.so")
 Q8_0 = 8
 Q4_K = 12
 Q8_K = 15  # activation dot type of Q4_K (thq_quantize_act)
+MLX_Q4 = 100  # MLX affine 4-bit: the engine's QLin (wq u32 [N, K/8], sb bf16 [N, 2K/gs])
 BLOCK = {Q8_0: 32, Q4_K: 256, Q8_K: 256}
 BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q8_K: 292}
 
@@ -39,7 +40,8 @@ EINVAL, ESHAPE, EDTYPE, EALIGN, EHIP, ENOMEM = -1, -2, -3, -4, -5, -6
 EXPORTS = (
     "thq_init", "thq_destroy", "thq_last_error", "thq_version", "thq_weight_upload", "thq_weight_from_device",
     "thq_quantize", "thq_weight_fuse", "thq_weight_free", "thq_weight_info", "thq_weight_download",
-    "thq_dequantize", "thq_quantize_act", "thq_matmul", "thq_gate_up_silu", "thq_matmul_argmax", "thq_argmax",
+    "thq_affine_upload", "thq_affine_from_device", "thq_affine_download",
+    "thq_dequantize", "thq_dequantize_bf16", "thq_quantize_act", "thq_matmul", "thq_gate_up_silu", "thq_matmul_argmax", "thq_argmax",
 )
 
 
@@ -68,6 +70,10 @@ def _load():
         "thq_weight_info": ([P, C.POINTER(C.c_int), C.POINTER(i64), C.POINTER(i64), C.POINTER(C.c_size_t)], I),
         "thq_weight_download": ([P, P], I),
         "thq_dequantize": ([P, P, P, P], I),
+        "thq_dequantize_bf16": ([P, P, P, P], I),
+        "thq_affine_upload": ([P, P, P, i64, i64, I, I, PP], I),
+        "thq_affine_from_device": ([P, P, P, i64, i64, I, I, P, PP], I),
+        "thq_affine_download": ([P, P, P], I),
         "thq_quantize_act": ([P, I, P, I, i64, i64, P, P], I),
         "thq_matmul": ([P, P, P, I, i64, P, I, u32, P], I),
         "thq_gate_up_silu": ([P, P, P, I, i64, P, I, u32, P], I),
@@ -177,7 +183,43 @@ class QTensor:
         arr = (C.c_void_p * len(parts))(*[p.h.value for p in parts])
         h = C.c_void_p()
         check(lib.thq_weight_fuse(parts[0].ctx.h, arr, len(parts), C.byref(h)))
-        return cls(h, parts[0].ctx)
+        qt = cls(h, parts[0].ctx)
+        qt.gs = getattr(parts[0], "gs", 0)
+        return qt
+
+    @classmethod
+    def from_affine(cls, wq, sb, n: int, k: int, gs: int = 64, tiled: bool = False,
+                    ctx: Context | None = None) -> "QTensor":
+        """MLX affine 4-bit weight from the engine's QLin arrays: wq u32 [N, K/8],
+        sb bf16 bits [N, 2*K/gs] (row-major, tiled=False) or the QLin::tiled
+        layout (tiled=True).  Host numpy arrays or device torch tensors."""
+        ctx = ctx or Context.get(torch.cuda.current_device())
+        h = C.c_void_p()
+        if isinstance(wq, torch.Tensor) and wq.is_cuda:
+            check(lib.thq_affine_from_device(ctx.h, _ptr(wq), _ptr(sb), n, k, gs, int(tiled), _stream(),
+                                             C.byref(h)))
+        else:
+            import numpy as np
+            w = np.ascontiguousarray(wq, dtype=np.uint32)
+            b = np.ascontiguousarray(sb, dtype=np.uint16)
+            check(lib.thq_affine_upload(ctx.h, w.ctypes.data_as(C.c_void_p), b.ctypes.data_as(C.c_void_p), n, k, gs,
+                                        int(tiled), C.byref(h)))
+        qt = cls(h, ctx)
+        qt.gs = gs
+        return qt
+
+    def affine_data(self):
+        """The row-major QLin arrays (wq u32 [N, K/8], sb bf16 bits [N, 2*K/gs])."""
+        import numpy as np
+        wq = np.empty((self.n, self.k // 8), dtype=np.uint32)
+        sb = np.empty((self.n, 2 * self.k // self.gs), dtype=np.uint16)
+        check(lib.thq_affine_download(self.h, wq.ctypes.data_as(C.c_void_p), sb.ctypes.data_as(C.c_void_p)))
+        return wq, sb
+
+    def dequantize_bf16(self) -> torch.Tensor:
+        out = torch.empty((self.n, self.k), dtype=torch.bfloat16, device="cuda")
+        check(lib.thq_dequantize_bf16(self.ctx.h, self.h, _ptr(out), _stream()))
+        return out
 
     def data(self):
         """GGUF block bytes (numpy uint8, [N, row_bytes])."""
