@@ -132,8 +132,8 @@ __device__ __forceinline__ void q4k_unit_load(Q4Unit<GU>& U, const uint8_t* W, i
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
-                U.nib[qi][r][h] = *reinterpret_cast<const uint4*>(g + (int64_t)r * nsb * 128 + (int64_t)h * nsb * 64);
-        U.hdr[qi] = *reinterpret_cast<const uint4*>(g + (int64_t)nsb * 512);
+                U.nib[qi][r][h] = ld_stream16(g + (int64_t)r * nsb * 128 + (int64_t)h * nsb * 64);
+        U.hdr[qi] = ld_stream16(g + (int64_t)nsb * 512);
     }
 }
 
@@ -401,25 +401,23 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_bf16_1s(const uint8_t* W, con
     if (c1 < nx) lds[c1] = xv1;
     __syncthreads();
     if (gq >= nquads) return;
+    // lanes past K (K < 4096) read a valid superblock and mask it to zero:
+    // branch-free, so the LDS reads issue right after the barrier
     const int s = lane >> 2;
+    const uint32_t live = s < nsb ? 0xFFFFFFFFu : 0u;
+    const uint4* xp = lds + (s < nsb ? s : 0) * 32 + 8 * (lane & 3);
     uint32_t xlo[16], xhi[16];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const uint4 p = xp[v], q = xp[4 + v];
+        xlo[4 * v] = p.x & live; xlo[4 * v + 1] = p.y & live; xlo[4 * v + 2] = p.z & live; xlo[4 * v + 3] = p.w & live;
+        xhi[4 * v] = q.x & live; xhi[4 * v + 1] = q.y & live; xhi[4 * v + 2] = q.z & live; xhi[4 * v + 3] = q.w & live;
+    }
     float sxlo = 0.0f, sxhi = 0.0f;
-    if (s < nsb) {
-        const uint4* xp = lds + s * 32 + 8 * (lane & 3);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const uint4 p = xp[v], q = xp[4 + v];
-            xlo[4 * v] = p.x; xlo[4 * v + 1] = p.y; xlo[4 * v + 2] = p.z; xlo[4 * v + 3] = p.w;
-            xhi[4 * v] = q.x; xhi[4 * v + 1] = q.y; xhi[4 * v + 2] = q.z; xhi[4 * v + 3] = q.w;
-        }
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            sxlo = dot2_bf16(xlo[i], 0x3F803F80u, sxlo);  // bf16 (1, 1)
-            sxhi = dot2_bf16(xhi[i], 0x3F803F80u, sxhi);
-        }
-    } else {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) { xlo[i] = 0; xhi[i] = 0; }
+    for (int i = 0; i < 16; ++i) {
+        sxlo = dot2_bf16(xlo[i], 0x3F803F80u, sxlo);  // bf16 (1, 1)
+        sxhi = dot2_bf16(xhi[i], 0x3F803F80u, sxhi);
     }
     float acc[GU ? 8 : 4];
 #pragma unroll
@@ -539,7 +537,7 @@ __global__ __launch_bounds__(256) void k_gemv1_q8(const int8_t* __restrict__ Q, 
         for (int c = 0; c < KC; ++c) {
             const int k0 = 1024 * c + 16 * lane;
             if (k0 < K) {
-                qv[r][c] = *reinterpret_cast<const uint4*>(Q + row * K + k0);
+                qv[r][c] = ld_stream16(Q + row * K + k0);
                 dv[r][c] = D[row * nb + (k0 >> 5)];
             } else {
                 qv[r][c] = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
