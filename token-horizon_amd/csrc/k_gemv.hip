@@ -128,12 +128,14 @@ __device__ __forceinline__ void q4k_unit_load(Q4Unit<GU>& U, const uint8_t* W, i
 #pragma unroll
     for (int qi = 0; qi < Q4Unit<GU>::NQ; ++qi) {
         const uint8_t* g = W + (qi ? (gq + (up_off >> 2)) : gq) * qb + (int64_t)li * 16;
+        // headers first: the in-order wait counters then let row r's math
+        // start once its own two pieces have landed
+        U.hdr[qi] = ld_stream16(g + (int64_t)nsb * 512);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
             for (int h = 0; h < 2; ++h)
                 U.nib[qi][r][h] = ld_stream16(g + (int64_t)r * nsb * 128 + (int64_t)h * nsb * 64);
-        U.hdr[qi] = ld_stream16(g + (int64_t)nsb * 512);
     }
 }
 
@@ -381,7 +383,7 @@ __global__ __launch_bounds__(256 * KC) void k_gemv1_q4k_bf16_ks(const uint8_t* W
 // every weight byte has landed, and each row's math starts as its data
 // arrives.  W and x are not __restrict__ so that the compiler barrier keeps
 // that order.
-template <bool GU, bool AFF, typename YT>
+template <bool GU, bool AFF, bool FULL, typename YT>
 __global__ __launch_bounds__(256) void k_gemv1_q4k_bf16_1s(const uint8_t* W, const bf16_t* x, YT* __restrict__ y,
                                                           int64_t nout, int K, int64_t up_off, int64_t nquads) {
     extern __shared__ uint4 lds[];  // x (K bf16)
@@ -401,11 +403,11 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_bf16_1s(const uint8_t* W, con
     if (c1 < nx) lds[c1] = xv1;
     __syncthreads();
     if (gq >= nquads) return;
-    // lanes past K (K < 4096) read a valid superblock and mask it to zero:
-    // branch-free, so the LDS reads issue right after the barrier
+    // K = 4096 (FULL): every lane has a superblock; otherwise lanes past K
+    // read a valid one and mask it to zero (branch-free either way)
     const int s = lane >> 2;
-    const uint32_t live = s < nsb ? 0xFFFFFFFFu : 0u;
-    const uint4* xp = lds + (s < nsb ? s : 0) * 32 + 8 * (lane & 3);
+    const uint32_t live = (FULL || s < nsb) ? 0xFFFFFFFFu : 0u;
+    const uint4* xp = lds + ((FULL || s < nsb) ? s : 0) * 32 + 8 * (lane & 3);
     uint32_t xlo[16], xhi[16];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -660,8 +662,12 @@ static void launch_q4k_bf16_t(const uint8_t* W, const bf16_t* x, YT* y, int64_t 
     if (waves > nquads) waves = nquads;
     const size_t lds = (size_t)K * 2;
     if (K <= 4096 && env_int("THQ_GEMV_ONESHOT", 1)) {
-        hipLaunchKernelGGL((k_gemv1_q4k_bf16_1s<GU, AFF, YT>), dim3((unsigned)((nquads + 3) / 4)), dim3(256), lds, s, W, x,
-                           y, nout, K, up_off, nquads);
+        if (K == 4096)
+            hipLaunchKernelGGL((k_gemv1_q4k_bf16_1s<GU, AFF, true, YT>), dim3((unsigned)((nquads + 3) / 4)), dim3(256),
+                               lds, s, W, x, y, nout, K, up_off, nquads);
+        else
+            hipLaunchKernelGGL((k_gemv1_q4k_bf16_1s<GU, AFF, false, YT>), dim3((unsigned)((nquads + 3) / 4)), dim3(256),
+                               lds, s, W, x, y, nout, K, up_off, nquads);
         return;
     }
     if (K <= 4 * 4096 && env_int("THQ_GEMV_ONESHOT", 1)) {
