@@ -303,31 +303,41 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_bf16(const uint8_t* __restric
     }
 }
 
-// K-split one-shot variant for 4096 < K <= KC * 4096: a block holds 4 row
+// K-split one-shot variant for 4096 < K <= KC * 4096: a block holds QPB row
 // quads x KC waves, wave (quad, chunk) loads its 4096-wide chunk of the quad
 // at entry (after the block's x loads, as in the one-shot kernel) and the
 // chunks' row totals are summed in LDS in chunk order before the epilogue.
-template <int KC, bool GU, bool AFF, typename YT>
-__global__ __launch_bounds__(256 * KC) void k_gemv1_q4k_bf16_ks(const uint8_t* W, const bf16_t* x,
-                                                               YT* __restrict__ y, int64_t nout, int K,
-                                                               int64_t up_off, int64_t nquads) {
+// x is staged with 8 / QPB 16-B chunks per thread (K / 8 <= 512 * KC).
+template <int KC, int QPB, bool GU, bool AFF, typename YT>
+__global__ __launch_bounds__(64 * QPB * KC) void k_gemv1_q4k_bf16_ks(const uint8_t* W, const bf16_t* x,
+                                                                    YT* __restrict__ y, int64_t nout, int K,
+                                                                    int64_t up_off, int64_t nquads) {
+    static_assert(QPB == 2 || QPB == 4, "x staging uses two or four chunks per thread");
     extern __shared__ uint4 lds[];  // x (K bf16)
-    __shared__ float red[4][KC][8];
+    __shared__ float red[QPB][KC][8];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int c = wv % KC, qb = wv / KC;
-    const int64_t gq = (int64_t)blockIdx.x * 4 + qb;
+    const int64_t gq = (int64_t)blockIdx.x * QPB + qb;
     const int nsb = K >> 8;
-    // x: two 16-B chunks per thread (K / 8 <= 512 * KC = 2 * blockDim)
-    const int nx = K >> 3, nt = 256 * KC;
-    const int x0 = threadIdx.x, x1 = threadIdx.x + nt;
+    const int nx = K >> 3, nt = 64 * QPB * KC;
+    const int x0 = threadIdx.x, x1 = x0 + nt, x2 = x1 + nt, x3 = x2 + nt;
     const uint4 xv0 = reinterpret_cast<const uint4*>(x)[x0 < nx ? x0 : nx - 1];
     const uint4 xv1 = reinterpret_cast<const uint4*>(x)[x1 < nx ? x1 : nx - 1];
+    uint4 xv2 = xv1, xv3 = xv1;
+    if constexpr (QPB == 2) {
+        xv2 = reinterpret_cast<const uint4*>(x)[x2 < nx ? x2 : nx - 1];
+        xv3 = reinterpret_cast<const uint4*>(x)[x3 < nx ? x3 : nx - 1];
+    }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     Q4Unit<GU> A;
     q4k_unit_load<GU>(A, W, gq < nquads ? gq : nquads - 1, c, up_off, nsb, lane);
     if (x0 < nx) lds[x0] = xv0;
     if (x1 < nx) lds[x1] = xv1;
+    if constexpr (QPB == 2) {
+        if (x2 < nx) lds[x2] = xv2;
+        if (x3 < nx) lds[x3] = xv3;
+    }
     __syncthreads();
     const int s = 16 * c + (lane >> 2);
     uint32_t xlo[16], xhi[16];
@@ -362,7 +372,7 @@ __global__ __launch_bounds__(256 * KC) void k_gemv1_q4k_bf16_ks(const uint8_t* W
         if (!(lane & 15)) red[qb][c][slot_of_lane<4>(lane)] = tot;
     }
     __syncthreads();
-    if (threadIdx.x < 16) {
+    if (threadIdx.x < 4 * QPB) {
         const int q2 = threadIdx.x >> 2, r = threadIdx.x & 3;
         float g = 0.0f, u = 0.0f;
 #pragma unroll
@@ -370,7 +380,7 @@ __global__ __launch_bounds__(256 * KC) void k_gemv1_q4k_bf16_ks(const uint8_t* W
             g += red[q2][cc][r];
             if (GU) u += red[q2][cc][r + 4];
         }
-        const int64_t o = 4 * ((int64_t)blockIdx.x * 4 + q2) + r;
+        const int64_t o = 4 * ((int64_t)blockIdx.x * QPB + q2) + r;
         if (o < nout) store_y<YT>(y + o, GU ? silu_mul(g, u) : g);
     }
 }
@@ -671,12 +681,19 @@ static void launch_q4k_bf16_t(const uint8_t* W, const bf16_t* x, YT* y, int64_t 
         return;
     }
     if (K <= 4 * 4096 && env_int("THQ_GEMV_ONESHOT", 1)) {
-        const dim3 grid((unsigned)((nquads + 3) / 4));
-        switch ((K + 4095) / 4096) {
-            case 2: hipLaunchKernelGGL((k_gemv1_q4k_bf16_ks<2, GU, AFF, YT>), grid, dim3(512), lds, s, W, x, y, nout, K, up_off, nquads); return;
-            case 3: hipLaunchKernelGGL((k_gemv1_q4k_bf16_ks<3, GU, AFF, YT>), grid, dim3(768), lds, s, W, x, y, nout, K, up_off, nquads); return;
-            default: hipLaunchKernelGGL((k_gemv1_q4k_bf16_ks<4, GU, AFF, YT>), grid, dim3(1024), lds, s, W, x, y, nout, K, up_off, nquads); return;
+        // 2 quads per block (twice the blocks of 4) measured 8.4 -> 8.25 us at K = 12288
+        static const int qpb = env_int("THQ_GEMV_QPB", 2) == 4 ? 4 : 2;
+        const dim3 grid((unsigned)((nquads + qpb - 1) / qpb));
+#define THQ_KS(KC_, QPB_) \
+    hipLaunchKernelGGL((k_gemv1_q4k_bf16_ks<KC_, QPB_, GU, AFF, YT>), grid, dim3(64 * QPB_ * KC_), lds, s, W, x, y, nout, K, up_off, nquads)
+        const int kc = (K + 4095) / 4096;
+        if (qpb == 2) {
+            if (kc == 2) THQ_KS(2, 2); else if (kc == 3) THQ_KS(3, 2); else THQ_KS(4, 2);
+        } else {
+            if (kc == 2) THQ_KS(2, 4); else if (kc == 3) THQ_KS(3, 4); else THQ_KS(4, 4);
         }
+#undef THQ_KS
+        return;
     }
     const unsigned grid = (unsigned)((waves + 3) / 4);
     switch ((K / 256 + 15) / 16) {
