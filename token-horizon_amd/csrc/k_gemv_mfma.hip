@@ -48,11 +48,6 @@ namespace {
 __device__ __forceinline__ f32x16_t mfma32x16(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
-__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
-    bf16x8_t r;
-    __builtin_memcpy(&r, &v, 16);
-    return r;
-}
 // low nibbles of the bytes of a, b (already masked to 4 bits) -> bf16(128 + q) x 8
 __device__ __forceinline__ bf16x8_t nib_bf16x8(uint32_t a, uint32_t b) {
     const uint32_t C = 0x43434343u;

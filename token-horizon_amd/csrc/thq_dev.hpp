@@ -51,6 +51,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 __device__ __forceinline__ float bf16_round(float f) { return bf16_to_f32(f32_to_bf16(f)); }
 
+// 16 bytes as an MFMA operand of eight bf16
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
+    bf16x8_t r;
+    __builtin_memcpy(&r, &v, 16);
+    return r;
+}
+
 // GGML get_scale_min_k4 on the 12 scale bytes held as three dwords
 // s0 = scales[0..3], s1 = scales[4..7], s2 = scales[8..11].
 __host__ __device__ __forceinline__ void scale_min_k4(int j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t& sc,
