@@ -16,8 +16,9 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 Q8_0 = 8
 Q4_K = 12
-BLOCK = {Q8_0: 32, Q4_K: 256}
-BLOCK_BYTES = {Q8_0: 34, Q4_K: 144}
+Q6_K = 14
+BLOCK = {Q8_0: 32, Q4_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q6_K: 210}
 Q8_K_BYTES = 292
 
 MODE_DEQUANT_F32 = 0
@@ -44,7 +45,7 @@ def lib():
         L.o_row_bytes.argtypes = [C.c_int, i64]
         L.o_row_bytes.restype = C.c_size_t
         for name in ("o_quantize_q8_0", "o_dequantize_q8_0", "o_quantize_q4_k", "o_dequantize_q4_k",
-                     "o_quantize_q8_k"):
+                     "o_quantize_q8_k", "o_dequantize_q6_k"):
             getattr(L, name).argtypes = [P, P, i64]
         L.o_get_scale_min_k4.argtypes = [C.c_int, P, P, P]
         L.o_make_qkx1_quants.argtypes = [C.c_int, C.c_int, P, C.c_int, P, P]

@@ -111,6 +111,7 @@ void o_randn(uint64_t seed, uint64_t stream, float sigma, float* out, size_t n) 
 size_t o_row_bytes(int type, int64_t k) {
     if (type == O_TYPE_Q8_0) return (size_t)(k / OQK8_0) * O_Q8_0_BYTES;
     if (type == O_TYPE_Q4_K) return (size_t)(k / OQK_K) * O_Q4_K_BYTES;
+    if (type == O_TYPE_Q6_K) return (size_t)(k / OQK_K) * O_Q6_K_BYTES;
     return 0;
 }
 
@@ -161,6 +162,39 @@ void o_dequantize_q8_0(const uint8_t* blocks, float* y, int64_t k) {
         const uint8_t* blk = blocks + b * O_Q8_0_BYTES;
         float d = o_f16_to_f32(rd16(blk));
         for (int i = 0; i < OQK8_0; ++i) y[b * OQK8_0 + i] = (float)(int8_t)blk[2 + i] * d;
+    }
+}
+
+/* [ext] BlockQ6K::to_float (GGML's dequantize_row_q6_K): per 128-element
+ * half n of a superblock (ql += 64n, qh += 32n, sc += 8n) and l = 0..31,
+ * is = l / 16:
+ *   y[l]      = d * sc[is]     * ((ql[l]      & 0xF) | ((qh[l] >> 0) & 3) << 4) - 32)
+ *   y[l + 32] = d * sc[is + 2] * ((ql[l + 32] & 0xF) | ((qh[l] >> 2) & 3) << 4) - 32)
+ *   y[l + 64] = d * sc[is + 4] * ((ql[l]      >> 4) | ((qh[l] >> 4) & 3) << 4) - 32)
+ *   y[l + 96] = d * sc[is + 6] * ((ql[l + 32] >> 4) | ((qh[l] >> 6) & 3) << 4) - 32)
+ * with the products evaluated left to right in f32 (d * sc first). */
+void o_dequantize_q6_k(const uint8_t* blocks, float* y, int64_t k) {
+    for (int64_t b = 0; b < k / OQK_K; ++b) {
+        const uint8_t* blk = blocks + b * O_Q6_K_BYTES;
+        const float d = o_f16_to_f32(rd16(blk + 208));
+        float* yb = y + b * OQK_K;
+        for (int n = 0; n < 2; ++n) {
+            const uint8_t* ql = blk + 64 * n;
+            const uint8_t* qh = blk + 128 + 32 * n;
+            const int8_t* sc = (const int8_t*)(blk + 192 + 8 * n);
+            float* yy = yb + 128 * n;
+            for (int l = 0; l < 32; ++l) {
+                const int is = l / 16;
+                const int q1 = (int)((ql[l] & 0xF) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                const int q2 = (int)((ql[l + 32] & 0xF) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                const int q3 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                const int q4 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                yy[l] = d * (float)sc[is] * (float)q1;
+                yy[l + 32] = d * (float)sc[is + 2] * (float)q2;
+                yy[l + 64] = d * (float)sc[is + 4] * (float)q3;
+                yy[l + 96] = d * (float)sc[is + 6] * (float)q4;
+            }
+        }
     }
 }
 
@@ -400,11 +434,18 @@ float o_vec_dot_q4_k_q8_k(int64_t k, const uint8_t* w, const uint8_t* x) {
 /* whole-matrix helpers                                                 */
 /* ------------------------------------------------------------------ */
 
-static int block_of(int type) { return type == O_TYPE_Q8_0 ? OQK8_0 : type == O_TYPE_Q4_K ? OQK_K : 0; }
+static int block_of(int type) {
+    return type == O_TYPE_Q8_0 ? OQK8_0 : (type == O_TYPE_Q4_K || type == O_TYPE_Q6_K) ? OQK_K : 0;
+}
+static void dequant_row(int type, const uint8_t* b, float* y, int64_t k) {
+    if (type == O_TYPE_Q8_0) o_dequantize_q8_0(b, y, k);
+    else if (type == O_TYPE_Q4_K) o_dequantize_q4_k(b, y, k);
+    else o_dequantize_q6_k(b, y, k);
+}
 
 int o_quantize(int type, const float* w, int64_t n, int64_t k, uint8_t* out) {
     int bs = block_of(type);
-    if (!bs || k % bs) return -1;
+    if (!bs || k % bs || type == O_TYPE_Q6_K) return -1;  /* no Q6_K quantizer: files carry Q6_K */
     size_t rb = o_row_bytes(type, k);
 #pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < n; ++r) {
@@ -420,8 +461,7 @@ int o_dequantize(int type, const uint8_t* blocks, int64_t n, int64_t k, float* o
     size_t rb = o_row_bytes(type, k);
 #pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < n; ++r) {
-        if (type == O_TYPE_Q8_0) o_dequantize_q8_0(blocks + r * rb, out + r * k, k);
-        else o_dequantize_q4_k(blocks + r * rb, out + r * k, k);
+        dequant_row(type, blocks + r * rb, out + r * k, k);
     }
     return 0;
 }
@@ -446,8 +486,7 @@ int o_matmul(int type, int mode, const uint8_t* w, int64_t n, int64_t k, const f
             float* wrow = (float*)malloc(sizeof(float) * (size_t)k);
 #pragma omp for schedule(static)
             for (int64_t c = 0; c < n; ++c) {
-                if (type == O_TYPE_Q8_0) o_dequantize_q8_0(w + c * rb, wrow, k);
-                else o_dequantize_q4_k(w + c * rb, wrow, k);
+                dequant_row(type, w + c * rb, wrow, k);
                 for (int64_t r = 0; r < m; ++r) {
                     const float* xr = x + r * k;
                     double acc = 0.0;
@@ -459,7 +498,7 @@ int o_matmul(int type, int mode, const uint8_t* w, int64_t n, int64_t k, const f
         }
         return 0;
     }
-    if (mode != 1) return -1;
+    if (mode != 1 || type == O_TYPE_Q6_K) return -1;  /* Q8ACT is restated for Q8_0 / Q4_K */
     size_t xrb = type == O_TYPE_Q8_0 ? (size_t)(k / OQK8_0) * O_Q8_0_BYTES : (size_t)(k / OQK_K) * O_Q8_K_BYTES;
     uint8_t* xq = (uint8_t*)malloc(xrb * (size_t)(m > 0 ? m : 1));
     for (int64_t r = 0; r < m; ++r) {

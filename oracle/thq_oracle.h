@@ -29,6 +29,9 @@
  *   matmul DEQUANT_F32          brute force f64 on tiny shapes
  *   argmax                      the reference's own tie vectors
  *   gate/up SiLU epilogue       the reference test's closed form
+ *   Q6_K dequant                hand-built blocks with literal expected floats,
+ *                               every 6-bit code and every scale byte, and an
+ *                               independent numpy formula on random bytes
  *   MLX affine dequant          an independent numpy formula with correct
  *                               rounding (equal wherever half's truncation of
  *                               the low f64 bits cannot matter); the half
@@ -52,10 +55,12 @@ extern "C" {
 #define O_Q8_0_BYTES 34  /* f16 d + 32 x i8 */
 #define O_Q4_K_BYTES 144 /* f16 d + f16 dmin + 12 B scales + 128 B nibbles */
 #define O_Q8_K_BYTES 292 /* f32 d + 256 x i8 + 16 x i16 bsums */
+#define O_Q6_K_BYTES 210 /* u8 ql[128] + u8 qh[64] + i8 scales[16] + f16 d */
 
 /* GGML type ids (the values GGUF files carry) */
 #define O_TYPE_Q8_0 8
 #define O_TYPE_Q4_K 12
+#define O_TYPE_Q6_K 14
 
 /* ---- scalar conversions ---- */
 float o_f16_to_f32(uint16_t h);
@@ -74,6 +79,7 @@ void o_dequantize_q8_0(const uint8_t* blocks, float* y, int64_t k);
 void o_quantize_q4_k(const float* x, uint8_t* blocks, int64_t k);
 void o_dequantize_q4_k(const uint8_t* blocks, float* y, int64_t k);
 void o_quantize_q8_k(const float* x, uint8_t* blocks, int64_t k);
+void o_dequantize_q6_k(const uint8_t* blocks, float* y, int64_t k);
 void o_get_scale_min_k4(int j, const uint8_t* scales, uint8_t* sc, uint8_t* m);
 void o_make_qkx1_quants(int nmax, int ntry, const float* x, int n, float* scale, float* min_out);
 

@@ -333,3 +333,86 @@ def test_argmax_reference_tie_vectors():
     assert O.argmax_rows(np.array([np.nan, 1.0, 1.0], np.float32))[0] == 1
     assert O.argmax_rows(np.full(4, -np.inf, np.float32))[0] == 0
     assert O.lib().o_argmax(None, 0) == 0
+
+
+# ------------------------------------------------------------------ Q6_K
+def _q6k_numpy(blocks: np.ndarray, k: int) -> np.ndarray:
+    """Independent vectorized Q6_K decode: per 128-half, the four 32-element
+    quarters take (ql low, qh bits 0-1), (ql+32 low, qh bits 2-3), (ql high,
+    qh bits 4-5), (ql+32 high, qh bits 6-7); scales in groups of 16."""
+    nb = k // 256
+    b = blocks.reshape(-1, nb, 210)
+    ql = b[..., :128].reshape(-1, nb, 2, 64).astype(np.int32)
+    qh = b[..., 128:192].reshape(-1, nb, 2, 32).astype(np.int32)
+    sc = b[..., 192:208].view(np.int8).reshape(-1, nb, 2, 8).astype(np.float32)
+    d = b[..., 208:210].copy().view(np.float16).astype(np.float32)[..., 0]
+    quarters = [
+        (ql[..., :32] & 0xF) | ((qh & 3) << 4),
+        (ql[..., 32:] & 0xF) | (((qh >> 2) & 3) << 4),
+        (ql[..., :32] >> 4) | (((qh >> 4) & 3) << 4),
+        (ql[..., 32:] >> 4) | (((qh >> 6) & 3) << 4),
+    ]
+    q = np.stack(quarters, axis=-2) - 32                       # [.., nb, 2, 4, 32]
+    s = sc.reshape(*sc.shape[:-1], 4, 2).repeat(16, axis=-1)    # [.., nb, 2, 4, 32]
+    y = (d[..., None, None, None] * s) * q.astype(np.float32)   # (d * sc) * q in f32
+    return y.reshape(-1, k).astype(np.float32)
+
+
+def test_q6k_literal_bytes():
+    """Byte-level known answers: d = 1, scales 1..16; one code per quarter."""
+    blk = np.zeros(210, np.uint8)
+    blk[192:208] = np.arange(1, 17, dtype=np.int8).view(np.uint8)
+    blk[208:210] = np.array([1.0], np.float16).view(np.uint8)
+    blk[:128] = 0x00
+    blk[128:192] = 0x00
+    # element 0: ql[0] low = 0xF, qh[0] bits 0-1 = 3 -> code 63 -> (63 - 32) * sc[0] = 31
+    blk[0] = 0x0F
+    blk[128 + 0] = 0x03
+    # element 64 + 17: ql[17] high nibble = 8, qh[17] bits 4-5 = 2 -> code 40 -> 8 * sc[5] = 48
+    blk[17] = 0x80
+    blk[128 + 17] = 0x20
+    # element 32 + 20: ql[52] low nibble = 1, qh[20] bits 2-3 = 0 -> code 1 -> -31 * sc[3] = -124
+    blk[52] = 0x01
+    # element 128 + 96 + 31 (second half): ql[64 + 63] high = 2, qh[32 + 31] bits 6-7 = 1 -> code 18
+    #   -> -14 * sc[8 + 7] = -14 * 16 = -224
+    blk[64 + 63] = 0x20
+    blk[128 + 32 + 31] = 0x40
+    y = O.dequantize(O.Q6_K, blk.reshape(1, -1), 1, 256)[0]
+    assert y[0] == 31.0
+    assert y[64 + 17] == 48.0
+    assert y[32 + 20] == -124.0
+    assert y[128 + 96 + 31] == -224.0
+    # every other element has code 0 -> -32 * its group scale
+    assert y[1] == -32.0 and y[16] == -64.0 and y[128] == -32.0 * 9
+
+
+def test_q6k_every_code_and_random_bytes():
+    rng = np.random.default_rng(14)
+    n, k = 16, 1024
+    raw = rng.integers(0, 256, (n, k // 256, 210), dtype=np.uint8)
+    d = (rng.standard_normal((n, k // 256)) * 0.01).astype(np.float16)
+    raw[:, :, 208:210] = d.view(np.uint8).reshape(n, k // 256, 2)
+    # first block: ql / qh so that element e of quarter 0 has code e (0..31) and
+    # quarter 1 has code 32 + e: together with the random rest every code appears
+    raw[0, 0, :32] = np.arange(32) & 0xF
+    raw[0, 0, 128:160] = (np.arange(32) >> 4) | (((32 + np.arange(32)) >> 4) << 2)
+    raw[0, 0, 32:64] = (32 + np.arange(32)) & 0xF
+    raw = raw.reshape(n, -1)
+    got = O.dequantize(O.Q6_K, raw, n, k)
+    want = _q6k_numpy(raw, k)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    dd = float(d[0, 0])
+    sc0 = raw[0, 192].astype(np.int8)
+    assert got[0, 5] == np.float32(np.float32(dd) * np.float32(sc0)) * np.float32(5 - 32)
+
+
+def test_q6k_matmul_dequant_mode_brute_force():
+    rng = np.random.default_rng(3)
+    n, k = 5, 512
+    raw = rng.integers(0, 256, (n, k // 256, 210), dtype=np.uint8)
+    raw[:, :, 208:210] = (rng.standard_normal((n, k // 256)) * 0.01).astype(np.float16).view(np.uint8).reshape(n, k // 256, 2)
+    raw = raw.reshape(n, -1)
+    x = O.randn(1, 2, 1.0, (3, k))
+    y = O.matmul(O.Q6_K, raw, n, k, x)
+    ref = x.astype(np.float64) @ _q6k_numpy(raw, k).astype(np.float64).T
+    assert np.allclose(y, ref, rtol=1e-6, atol=1e-6)
