@@ -39,6 +39,11 @@ extern "C" {
 typedef enum thq_dtype {
     THQ_Q8_0 = 8,  /* 32 weights / 34 B: f16 d, i8 qs[32]                        */
     THQ_Q4_K = 12, /* 256 weights / 144 B: f16 d, f16 dmin, u8 scales[12], u8 qs[128] */
+    THQ_Q6_K = 14, /* 256 weights / 210 B: u8 ql[128], u8 qh[64], i8 scales[16], f16 d;
+                      w = d * scale[j/16] * (6-bit code - 32) ([ext] candle-core 0.11
+                      BlockQ6K::to_float); the type a Q4_K_M file keeps its output
+                      head and part of ffn_down / attn_v in (read by the loader at
+                      engine/src/model.rs:526-562)                               */
     THQ_Q8_K = 15, /* 256 activations / 292 B: f32 d, i8 qs[256], i16 bsums[16]
                       (dot type of Q4_K; thq_quantize_act only)                   */
     THQ_MLX_Q4 = 100 /* MLX affine 4-bit, the engine's own QLin format (not a GGML id):
@@ -96,7 +101,8 @@ const char* thq_version(void);
 int thq_weight_upload(thq_ctx* ctx, thq_dtype dtype, const void* host_blocks, int64_t n, int64_t k,
                       thq_weight** out);
 
-/* As thq_weight_upload, from GGUF block bytes already in device memory. */
+/* As thq_weight_upload, from GGUF block bytes already in device memory
+ * (16-byte aligned for Q4_K, 2-byte aligned for Q8_0 and Q6_K). */
 int thq_weight_from_device(thq_ctx* ctx, thq_dtype dtype, const void* dev_blocks, int64_t n, int64_t k,
                            void* stream, thq_weight** out);
 

@@ -50,6 +50,21 @@ def weight_bytes(qtype: int, n: int, k: int, seed: int = 0, sigma: float = 0.02)
     return _cache[key]
 
 
+def q6k_bytes(n: int, k: int, seed: int = 0, dscale: float = 2e-4) -> np.ndarray:
+    """Random Q6_K GGUF bytes [n, k/256 * 210]: every ql / qh / scale byte
+    uniform (all 6-bit codes, scales -128..127), d = f16 of N(0, dscale)
+    (both signs, a few f16 subnormals near zero).  There is no Q6_K quantizer
+    in the library or the oracle: GGUF files bring Q6_K tensors ready-made."""
+    key = ("q6k", n, k, seed, dscale)
+    if key not in _cache:
+        rng = np.random.default_rng(seed + 977 * n + k)
+        raw = rng.integers(0, 256, (n, k // 256, 210), dtype=np.uint8)
+        d = (rng.standard_normal((n, k // 256)) * dscale).astype(np.float16)
+        raw[:, :, 208:210] = d.view(np.uint8).reshape(n, k // 256, 2)
+        _cache[key] = raw.reshape(n, -1)
+    return _cache[key]
+
+
 def activations(m: int, k: int, seed: int = 0) -> np.ndarray:
     """X ~ N(0, 1) [m, k] f32 from the oracle generator (stream 2)."""
     return O.randn(seed, 2_000_000 + 13 * m + k, 1.0, (m, k))

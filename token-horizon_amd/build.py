@@ -25,7 +25,10 @@ BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libthq.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
-SOURCES = ["thq_api.cpp", "k_weights.hip", "k_gemv.hip", "k_gemv_mfma.hip", "k_gemm.hip", "k_argmax.hip", "k_q8act.hip"]
+SOURCES = [
+    "thq_api.cpp", "k_weights.hip", "k_gemv.hip", "k_gemv_mfma.hip", "k_gemm.hip", "k_argmax.hip", "k_q8act.hip",
+    "k_q6k.hip",
+]
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -13,89 +13,9 @@
 // 64p+32+i (high nibble, sub-block 2p+1).
 #include "thq_dev.hpp"
 #include "thq_kernels.hpp"
+#include "thq_wave.hpp"
 
 namespace thq {
-
-// ------------------------------------------------------------------ helpers
-__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
-    bf16x2_t av, bv;
-    __builtin_memcpy(&av, &a, 4);
-    __builtin_memcpy(&bv, &b, 4);
-    return __builtin_amdgcn_fdot2_f32_bf16(av, bv, c, false);
-}
-
-// row index of slot r for a wave that starts at row0; in gate/up mode the
-// wave owns outputs i0 .. i0+R/2-1 and its slots alternate gate/up rows
-template <int R, bool GU>
-__device__ __forceinline__ int64_t slot_row(int64_t base, int r, int64_t up_off) {
-    if (GU) return base + (r >> 1) + ((r & 1) ? up_off : 0);
-    return base + r;
-}
-
-template <int R, bool GU, typename YT>
-__device__ __forceinline__ void write_rows(YT* __restrict__ y, int64_t base, int64_t nout, const float* acc) {
-    if (threadIdx.x % 64 != 0) return;
-    if (GU) {
-#pragma unroll
-        for (int p = 0; p < R / 2; ++p)
-            if (base + p < nout) store_y<YT>(y + base + p, silu_mul(acc[2 * p], acc[2 * p + 1]));
-    } else {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-            if (base + r < nout) store_y<YT>(y + base + r, acc[r]);
-    }
-}
-
-// ------------------------------------------------------------------ wave helpers
-// value of lane P of each quad, in every lane of the quad (DPP quad_perm)
-template <int P>
-__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, P | (P << 2) | (P << 4) | (P << 6), 0xF, 0xF, false);
-}
-
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-
-// sum over the 16 lanes of each DPP row; every lane of the row gets it
-__device__ __forceinline__ float row16_sum(float v) {
-    v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
-    v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
-    v += dpp_f<0x141>(v);  // row_half_mirror
-    v += dpp_f<0x140>(v);  // row_mirror
-    return v;
-}
-
-// Transposed reduction of R per-lane partials over the 64 lanes: each step
-// halves the values a lane carries, so R rows cost about as much as one.
-// Afterwards every lane holds the total of slot slot_of_lane<R>(lane): R=1
-// slot 0 everywhere; R=2 slot lane/32; R=4 slot 2*(lane/32) + (lane/16)%2.
-template <int R>
-__device__ __forceinline__ float reduce_slots(const float (&v)[R], int lane) {
-    const bool up = lane & 32, b4 = lane & 16;
-    float k;
-    if constexpr (R == 4) {
-        const float s0 = up ? v[0] : v[2], s1 = up ? v[1] : v[3];
-        const float k0 = (up ? v[2] : v[0]) + __shfl_xor(s0, 32, 64);
-        const float k1 = (up ? v[3] : v[1]) + __shfl_xor(s1, 32, 64);
-        k = (b4 ? k1 : k0) + __shfl_xor(b4 ? k0 : k1, 16, 64);
-    } else if constexpr (R == 2) {
-        k = (up ? v[1] : v[0]) + __shfl_xor(up ? v[0] : v[1], 32, 64);
-        k += __shfl_xor(k, 16, 64);
-    } else {
-        k = v[0] + __shfl_xor(v[0], 32, 64);
-        k += __shfl_xor(k, 16, 64);
-    }
-    return row16_sum(k);
-}
-
-template <int R>
-__device__ __forceinline__ int slot_of_lane(int lane) {
-    if constexpr (R == 4) return 2 * (lane >> 5) + ((lane >> 4) & 1);
-    if constexpr (R == 2) return lane >> 5;
-    return 0;
-}
 
 // ------------------------------------------------------------------ Q4_K M=1, bf16 x
 // Persistent: a fixed grid of waves walks "units" = (row quad, 4096-wide K
@@ -587,7 +507,8 @@ __global__ __launch_bounds__(256) void k_gemv1_q8(const int8_t* __restrict__ Q, 
 template <int QT, bool GU, typename XT, typename YT>
 __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Wa,
                                                      const XT* __restrict__ x, YT* __restrict__ y, int M,
-                                                     int64_t nout, int K, int64_t up_off, int64_t ldy) {
+                                                     int64_t nout, int K, int64_t up_off, int64_t ldy,
+                                                     int64_t nrows) {
     const int lane = threadIdx.x & 63;
     const int64_t o = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     if (o >= nout) return;
@@ -603,7 +524,22 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict_
         for (int r = 0; r < NR; ++r) {
             const int64_t row = o + (r ? up_off : 0);
             float wv[32];
-            if (QT != 8) {
+            if (QT == 14) {
+                // Q6_K planes: sub-block sbi = 8s + 4h + Q holds w[256s + 128h + 32Q + l]
+                const Q6Layout L = q6k_layout(nrows, K);
+                const int s = sbi >> 3, h = (sbi >> 2) & 1, Q = sbi & 3;
+                const uint8_t* ql = Wq + row * (K / 2) + s * 128 + h * 64 + (Q & 1) * 32;
+                const uint8_t* qh = Wq + L.qh + row * (K / 4) + s * 64 + h * 32;
+                const int8_t* sc = reinterpret_cast<const int8_t*>(Wq + L.sc + row * (K / 16) + s * 16 + h * 8 + 2 * Q);
+                const float d = f16_to_f32(reinterpret_cast<const uint16_t*>(Wq + L.d)[row * (K / 256) + s]);
+                const float ds0 = d * (float)sc[0], ds1 = d * (float)sc[1];
+                const int nsh = (Q >> 1) * 4, hsh = 2 * Q;
+#pragma unroll
+                for (int i = 0; i < 32; ++i) {
+                    const int code = ((ql[i] >> nsh) & 0xF) | (((qh[i] >> hsh) & 3) << 4);
+                    wv[i] = (i < 16 ? ds0 : ds1) * (float)(code - 32);  // (d * sc) * q, candle's order
+                }
+            } else if (QT != 8) {
                 // affine weights may pad K to whole superblocks: address with the padded count
                 const int nsb = (K + 255) >> 8, s = sbi >> 3, j = sbi & 7;
                 uint4 h;
@@ -756,6 +692,7 @@ static hipError_t gemv1_q8_t(const int8_t* Q, const uint16_t* D, const XT* x, YT
 }
 
 bool gemv1_supported(int qtype, int K, bool gu, int64_t n_rows) {
+    if (qtype == 14) return K % 256 == 0 && K <= 4 * 4096;
     if (qtype != 8) return K % 256 == 0 && K <= 4 * 4096 && (!gu || (n_rows / 2) % 4 == 0);
     return K % 32 == 0 && K <= 8 * 1024;
 }
@@ -763,6 +700,10 @@ bool gemv1_supported(int qtype, int K, bool gu, int64_t n_rows) {
 hipError_t launch_gemv1(const WeightView& w, const void* x, bool xf32, void* y, bool yf32, bool gu, int64_t nout,
                         int64_t up_off, hipStream_t s) {
     const int K = (int)w.K;
+    if (w.qtype == 14) {
+        if (xf32) return launch_generic(w, x, xf32, y, yf32, gu, 1, nout, up_off, s);
+        return launch_gemv1_q6k(w, x, y, yf32, gu, nout, up_off, s);
+    }
     if (w.qtype == 12) {
         if (gu) {
             return yf32 ? gemv1_q4k_t<true, false, float>(w.q, x, xf32, (float*)y, nout, K, up_off, s)
@@ -797,7 +738,7 @@ static hipError_t generic_t(const WeightView& w, const XT* x, YT* y, int M, int6
     for (int m0 = 0; m0 < M; m0 += 8) {
         const int mm = M - m0 < 8 ? M - m0 : 8;
         hipLaunchKernelGGL((k_gemv_generic<QT, GU, XT, YT>), dim3((unsigned)((nout + 3) / 4)), dim3(256), 0, s, w.q,
-                           w.aux, x + (int64_t)m0 * w.K, y + (int64_t)m0 * ldy, mm, nout, (int)w.K, up_off, ldy);
+                           w.aux, x + (int64_t)m0 * w.K, y + (int64_t)m0 * ldy, mm, nout, (int)w.K, up_off, ldy, w.N);
     }
     return hipGetLastError();
 }
@@ -811,6 +752,7 @@ hipError_t launch_generic(const WeightView& w, const void* x, bool xf32, void* y
           : (yf32 ? THQ_G(QT_, GU_, bf16_t, float) : THQ_G(QT_, GU_, bf16_t, bf16_t)))
     if (w.qtype == 12) return gu ? THQ_G2(12, true) : THQ_G2(12, false);
     if (w.qtype == 13) return gu ? THQ_G2(13, true) : THQ_G2(13, false);
+    if (w.qtype == 14) return gu ? THQ_G2(14, true) : THQ_G2(14, false);
     return gu ? THQ_G2(8, true) : THQ_G2(8, false);
 #undef THQ_G2
 #undef THQ_G

@@ -278,6 +278,65 @@ __global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__
     }
 }
 
+// ---------------------------------------------------------------- Q6_K
+// GGUF 210-B blocks (2-B aligned) -> planes; one thread per superblock
+__global__ __launch_bounds__(256) void k_repack_q6k(const uint8_t* __restrict__ gguf, uint8_t* __restrict__ dst,
+                                                    int64_t n, int nsb) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= n * nsb) return;
+    const int64_t row = b / nsb;
+    const int s = (int)(b - row * nsb);
+    const int64_t K = (int64_t)nsb * 256;
+    const Q6Layout L = q6k_layout(n, K);
+    const uint16_t* src = reinterpret_cast<const uint16_t*>(gguf + b * 210);
+    uint32_t w[52];
+#pragma unroll
+    for (int i = 0; i < 52; ++i) w[i] = (uint32_t)src[2 * i] | ((uint32_t)src[2 * i + 1] << 16);
+    uint4* ql = reinterpret_cast<uint4*>(dst + row * (K / 2) + s * 128);
+    uint4* qh = reinterpret_cast<uint4*>(dst + L.qh + row * (K / 4) + s * 64);
+    uint4* sc = reinterpret_cast<uint4*>(dst + L.sc + row * (K / 16) + s * 16);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ql[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) qh[i] = make_uint4(w[32 + 4 * i], w[33 + 4 * i], w[34 + 4 * i], w[35 + 4 * i]);
+    sc[0] = make_uint4(w[48], w[49], w[50], w[51]);
+    reinterpret_cast<uint16_t*>(dst + L.d)[row * nsb + s] = src[104];
+}
+
+// one thread per (row, 128-weight half): w = (d * sc) * (code - 32), GGML order
+template <typename OT>
+__global__ __launch_bounds__(256) void k_dequant_q6k(const uint8_t* __restrict__ src, OT* __restrict__ out, int64_t n,
+                                                     int nsb) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= n * nsb * 2) return;
+    const int64_t row = t / (2 * nsb);
+    const int u = (int)(t - row * 2 * nsb);  // half index in the row
+    const int64_t K = (int64_t)nsb * 256;
+    const Q6Layout L = q6k_layout(n, K);
+    const uint8_t* ql = src + row * (K / 2) + u * 64;
+    const uint8_t* qh = src + L.qh + row * (K / 4) + u * 32;
+    const int8_t* sc = reinterpret_cast<const int8_t*>(src + L.sc + row * (K / 16) + u * 8);
+    const float d = f16_to_f32(reinterpret_cast<const uint16_t*>(src + L.d)[row * nsb + (u >> 1)]);
+    OT* y = out + row * K + u * 128;
+    for (int l = 0; l < 32; l += 4) {
+        float v[4][4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ll = l + i, is = ll / 16;
+            const int q1 = (int)((ql[ll] & 0xF) | (((qh[ll] >> 0) & 3) << 4)) - 32;
+            const int q2 = (int)((ql[ll + 32] & 0xF) | (((qh[ll] >> 2) & 3) << 4)) - 32;
+            const int q3 = (int)((ql[ll] >> 4) | (((qh[ll] >> 4) & 3) << 4)) - 32;
+            const int q4 = (int)((ql[ll + 32] >> 4) | (((qh[ll] >> 6) & 3) << 4)) - 32;
+            v[0][i] = d * (float)sc[is] * (float)q1;
+            v[1][i] = d * (float)sc[is + 2] * (float)q2;
+            v[2][i] = d * (float)sc[is + 4] * (float)q3;
+            v[3][i] = d * (float)sc[is + 6] * (float)q4;
+        }
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) put4(y + 32 * qq + l, v[qq][0], v[qq][1], v[qq][2], v[qq][3]);
+    }
+}
+
 // ---------------------------------------------------------------- MLX affine 4-bit
 // half 2.7.1 bf16::from_f64 (its f64_to_bf16, the rounding dequant_affine
 // uses, engine/src/qwen35.rs:110-134): the low 32 bits of the f64 mantissa
@@ -502,6 +561,24 @@ hipError_t launch_dequant_q4k(const uint8_t* src, void* out, bool bf16, int64_t 
     else
         hipLaunchKernelGGL(k_dequant_q4k<float>, dim3(grid_for(nsuper * 8, 256)), dim3(256), 0, s, src,
                            static_cast<float*>(out), nsuper, nsb);
+    return hipGetLastError();
+}
+
+hipError_t launch_repack_q6k(const uint8_t* gguf, uint8_t* dst, int64_t n, int nsb, hipStream_t s) {
+    if (n * nsb == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_repack_q6k, dim3(grid_for(n * nsb, 256)), dim3(256), 0, s, gguf, dst, n, nsb);
+    return hipGetLastError();
+}
+
+hipError_t launch_dequant_q6k(const uint8_t* src, void* out, bool bf16, int64_t n, int nsb, hipStream_t s) {
+    const int64_t t = n * nsb * 2;
+    if (t == 0) return hipSuccess;
+    if (bf16)
+        hipLaunchKernelGGL(k_dequant_q6k<bf16_t>, dim3(grid_for(t, 256)), dim3(256), 0, s, src, static_cast<bf16_t*>(out),
+                           n, nsb);
+    else
+        hipLaunchKernelGGL(k_dequant_q6k<float>, dim3(grid_for(t, 256)), dim3(256), 0, s, src, static_cast<float*>(out),
+                           n, nsb);
     return hipGetLastError();
 }
 

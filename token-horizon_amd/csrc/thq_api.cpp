@@ -33,7 +33,7 @@ struct thq_weight {
     int qtype = 0;           // thq_dtype
     int64_t N = 0, K = 0;
     int gs = 0;              // MLX affine group size
-    uint8_t* q = nullptr;    // Q8_0 i8 plane / Q4_K and MLX affine row-quad plane
+    uint8_t* q = nullptr;    // Q8_0 i8 plane / Q4_K and MLX affine row-quad plane / Q6_K planes
     uint8_t* aux = nullptr;  // Q8_0 f16 scale plane
 };
 
@@ -58,26 +58,34 @@ int fail(int code, const char* fmt, ...) {
     } while (0)
 
 int block_of(int qtype) {
-    return qtype == THQ_Q8_0 ? 32 : (qtype == THQ_Q4_K ? 256 : (qtype == THQ_MLX_Q4 ? 64 : 0));
+    switch (qtype) {
+        case THQ_Q8_0: return 32;
+        case THQ_Q4_K: return 256;
+        case THQ_Q6_K: return 256;
+        case THQ_MLX_Q4: return 64;
+        default: return 0;
+    }
 }
 
 // GGUF block bytes; for MLX affine weights the QLin arrays (wq + sb)
 size_t gguf_bytes(int qtype, int64_t n, int64_t k, int gs = 64) {
     if (qtype == THQ_Q8_0) return (size_t)n * (size_t)(k / 32) * 34;
     if (qtype == THQ_MLX_Q4) return (size_t)n * (size_t)k / 2 + (size_t)n * 2 * (size_t)(k / gs) * 2;
+    if (qtype == THQ_Q6_K) return (size_t)n * (size_t)(k / 256) * 210;
     return (size_t)n * (size_t)(k / 256) * 144;
 }
 
-// the kernels' type ids: 8 Q8_0, 12 Q4_K, 13 MLX affine on the Q4_K layout
+// the kernels' type ids: 8 Q8_0, 12 Q4_K, 13 MLX affine on the Q4_K layout, 14 Q6_K
 thq::WeightView view(const thq_weight* w) {
     return thq::WeightView{w->qtype == THQ_MLX_Q4 ? 13 : w->qtype, w->N, w->K, w->q, w->aux};
 }
 
 // device plane sizes: Q8_0 = i8 plane + f16 scale plane; Q4_K / MLX affine =
 // one row-quad plane (rows padded to a multiple of 4 and, for MLX affine, K
-// to whole superblocks; padding zero)
+// to whole superblocks; padding zero); Q6_K = the QL/QH/SC/D planes
 size_t q_plane_bytes(int qtype, int64_t n, int64_t k) {
     if (qtype == THQ_Q8_0) return (size_t)n * (size_t)k;
+    if (qtype == THQ_Q6_K) return thq::q6k_layout(n, k).total;
     return (size_t)((n + 3) / 4) * (size_t)((k + 255) / 256) * 576;
 }
 size_t aux_plane_bytes(int qtype, int64_t n, int64_t k) {
@@ -86,7 +94,8 @@ size_t aux_plane_bytes(int qtype, int64_t n, int64_t k) {
 
 int check_dtype_shape(int dtype, int64_t n, int64_t k) {
     const int bs = block_of(dtype);
-    if (!bs) return fail(THQ_EDTYPE, "unsupported weight dtype %d (want Q8_0=8, Q4_K=12 or MLX_Q4=100)", dtype);
+    if (!bs)
+        return fail(THQ_EDTYPE, "unsupported weight dtype %d (want Q8_0=8, Q4_K=12, Q6_K=14 or MLX_Q4=100)", dtype);
     if (n <= 0 || k <= 0) return fail(THQ_ESHAPE, "weight shape [%lld, %lld] must be positive", (long long)n, (long long)k);
     if (k % bs) return fail(THQ_ESHAPE, "K=%lld is not a multiple of the block size %d", (long long)k, bs);
     if (k > (int64_t)1 << 30 || n > (int64_t)1 << 40) return fail(THQ_ESHAPE, "weight shape too large");
@@ -102,7 +111,8 @@ int alloc_weight(thq_ctx* ctx, int dtype, int64_t n, int64_t k, thq_weight** out
     w->K = k;
     const size_t qb = q_plane_bytes(dtype, n, k), ab = aux_plane_bytes(dtype, n, k);
     hipError_t e = hipMalloc((void**)&w->q, qb);
-    if (e == hipSuccess && dtype != THQ_Q8_0 && (n & 3)) e = hipMemset(w->q, 0, qb);  // zero padding rows
+    if (e == hipSuccess && (dtype == THQ_Q4_K || dtype == THQ_MLX_Q4) && (n & 3))
+        e = hipMemset(w->q, 0, qb);  // zero padding rows
     if (e == hipSuccess && ab) {
         e = hipMalloc((void**)&w->aux, ab);
         if (e != hipSuccess) (void)hipFree(w->q);
@@ -168,6 +178,7 @@ hipError_t dequant_any(const thq_weight* w, void* out, bool bf16, hipStream_t s)
         return thq::launch_dequant_q8_0(reinterpret_cast<const int8_t*>(w->q), reinterpret_cast<const uint16_t*>(w->aux),
                                         out, bf16, w->N * (w->K / 32), s);
     if (w->qtype == THQ_MLX_Q4) return thq::launch_dequant_affine(w->q, out, bf16, w->N, (int)w->K, s);
+    if (w->qtype == THQ_Q6_K) return thq::launch_dequant_q6k(w->q, out, bf16, w->N, (int)(w->K / 256), s);
     return thq::launch_dequant_q4k(w->q, out, bf16, w->N, (int)(w->K / 256), s);
 }
 
@@ -192,6 +203,7 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
     hipError_t e;
     if (flags & THQ_MODE_Q8ACT) {
         if (w->qtype == THQ_MLX_Q4) return fail(THQ_EDTYPE, "THQ_MODE_Q8ACT applies to GGUF weights only");
+        if (w->qtype == THQ_Q6_K) return fail(THQ_EDTYPE, "THQ_MODE_Q8ACT is not implemented for Q6_K weights");
         if (!thq::q8act_supported(w->qtype, w->K))
             return fail(THQ_ESHAPE, "K=%lld too large for THQ_MODE_Q8ACT", (long long)w->K);
         if (!aligned16(x)) return fail(THQ_EALIGN, "THQ_MODE_Q8ACT needs 16-byte aligned x");
@@ -207,11 +219,13 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
         const char* v = getenv("THQ_GEMV_M1");
         return v && !strcmp(v, "mfma");
     }();
-    const thq::GemvPlan gp = (!xf32 && aligned16(x) && m <= 8) ? thq::plan_gemv_mfma(v.qtype, m, w->N, w->K, gu)
-                                                                 : thq::GemvPlan{};
+    const bool q6 = w->qtype == THQ_Q6_K;
+    const thq::GemvPlan gp = (!xf32 && !q6 && aligned16(x) && m <= 8)
+                                 ? thq::plan_gemv_mfma(v.qtype, m, w->N, w->K, gu)
+                                 : thq::GemvPlan{};
     const bool skinny = gp.waves > 0;
     // the 4-bit tile kernels need whole superblocks (MLX affine K % 256 != 0 runs the generic kernel)
-    const bool q4 = w->qtype != THQ_Q8_0;
+    const bool q4 = w->qtype == THQ_Q4_K || w->qtype == THQ_MLX_Q4;
     if (m == 1 && !(m1_mfma && skinny) && aligned16(x) && thq::gemv1_supported(v.qtype, (int)w->K, gu, w->N)) {
         e = thq::launch_gemv1(v, x, xf32, y, yf32, gu, nout, up_off, s);
     } else if (skinny) {
@@ -221,7 +235,7 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
             if (rc) return rc;
         }
         e = thq::launch_gemv_mfma(gp, v, x, y, yf32, gu, (int)m, nout, up_off, static_cast<float*>(ctx->ws), s);
-    } else if (!xf32 && aligned16(x) && !(q4 && ((flags & THQ_MODE_EXACT_W) || w->K % 256))) {
+    } else if (!xf32 && !q6 && aligned16(x) && !(q4 && ((flags & THQ_MODE_EXACT_W) || w->K % 256))) {
         const bool exact = (flags & THQ_MODE_EXACT_W) || (w->qtype == THQ_Q8_0 && m <= 64);
         thq::GemmPlan p = thq::plan_gemm(v.qtype, exact, m, w->N, w->K, gu);
         std::lock_guard<std::mutex> lk(ctx->mu);
@@ -294,16 +308,24 @@ int thq_weight_from_device(thq_ctx* ctx, thq_dtype dtype, const void* dev_blocks
     if (dtype == THQ_MLX_Q4) return fail(THQ_EDTYPE, "MLX affine weights load with thq_affine_from_device");
     int rc = check_dtype_shape(dtype, n, k);
     if (rc) return rc;
+    // the repack kernels read Q4_K blocks as 16-B vectors, Q8_0 / Q6_K blocks as 2-B words
+    const uintptr_t need = dtype == THQ_Q4_K ? 16 : 2;
+    if ((uintptr_t)dev_blocks % need)
+        return fail(THQ_EALIGN, "dev_blocks must be %d-byte aligned for this dtype", (int)need);
     DeviceGuard g(ctx->device);
     hipStream_t s = static_cast<hipStream_t>(stream);
     thq_weight* w = nullptr;
     rc = alloc_weight(ctx, dtype, n, k, &w);
     if (rc) return rc;
     const uint8_t* src = static_cast<const uint8_t*>(dev_blocks);
-    hipError_t e = dtype == THQ_Q4_K
-                       ? thq::launch_repack_q4k(src, w->q, n, (int)(k / 256), s)
-                       : thq::launch_repack_q8_0(src, reinterpret_cast<int8_t*>(w->q),
-                                                 reinterpret_cast<uint16_t*>(w->aux), n * (k / 32), s);
+    hipError_t e;
+    if (dtype == THQ_Q4_K)
+        e = thq::launch_repack_q4k(src, w->q, n, (int)(k / 256), s);
+    else if (dtype == THQ_Q6_K)
+        e = thq::launch_repack_q6k(src, w->q, n, (int)(k / 256), s);
+    else
+        e = thq::launch_repack_q8_0(src, reinterpret_cast<int8_t*>(w->q), reinterpret_cast<uint16_t*>(w->aux),
+                                    n * (k / 32), s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
         thq_weight_free(w);
@@ -317,6 +339,7 @@ int thq_quantize(thq_ctx* ctx, thq_dtype dtype, const float* w_dev, int64_t n, i
                  thq_weight** out) {
     if (!ctx || !w_dev || !out) return fail(THQ_EINVAL, "null argument");
     if (dtype == THQ_MLX_Q4) return fail(THQ_EDTYPE, "no MLX affine quantizer (the engine loads MLX checkpoints)");
+    if (dtype == THQ_Q6_K) return fail(THQ_EDTYPE, "no Q6_K quantizer (Q6_K tensors are read from GGUF files)");
     int rc = check_dtype_shape(dtype, n, k);
     if (rc) return rc;
     if (!aligned16(w_dev)) return fail(THQ_EALIGN, "w_dev must be 16-byte aligned");
@@ -360,8 +383,16 @@ int thq_weight_fuse(thq_ctx* ctx, const thq_weight* const* parts, int nparts, th
     size_t qoff = 0, aoff = 0;
     int64_t row0 = 0;
     for (int i = 0; i < nparts; ++i) {
-        hipError_t e;
-        if (dtype != THQ_Q8_0) {
+        hipError_t e = hipSuccess;
+        if (dtype == THQ_Q6_K) {
+            // each plane is row-major: copy the part's rows of all four
+            const thq::Q6Layout dl = thq::q6k_layout(n, k), sl = thq::q6k_layout(parts[i]->N, k);
+            const size_t doff[4] = {0, dl.qh, dl.sc, dl.d}, soff[4] = {0, sl.qh, sl.sc, sl.d};
+            const size_t rowb[4] = {(size_t)k / 2, (size_t)k / 4, (size_t)k / 16, (size_t)(k / 256) * 2};
+            for (int pl = 0; pl < 4 && e == hipSuccess; ++pl)
+                e = hipMemcpy(w->q + doff[pl] + (size_t)row0 * rowb[pl], parts[i]->q + soff[pl],
+                              (size_t)parts[i]->N * rowb[pl], hipMemcpyDeviceToDevice);
+        } else if (dtype != THQ_Q8_0) {
             e = thq::launch_q4k_copy_rows(parts[i]->q, parts[i]->N, w->q, row0, (int)((k + 255) / 256), nullptr);
         } else {
             const size_t qb = q_plane_bytes(dtype, parts[i]->N, k), ab = aux_plane_bytes(dtype, parts[i]->N, k);
@@ -411,6 +442,20 @@ int thq_weight_download(const thq_weight* w, void* host_blocks) {
     HIP_TRY(hipMemcpy(qs.data(), w->q, qs.size(), hipMemcpyDeviceToHost));
     if (!aux.empty()) HIP_TRY(hipMemcpy(aux.data(), w->aux, aux.size(), hipMemcpyDeviceToHost));
     uint8_t* dst = static_cast<uint8_t*>(host_blocks);
+    if (w->qtype == THQ_Q6_K) {
+        const int64_t nsb = w->K / 256;
+        const thq::Q6Layout L = thq::q6k_layout(w->N, w->K);
+        for (int64_t n = 0; n < w->N; ++n) {
+            for (int64_t s = 0; s < nsb; ++s) {
+                uint8_t* blk = dst + (n * nsb + s) * 210;
+                std::memcpy(blk, qs.data() + n * (w->K / 2) + s * 128, 128);
+                std::memcpy(blk + 128, qs.data() + L.qh + n * (w->K / 4) + s * 64, 64);
+                std::memcpy(blk + 192, qs.data() + L.sc + n * (w->K / 16) + s * 16, 16);
+                std::memcpy(blk + 208, qs.data() + L.d + (n * nsb + s) * 2, 2);
+            }
+        }
+        return THQ_OK;
+    }
     if (w->qtype == THQ_Q4_K) {
         const int nsb = (int)(w->K / 256);
         for (int64_t n = 0; n < w->N; ++n) {

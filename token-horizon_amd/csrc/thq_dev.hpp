@@ -177,6 +177,30 @@ __device__ __forceinline__ uint4 ld_stream16(const void* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Q6_K (GGML type 14, 210 B per 256 weights: u8 ql[128], u8 qh[64], i8
+// scales[16], f16 d) on the device: four row-major planes, each starting on a
+// 256-B boundary, with the bytes of every superblock in GGUF order:
+//   QL [N][K/2]   QH [N][K/4]   SC [N][K/16] (int8)   D [N][K/256] (f16)
+// A 128-weight half h of superblock s is then 64 contiguous QL bytes, 32 QH
+// bytes and 8 scales: w[128h + 32Q + l] = (d * sc[8h + 2Q + l/16]) *
+// (code - 32), code = ql nibble | qh 2-bit field << 4 (GGML's order).
+struct Q6Layout {
+    size_t qh, sc, d, total;
+};
+__host__ __device__ __forceinline__ Q6Layout q6k_layout(int64_t n, int64_t k) {
+    auto al = [](size_t b) { return (b + 255) & ~(size_t)255; };
+    Q6Layout L;
+    size_t o = al((size_t)n * (size_t)k / 2);
+    L.qh = o;
+    o += al((size_t)n * (size_t)k / 4);
+    L.sc = o;
+    o += al((size_t)n * (size_t)k / 16);
+    L.d = o;
+    o += al((size_t)n * (size_t)(k / 256) * 2);
+    L.total = o;
+    return L;
+}
+
 // byte I of w as f32 (selected to v_cvt_f32_ubyteI)
 template <int I>
 __device__ __forceinline__ float ubyte_f32(uint32_t w) {

@@ -12,6 +12,7 @@ namespace thq {
 //   MLX affine 4-bit (qtype 13): q = the same row-quad plane with affine
 //                    headers (thq_dev.hpp, aff_scale); K may be padded to
 //                    whole superblocks (zero groups)
+//   Q6_K (qtype 14): q   = QL, QH, SC, D planes (thq_dev.hpp, q6k_layout)
 //   Q4_K (qtype 12): q   = row-quad plane, ceil(N/4) groups of 4 x K/256 x
 //                          144 B (layout in thq_dev.hpp, q4k_group); padding
 //                          rows are zero
@@ -42,6 +43,9 @@ hipError_t launch_q4k_copy_rows(const uint8_t* src, int64_t n, uint8_t* dst, int
 hipError_t launch_dequant_q8_0(const int8_t* qs, const uint16_t* d, void* out, bool bf16, int64_t nblocks,
                                hipStream_t s);
 hipError_t launch_dequant_q4k(const uint8_t* src, void* out, bool bf16, int64_t n, int nsb, hipStream_t s);
+// Q6_K (qtype 14): GGUF blocks -> planes (thq_dev.hpp, q6k_layout), dequantization
+hipError_t launch_repack_q6k(const uint8_t* gguf, uint8_t* dst, int64_t n, int nsb, hipStream_t s);
+hipError_t launch_dequant_q6k(const uint8_t* src, void* out, bool bf16, int64_t n, int nsb, hipStream_t s);
 // MLX affine 4-bit (qtype 13): QLin arrays -> row-quad plane (K padded to whole
 // superblocks), and its dequantization (bf16: the reference's f64 rounding)
 hipError_t launch_repack_affine(const uint32_t* wq, const uint16_t* sb, uint8_t* dst, int64_t n, int K, int gs,
@@ -50,6 +54,9 @@ hipError_t launch_dequant_affine(const uint8_t* src, void* out, bool bf16, int64
 
 // decode GEMV (M = 1); gu = fused gate/up over a [gate; up] weight
 bool gemv1_supported(int qtype, int K, bool gu, int64_t n_rows);
+// Q6_K M = 1 with bf16 x (K % 256 == 0, K <= 16384), k_q6k.hip
+hipError_t launch_gemv1_q6k(const WeightView& w, const void* x, void* y, bool yf32, bool gu, int64_t nout,
+                            int64_t up_off, hipStream_t s);
 hipError_t launch_gemv1(const WeightView& w, const void* x, bool xf32, void* y, bool yf32, bool gu, int64_t nout,
                         int64_t up_off, hipStream_t s);
 // decode GEMV on MFMA: 1 <= M <= 8 bf16 activation rows, exact weights

@@ -22,10 +22,11 @@ LIB_PATH = os.path.join(HERE, "libthq.so")
 
 Q8_0 = 8
 Q4_K = 12
+Q6_K = 14
 Q8_K = 15  # activation dot type of Q4_K (thq_quantize_act)
 MLX_Q4 = 100  # MLX affine 4-bit: the engine's QLin (wq u32 [N, K/8], sb bf16 [N, 2K/gs])
-BLOCK = {Q8_0: 32, Q4_K: 256, Q8_K: 256}
-BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q8_K: 292}
+BLOCK = {Q8_0: 32, Q4_K: 256, Q6_K: 256, Q8_K: 256}
+BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q6_K: 210, Q8_K: 292}
 
 ACT_F32 = 0
 ACT_BF16 = 1
