@@ -73,6 +73,9 @@ typedef enum thq_act {
 #define THQ_EALIGN (-4)       /* device pointer alignment the call requires   */
 #define THQ_EHIP (-5)         /* HIP runtime error                            */
 #define THQ_ENOMEM (-6)       /* device allocation failed                     */
+#define THQ_EIO (-7)          /* a file cannot be opened or mapped            */
+#define THQ_EFORMAT (-8)      /* malformed or unsupported GGUF file           */
+#define THQ_ENOTFOUND (-9)    /* no such GGUF tensor or metadata key          */
 
 typedef struct thq_ctx thq_ctx;
 typedef struct thq_weight thq_weight;
@@ -143,7 +146,7 @@ int thq_affine_download(const thq_weight* w, uint32_t* wq_host, uint16_t* sb_hos
 /* ---- compute ---- */
 
 /* Exact f32 dequantization, out_dev [N, K] (QTensor::dequantize). Bit-exact
- * with candle's BlockQ8_0/BlockQ4K::to_float.  MLX affine: q*scale + bias
+ * with candle's BlockQ8_0/BlockQ4K/BlockQ6K::to_float.  MLX affine: q*scale + bias
  * rounded once to f32. */
 int thq_dequantize(thq_ctx* ctx, const thq_weight* w, float* out_dev, void* stream);
 
@@ -171,7 +174,8 @@ int thq_quantize_act(thq_ctx* ctx, thq_dtype dot_type, const void* x_dev, thq_ac
  *   M == 1     decode GEMV (exact dequantized weights)
  *   M >= 2     MFMA GEMM; weights are rounded to bf16 on the MFMA path unless
  *              THQ_MODE_EXACT_W (or Q8_0 with M <= 64), activations bf16.
- *   x f32 with M >= 2 runs an exact f32 path.
+ *   x f32 with M >= 2 runs an exact f32 path, and so does Q6_K at M >= 2
+ *   or with f32 x.
  * THQ_MODE_Q8ACT instead reproduces candle's default CPU k_quants::matmul:
  * x rows are quantized as thq_quantize_act does (into the context
  * workspace), every block dot is exact in integers and scaled in f32; only
@@ -205,6 +209,74 @@ int thq_matmul_argmax(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_
 /* Per-row argmax of an f32 [M, N] device matrix, same tie rule
  * (candle Tensor::argmax(D::Minus1) / engine.rs greedy_argmax). */
 int thq_argmax(thq_ctx* ctx, const float* v_dev, int64_t m, int64_t n, uint32_t* idx_dev, void* stream);
+
+/* ---- GGUF files ----
+ * The loader's first step (engine/src/model.rs:526-562): parse a GGUF file,
+ * read metadata, hand 2-D Q8_0 / Q4_K / Q6_K tensors to the device.  Mirrors
+ * [ext] candle-core 0.11 gguf_file::Content (read, metadata, tensor_infos,
+ * tensor): versions 1-3, either byte order of the "GGUF" magic, strings with
+ * trailing NULs dropped and invalid UTF-8 replaced by U+FFFD, dims in
+ * row-major order (GGUF's ne reversed, as candle's Shape), tensor data at
+ * the first multiple of general.alignment (U8/U16/U32 or non-negative
+ * I8/I16/I32; else 32) after the header; a repeated key or tensor name
+ * replaces the earlier one.  Host-only except thq_weight_from_gguf.  The
+ * file stays memory-mapped until thq_gguf_close; returned strings and data
+ * pointers live as long as the handle. */
+typedef struct thq_gguf thq_gguf;
+
+/* metadata value types (the GGUF file format's ids) */
+typedef enum thq_gguf_type {
+    THQ_GGUF_U8 = 0, THQ_GGUF_I8 = 1, THQ_GGUF_U16 = 2, THQ_GGUF_I16 = 3, THQ_GGUF_U32 = 4, THQ_GGUF_I32 = 5,
+    THQ_GGUF_F32 = 6, THQ_GGUF_BOOL = 7, THQ_GGUF_STRING = 8, THQ_GGUF_ARRAY = 9, THQ_GGUF_U64 = 10,
+    THQ_GGUF_I64 = 11, THQ_GGUF_F64 = 12
+} thq_gguf_type;
+
+/* Content::read: THQ_EIO (open / map), THQ_EFORMAT (bad magic or version,
+ * truncated header, unknown value type, bool byte > 1, unknown ggml type id). */
+int thq_gguf_open(const char* path, thq_gguf** out);
+void thq_gguf_close(thq_gguf* g);
+int thq_gguf_version(const thq_gguf* g, uint32_t* version);
+
+/* Counts of distinct tensor names / metadata keys (-1 for a null handle). */
+int64_t thq_gguf_tensor_count(const thq_gguf* g);
+int64_t thq_gguf_metadata_count(const thq_gguf* g);
+
+/* Index of tensor `name` (Content::tensor_infos lookup), -1 if absent. */
+int64_t thq_gguf_find_tensor(const thq_gguf* g, const char* name);
+
+/* TensorInfo of tensor i: name, ggml type id, n_dims (<= 4), dims[4]
+ * row-major (unused entries 0), absolute file offset of its data and
+ * elems / block_size * type_size bytes.  Any argument but g may be NULL. */
+int thq_gguf_tensor_info(const thq_gguf* g, int64_t i, const char** name, uint32_t* ggml_type, uint32_t* n_dims,
+                         uint64_t* dims, uint64_t* offset, uint64_t* nbytes);
+
+/* The block bytes of tensor i (TensorInfo::read): a pointer into the mapping.
+ * THQ_ESHAPE if elems is not a multiple of the block size, THQ_EFORMAT if
+ * the bytes lie past the end of the file. */
+int thq_gguf_tensor_data(const thq_gguf* g, int64_t i, const void** data, uint64_t* nbytes);
+
+/* Key and value type of metadata entry i (the order keys first appear).
+ * Keys and tensor names come back NUL-terminated (a NUL inside one ends it
+ * early; GGUF writers emit none). */
+int thq_gguf_metadata_key(const thq_gguf* g, int64_t i, const char** key, uint32_t* value_type);
+
+/* Typed metadata lookups, as strict as Value::to_u32 / to_f32 / to_string:
+ * THQ_ENOTFOUND if the key is absent, THQ_EDTYPE if the value has another
+ * type (a U8 is not a u32).  The engine reads general.architecture,
+ * {arch}.context_length and tokenizer.ggml.eos_token_id this way
+ * (engine/src/model.rs:536-549). */
+int thq_gguf_metadata_u32(const thq_gguf* g, const char* key, uint32_t* out);
+int thq_gguf_metadata_f32(const thq_gguf* g, const char* key, float* out);
+/* `len` (may be NULL) receives the byte length: a GGUF string may hold NULs */
+int thq_gguf_metadata_str(const thq_gguf* g, const char* key, const char** out, uint64_t* len);
+/* Element type and length of an array value (elements are not exposed). */
+int thq_gguf_metadata_array(const thq_gguf* g, const char* key, uint32_t* elem_type, uint64_t* count);
+
+/* Upload tensor `name` as a weight: Content::tensor + QMatMul::from_qtensor
+ * for the projections ModelWeights::from_gguf builds.  The tensor must be
+ * 2-D [N, K] of type Q8_0, Q4_K or Q6_K (THQ_EDTYPE / THQ_ESHAPE otherwise).
+ * Synchronous, as thq_weight_upload. */
+int thq_weight_from_gguf(thq_ctx* ctx, const thq_gguf* g, const char* name, thq_weight** out);
 
 #ifdef __cplusplus
 }

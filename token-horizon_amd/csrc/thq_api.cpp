@@ -37,18 +37,29 @@ struct thq_weight {
     uint8_t* aux = nullptr;  // Q8_0 f16 scale plane
 };
 
-namespace {
+namespace thq {
 
 thread_local std::string g_err;
 
-int fail(int code, const char* fmt, ...) {
+// the calling thread's last error message (thq_last_error); shared with the
+// GGUF reader in thq_gguf.cpp
+int fail_v(int code, const char* fmt, va_list ap) {
     char buf[512];
-    va_list ap;
-    va_start(ap, fmt);
     vsnprintf(buf, sizeof(buf), fmt, ap);
-    va_end(ap);
     g_err = buf;
     return code;
+}
+
+}  // namespace thq
+
+namespace {
+
+int fail(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    const int rc = thq::fail_v(code, fmt, ap);
+    va_end(ap);
+    return rc;
 }
 
 #define HIP_TRY(expr)                                                                            \
@@ -255,7 +266,7 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
 
 extern "C" {
 
-const char* thq_last_error(void) { return g_err.c_str(); }
+const char* thq_last_error(void) { return thq::g_err.c_str(); }
 
 const char* thq_version(void) { return "thq 0.1 gfx950"; }
 

@@ -36,6 +36,11 @@ MODE_EXACT_W = 0x10
 
 OK = 0
 EINVAL, ESHAPE, EDTYPE, EALIGN, EHIP, ENOMEM = -1, -2, -3, -4, -5, -6
+EIO, EFORMAT, ENOTFOUND = -7, -8, -9
+
+# GGUF metadata value types (thq_gguf_type)
+GGUF_U8, GGUF_I8, GGUF_U16, GGUF_I16, GGUF_U32, GGUF_I32, GGUF_F32, GGUF_BOOL = range(8)
+GGUF_STRING, GGUF_ARRAY, GGUF_U64, GGUF_I64, GGUF_F64 = range(8, 13)
 
 # every symbol include/thq.h declares
 EXPORTS = (
@@ -43,6 +48,10 @@ EXPORTS = (
     "thq_quantize", "thq_weight_fuse", "thq_weight_free", "thq_weight_info", "thq_weight_download",
     "thq_affine_upload", "thq_affine_from_device", "thq_affine_download",
     "thq_dequantize", "thq_dequantize_bf16", "thq_quantize_act", "thq_matmul", "thq_gate_up_silu", "thq_matmul_argmax", "thq_argmax",
+    "thq_gguf_open", "thq_gguf_close", "thq_gguf_version", "thq_gguf_tensor_count", "thq_gguf_metadata_count",
+    "thq_gguf_find_tensor", "thq_gguf_tensor_info", "thq_gguf_tensor_data", "thq_gguf_metadata_key",
+    "thq_gguf_metadata_u32", "thq_gguf_metadata_f32", "thq_gguf_metadata_str", "thq_gguf_metadata_array",
+    "thq_weight_from_gguf",
 )
 
 
@@ -80,6 +89,21 @@ def _load():
         "thq_gate_up_silu": ([P, P, P, I, i64, P, I, u32, P], I),
         "thq_matmul_argmax": ([P, P, P, I, i64, P, P, u32, P], I),
         "thq_argmax": ([P, P, i64, i64, P, P], I),
+        "thq_gguf_open": ([C.c_char_p, PP], I),
+        "thq_gguf_close": ([P], None),
+        "thq_gguf_version": ([P, C.POINTER(u32)], I),
+        "thq_gguf_tensor_count": ([P], i64),
+        "thq_gguf_metadata_count": ([P], i64),
+        "thq_gguf_find_tensor": ([P, C.c_char_p], i64),
+        "thq_gguf_tensor_info": ([P, i64, C.POINTER(C.c_char_p), C.POINTER(u32), C.POINTER(u32),
+                                  C.POINTER(C.c_uint64), C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)], I),
+        "thq_gguf_tensor_data": ([P, i64, PP, C.POINTER(C.c_uint64)], I),
+        "thq_gguf_metadata_key": ([P, i64, C.POINTER(C.c_char_p), C.POINTER(u32)], I),
+        "thq_gguf_metadata_u32": ([P, C.c_char_p, C.POINTER(u32)], I),
+        "thq_gguf_metadata_f32": ([P, C.c_char_p, C.POINTER(C.c_float)], I),
+        "thq_gguf_metadata_str": ([P, C.c_char_p, C.POINTER(C.c_void_p), C.POINTER(C.c_uint64)], I),
+        "thq_gguf_metadata_array": ([P, C.c_char_p, C.POINTER(u32), C.POINTER(C.c_uint64)], I),
+        "thq_weight_from_gguf": ([P, P, C.c_char_p, PP], I),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -313,3 +337,99 @@ class QMatMul:
 
     def forward(self, x: torch.Tensor, out_dtype=None) -> torch.Tensor:
         return matmul(self.w, x, out_dtype or x.dtype)
+
+
+class GGUFFile:
+    """A GGUF file opened through thq_gguf_open: candle's gguf_file::Content
+    (Content::read, .metadata lookups, .tensor_infos, .tensor) as the loader
+    engine/src/model.rs:526-562 uses it.  Host-only except .weight()."""
+
+    def __init__(self, path: str):
+        h = C.c_void_p()
+        check(lib.thq_gguf_open(os.fsencode(path), C.byref(h)))
+        self.h = h
+        v = C.c_uint32()
+        check(lib.thq_gguf_version(self.h, C.byref(v)))
+        self.version = v.value
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib.thq_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        if lib is not None:
+            self.close()
+
+    def metadata_keys(self) -> dict:
+        """{key: value type} in the order keys first appear."""
+        out = {}
+        for i in range(lib.thq_gguf_metadata_count(self.h)):
+            k, t = C.c_char_p(), C.c_uint32()
+            check(lib.thq_gguf_metadata_key(self.h, i, C.byref(k), C.byref(t)))
+            out[k.value.decode()] = t.value
+        return out
+
+    def u32(self, key: str) -> int:
+        v = C.c_uint32()
+        check(lib.thq_gguf_metadata_u32(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def f32(self, key: str) -> float:
+        v = C.c_float()
+        check(lib.thq_gguf_metadata_f32(self.h, key.encode(), C.byref(v)))
+        return v.value
+
+    def string(self, key: str) -> str:
+        v, n = C.c_void_p(), C.c_uint64()
+        check(lib.thq_gguf_metadata_str(self.h, key.encode(), C.byref(v), C.byref(n)))
+        return C.string_at(v.value, n.value).decode() if n.value else ""
+
+    def array(self, key: str) -> tuple[int, int]:
+        t, n = C.c_uint32(), C.c_uint64()
+        check(lib.thq_gguf_metadata_array(self.h, key.encode(), C.byref(t), C.byref(n)))
+        return t.value, n.value
+
+    def tensor_names(self) -> list[str]:
+        return [self.tensor_info(i)["name"] for i in range(lib.thq_gguf_tensor_count(self.h))]
+
+    def find(self, name: str) -> int:
+        return lib.thq_gguf_find_tensor(self.h, name.encode())
+
+    def tensor_info(self, i) -> dict:
+        if isinstance(i, str):
+            j = self.find(i)
+            if j < 0:
+                raise ThqError(ENOTFOUND, f"no tensor {i}")
+            i = j
+        name, t, nd = C.c_char_p(), C.c_uint32(), C.c_uint32()
+        dims = (C.c_uint64 * 4)()
+        off, nb = C.c_uint64(), C.c_uint64()
+        check(lib.thq_gguf_tensor_info(self.h, i, C.byref(name), C.byref(t), C.byref(nd), dims, C.byref(off),
+                                       C.byref(nb)))
+        return {"name": name.value.decode(), "type": t.value, "shape": tuple(dims[:nd.value]),
+                "offset": off.value, "nbytes": nb.value}
+
+    def tensor_bytes(self, name: str):
+        """The tensor's block bytes, copied out of the mapping (numpy uint8)."""
+        import numpy as np
+        i = self.find(name)
+        if i < 0:
+            raise ThqError(ENOTFOUND, f"no tensor {name}")
+        p, n = C.c_void_p(), C.c_uint64()
+        check(lib.thq_gguf_tensor_data(self.h, i, C.byref(p), C.byref(n)))
+        return np.ctypeslib.as_array((C.c_uint8 * n.value).from_address(p.value)).copy() if n.value else \
+            np.empty(0, np.uint8)
+
+    def weight(self, name: str, ctx: "Context | None" = None) -> "QTensor":
+        """Upload a 2-D Q8_0 / Q4_K / Q6_K tensor (thq_weight_from_gguf)."""
+        ctx = ctx or Context.get(torch.cuda.current_device())
+        h = C.c_void_p()
+        check(lib.thq_weight_from_gguf(ctx.h, self.h, name.encode(), C.byref(h)))
+        return QTensor(h, ctx)
