@@ -525,18 +525,18 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict_
             const int64_t row = o + (r ? up_off : 0);
             float wv[32];
             if (QT == 14) {
-                // Q6_K planes: sub-block sbi = 8s + 4h + Q holds w[256s + 128h + 32Q + l]
+                // Q6_K: sub-block sbi is half o of 64-weight step g = sbi / 2
+                // (thq_dev.hpp, q6k_layout)
                 const Q6Layout L = q6k_layout(nrows, K);
-                const int s = sbi >> 3, h = (sbi >> 2) & 1, Q = sbi & 3;
-                const uint8_t* ql = Wq + row * (K / 2) + s * 128 + h * 64 + (Q & 1) * 32;
-                const uint8_t* qh = Wq + L.qh + row * (K / 4) + s * 64 + h * 32;
-                const int8_t* sc = reinterpret_cast<const int8_t*>(Wq + L.sc + row * (K / 16) + s * 16 + h * 8 + 2 * Q);
-                const float d = f16_to_f32(reinterpret_cast<const uint16_t*>(Wq + L.d)[row * (K / 256) + s]);
+                const int g = sbi >> 1, o = sbi & 1;
+                const uint8_t* ql = Wq + row * (K / 2) + g * 32;
+                const uint8_t* qh = Wq + L.qh + row * (K / 4) + g * 16;
+                const int8_t* sc = reinterpret_cast<const int8_t*>(Wq + L.sc + row * (K / 16) + g * 4 + 2 * o);
+                const float d = f16_to_f32(reinterpret_cast<const uint16_t*>(Wq + L.d)[row * (K / 256) + (g >> 2)]);
                 const float ds0 = d * (float)sc[0], ds1 = d * (float)sc[1];
-                const int nsh = (Q >> 1) * 4, hsh = 2 * Q;
 #pragma unroll
                 for (int i = 0; i < 32; ++i) {
-                    const int code = ((ql[i] >> nsh) & 0xF) | (((qh[i] >> hsh) & 3) << 4);
+                    const int code = ((ql[i] >> (4 * o)) & 0xF) | (((qh[i & 15] >> (2 * (2 * o + (i >> 4)))) & 3) << 4);
                     wv[i] = (i < 16 ? ds0 : ds1) * (float)(code - 32);  // (d * sc) * q, candle's order
                 }
             } else if (QT != 8) {

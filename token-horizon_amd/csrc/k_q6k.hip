@@ -6,15 +6,11 @@
 // HBM-bound like the Q4_K GEMV: every weight byte is read once, x is staged
 // in LDS once per block and held in registers across the rows a wave owns.
 //
-// Weights come from the QL / QH / SC / D planes (thq_dev.hpp, q6k_layout).
-// Lane map for one 4096-wide K chunk: lane = 2u' + cc, unit u = 32c + u' is
-// the 128-weight half of superblock u/2, and the lane takes the 16 positions
-// l = 16cc .. 16cc+15 of that half in all four of its 32-weight quarters Q:
-// weights 128u + 32Q + l.  Its 16 low-nibble bytes are ql[l] (Q = 0, 2 use
-// the low / high nibble) and ql[l + 32] (Q = 1, 3), its 16 qh bytes are
-// qh[l] (Q's 2-bit field at bits 2Q), and each quarter's 16 positions share
-// one scale sc[2Q + cc]: a lane owns four whole scale groups, so the scale
-// multiply happens once per 16 weights.
+// Weights come from the QL / QH / SC / D planes, regrouped by 64-weight
+// step (thq_dev.hpp, q6k_layout).  Lane map for one 4096-wide K chunk c: the
+// lane takes step g = 64c + lane, i.e. 32 contiguous QL bytes, 16 QH bytes,
+// one dword of 4 scales (one per 16-weight group) and its superblock's d, so
+// the scale multiply happens once per 16 weights.
 //
 // Per 4 weights: 3 bit ops build four 6-bit codes in a dword, 2 v_perm put
 // them under a constant 0x43 byte (bf16 0x43nn = 128 + code), 2
@@ -33,28 +29,29 @@ struct Q6Planes {
     const uint16_t* d;
 };
 
-// one row's share of a lane: 64 weights in four scale groups of 16
+// one row's share of a lane: one 64-weight step in four scale groups of 16
 struct Q6Row {
-    uint2 sc;     // the half's 8 scales (bytes 2Q + cc are this lane's)
-    uint32_t d;   // the superblock's f16 d
-    uint4 lo, hi; // ql[l], ql[l + 32]
-    uint4 h;      // qh[l]
+    uint32_t sc;   // the step's 4 scales, group G in byte G
+    uint32_t d;    // the superblock's f16 d
+    uint4 lo, hi;  // QL bytes 0..15 (weights t and t + 32), 16..31 (t + 16, t + 48)
+    uint4 h;       // QH bytes 0..15 (2-bit fields of weights t, t+16, t+32, t+48)
 };
 
-__device__ __forceinline__ void q6_row_load(Q6Row& R, const Q6Planes& P, int64_t row, int K, int u, int cc) {
+__device__ __forceinline__ void q6_row_load(Q6Row& R, const Q6Planes& P, int64_t row, int K, int g) {
     const int nsb = K >> 8;
     // scales and d first: the in-order wait counters then release a row's
     // math as soon as its own bytes have landed
-    R.sc = *reinterpret_cast<const uint2*>(P.sc + row * (K >> 4) + 8 * u);
-    R.d = P.d[row * nsb + (u >> 1)];
-    const uint8_t* ql = P.ql + row * (K >> 1) + 64 * u + 16 * cc;
+    R.sc = *reinterpret_cast<const uint32_t*>(P.sc + row * (K >> 4) + 4 * g);
+    R.d = P.d[row * nsb + (g >> 2)];
+    const uint8_t* ql = P.ql + row * (K >> 1) + 32 * g;
     R.lo = *reinterpret_cast<const uint4*>(ql);
-    R.hi = *reinterpret_cast<const uint4*>(ql + 32);
-    R.h = *reinterpret_cast<const uint4*>(P.qh + row * (K >> 2) + 32 * u + 16 * cc);
+    R.hi = *reinterpret_cast<const uint4*>(ql + 16);
+    R.h = *reinterpret_cast<const uint4*>(P.qh + row * (K >> 2) + 16 * g);
 }
 
-// sum over the lane's 64 weights of x * w, w = (d * sc) * (code - 32)
-__device__ __forceinline__ float q6_row_dot(const Q6Row& R, const uint32_t (&xq)[4][8], const float (&sx)[4], int cc,
+// sum over the lane's 64 weights of x * w, w = (d * sc) * (code - 32); xq[G]
+// holds the bf16 pairs of group G (weights 16G .. 16G + 15), sx[G] their sum
+__device__ __forceinline__ float q6_row_dot(const Q6Row& R, const uint32_t (&xq)[4][8], const float (&sx)[4],
                                             float dlive) {
     const uint32_t C43 = 0x43434343u;
     const uint32_t lo[4] = {R.lo.x, R.lo.y, R.lo.z, R.lo.w};
@@ -65,10 +62,10 @@ __device__ __forceinline__ float q6_row_dot(const Q6Row& R, const uint32_t (&xq)
     for (int t = 0; t < 4; ++t) {
         const uint32_t A = lo[t], B = hi[t], H = hh[t];
         uint32_t c[4];
-        c[0] = (A & 0x0F0F0F0Fu) | ((H & 0x03030303u) << 4);
-        c[1] = (B & 0x0F0F0F0Fu) | ((H & 0x0C0C0C0Cu) << 2);
-        c[2] = ((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u);
-        c[3] = ((B >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u);
+        c[0] = (A & 0x0F0F0F0Fu) | ((H & 0x03030303u) << 4);          // weights 4t .. 4t+3
+        c[1] = (B & 0x0F0F0F0Fu) | ((H & 0x0C0C0C0Cu) << 2);          // 16 + 4t ..
+        c[2] = ((A >> 4) & 0x0F0F0F0Fu) | (H & 0x30303030u);          // 32 + 4t ..
+        c[3] = ((B >> 4) & 0x0F0F0F0Fu) | ((H >> 2) & 0x30303030u);   // 48 + 4t ..
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             // perm(C43, v, sel): bytes [v.b_i, 0x43, v.b_i+1, 0x43] = bf16 pair (128+q_i, 128+q_i+1)
@@ -76,9 +73,8 @@ __device__ __forceinline__ float q6_row_dot(const Q6Row& R, const uint32_t (&xq)
             a[q] = dot2_bf16(__builtin_amdgcn_perm(C43, c[q], 0x04030402u), xq[q][2 * t + 1], a[q]);
         }
     }
-    const int sh = 8 * cc;
-    const float s0 = (float)(int)(int8_t)(R.sc.x >> sh), s1 = (float)(int)(int8_t)(R.sc.x >> (sh + 16));
-    const float s2 = (float)(int)(int8_t)(R.sc.y >> sh), s3 = (float)(int)(int8_t)(R.sc.y >> (sh + 16));
+    const float s0 = (float)(int)(int8_t)R.sc, s1 = (float)(int)(int8_t)(R.sc >> 8);
+    const float s2 = (float)(int)(int8_t)(R.sc >> 16), s3 = (float)(int)(int8_t)(R.sc >> 24);
     float p = s0 * __builtin_fmaf(-160.0f, sx[0], a[0]);
     p = __builtin_fmaf(s1, __builtin_fmaf(-160.0f, sx[1], a[1]), p);
     p = __builtin_fmaf(s2, __builtin_fmaf(-160.0f, sx[2], a[2]), p);
@@ -115,10 +111,9 @@ __global__ __launch_bounds__(64 * QPB * KC) void k_gemv1_q6k_bf16(Q6Planes P, co
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
 
-    // lanes past K read unit 0 / 1 of superblock 0 and are masked to zero
+    // lanes past K read step 0 and are masked to zero
     const bool live = 16 * c + (lane >> 2) < nsb;
-    const int u = live ? 32 * c + (lane >> 1) : ((lane >> 1) & 1);
-    const int cc = lane & 1;
+    const int gs = live ? 64 * c + lane : 0;
     const int64_t base = GU ? 2 * g : 4 * g;
     Q6Row A0, A1, A2, A3;
     {
@@ -126,10 +121,10 @@ __global__ __launch_bounds__(64 * QPB * KC) void k_gemv1_q6k_bf16(Q6Planes P, co
             const int64_t o = GU ? base + (r >> 1) : base + r;  // output index of slot r
             return (g < ngroups && o < nout) ? slot_row<4, GU>(base, r, up_off) : 0;
         };
-        q6_row_load(A0, P, row_of(0), K, u, cc);
-        q6_row_load(A1, P, row_of(1), K, u, cc);
-        q6_row_load(A2, P, row_of(2), K, u, cc);
-        q6_row_load(A3, P, row_of(3), K, u, cc);
+        q6_row_load(A0, P, row_of(0), K, gs);
+        q6_row_load(A1, P, row_of(1), K, gs);
+        q6_row_load(A2, P, row_of(2), K, gs);
+        q6_row_load(A3, P, row_of(3), K, gs);
     }
     if (x0 < nx) lds[x0] = xv0;
     if (x1 < nx) lds[x1] = xv1;
@@ -139,13 +134,13 @@ __global__ __launch_bounds__(64 * QPB * KC) void k_gemv1_q6k_bf16(Q6Planes P, co
     }
     __syncthreads();
 
-    // the lane's activations: quarter Q = elements 128u + 32Q + 16cc .. +15
+    // the lane's activations: elements 64 gs .. 64 gs + 63, group G = 16 of them
     const uint32_t m = live ? 0xFFFFFFFFu : 0u;
     uint32_t xq[4][8];
     float sx[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const uint4* xp = lds + 16 * u + 4 * q + 2 * cc;
+        const uint4* xp = lds + 8 * gs + 2 * q;
         const uint4 p0 = xp[0], p1 = xp[1];
         xq[q][0] = p0.x & m; xq[q][1] = p0.y & m; xq[q][2] = p0.z & m; xq[q][3] = p0.w & m;
         xq[q][4] = p1.x & m; xq[q][5] = p1.y & m; xq[q][6] = p1.z & m; xq[q][7] = p1.w & m;
@@ -155,8 +150,8 @@ __global__ __launch_bounds__(64 * QPB * KC) void k_gemv1_q6k_bf16(Q6Planes P, co
         sx[q] = t;
     }
     const float dl = live ? 1.0f : 0.0f;  // a dead lane's d may be any f16, even inf
-    const float acc[4] = {q6_row_dot(A0, xq, sx, cc, dl), q6_row_dot(A1, xq, sx, cc, dl),
-                          q6_row_dot(A2, xq, sx, cc, dl), q6_row_dot(A3, xq, sx, cc, dl)};
+    const float acc[4] = {q6_row_dot(A0, xq, sx, dl), q6_row_dot(A1, xq, sx, dl), q6_row_dot(A2, xq, sx, dl),
+                          q6_row_dot(A3, xq, sx, dl)};
     const float tot = reduce_slots<4>(acc, lane);
     if (!(lane & 15)) red[qb][c][slot_of_lane<4>(lane)] = tot;
     __syncthreads();

@@ -279,7 +279,8 @@ __global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__
 }
 
 // ---------------------------------------------------------------- Q6_K
-// GGUF 210-B blocks (2-B aligned) -> planes; one thread per superblock
+// GGUF 210-B blocks (2-B aligned) -> planes regrouped by 64-weight step
+// (thq_dev.hpp, q6k_layout); one thread per superblock
 __global__ __launch_bounds__(256) void k_repack_q6k(const uint8_t* __restrict__ gguf, uint8_t* __restrict__ dst,
                                                     int64_t n, int nsb) {
     const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -292,48 +293,64 @@ __global__ __launch_bounds__(256) void k_repack_q6k(const uint8_t* __restrict__ 
     uint32_t w[52];
 #pragma unroll
     for (int i = 0; i < 52; ++i) w[i] = (uint32_t)src[2 * i] | ((uint32_t)src[2 * i + 1] << 16);
-    uint4* ql = reinterpret_cast<uint4*>(dst + row * (K / 2) + s * 128);
-    uint4* qh = reinterpret_cast<uint4*>(dst + L.qh + row * (K / 4) + s * 64);
+    const uint32_t* ql = w;        // ql[128]
+    const uint32_t* qh = w + 32;   // qh[64]
+    uint32_t* qlo = reinterpret_cast<uint32_t*>(dst + row * (K / 2) + s * 128);
+    uint32_t* qho = reinterpret_cast<uint32_t*>(dst + L.qh + row * (K / 4) + s * 64);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        // QL: step 2h takes the low nibbles of ql[64h + t] (weight t) and
+        // ql[64h + 32 + t] (weight t + 32), step 2h + 1 the high nibbles
+#pragma unroll
+        for (int t4 = 0; t4 < 8; ++t4) {
+            const uint32_t a = ql[16 * h + t4], c = ql[16 * h + 8 + t4];
+            qlo[16 * h + t4] = (a & 0x0F0F0F0Fu) | ((c & 0x0F0F0F0Fu) << 4);
+            qlo[16 * h + 8 + t4] = ((a >> 4) & 0x0F0F0F0Fu) | (c & 0xF0F0F0F0u);
+        }
+        // QH: step weight w of step 2h + e sits in quarter 2e + w/32 at l = w % 32,
+        // i.e. in bits 2(2e + w/32) of qh[32h + w % 32]; byte t collects w = t,
+        // t + 16, t + 32, t + 48
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+#pragma unroll
+            for (int t4 = 0; t4 < 4; ++t4) {
+                const uint32_t lo = qh[8 * h + t4], hi = qh[8 * h + 4 + t4];  // qh[32h + 4t4 ..], qh[32h + 16 + 4t4 ..]
+                const int s0 = 4 * e, s1 = 4 * e + 2;
+                const uint32_t v = ((lo >> s0) & 0x03030303u) | (((hi >> s0) & 0x03030303u) << 2) |
+                                   (((lo >> s1) & 0x03030303u) << 4) | (((hi >> s1) & 0x03030303u) << 6);
+                qho[8 * h + 4 * e + t4] = v;
+            }
+        }
+    }
     uint4* sc = reinterpret_cast<uint4*>(dst + L.sc + row * (K / 16) + s * 16);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ql[i] = make_uint4(w[4 * i], w[4 * i + 1], w[4 * i + 2], w[4 * i + 3]);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) qh[i] = make_uint4(w[32 + 4 * i], w[33 + 4 * i], w[34 + 4 * i], w[35 + 4 * i]);
     sc[0] = make_uint4(w[48], w[49], w[50], w[51]);
     reinterpret_cast<uint16_t*>(dst + L.d)[row * nsb + s] = src[104];
 }
 
-// one thread per (row, 128-weight half): w = (d * sc) * (code - 32), GGML order
+// one thread per (row, 64-weight step): w = (d * sc) * (code - 32), GGML's order
 template <typename OT>
 __global__ __launch_bounds__(256) void k_dequant_q6k(const uint8_t* __restrict__ src, OT* __restrict__ out, int64_t n,
                                                      int nsb) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t >= n * nsb * 2) return;
-    const int64_t row = t / (2 * nsb);
-    const int u = (int)(t - row * 2 * nsb);  // half index in the row
+    if (t >= n * nsb * 4) return;
+    const int64_t row = t / (4 * nsb);
+    const int j = (int)(t - row * 4 * nsb);  // step index in the row
     const int64_t K = (int64_t)nsb * 256;
     const Q6Layout L = q6k_layout(n, K);
-    const uint8_t* ql = src + row * (K / 2) + u * 64;
-    const uint8_t* qh = src + L.qh + row * (K / 4) + u * 32;
-    const int8_t* sc = reinterpret_cast<const int8_t*>(src + L.sc + row * (K / 16) + u * 8);
-    const float d = f16_to_f32(reinterpret_cast<const uint16_t*>(src + L.d)[row * nsb + (u >> 1)]);
-    OT* y = out + row * K + u * 128;
-    for (int l = 0; l < 32; l += 4) {
-        float v[4][4];
+    const uint8_t* ql = src + row * (K / 2) + j * 32;
+    const uint8_t* qh = src + L.qh + row * (K / 4) + j * 16;
+    const int8_t* sc = reinterpret_cast<const int8_t*>(src + L.sc + row * (K / 16) + j * 4);
+    const float d = f16_to_f32(reinterpret_cast<const uint16_t*>(src + L.d)[row * nsb + (j >> 2)]);
+    OT* y = out + row * K + j * 64;
+    for (int w0 = 0; w0 < 64; w0 += 4) {
+        float v[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int ll = l + i, is = ll / 16;
-            const int q1 = (int)((ql[ll] & 0xF) | (((qh[ll] >> 0) & 3) << 4)) - 32;
-            const int q2 = (int)((ql[ll + 32] & 0xF) | (((qh[ll] >> 2) & 3) << 4)) - 32;
-            const int q3 = (int)((ql[ll] >> 4) | (((qh[ll] >> 4) & 3) << 4)) - 32;
-            const int q4 = (int)((ql[ll + 32] >> 4) | (((qh[ll] >> 6) & 3) << 4)) - 32;
-            v[0][i] = d * (float)sc[is] * (float)q1;
-            v[1][i] = d * (float)sc[is + 2] * (float)q2;
-            v[2][i] = d * (float)sc[is + 4] * (float)q3;
-            v[3][i] = d * (float)sc[is + 6] * (float)q4;
+            const int w = w0 + i;
+            const int code = ((ql[w & 31] >> (4 * (w >> 5))) & 0xF) | (((qh[w & 15] >> (2 * (w >> 4))) & 3) << 4);
+            v[i] = d * (float)sc[w >> 4] * (float)(code - 32);
         }
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) put4(y + 32 * qq + l, v[qq][0], v[qq][1], v[qq][2], v[qq][3]);
+        put4(y + w0, v[0], v[1], v[2], v[3]);
     }
 }
 
@@ -571,7 +588,7 @@ hipError_t launch_repack_q6k(const uint8_t* gguf, uint8_t* dst, int64_t n, int n
 }
 
 hipError_t launch_dequant_q6k(const uint8_t* src, void* out, bool bf16, int64_t n, int nsb, hipStream_t s) {
-    const int64_t t = n * nsb * 2;
+    const int64_t t = n * nsb * 4;
     if (t == 0) return hipSuccess;
     if (bf16)
         hipLaunchKernelGGL(k_dequant_q6k<bf16_t>, dim3(grid_for(t, 256)), dim3(256), 0, s, src, static_cast<bf16_t*>(out),

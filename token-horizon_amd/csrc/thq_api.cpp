@@ -459,8 +459,26 @@ int thq_weight_download(const thq_weight* w, void* host_blocks) {
         for (int64_t n = 0; n < w->N; ++n) {
             for (int64_t s = 0; s < nsb; ++s) {
                 uint8_t* blk = dst + (n * nsb + s) * 210;
-                std::memcpy(blk, qs.data() + n * (w->K / 2) + s * 128, 128);
-                std::memcpy(blk + 128, qs.data() + L.qh + n * (w->K / 4) + s * 64, 64);
+                // undo the regrouping by 64-weight step (thq_dev.hpp, q6k_layout)
+                const uint8_t* QL = qs.data() + n * (w->K / 2) + s * 128;
+                const uint8_t* QH = qs.data() + L.qh + n * (w->K / 4) + s * 64;
+                for (int h = 0; h < 2; ++h) {
+                    const uint8_t* a = QL + 64 * h;  // step 2h
+                    const uint8_t* b = a + 32;       // step 2h + 1
+                    for (int t = 0; t < 32; ++t) {
+                        blk[64 * h + t] = (uint8_t)((a[t] & 0x0F) | ((b[t] & 0x0F) << 4));
+                        blk[64 * h + 32 + t] = (uint8_t)((a[t] >> 4) | (b[t] & 0xF0));
+                    }
+                    // qh[32h + l] bits 2Q: quarter Q = 2e + o is step 2h + e, weight 32o + l
+                    for (int l = 0; l < 32; ++l) {
+                        uint8_t v = 0;
+                        for (int q = 0; q < 4; ++q) {
+                            const int w = 32 * (q & 1) + l;
+                            v |= (uint8_t)(((QH[16 * (2 * h + (q >> 1)) + (w & 15)] >> (2 * (w >> 4))) & 3) << (2 * q));
+                        }
+                        blk[128 + 32 * h + l] = v;
+                    }
+                }
                 std::memcpy(blk + 192, qs.data() + L.sc + n * (w->K / 16) + s * 16, 16);
                 std::memcpy(blk + 208, qs.data() + L.d + (n * nsb + s) * 2, 2);
             }

@@ -179,11 +179,18 @@ __device__ __forceinline__ uint4 ld_stream16(const void* p) {
 
 // Q6_K (GGML type 14, 210 B per 256 weights: u8 ql[128], u8 qh[64], i8
 // scales[16], f16 d) on the device: four row-major planes, each starting on a
-// 256-B boundary, with the bytes of every superblock in GGUF order:
-//   QL [N][K/2]   QH [N][K/4]   SC [N][K/16] (int8)   D [N][K/256] (f16)
-// A 128-weight half h of superblock s is then 64 contiguous QL bytes, 32 QH
-// bytes and 8 scales: w[128h + 32Q + l] = (d * sc[8h + 2Q + l/16]) *
-// (code - 32), code = ql nibble | qh 2-bit field << 4 (GGML's order).
+// 256-B boundary,
+//   QL [N][K/2]   QH [N][K/4]   SC [N][K/16] (int8)   D [N][K/256] (f16),
+// with the code bits regrouped by 64-weight step j (weights 64j .. 64j+63 of
+// the row): step j owns 32 QL bytes at 32j, 16 QH bytes at 16j, 4 scales at
+// 4j (GGUF order already groups them so) and d of superblock j/4:
+//   code(w) = (QL[32j + w % 32] >> 4 * (w / 32)) & 15
+//           | ((QH[16j + w % 16] >> 2 * (w / 16)) & 3) << 4,   w = 0..63
+//   weight  = (d * SC[4j + w / 16]) * (code - 32)               (GGML's order)
+// so every consumer of a step reads exactly its 52.5 bytes.  In GGUF order
+// (GGML dequantize_row_q6_K) step j = 2h + e of half h covers quarters 2e,
+// 2e + 1 (32 weights each), whose low nibbles share bytes with the other
+// step's and whose high bits share bytes with all four quarters.
 struct Q6Layout {
     size_t qh, sc, d, total;
 };
