@@ -174,8 +174,8 @@ int thq_quantize_act(thq_ctx* ctx, thq_dtype dot_type, const void* x_dev, thq_ac
  *   M == 1     decode GEMV (exact dequantized weights)
  *   M >= 2     MFMA GEMM; weights are rounded to bf16 on the MFMA path unless
  *              THQ_MODE_EXACT_W (or Q8_0 with M <= 64), activations bf16.
- *   x f32 with M >= 2 runs an exact f32 path, and so does Q6_K at M >= 2
- *   or with f32 x.
+ *   x f32 with M >= 2 runs an exact f32 path, and so does Q6_K with f32 x,
+ *   at M = 2..8 and with THQ_MODE_EXACT_W.
  * THQ_MODE_Q8ACT instead reproduces candle's default CPU k_quants::matmul:
  * x rows are quantized as thq_quantize_act does (into the context
  * workspace), every block dot is exact in integers and scaled in f32; only

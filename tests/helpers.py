@@ -50,6 +50,26 @@ def weight_bytes(qtype: int, n: int, k: int, seed: int = 0, sigma: float = 0.02)
     return _cache[key]
 
 
+def assert_close_dot(tag: str, got: np.ndarray, want: np.ndarray, x: np.ndarray, w: np.ndarray, rel: float,
+                     out_rel: float = 0.0):
+    """|got - want| <= rel * sqrt(sum_i (x[m, i] * w[n, i])^2) per element: the
+    scale of the error that rounding each weight to bf16 (unit roundoff 2^-8)
+    leaves in one dot product, whatever the norm of its weight row.  Its
+    ratio to that scale has sd ~1e-3 and a heavy tail: over 36864 outputs of
+    4096 x 12288 the largest is 8.3e-3 (Q6_K test weights) and 7.0e-3 (Q4_K),
+    measured with the f64 product of bf16-rounded weights, so rel = 2^-6
+    leaves a margin of ~2; out_rel * |want| is added for bf16 outputs."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    scale = np.sqrt(np.square(np.asarray(x, np.float64)) @ np.square(np.asarray(w, np.float64)).T)
+    bad = np.abs(got - want) > rel * scale + out_rel * np.abs(want) + 1e-30
+    if bad.any():
+        i = tuple(np.argwhere(bad)[0])
+        raise AssertionError(f"{tag}: {bad.sum()} elements out of tolerance; first {i}: got {got[i]} "
+                             f"want {want[i]} scale {scale[i]}")
+    return float((np.abs(got - want) / np.maximum(scale, 1e-30)).max())
+
+
 def q6k_bytes(n: int, k: int, seed: int = 0, dscale: float = 2e-4) -> np.ndarray:
     """Random Q6_K GGUF bytes [n, k/256 * 210]: every ql / qh / scale byte
     uniform (all 6-bit codes, scales -128..127), d = f16 of N(0, dscale)

@@ -10,10 +10,15 @@ The bars are as follows:
   - Upload / download / device upload / fuse round-trip the GGUF bytes exactly.
   - Dequantization is bit-exact: f32 against the oracle, and bf16 is the RNE
     of that f32.
-  - The weights stay exact in every Q6_K matmul kernel: the f32 bar of 1e-4
-    of the row L2 norm applies to bf16 and f32 activations alike, and so does
-    the per-element bound 2^-12 * max(|want|, 0.02 max|want|). bf16 outputs
-    get the reference's 2^-7 per element.
+  - The weights stay exact in the M = 1 GEMV and the generic kernel (M = 2..8,
+    f32 x): the f32 bar of 1e-4 of the row L2 norm applies to bf16 and f32
+    activations alike, and so does the per-element bound
+    2^-12 * max(|want|, 0.02 max|want|). bf16 outputs get the reference's
+    2^-7 per element.
+  - The MFMA GEMM (M > 8, bf16 x) rounds dequantized weights to bf16. It
+    equals the f64 product with bf16(dequant) weights to 1e-5 of the row
+    norm, and the exact product to 1e-2 of the row norm and, per element, to
+    2^-6 of that dot product's rounding-error scale sqrt(sum (x w)^2).
   - For argmax, indices are bit-exact against the argmax of the returned
     logits.
   - At the full LM-head shape (151936 x 4096), the check is against the f32
@@ -25,7 +30,7 @@ import pytest
 import torch
 
 import oracle as O
-from helpers import activations, assert_close_elem, q6k_bytes, rel_row_err
+from helpers import activations, assert_close_dot, assert_close_elem, q6k_bytes, rel_row_err
 
 pytestmark = pytest.mark.gpu
 
@@ -108,9 +113,9 @@ def test_q6k_gemv_m1(n, k):
     assert rel_row_err(yf, O.matmul(O.Q6_K, raw, n, k, xf)) <= 1e-4
 
 
-@pytest.mark.parametrize("m", [2, 5, 8, 17])
+@pytest.mark.parametrize("m", [2, 5, 8])
 @pytest.mark.parametrize("n,k", [(300, 2816), (1024, 4096)])
-def test_q6k_matmul_m_gt_1(n, k, m):
+def test_q6k_matmul_m_2_to_8(n, k, m):
     raw = q6k_bytes(n, k, seed=6)
     w = thq.QTensor.from_gguf_bytes(thq.Q6_K, raw, n, k)
     x = O.bf16_round(activations(m, k, seed=7))
@@ -118,6 +123,63 @@ def test_q6k_matmul_m_gt_1(n, k, m):
     y = tonp(thq.matmul(w, xdev(x), torch.float32))
     assert rel_row_err(y, want) <= 1e-4
     assert_close_elem(f"q6k m={m} {n}x{k}", y, want, 2.0 ** -12)
+
+
+@pytest.mark.parametrize("m", [9, 64, 300])
+@pytest.mark.parametrize("n,k", [(300, 2816), (4096, 12288)])
+def test_q6k_gemm(n, k, m):
+    """M > 8 with bf16 x: the MFMA GEMM, dequantized weights rounded to bf16
+    on the tile.  The kernel is pinned to the f64 product with exactly those
+    bf16 weights at 1e-5 of the row norm; against the exact product the bound
+    is 1e-2 of the row norm and, per element, 2^-6 of that dot product's own
+    rounding-error scale sqrt(sum (x w)^2) (the random d of the test weights
+    makes row norms vary, so a row-wide rms is no measure for one output);
+    bf16 outputs add their own rounding.  All rows beyond the 16 the oracle
+    checks are compared with the f32 product of the exact dequantization at
+    1e-2 of the row norm."""
+    raw = q6k_bytes(n, k, seed=18)
+    w = thq.QTensor.from_gguf_bytes(thq.Q6_K, raw, n, k)
+    x = O.bf16_round(activations(m, k, seed=19))
+    rows = slice(0, min(m, 16))
+    wdeq = O.dequantize(O.Q6_K, raw, n, k)
+    want = O.matmul(O.Q6_K, raw, n, k, x[rows])
+    # the tile's weights are exactly bf16(dequant): the kernel is pinned to the
+    # f64 product with those weights at the f32 accumulation bar
+    rounded = x[rows].astype(np.float64) @ O.bf16_round(wdeq).astype(np.float64).T
+    for out_dtype in (torch.float32, torch.bfloat16):
+        y = tonp(thq.matmul(w, xdev(x), out_dtype))
+        assert rel_row_err(y[rows], want) <= 1e-2
+        if out_dtype == torch.float32:
+            assert rel_row_err(y[rows], rounded) <= 1e-5
+            assert_close_dot(f"q6k gemm {n}x{k} m={m}", y[rows], want, x[rows], wdeq, 2.0 ** -6)
+        else:
+            assert_close_dot(f"q6k gemm bf16 {n}x{k} m={m}", y[rows], want, x[rows], wdeq, 2.0 ** -6, 2.0 ** -8)
+        if m > 16:
+            ref = (torch.from_numpy(x).cuda() @ w.dequantize().T).cpu().numpy()
+            assert rel_row_err(y, ref) <= 1e-2
+
+
+def test_q6k_gemm_prefill_and_gate_up():
+    """M = 2048 on the down shape (a Q4_K_M file's Q6_K ffn_down at prefill)
+    and the fused gate/up GEMM epilogue at M = 64."""
+    n, k, m = 4096, 12288, 2048
+    raw = q6k_bytes(n, k, seed=20)
+    w = thq.QTensor.from_gguf_bytes(thq.Q6_K, raw, n, k)
+    xt = torch.from_numpy(O.bf16_round(activations(m, k, seed=21))).cuda()
+    y = thq.matmul(w, xt.to(torch.bfloat16), torch.float32)
+    ref = xt @ w.dequantize().T
+    assert rel_row_err(tonp(y), tonp(ref)) <= 1e-2
+    half, k2, m2 = 520, 4096, 64
+    g_raw, u_raw = q6k_bytes(half, k2, seed=22), q6k_bytes(half, k2, seed=23)
+    fused = thq.QTensor.fuse([thq.QTensor.from_gguf_bytes(thq.Q6_K, g_raw, half, k2),
+                              thq.QTensor.from_gguf_bytes(thq.Q6_K, u_raw, half, k2)])
+    x2 = xdev(O.bf16_round(activations(m2, k2, seed=24)))
+    gu = tonp(thq.matmul(fused, x2, torch.float32))
+    got = tonp(thq.gate_up_silu(fused, x2, torch.bfloat16))
+    assert_close_elem("q6k gemm gate/up vs own matmul", got, O.bf16_bits_to_f32(O.gate_up_silu(gu)), 2.0 ** -7)
+    both = np.concatenate([g_raw, u_raw])
+    want = O.matmul(O.Q6_K, both, 2 * half, k2, tonp(x2)[:8])
+    assert rel_row_err(gu[:8], want) <= 1e-2
 
 
 def test_q6k_unaligned_x_and_empty():

@@ -337,18 +337,21 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict
     static_assert(MT >= 1 && (NW == 4 || NW == 8), "tile configuration");
     // copies per wave per K step: X = 8*BM 16-B slots over NW waves; packed
     // weights: Q4_K 256 slots of nibbles + 512 header dwords, Q8_0 512 slots
-    // of int8 + 128 scale dwords, spread so that every wave issues the same
-    // number of copies (some with part of the wave active)
+    // of int8 + 128 scale dwords, Q6_K 384 slots (QL low / high piece, QH
+    // piece of each row) + 128 scale dwords + 128 dwords holding d, spread so
+    // that every wave issues the same number of copies (some with part of
+    // the wave active)
+    constexpr bool Q6 = QT == 14;
     constexpr int XI = BM / (8 * NW);
-    constexpr int NIB = QT != 8 ? BN * 32 : BN * 64;   // packed weight bytes per raw slot
-    constexpr int AUX = QT != 8 ? BN * 16 : BN * 4;     // header / scale bytes per raw slot
+    constexpr int NIB = Q6 ? BN * 48 : (QT != 8 ? BN * 32 : BN * 64);  // packed weight bytes per raw slot
+    constexpr int AUX = Q6 ? BN * 8 : (QT != 8 ? BN * 16 : BN * 4);    // header / scale bytes per raw slot
     constexpr int RAW = NIB + AUX;
-    constexpr int NSLOT = QT != 8 ? 256 / NW : 512 / NW;      // 16-B weight slots per wave
-    constexpr int NI = NSLOT >= 64 ? NSLOT / 64 : 1;           // their copies
-    constexpr int NL = NSLOT >= 64 ? 64 : NSLOT;               // active lanes per copy
-    constexpr int HSLOT = QT != 8 ? 512 / NW : 128 / NW;      // header / scale dwords per wave
-    constexpr int HI = HSLOT >= 64 ? HSLOT / 64 : 1;
-    constexpr int HL = HSLOT >= 64 ? 64 : HSLOT;
+    constexpr int NSLOT = (Q6 ? 384 : (QT != 8 ? 256 : 512)) / NW;   // 16-B weight slots per wave
+    constexpr int NI = (NSLOT + 63) / 64;                            // their copies
+    constexpr int NL = NSLOT / NI;                                   // active lanes per copy
+    constexpr int HSLOT = (Q6 ? 256 : (QT != 8 ? 512 : 128)) / NW;   // header / scale dwords per wave
+    constexpr int HI = (HSLOT + 63) / 64;
+    constexpr int HL = HSLOT / HI;
     constexpr int WI = NI + HI;
     static_assert(XI >= 1 && NI * NL == NSLOT && HI * HL == HSLOT, "copy split");
     __shared__ __attribute__((aligned(16))) bf16_t Xs[3][BM * BK];
@@ -387,21 +390,42 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict
         return v ? r : (int64_t)0;
     };
     // packed weights: Q4_K slot j = h*128 + row (piece h of the row),
-    // Q8_0 slot j = (half*2 + c)*128 + row (bytes 32*half + 16*c .. +15);
-    // headers: Q4_K dword j = row*4 + p, Q8_0 dword j = row (two f16 scales)
-    uint32_t noff[NI], hoff[HI];
+    // Q8_0 slot j = (half*2 + c)*128 + row (bytes 32*half + 16*c .. +15),
+    // Q6_K slot j = p*128 + row (p = 0, 1: QL bytes 16p .. 16p+15 of the
+    // step, p = 2: its 16 QH bytes); headers: Q4_K dword j = row*4 + p, Q8_0
+    // dword j = row (two f16 scales), Q6_K dword j = row (the step's 4
+    // scales) and 128 + row (the dword holding the superblock's f16 d)
+    const Q6Layout q6l = q6k_layout(Q6 ? (GU ? 2 * up_off : nout) : 0, K);
+    uint32_t noff[NI], hoff[HI], nstr[NI], hq[HI];
+    bool hd[HI];
 #pragma unroll
     for (int i = 0; i < NI; ++i) {
-        const int j = wave * NSLOT + 64 * i + (lane < NL ? lane : 0);
+        const int j = wave * NSLOT + NL * i + (lane < NL ? lane : 0);
         const int row = j & 127, hc = j >> 7;
-        if (QT != 8) noff[i] = (uint32_t)q4k_piece(clamp_row(row), nsb, 0, hc, 0);
-        else noff[i] = (uint32_t)(clamp_row(row) * K + 32 * (hc >> 1) + 16 * (hc & 1));
+        if (Q6) {
+            noff[i] = hc < 2 ? (uint32_t)(clamp_row(row) * (K >> 1) + 16 * hc)
+                             : (uint32_t)(q6l.qh + clamp_row(row) * (K >> 2));
+            nstr[i] = hc < 2 ? 32u : 16u;  // bytes per K step
+        } else if (QT != 8) {
+            noff[i] = (uint32_t)q4k_piece(clamp_row(row), nsb, 0, hc, 0);
+        } else {
+            noff[i] = (uint32_t)(clamp_row(row) * K + 32 * (hc >> 1) + 16 * (hc & 1));
+        }
     }
 #pragma unroll
     for (int i = 0; i < HI; ++i) {
-        const int j = wave * HSLOT + 64 * i + (lane < HL ? lane : 0);
-        if (QT != 8) hoff[i] = (uint32_t)q4k_hdword(clamp_row(j >> 2), nsb, 0, j & 3);
-        else hoff[i] = (uint32_t)(clamp_row(j) * (K >> 5) * 2);
+        const int j = wave * HSLOT + HL * i + (lane < HL ? lane : 0);
+        hd[i] = false;
+        if (Q6) {
+            hd[i] = j >= 128;
+            const int64_t r = clamp_row(j & 127);
+            hoff[i] = (uint32_t)(q6l.sc + r * (K >> 4));
+            hq[i] = (uint32_t)(r * nsb);
+        } else if (QT != 8) {
+            hoff[i] = (uint32_t)q4k_hdword(clamp_row(j >> 2), nsb, 0, j & 3);
+        } else {
+            hoff[i] = (uint32_t)(clamp_row(j) * (K >> 5) * 2);
+        }
     }
     auto xcopy = [&](int kit, int slot) {
         const bf16_t* base = X + kit * BK;
@@ -410,15 +434,20 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict
     };
     auto wcopy = [&](int kit, int slot) {
         const uint32_t l = wlds + slot * RAW;
-        const uint8_t* nb = QT != 8 ? Wq + kit * 16 : Wq + kit * 64;
-        const uint8_t* hb = QT != 8 ? Wq + (kit >> 2) * 64 : Wa + kit * 4;
+        const uint8_t* nb = Q6 ? Wq : (QT != 8 ? Wq + kit * 16 : Wq + kit * 64);
+        const uint8_t* hb = Q6 ? Wq : (QT != 8 ? Wq + (kit >> 2) * 64 : Wa + kit * 4);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
-            if (NL == 64 || lane < NL) dma16(l + (wave * NSLOT + 64 * i) * 16, nb, noff[i]);
+            const uint32_t off = Q6 ? noff[i] + (uint32_t)kit * nstr[i] : noff[i];
+            if (NL == 64 || lane < NL) dma16(l + (wave * NSLOT + NL * i) * 16, nb, off);
         }
 #pragma unroll
         for (int i = 0; i < HI; ++i) {
-            if (HL == 64 || lane < HL) dma4(l + NIB + (wave * HSLOT + 64 * i) * 4, hb, hoff[i]);
+            // Q6_K d: the dword holding f16 number r*nsb + kit/4 of the D plane
+            const uint32_t off = !Q6 ? hoff[i]
+                                     : (hd[i] ? (uint32_t)q6l.d + (((hq[i] + (uint32_t)(kit >> 2)) * 2u) & ~3u)
+                                              : hoff[i] + 4u * (uint32_t)kit);
+            if (HL == 64 || lane < HL) dma4(l + NIB + (wave * HSLOT + HL * i) * 4, hb, off);
         }
     };
 
@@ -430,7 +459,8 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict
     const int wh = NW == 4 ? q : q >> 1;
     const int qbase = NW == 4 ? 0 : 2 * (q & 1);
     bool wvalid;
-    (void)tile_row<GU>(wc, bx, nout, up_off, wvalid);
+    const int64_t wrow = tile_row<GU>(wc, bx, nout, up_off, wvalid);
+    const uint32_t wpar = Q6 ? (uint32_t)((wvalid ? wrow : 0) * nsb) & 1u : 0u;  // parity of the row's first d
     // Per K step each thread converts 32 weights.  Byte -> f32 goes through
     // v_perm_b32 with an exponent byte (no int->float conversion):
     //   Q4_K nibble q:   bytes [0, 0, q, 0x43]        = 128 + q
@@ -441,14 +471,35 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict
     // sits in mantissa bits only; (2^15 + 128)*d = 257*128*d is exact in f32,
     // so the Q8_0 result is exact; Q4_K differs from d1*q - m1 by far less
     // than the bf16 rounding that follows).
+    //   Q6_K code c:     bytes [0, 0, c, 0x43]        = 128 + c
+    //                    w = fma(s, 128 + c, -160*s) = s*(c - 32), s = d*sc,
+    //                    exact before the bf16 rounding (one rounding, as
+    //                    the product (d*sc)*(c - 32))
     struct Raw {
         uint4 q0, q1;
-        float s0, c0, s1, c1;  // scale and offset of the tile row's two 32-weight halves
+        uint4 h;               // Q6_K QH bytes of the step
+        float s0, c0, s1, c1;  // scale and offset of the tile row's two 32-weight halves (Q6_K: 16-weight groups)
     };
     auto rload = [&](int slot, int kit) {
         Raw R;
         const uint8_t* w = &Wr[slot][0];
-        if (QT != 8) {
+        if constexpr (Q6) {
+            // 4 waves: thread half wh covers step weights 32wh .. +31 (QL pieces 0, 1,
+            // groups 2wh, 2wh + 1); 8 waves: weights 32wh + 16(q & 1) .. +15 (QL piece q & 1,
+            // group 2wh + (q & 1))
+            R.q0 = *reinterpret_cast<const uint4*>(w + ((NW == 4 ? 0 : (q & 1)) * BN + wc) * 16);
+            R.q1 = NW == 4 ? *reinterpret_cast<const uint4*>(w + (BN + wc) * 16) : R.q0;
+            R.h = *reinterpret_cast<const uint4*>(w + (2 * BN + wc) * 16);
+            const uint32_t scw = *reinterpret_cast<const uint32_t*>(w + NIB + wc * 4);
+            const uint32_t dw = *reinterpret_cast<const uint32_t*>(w + NIB + (BN + wc) * 4);
+            float d = f16_to_f32((uint16_t)(((wpar ^ ((uint32_t)kit >> 2)) & 1u) ? dw >> 16 : dw));
+            if (!wvalid) d = 0.0f;
+            const int g0 = NW == 4 ? 2 * wh : 2 * wh + (q & 1);
+            R.s0 = d * (float)(int)(int8_t)(scw >> (8 * g0));
+            R.s1 = NW == 4 ? d * (float)(int)(int8_t)(scw >> (8 * g0 + 8)) : R.s0;
+            R.c0 = 160.0f * R.s0;
+            R.c1 = 160.0f * R.s1;
+        } else if (QT != 8) {
             R.q0 = *reinterpret_cast<const uint4*>(w + (wh * BN + wc) * 16);
             R.q1 = R.q0;
             const uint32_t hw = *reinterpret_cast<const uint32_t*>(w + NIB + wc * 16 + (kit & 3) * 4);
@@ -484,7 +535,23 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict
         float sc, c;
         int ch;
         uint32_t E;
-        if (QT != 8) {
+        if constexpr (Q6) {
+            // chunk k: weights w0 .. w0+7 of the step, 4 waves w0 = 32wh + 8k,
+            // 8 waves w0 = 32wh + 16(q & 1) + 8k; codes from QL bytes w0 % 32 ..
+            // (nibble wh) and QH bytes w0 % 16 .. (field w0 / 16)
+            const uint4 src = (NW == 4 && k >= 2) ? R.q1 : R.q0;
+            const int sel = k & 1;
+            const uint32_t qa = sel ? src.z : src.x, qb = sel ? src.w : src.y;
+            const uint32_t ha = sel ? R.h.z : R.h.x, hb = sel ? R.h.w : R.h.y;
+            const int grp = NW == 4 ? 2 * wh + (k >> 1) : 2 * wh + (q & 1);
+            const int ns = 4 * wh, hs = 2 * grp;
+            a = ((qa >> ns) & 0x0F0F0F0Fu) | (((ha >> hs) & 0x03030303u) << 4);
+            b = ((qb >> ns) & 0x0F0F0F0Fu) | (((hb >> hs) & 0x03030303u) << 4);
+            sc = (NW == 4 && k >= 2) ? R.s1 : R.s0;
+            c = (NW == 4 && k >= 2) ? R.c1 : R.c0;
+            ch = NW == 4 ? 4 * wh + k : 4 * wh + 2 * (q & 1) + k;
+            E = 0x43434343u;
+        } else if (QT != 8) {
             // low nibbles = first 32 weights of the step, high = second 32; 4 waves:
             // quarters 0,1 low and 2,3 high; 8 waves: the half is q & 1
             const int hi = NW == 4 ? (k >> 1) : (q & 1);
@@ -709,9 +776,14 @@ static hipError_t gemm_t(const GemmPlan& p, const WeightView& w, const bf16_t* x
     const int64_t up_off = GU ? w.N / 2 : 0;
     dim3 grid((unsigned)p.tiles_n, (unsigned)p.tiles_m, (unsigned)p.splits);
     const uint64_t xbytes = (uint64_t)M * (uint64_t)w.K * 2;
-    const uint64_t wbytes = QT != 8 ? (uint64_t)((w.N + 3) / 4) * (uint64_t)(w.K / 256) * 576
-                                     : (uint64_t)w.N * (uint64_t)w.K;
-    if (!EXACT && xbytes < (1ull << 32) && wbytes < (1ull << 32) && !env_int("THQ_GEMM_V1", 0)) {
+    const uint64_t wbytes = QT == 14  ? (uint64_t)q6k_layout(w.N, w.K).total
+                            : QT != 8 ? (uint64_t)((w.N + 3) / 4) * (uint64_t)(w.K / 256) * 576
+                                      : (uint64_t)w.N * (uint64_t)w.K;
+    if constexpr (QT == 14) {
+        // Q6_K runs the DMA kernel only (32-bit copy offsets, rounded weights)
+        if (EXACT || xbytes >= (1ull << 32) || wbytes >= (1ull << 32)) return hipErrorInvalidValue;
+    }
+    if (QT == 14 || (!EXACT && xbytes < (1ull << 32) && wbytes < (1ull << 32) && !env_int("THQ_GEMM_V1", 0))) {
         const unsigned nb = (unsigned)(p.tiles_n * p.tiles_m * p.splits);
         constexpr int WM = BM == 64 ? 2 : 4;  // 8 waves (2 per SIMD) for the large tiles
         if (p.splits == 1) {
@@ -727,18 +799,22 @@ static hipError_t gemm_t(const GemmPlan& p, const WeightView& w, const bf16_t* x
                            static_cast<YT*>(y), M, nout, up_off, (int64_t)w.N, p.splits);
         return hipGetLastError();
     }
-    if (p.splits == 1) {
-        hipLaunchKernelGGL((k_gemm<QT, EXACT, BM, GU, YT, false>), grid, dim3(256), 0, s, w.q, w.aux, x, y, M,
-                           (int)w.K, nout, up_off, nout, p.kps);
+    if constexpr (QT == 14) {
+        return hipErrorInvalidValue;
+    } else {
+        if (p.splits == 1) {
+            hipLaunchKernelGGL((k_gemm<QT, EXACT, BM, GU, YT, false>), grid, dim3(256), 0, s, w.q, w.aux, x, y, M,
+                               (int)w.K, nout, up_off, nout, p.kps);
+            return hipGetLastError();
+        }
+        // partials in natural weight-row order: ld = N rows
+        hipLaunchKernelGGL((k_gemm<QT, EXACT, BM, GU, float, true>), grid, dim3(256), 0, s, w.q, w.aux, x, (void*)ws,
+                           M, (int)w.K, nout, up_off, (int64_t)w.N, p.kps);
+        const int64_t total = (int64_t)M * nout;
+        hipLaunchKernelGGL((k_split_reduce<GU, YT>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ws,
+                           static_cast<YT*>(y), M, nout, up_off, (int64_t)w.N, p.splits);
         return hipGetLastError();
     }
-    // partials in natural weight-row order: ld = N rows
-    hipLaunchKernelGGL((k_gemm<QT, EXACT, BM, GU, float, true>), grid, dim3(256), 0, s, w.q, w.aux, x, (void*)ws, M,
-                       (int)w.K, nout, up_off, (int64_t)w.N, p.kps);
-    const int64_t total = (int64_t)M * nout;
-    hipLaunchKernelGGL((k_split_reduce<GU, YT>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ws,
-                       static_cast<YT*>(y), M, nout, up_off, (int64_t)w.N, p.splits);
-    return hipGetLastError();
 }
 
 template <int QT, bool EXACT, bool GU, typename YT>
@@ -769,6 +845,13 @@ hipError_t launch_gemm(const GemmPlan& p, const WeightView& w, const void* x, vo
                             : gemm_bm<13, false, true, bf16_t>(p, w, xb, y, M, ws, s);
         return yf32 ? gemm_bm<13, false, false, float>(p, w, xb, y, M, ws, s)
                     : gemm_bm<13, false, false, bf16_t>(p, w, xb, y, M, ws, s);
+    }
+    if (w.qtype == 14) {
+        if (exact) return hipErrorInvalidValue;
+        if (gu) return yf32 ? gemm_bm<14, false, true, float>(p, w, xb, y, M, ws, s)
+                            : gemm_bm<14, false, true, bf16_t>(p, w, xb, y, M, ws, s);
+        return yf32 ? gemm_bm<14, false, false, float>(p, w, xb, y, M, ws, s)
+                    : gemm_bm<14, false, false, bf16_t>(p, w, xb, y, M, ws, s);
     }
     if (exact) {
         if (gu) return yf32 ? gemm_bm<8, true, true, float>(p, w, xb, y, M, ws, s)

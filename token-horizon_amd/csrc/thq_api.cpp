@@ -246,7 +246,9 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
             if (rc) return rc;
         }
         e = thq::launch_gemv_mfma(gp, v, x, y, yf32, gu, (int)m, nout, up_off, static_cast<float*>(ctx->ws), s);
-    } else if (!xf32 && !q6 && aligned16(x) && !(q4 && ((flags & THQ_MODE_EXACT_W) || w->K % 256))) {
+    } else if (!xf32 && aligned16(x) && !((q4 || q6) && ((flags & THQ_MODE_EXACT_W) || w->K % 256)) &&
+               !(q6 && (m <= 8 || thq::q6k_layout(w->N, w->K).total >= (1ull << 32) ||
+                        (uint64_t)m * (uint64_t)w->K * 2 >= (1ull << 32)))) {
         const bool exact = (flags & THQ_MODE_EXACT_W) || (w->qtype == THQ_Q8_0 && m <= 64);
         thq::GemmPlan p = thq::plan_gemm(v.qtype, exact, m, w->N, w->K, gu);
         std::lock_guard<std::mutex> lk(ctx->mu);
