@@ -32,6 +32,13 @@
 //         second sub-block (k0 + 32 + ...).
 //   Q8_0  lane loads bytes 16g..16g+15 of each of the unit's two blocks, same
 //         k mapping (first block = k0..k0+31, second = k0+32..k0+63).
+//   Q6_K  a unit is one 64-weight step of the QL / QH planes (thq_dev.hpp,
+//         q6k_layout); each MFMA takes one whole 16-weight scale group G,
+//         lane half g supplying its positions 8g..8g+7: QL bytes 8g..8g+7
+//         (groups 0 / 2 in the low / high nibbles) and 16+8g.. (groups 1 / 3),
+//         QH bytes 8g..8g+7 (group G in bits 2G).  B = bf16(128 + code), and
+//         per group sum x*w = s*(A - 160*S16), s = d*sc, S16 = sum x over the
+//         group; the block's K range is at most 4096 (256 group sums in LDS).
 // The MFMA output lane holds column n and rows 8*(e/4) + 4*g + e%4; with
 // M <= 8 only e = 0..3 (rows 4g + e) are live.  Each wave accumulates its
 // slice in registers; the block sums the slices in LDS in wave order
@@ -72,6 +79,8 @@ template <int QT>
 struct Chunk {
     uint4 w[QT != 8 ? 4 : 8];
     uint32_t s[4];
+    uint2 h[4];   // Q6_K QH bytes per unit
+    uint32_t d;   // Q6_K f16 d
 };
 
 template <int CTRL>
@@ -90,7 +99,7 @@ __global__ __launch_bounds__(512, QT != 8 ? 4 : 2) void k_gemv_mfma(const uint8_
     // staged activation rows (row stride Kb + 8: rows start 16 B apart in bank
     // order), sub-block sums S[sb][8] and the cross-wave reduction buffer
     __shared__ __attribute__((aligned(16))) bf16_t xs[XS_ELEMS + 8 * 8];
-    __shared__ __attribute__((aligned(16))) float Ss[QT != 8 ? KB_MAX / 32 : 1][8];
+    __shared__ __attribute__((aligned(16))) float Ss[QT != 8 ? KB_MAX / 32 : 1][8];  // Q6_K: 16-wide sums, Kb <= 4096
     // the cross-wave reduction reuses the staging buffer once all waves are done with it
     float(*red)[8][32] = reinterpret_cast<float(*)[8][32]>(&xs[0]);
     static_assert(MAXW * 8 * 32 * 4 <= XS_ELEMS * 2, "reduction buffer exceeds the staging buffer");
@@ -119,7 +128,15 @@ __global__ __launch_bounds__(512, QT != 8 ? 4 : 2) void k_gemv_mfma(const uint8_
 
     const uint8_t* pw;
     const uint8_t* ps;
-    if (QT != 8) {
+    const uint8_t* ph = nullptr;
+    const uint16_t* pd = nullptr;
+    if (QT == 14) {
+        const Q6Layout L = q6k_layout(nrows, K);
+        pw = Wq + row * (K >> 1) + 8 * g;
+        ph = Wq + L.qh + row * (K >> 2) + 8 * g;
+        ps = Wq + L.sc + row * (K >> 4);
+        pd = reinterpret_cast<const uint16_t*>(Wq + L.d) + row * (K >> 8);
+    } else if (QT != 8) {
         const int nsb = K >> 8;
         pw = Wq + q4k_piece(row, nsb, 0, g, 0);
         ps = Wq + q4k_hdword(row, nsb, 0, 0);
@@ -128,7 +145,22 @@ __global__ __launch_bounds__(512, QT != 8 ? 4 : 2) void k_gemv_mfma(const uint8_
         ps = Wa + row * (K >> 5) * 2;
     }
     auto load = [&](Chunk<QT>& C, int c) {
-        if (QT != 8) {
+        if constexpr (QT == 14) {
+            // scales and d first (in-order wait counters)
+            const uint4 sv = *reinterpret_cast<const uint4*>(ps + (int64_t)c * 16);
+            C.s[0] = sv.x; C.s[1] = sv.y; C.s[2] = sv.z; C.s[3] = sv.w;
+            C.d = pd[c];
+            // one base per chunk: the unit offsets fold into the loads' immediates
+            const uint8_t* qlc = pw + (int64_t)c * 128;
+            const uint8_t* qhc = ph + (int64_t)c * 64;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const uint2 lo = *reinterpret_cast<const uint2*>(qlc + u * 32);
+                const uint2 hi = *reinterpret_cast<const uint2*>(qlc + u * 32 + 16);
+                C.w[u] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+                C.h[u] = *reinterpret_cast<const uint2*>(qhc + u * 16);
+            }
+        } else if (QT != 8) {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 C.w[u] = *reinterpret_cast<const uint4*>(pw + (int64_t)c * 64 + u * 16);
@@ -172,7 +204,18 @@ __global__ __launch_bounds__(512, QT != 8 ? 4 : 2) void k_gemv_mfma(const uint8_
             const int m = ch / cpr, c = ch - m * cpr;
             const uint4 v = xv[i];
             *reinterpret_cast<uint4*>(&xs[m * XR + 8 * c]) = v;
-            if (QT != 8) {
+            if (QT == 14) {
+                // lanes 2j, 2j+1 hold the 2 chunks of one 16-wide group (pairs stay whole)
+                const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+                bf16x2_t p[4];
+                __builtin_memcpy(p, &v, 16);
+                float t = __builtin_amdgcn_fdot2_f32_bf16(p[0], one, 0.0f, false);
+                t = __builtin_amdgcn_fdot2_f32_bf16(p[1], one, t, false);
+                t = __builtin_amdgcn_fdot2_f32_bf16(p[2], one, t, false);
+                t = __builtin_amdgcn_fdot2_f32_bf16(p[3], one, t, false);
+                t = dpp_add<0xB1>(t);  // quad_perm [1,0,3,2]
+                if ((c & 1) == 0) Ss[c >> 1][m] = t;
+            } else if (QT != 8) {
                 // lanes 4j..4j+3 hold the 4 chunks of one sub-block (quads stay whole)
                 const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
                 bf16x2_t p[4];
@@ -190,13 +233,49 @@ __global__ __launch_bounds__(512, QT != 8 ? 4 : 2) void k_gemv_mfma(const uint8_
     __syncthreads();
 
     // 32x32 A operand row n (clamped to M-1)
-    const bf16_t* xa = &xs[(n < M ? n : M - 1) * XR + 16 * g];
+    const bf16_t* xa = &xs[(n < M ? n : M - 1) * XR + (QT == 14 ? 8 : 16) * g];
     const f32x16_t z16 = {};
     float tot[E];
 #pragma unroll
     for (int e = 0; e < E; ++e) tot[e] = 0.0f;
 
     auto compute = [&](const Chunk<QT>& C, int c) {
+        if constexpr (QT == 14) {
+            const float dd = valid ? f16_to_f32((uint16_t)C.d) : 0.0f;
+            const uint32_t M4 = 0x0F0F0F0Fu;
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int kl = (c * 4 + u) * 64 - kb0;  // offset inside the staged range
+                const uint4 q = C.w[u];
+                const uint2 h = C.h[u];
+                uint32_t lo[4], hi[4];
+                lo[0] = (q.x & M4) | ((h.x & 0x03030303u) << 4);
+                hi[0] = (q.y & M4) | ((h.y & 0x03030303u) << 4);
+                lo[1] = (q.z & M4) | ((h.x & 0x0C0C0C0Cu) << 2);
+                hi[1] = (q.w & M4) | ((h.y & 0x0C0C0C0Cu) << 2);
+                lo[2] = ((q.x >> 4) & M4) | (h.x & 0x30303030u);
+                hi[2] = ((q.y >> 4) & M4) | (h.y & 0x30303030u);
+                lo[3] = ((q.z >> 4) & M4) | ((h.x >> 2) & 0x30303030u);
+                hi[3] = ((q.w >> 4) & M4) | ((h.y >> 2) & 0x30303030u);
+#pragma unroll
+                for (int G = 0; G < 4; ++G) {
+                    const uint4 a = *reinterpret_cast<const uint4*>(xa + kl + 16 * G);
+                    const f32x4_t S = *reinterpret_cast<const f32x4_t*>(&Ss[(kl >> 4) + G][4 * g]);
+                    const float sg = dd * (float)(int)(int8_t)(C.s[u] >> (8 * G));
+                    const f32x16_t A = mfma32x16(as_bf16x8(a), nib_bf16x8(lo[G], hi[G]), z16);
+#pragma unroll
+                    for (int e = 0; e < E; ++e) tot[e] = __builtin_fmaf(sg, __builtin_fmaf(-160.0f, S[e], A[e]), tot[e]);
+                    // the 16 MFMAs of a chunk are independent: left free, the compiler
+                    // issues them all first and sinks their FMAs past the next chunk's
+                    // loads, keeping every accumulator live; pinning tot here (and a
+                    // scheduling barrier) keeps one group in flight at a time
+#pragma unroll
+                    for (int e = 0; e < E; ++e) asm volatile("" : "+v"(tot[e]));
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            return;
+        }
         float d = 0.0f, dm = 0.0f;
         if (QT == 12) {
             d = f16_to_f32((uint16_t)__builtin_amdgcn_perm(C.s[1], C.s[0], 0x0c0c0703u));
@@ -357,7 +436,7 @@ hipError_t run_e(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* 
 GemvPlan plan_gemv_mfma(int qtype, int64_t M, int64_t N_rows, int64_t K, bool gu) {
     GemvPlan p;
     if (M < 1 || M > 8 || K < 256 || K % 256 || K > (1 << 20)) return p;
-    if (qtype != 8 && qtype != 12 && qtype != 13) return p;
+    if (qtype != 8 && qtype != 12 && qtype != 13 && qtype != 14) return p;
     const int64_t nout = gu ? N_rows / 2 : N_rows;
     const int64_t tiles = gu ? (nout + 15) / 16 : (nout + 31) / 32;
     const int chunks = (int)(K / 256);
@@ -368,7 +447,7 @@ GemvPlan plan_gemv_mfma(int qtype, int64_t M, int64_t N_rows, int64_t K, bool gu
     for (int s = 1; s <= chunks && s <= 16; ++s) {
         if (chunks % s || (fs && s != fs)) continue;
         const int64_t kb = K / s;
-        if (kb > KB_MAX || M * kb > XS_ELEMS) continue;
+        if (kb > KB_MAX || M * kb > XS_ELEMS || (qtype == 14 && kb > 4096)) continue;
         const int cps = chunks / s;
         int w = 0;
         for (int c = MAXW; c >= 1; --c)
@@ -401,6 +480,12 @@ hipError_t launch_gemv_mfma(const GemvPlan& p, const WeightView& w, const void* 
                             : run_e<13, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
         return yf32 ? run_e<13, false, float>(p, w, xb, y, M, nout, up_off, ws, s)
                     : run_e<13, false, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
+    }
+    if (w.qtype == 14) {
+        if (gu) return yf32 ? run_e<14, true, float>(p, w, xb, y, M, nout, up_off, ws, s)
+                            : run_e<14, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
+        return yf32 ? run_e<14, false, float>(p, w, xb, y, M, nout, up_off, ws, s)
+                    : run_e<14, false, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
     }
     if (gu) return yf32 ? run_e<8, true, float>(p, w, xb, y, M, nout, up_off, ws, s)
                         : run_e<8, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);

@@ -231,7 +231,7 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
         return v && !strcmp(v, "mfma");
     }();
     const bool q6 = w->qtype == THQ_Q6_K;
-    const thq::GemvPlan gp = (!xf32 && !q6 && aligned16(x) && m <= 8)
+    const thq::GemvPlan gp = (!xf32 && aligned16(x) && m <= 8)
                                  ? thq::plan_gemv_mfma(v.qtype, m, w->N, w->K, gu)
                                  : thq::GemvPlan{};
     const bool skinny = gp.waves > 0;
