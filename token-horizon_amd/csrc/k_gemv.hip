@@ -358,6 +358,150 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_bf16_1s(const uint8_t* W, con
     q4k_unit_store<GU, YT>(y, gq, nout, lane, acc);
 }
 
+// ------------------------------------------------------------------ Q4_K M = 2..4, bf16 x
+// The one-shot kernel with MR activation rows (K <= 4096): every weight byte
+// is still read once per call, and each nibble pair's v_perm (bf16 128 + q)
+// is built once and shared by the MR rows' v_dot2.  Rows m >= M are staged
+// from row M-1 (in bounds) and never stored.
+template <bool GU, bool AFF, int MR>
+__device__ __forceinline__ void q4k_unit_compute_rows(float (&acc)[MR][GU ? 8 : 4], const Q4Unit<GU>& U,
+                                                      const uint32_t (&xlo)[MR][16], const uint32_t (&xhi)[MR][16],
+                                                      const float (&sxlo)[MR], const float (&sxhi)[MR]) {
+    const uint32_t C43 = 0x43434343u;
+#pragma unroll
+    for (int qi = 0; qi < Q4Unit<GU>::NQ; ++qi) {
+        const uint32_t hq[4] = {U.hdr[qi].x, U.hdr[qi].y, U.hdr[qi].z, U.hdr[qi].w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint4 v0 = U.nib[qi][r][0], v1 = U.nib[qi][r][1];
+            const uint32_t qw[8] = {v0.x, v0.y, v0.z, v0.w, v1.x, v1.y, v1.z, v1.w};
+            float alo[MR], ahi[MR];
+#pragma unroll
+            for (int m = 0; m < MR; ++m) alo[m] = ahi[m] = 0.0f;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const uint32_t lo = qw[t] & 0x0F0F0F0Fu, hi = (qw[t] >> 4) & 0x0F0F0F0Fu;
+                const uint32_t p0 = __builtin_amdgcn_perm(C43, lo, 0x04010400u);
+                const uint32_t p1 = __builtin_amdgcn_perm(C43, lo, 0x04030402u);
+                const uint32_t p2 = __builtin_amdgcn_perm(C43, hi, 0x04010400u);
+                const uint32_t p3 = __builtin_amdgcn_perm(C43, hi, 0x04030402u);
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    alo[m] = dot2_bf16(p0, xlo[m][2 * t], alo[m]);
+                    alo[m] = dot2_bf16(p1, xlo[m][2 * t + 1], alo[m]);
+                    ahi[m] = dot2_bf16(p2, xhi[m][2 * t], ahi[m]);
+                    ahi[m] = dot2_bf16(p3, xhi[m][2 * t + 1], ahi[m]);
+                }
+            }
+            const uint32_t h = hq[r];
+            if constexpr (AFF) {
+                const float sc = aff_scale(h), bi = aff_bias(h);
+#pragma unroll
+                for (int m = 0; m < MR; ++m) {
+                    const float sx = sxlo[m] + sxhi[m];
+                    const float a = __builtin_fmaf(sc, __builtin_fmaf(-128.0f, sx, alo[m] + ahi[m]), acc[m][4 * qi + r]);
+                    acc[m][4 * qi + r] = __builtin_fmaf(bi, sx, a);
+                    asm volatile("" : "+v"(acc[m][4 * qi + r]));
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                continue;
+            }
+            const uint32_t t0 = quad_bcast<0>(h), t1 = quad_bcast<1>(h);
+            const uint32_t t2 = quad_bcast<2>(h), t3 = quad_bcast<3>(h);
+            const float d = f16_to_f32((uint16_t)__builtin_amdgcn_perm(t1, t0, 0x0c0c0703u));
+            const float dmin = f16_to_f32((uint16_t)__builtin_amdgcn_perm(t3, t2, 0x0c0c0703u));
+            const float sc0 = (float)(h & 63u), m0 = (float)((h >> 6) & 63u);
+            const float sc1 = (float)((h >> 12) & 63u), m1 = (float)((h >> 18) & 63u);
+#pragma unroll
+            for (int m = 0; m < MR; ++m) {
+                const float dot = __builtin_fmaf(sc1, ahi[m], sc0 * alo[m]);
+                const float ssc = __builtin_fmaf(sc1, sxhi[m], sc0 * sxlo[m]);
+                const float smn = __builtin_fmaf(m1, sxhi[m], m0 * sxlo[m]);
+                const float a = __builtin_fmaf(d, __builtin_fmaf(-128.0f, ssc, dot), acc[m][4 * qi + r]);
+                acc[m][4 * qi + r] = __builtin_fmaf(-dmin, smn, a);
+            }
+            // one weight row at a time: left free, the compiler builds every row's
+            // perms up front (hundreds of VGPRs, occupancy 1)
+#pragma unroll
+            for (int m = 0; m < MR; ++m) asm volatile("" : "+v"(acc[m][4 * qi + r]));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+}
+
+template <int MR, bool GU, bool AFF, bool FULL, typename YT>
+__global__ __launch_bounds__(256) void k_gemv_q4k_bf16_rows(const uint8_t* W, const bf16_t* x, YT* __restrict__ y,
+                                                           int M, int64_t nout, int K, int64_t up_off,
+                                                           int64_t nquads) {
+    static_assert(MR == 2 || MR == 4, "two or four activation rows");
+    extern __shared__ uint4 lds[];  // x rows (MR x K bf16)
+    const int lane = threadIdx.x & 63;
+    const int64_t gq = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const int nsb = K >> 8;
+    const int nx = K >> 3;
+    const int c0 = threadIdx.x < nx ? threadIdx.x : nx - 1;
+    const int c1 = threadIdx.x + 256 < nx ? threadIdx.x + 256 : nx - 1;
+    const uint4* xg = reinterpret_cast<const uint4*>(x);
+    const int r1 = 1 < M ? 1 : M - 1, r2 = 2 < M ? 2 : M - 1, r3 = 3 < M ? 3 : M - 1;
+    // x loads first (named registers: arrays live across the compiler barrier spill)
+    const uint4 xa0 = xg[c0], xa1 = xg[c1];
+    const uint4 xb0 = xg[r1 * nx + c0], xb1 = xg[r1 * nx + c1];
+    uint4 xc0 = xb0, xc1 = xb1, xd0 = xb0, xd1 = xb1;
+    if constexpr (MR == 4) {
+        xc0 = xg[r2 * nx + c0];
+        xc1 = xg[r2 * nx + c1];
+        xd0 = xg[r3 * nx + c0];
+        xd1 = xg[r3 * nx + c1];
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    Q4Unit<GU> A;
+    q4k_unit_load<GU>(A, W, gq < nquads ? gq : nquads - 1, 0, up_off, nsb, lane);
+    const bool w0 = threadIdx.x < nx, w1 = threadIdx.x + 256 < nx;
+    if (w0) { lds[threadIdx.x] = xa0; lds[nx + threadIdx.x] = xb0; }
+    if (w1) { lds[threadIdx.x + 256] = xa1; lds[nx + threadIdx.x + 256] = xb1; }
+    if constexpr (MR == 4) {
+        if (w0) { lds[2 * nx + threadIdx.x] = xc0; lds[3 * nx + threadIdx.x] = xd0; }
+        if (w1) { lds[2 * nx + threadIdx.x + 256] = xc1; lds[3 * nx + threadIdx.x + 256] = xd1; }
+    }
+    __syncthreads();
+    if (gq >= nquads) return;
+    const int s = lane >> 2;
+    const uint32_t live = (FULL || s < nsb) ? 0xFFFFFFFFu : 0u;
+    const int xoff = ((FULL || s < nsb) ? s : 0) * 32 + 8 * (lane & 3);
+    uint32_t xlo[MR][16], xhi[MR][16];
+    float sxlo[MR], sxhi[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        const uint4* xp = lds + m * nx + xoff;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint4 p = xp[v], q = xp[4 + v];
+            xlo[m][4 * v] = p.x & live; xlo[m][4 * v + 1] = p.y & live;
+            xlo[m][4 * v + 2] = p.z & live; xlo[m][4 * v + 3] = p.w & live;
+            xhi[m][4 * v] = q.x & live; xhi[m][4 * v + 1] = q.y & live;
+            xhi[m][4 * v + 2] = q.z & live; xhi[m][4 * v + 3] = q.w & live;
+        }
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            a = dot2_bf16(xlo[m][i], 0x3F803F80u, a);  // bf16 (1, 1)
+            b = dot2_bf16(xhi[m][i], 0x3F803F80u, b);
+        }
+        sxlo[m] = a;
+        sxhi[m] = b;
+    }
+    float acc[MR][GU ? 8 : 4];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int i = 0; i < (GU ? 8 : 4); ++i) acc[m][i] = 0.0f;
+    q4k_unit_compute_rows<GU, AFF, MR>(acc, A, xlo, xhi, sxlo, sxhi);
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+        if (m < M) q4k_unit_store<GU, YT>(y + (int64_t)m * nout, gq, nout, lane, acc[m]);
+}
+
 // ------------------------------------------------------------------ Q4_K M=1, f32 x
 template <int KC, int R, bool GU, bool AFF, typename YT>
 __global__ __launch_bounds__(256) void k_gemv1_q4k_f32(const uint8_t* __restrict__ W, const float* __restrict__ x,
@@ -689,6 +833,46 @@ static hipError_t gemv1_q8_t(const int8_t* Q, const uint16_t* D, const XT* x, YT
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+bool gemv_rows_supported(int qtype, int M, int K, bool gu, int64_t n_rows) {
+    return (qtype == 12 || qtype == 13) && M >= 2 && M <= 4 && K % 256 == 0 && K <= 4096 &&
+           (!gu || (n_rows / 2) % 4 == 0);
+}
+
+template <int MR, bool GU, bool AFF, typename YT>
+static void rows_t(const uint8_t* W, const bf16_t* x, YT* y, int M, int64_t nout, int K, int64_t up_off,
+                   hipStream_t s) {
+    const int64_t nquads = (nout + 3) / 4;
+    const dim3 grid((unsigned)((nquads + 3) / 4));
+    const size_t lds = (size_t)MR * K * 2;
+    if (K == 4096)
+        hipLaunchKernelGGL((k_gemv_q4k_bf16_rows<MR, GU, AFF, true, YT>), grid, dim3(256), lds, s, W, x, y, M, nout, K,
+                           up_off, nquads);
+    else
+        hipLaunchKernelGGL((k_gemv_q4k_bf16_rows<MR, GU, AFF, false, YT>), grid, dim3(256), lds, s, W, x, y, M, nout,
+                           K, up_off, nquads);
+}
+
+template <bool GU, bool AFF, typename YT>
+static hipError_t rows_m(const uint8_t* W, const bf16_t* x, YT* y, int M, int64_t nout, int K, int64_t up_off,
+                         hipStream_t s) {
+    if (M == 2) rows_t<2, GU, AFF, YT>(W, x, y, M, nout, K, up_off, s);
+    else rows_t<4, GU, AFF, YT>(W, x, y, M, nout, K, up_off, s);
+    return hipGetLastError();
+}
+
+hipError_t launch_gemv_rows(const WeightView& w, const void* x, void* y, bool yf32, bool gu, int M, int64_t nout,
+                            int64_t up_off, hipStream_t s) {
+    const int K = (int)w.K;
+    if (!gemv_rows_supported(w.qtype, M, K, gu, w.N)) return hipErrorInvalidValue;
+    const bf16_t* xb = static_cast<const bf16_t*>(x);
+#define THQ_R(GU_, AFF_)                                                                   \
+    (yf32 ? rows_m<GU_, AFF_, float>(w.q, xb, (float*)y, M, nout, K, up_off, s)             \
+          : rows_m<GU_, AFF_, bf16_t>(w.q, xb, (bf16_t*)y, M, nout, K, up_off, s))
+    if (w.qtype == 13) return gu ? THQ_R(true, true) : THQ_R(false, true);
+    return gu ? THQ_R(true, false) : THQ_R(false, false);
+#undef THQ_R
 }
 
 bool gemv1_supported(int qtype, int K, bool gu, int64_t n_rows) {

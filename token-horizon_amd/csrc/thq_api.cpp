@@ -237,8 +237,15 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
     const bool skinny = gp.waves > 0;
     // the 4-bit tile kernels need whole superblocks (MLX affine K % 256 != 0 runs the generic kernel)
     const bool q4 = w->qtype == THQ_Q4_K || w->qtype == THQ_MLX_Q4;
+    // 2..4 bf16 rows of Q4_K / MLX affine at K <= 4096: the VALU row kernel (THQ_GEMV_ROWS=0: MFMA)
+    static const bool rows_on = [] {
+        const char* v = getenv("THQ_GEMV_ROWS");
+        return !(v && !strcmp(v, "0"));
+    }();
     if (m == 1 && !(m1_mfma && skinny) && aligned16(x) && thq::gemv1_supported(v.qtype, (int)w->K, gu, w->N)) {
         e = thq::launch_gemv1(v, x, xf32, y, yf32, gu, nout, up_off, s);
+    } else if (rows_on && !xf32 && aligned16(x) && thq::gemv_rows_supported(v.qtype, (int)m, (int)w->K, gu, w->N)) {
+        e = thq::launch_gemv_rows(v, x, y, yf32, gu, (int)m, nout, up_off, s);
     } else if (skinny) {
         std::lock_guard<std::mutex> lk(ctx->mu);
         if (gp.workspace_bytes) {
