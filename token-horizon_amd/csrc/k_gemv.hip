@@ -502,6 +502,93 @@ __global__ __launch_bounds__(256) void k_gemv_q4k_bf16_rows(const uint8_t* W, co
         if (m < M) q4k_unit_store<GU, YT>(y + (int64_t)m * nout, gq, nout, lane, acc[m]);
 }
 
+// K-split variant of the row kernel for 4096 < K <= 16384 and two activation
+// rows: the block and chunk structure of k_gemv1_q4k_bf16_ks with QPB = 2
+// row quads, both rows' x staged in LDS (4 pieces per thread per row).
+template <int KC, bool GU, bool AFF, typename YT>
+__global__ __launch_bounds__(128 * KC) void k_gemv_q4k_bf16_ks_rows(const uint8_t* W, const bf16_t* x,
+                                                                   YT* __restrict__ y, int M, int64_t nout, int K,
+                                                                   int64_t up_off, int64_t nquads) {
+    constexpr int QPB = 2, MR = 2;
+    extern __shared__ uint4 lds[];  // x rows (2 x K bf16)
+    __shared__ float red[QPB][KC][MR][8];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int c = wv % KC, qb = wv / KC;
+    const int64_t gq = (int64_t)blockIdx.x * QPB + qb;
+    const int nsb = K >> 8;
+    const int nx = K >> 3, nt = 64 * QPB * KC;
+    const int i0 = threadIdx.x, i1 = i0 + nt, i2 = i1 + nt, i3 = i2 + nt;
+    const int j0 = i0 < nx ? i0 : nx - 1, j1 = i1 < nx ? i1 : nx - 1;
+    const int j2 = i2 < nx ? i2 : nx - 1, j3 = i3 < nx ? i3 : nx - 1;
+    const uint4* xg = reinterpret_cast<const uint4*>(x);
+    const int r1 = M > 1 ? nx : 0;  // second row (row 0 again when M == 1)
+    const uint4 xa0 = xg[j0], xa1 = xg[j1], xa2 = xg[j2], xa3 = xg[j3];
+    const uint4 xb0 = xg[r1 + j0], xb1 = xg[r1 + j1], xb2 = xg[r1 + j2], xb3 = xg[r1 + j3];
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    Q4Unit<GU> A;
+    q4k_unit_load<GU>(A, W, gq < nquads ? gq : nquads - 1, c, up_off, nsb, lane);
+    if (i0 < nx) { lds[i0] = xa0; lds[nx + i0] = xb0; }
+    if (i1 < nx) { lds[i1] = xa1; lds[nx + i1] = xb1; }
+    if (i2 < nx) { lds[i2] = xa2; lds[nx + i2] = xb2; }
+    if (i3 < nx) { lds[i3] = xa3; lds[nx + i3] = xb3; }
+    __syncthreads();
+    const int s = 16 * c + (lane >> 2);
+    const uint32_t live = s < nsb ? 0xFFFFFFFFu : 0u;
+    const int xoff = (s < nsb ? s : 0) * 32 + 8 * (lane & 3);
+    uint32_t xlo[MR][16], xhi[MR][16];
+    float sxlo[MR], sxhi[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        const uint4* xp = lds + m * nx + xoff;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const uint4 p = xp[v], q = xp[4 + v];
+            xlo[m][4 * v] = p.x & live; xlo[m][4 * v + 1] = p.y & live;
+            xlo[m][4 * v + 2] = p.z & live; xlo[m][4 * v + 3] = p.w & live;
+            xhi[m][4 * v] = q.x & live; xhi[m][4 * v + 1] = q.y & live;
+            xhi[m][4 * v + 2] = q.z & live; xhi[m][4 * v + 3] = q.w & live;
+        }
+        float a = 0.0f, b = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            a = dot2_bf16(xlo[m][i], 0x3F803F80u, a);  // bf16 (1, 1)
+            b = dot2_bf16(xhi[m][i], 0x3F803F80u, b);
+        }
+        sxlo[m] = a;
+        sxhi[m] = b;
+    }
+    float acc[MR][GU ? 8 : 4];
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+        for (int i = 0; i < (GU ? 8 : 4); ++i) acc[m][i] = 0.0f;
+    q4k_unit_compute_rows<GU, AFF, MR>(acc, A, xlo, xhi, sxlo, sxhi);
+    // per-chunk row totals: slots 0..3 (gate rows for GU), 4..7 (up rows)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+        if constexpr (GU) {
+            const float tot = reduce_slots8(acc[m], lane);
+            if (!(lane & 7)) red[qb][c][m][4 * (lane >> 5) + 2 * ((lane >> 4) & 1) + ((lane >> 3) & 1)] = tot;
+        } else {
+            const float tot = reduce_slots<4>(acc[m], lane);
+            if (!(lane & 15)) red[qb][c][m][slot_of_lane<4>(lane)] = tot;
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 4 * QPB * MR) {
+        const int m = threadIdx.x / (4 * QPB), q2 = (threadIdx.x >> 2) % QPB, r = threadIdx.x & 3;
+        float g = 0.0f, u = 0.0f;
+#pragma unroll
+        for (int cc = 0; cc < KC; ++cc) {
+            g += red[q2][cc][m][r];
+            if (GU) u += red[q2][cc][m][r + 4];
+        }
+        const int64_t o = 4 * ((int64_t)blockIdx.x * QPB + q2) + r;
+        if (m < M && o < nout) store_y<YT>(y + (int64_t)m * nout + o, GU ? silu_mul(g, u) : g);
+    }
+}
+
 // ------------------------------------------------------------------ Q4_K M=1, f32 x
 template <int KC, int R, bool GU, bool AFF, typename YT>
 __global__ __launch_bounds__(256) void k_gemv1_q4k_f32(const uint8_t* __restrict__ W, const float* __restrict__ x,
@@ -836,8 +923,8 @@ static hipError_t gemv1_q8_t(const int8_t* Q, const uint16_t* D, const XT* x, YT
 }
 
 bool gemv_rows_supported(int qtype, int M, int K, bool gu, int64_t n_rows) {
-    return (qtype == 12 || qtype == 13) && M >= 2 && M <= 4 && K % 256 == 0 && K <= 4096 &&
-           (!gu || (n_rows / 2) % 4 == 0);
+    return (qtype == 12 || qtype == 13) && M >= 2 && M <= (K <= 4096 ? 4 : 2) && K % 256 == 0 &&
+           K <= 4 * 4096 && (!gu || (n_rows / 2) % 4 == 0);
 }
 
 template <int MR, bool GU, bool AFF, typename YT>
@@ -857,6 +944,17 @@ static void rows_t(const uint8_t* W, const bf16_t* x, YT* y, int M, int64_t nout
 template <bool GU, bool AFF, typename YT>
 static hipError_t rows_m(const uint8_t* W, const bf16_t* x, YT* y, int M, int64_t nout, int K, int64_t up_off,
                          hipStream_t s) {
+    if (K > 4096) {  // two rows, K split over KC waves per row-quad pair
+        const int64_t nquads = (nout + 3) / 4;
+        const dim3 grid((unsigned)((nquads + 1) / 2));
+        const size_t lds = (size_t)2 * K * 2;
+#define THQ_KSR(KC_) \
+    hipLaunchKernelGGL((k_gemv_q4k_bf16_ks_rows<KC_, GU, AFF, YT>), grid, dim3(128 * KC_), lds, s, W, x, y, M, nout, K, up_off, nquads)
+        const int kc = (K + 4095) / 4096;
+        if (kc == 2) THQ_KSR(2); else if (kc == 3) THQ_KSR(3); else THQ_KSR(4);
+#undef THQ_KSR
+        return hipGetLastError();
+    }
     if (M == 2) rows_t<2, GU, AFF, YT>(W, x, y, M, nout, K, up_off, s);
     else rows_t<4, GU, AFF, YT>(W, x, y, M, nout, K, up_off, s);
     return hipGetLastError();

@@ -54,7 +54,7 @@ hipError_t launch_dequant_affine(const uint8_t* src, void* out, bool bf16, int64
 
 // decode GEMV (M = 1); gu = fused gate/up over a [gate; up] weight
 bool gemv1_supported(int qtype, int K, bool gu, int64_t n_rows);
-// Q4_K / MLX affine, 2 <= M <= 4 bf16 rows (16-B aligned), K % 256 == 0, K <= 4096
+// Q4_K / MLX affine, bf16 rows (16-B aligned), K % 256 == 0: 2 <= M <= 4 for K <= 4096, M = 2 for K <= 16384
 bool gemv_rows_supported(int qtype, int M, int K, bool gu, int64_t n_rows);
 hipError_t launch_gemv_rows(const WeightView& w, const void* x, void* y, bool yf32, bool gu, int M, int64_t nout,
                             int64_t up_off, hipStream_t s);
