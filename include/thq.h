@@ -64,6 +64,8 @@ typedef enum thq_act {
                                    Q8_0 (Q8_0 W) or Q8_K (Q4_K W), exact integer
                                    block dots, f32 block scaling                     */
 #define THQ_MODE_EXACT_W 0x10u  /* never round dequantized weights to bf16 on MFMA   */
+#define THQ_MODE_ARGMAX_FUSED 0x20u /* thq_matmul_argmax with logits_dev NULL only: fuse
+                                       the argmax into the decode kernels' epilogue */
 
 /* error codes */
 #define THQ_OK 0
@@ -195,8 +197,15 @@ int thq_matmul(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_t
 int thq_gate_up_silu(thq_ctx* ctx, const thq_weight* fused, const void* x_dev, thq_act x_type, int64_t m,
                      void* y_dev, thq_act y_type, uint32_t flags, void* stream);
 
-/* LM head + per-row greedy argmax.  logits_dev [M, N] f32 may be NULL (a
- * context workspace is used).  idx_dev [M] u32.  Weights are never rounded
+/* LM head + per-row greedy argmax.  logits_dev [M, N] f32 may be NULL (the
+ * logits then live in the context workspace).  With logits_dev NULL and
+ * THQ_MODE_ARGMAX_FUSED, the decode kernels that have the fused epilogue
+ * (M <= 8: Q8_0, Q6_K and Q4_K / MLX affine at M = 1 with K <= 4096, and
+ * every type on the M = 2..8 matrix-core path) write one (max, index)
+ * partial per output tile instead of logits, and one pass reduces them;
+ * other shapes take the logits path.  Both give identical indices; on
+ * MI355X neither is measurably faster (the logits are ~1% of the weight
+ * bytes), so fusion is opt-in.  idx_dev [M] u32.  Weights are never rounded
  * (exact dequantized values), so the argmax follows the logits computed in
  * f32.  Tie rule of engine/src/engine.rs:1891-1898: lowest index among equal
  * maxima, NaN never selected, a row of -inf/NaN gives 0.

@@ -315,7 +315,8 @@ __global__ __launch_bounds__(64 * QPB * KC) void k_gemv1_q4k_bf16_ks(const uint8
 // that order.
 template <bool GU, bool AFF, bool FULL, typename YT>
 __global__ __launch_bounds__(256) void k_gemv1_q4k_bf16_1s(const uint8_t* W, const bf16_t* x, YT* __restrict__ y,
-                                                          int64_t nout, int K, int64_t up_off, int64_t nquads) {
+                                                          int64_t nout, int K, int64_t up_off, int64_t nquads,
+                                                          float* __restrict__ amv, uint32_t* __restrict__ ami) {
     extern __shared__ uint4 lds[];  // x (K bf16)
     const int lane = threadIdx.x & 63;
     const int64_t gq = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
@@ -355,6 +356,32 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_bf16_1s(const uint8_t* W, con
 #pragma unroll
     for (int i = 0; i < (GU ? 8 : 4); ++i) acc[i] = 0.0f;
     q4k_unit_compute<GU, AFF>(acc, A, xlo, xhi, sxlo, sxhi);
+    if constexpr (!GU) {
+        if (amv) {
+            // fused argmax: one (max, lowest index) partial per row quad; the
+            // quad's outputs 4gq + s sit in lanes 16s after the slot reduction
+            const float tot = reduce_slots<4>(acc, lane);
+            const int64_t o = 4 * gq + slot_of_lane<4>(lane);
+            float v = o < nout ? amax_key(tot) : -INFINITY;
+            uint32_t i = (uint32_t)o;
+            // every lane of a 16-lane group holds its slot's total: combine
+            // the groups (lanes 0, 16, 32, 48 meet through xor 16 and 32)
+#pragma unroll
+            for (int off = 16; off <= 32; off <<= 1) {
+                const float v2 = __shfl_xor(v, off, 64);
+                const uint32_t i2 = __shfl_xor(i, off, 64);
+                if (v2 > v || (v2 == v && i2 < i)) {
+                    v = v2;
+                    i = i2;
+                }
+            }
+            if (lane == 0) {
+                amv[gq] = v;
+                ami[gq] = i;
+            }
+            return;
+        }
+    }
     q4k_unit_store<GU, YT>(y, gq, nout, lane, acc);
 }
 
@@ -667,11 +694,11 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_f32(const uint8_t* __restrict
 template <int KC, int R, bool GU, typename XT, typename YT>
 __global__ __launch_bounds__(256) void k_gemv1_q8(const int8_t* __restrict__ Q, const uint16_t* __restrict__ D,
                                                  const XT* __restrict__ x, YT* __restrict__ y, int64_t nout, int K,
-                                                 int64_t up_off) {
+                                                 int64_t up_off, float* __restrict__ amv, uint32_t* __restrict__ ami) {
     const int lane = threadIdx.x & 63;
     const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
     const int64_t base = wave * (GU ? R / 2 : R);
-    if (base >= nout) return;
+    if (base >= nout && !amv) return;  // the fused argmax's block barrier needs every wave
     const int nb = K >> 5;
 
     float xv[KC][16], sx[KC];
@@ -727,6 +754,25 @@ __global__ __launch_bounds__(256) void k_gemv1_q8(const int8_t* __restrict__ Q, 
             a = __builtin_fmaf(f16_to_f32(dv[r][c]), s - 128.0f * sx[c], a);
         }
         acc[r] = wave_sum(a);
+    }
+    if (!GU && amv) {
+        // fused argmax (one row per wave): one (max, lowest index) partial per block
+        __shared__ float amx[4];
+        if (lane == 0) amx[threadIdx.x >> 6] = acc[0];
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            const int64_t o0 = (int64_t)blockIdx.x * (blockDim.x >> 6);
+            float bv = -INFINITY;
+            uint32_t bi = (uint32_t)o0;
+            for (int w = 0; w < (int)(blockDim.x >> 6) && o0 + w < nout; ++w)
+                if (amx[w] > bv) {
+                    bv = amx[w];
+                    bi = (uint32_t)(o0 + w);
+                }
+            amv[blockIdx.x] = bv;
+            ami[blockIdx.x] = bi;
+        }
+        return;
     }
     write_rows<R, GU, YT>(y, base, nout, acc);
 }
@@ -832,21 +878,30 @@ static inline int env_int(const char* name, int dflt) {
 // resident waves per CU (tunable: THQ_GEMV_WPC)
 template <bool GU, bool AFF, typename YT>
 static void launch_q4k_bf16_t(const uint8_t* W, const bf16_t* x, YT* y, int64_t nout, int K, int64_t up_off,
-                              hipStream_t s) {
+                              hipStream_t s, AmaxOut* am) {
     const int64_t nquads = (nout + 3) / 4;
     const int wpc = env_int("THQ_GEMV_WPC", 8);
     int64_t waves = (int64_t)256 * (wpc > 0 ? wpc : 8);
     if (waves > nquads) waves = nquads;
     const size_t lds = (size_t)K * 2;
     if (K <= 4096 && env_int("THQ_GEMV_ONESHOT", 1)) {
+        float* amv = nullptr;
+        uint32_t* ami = nullptr;
+        if (am) {  // one partial per row quad (M = 1)
+            if (GU || nquads > am->ld) return;
+            amv = am->v;
+            ami = am->i;
+            am->nb = nquads;
+        }
         if (K == 4096)
             hipLaunchKernelGGL((k_gemv1_q4k_bf16_1s<GU, AFF, true, YT>), dim3((unsigned)((nquads + 3) / 4)), dim3(256),
-                               lds, s, W, x, y, nout, K, up_off, nquads);
+                               lds, s, W, x, y, nout, K, up_off, nquads, amv, ami);
         else
             hipLaunchKernelGGL((k_gemv1_q4k_bf16_1s<GU, AFF, false, YT>), dim3((unsigned)((nquads + 3) / 4)), dim3(256),
-                               lds, s, W, x, y, nout, K, up_off, nquads);
+                               lds, s, W, x, y, nout, K, up_off, nquads, amv, ami);
         return;
     }
+    if (am) return;  // no fused epilogue on the K-split / persistent kernels
     if (K <= 4 * 4096 && env_int("THQ_GEMV_ONESHOT", 1)) {
         // 2 quads per block (twice the blocks of 4) measured 8.4 -> 8.25 us at K = 12288
         static const int qpb = env_int("THQ_GEMV_QPB", 2) == 4 ? 4 : 2;
@@ -873,10 +928,12 @@ static void launch_q4k_bf16_t(const uint8_t* W, const bf16_t* x, YT* y, int64_t 
 
 template <bool GU, bool AFF, typename YT>
 static hipError_t gemv1_q4k_t(const uint8_t* W, const void* x, bool xf32, YT* y, int64_t nout, int K, int64_t up_off,
-                              hipStream_t s) {
+                              hipStream_t s, AmaxOut* am) {
     const int kc = (K + 4095) / 4096;
     if (!xf32) {
-        launch_q4k_bf16_t<GU, AFF, YT>(W, static_cast<const bf16_t*>(x), y, nout, K, up_off, s);
+        launch_q4k_bf16_t<GU, AFF, YT>(W, static_cast<const bf16_t*>(x), y, nout, K, up_off, s, am);
+    } else if (am) {
+        return hipSuccess;  // no fused epilogue on the f32-x kernel
     } else {
         const float* xf = static_cast<const float*>(x);
         constexpr int RR = GU ? 2 : 1;
@@ -897,26 +954,35 @@ static hipError_t gemv1_q4k_t(const uint8_t* W, const void* x, bool xf32, YT* y,
 
 template <int KC, bool GU, typename XT, typename YT>
 static void launch_q8_t(const int8_t* Q, const uint16_t* D, const XT* x, YT* y, int64_t nout, int K, int64_t up_off,
-                        hipStream_t s) {
+                        hipStream_t s, AmaxOut* am) {
     constexpr int R = GU ? 2 : 1;
     const int64_t waves = nout;
-    hipLaunchKernelGGL((k_gemv1_q8<KC, R, GU, XT, YT>), dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, s, Q, D, x, y,
-                       nout, K, up_off);
+    const int64_t blocks = (waves + 3) / 4;
+    float* amv = nullptr;
+    uint32_t* ami = nullptr;
+    if (am) {  // one partial per block of 4 rows (M = 1)
+        if (GU || blocks > am->ld) return;
+        amv = am->v;
+        ami = am->i;
+        am->nb = blocks;
+    }
+    hipLaunchKernelGGL((k_gemv1_q8<KC, R, GU, XT, YT>), dim3((unsigned)blocks), dim3(256), 0, s, Q, D, x, y, nout, K,
+                       up_off, amv, ami);
 }
 
 template <bool GU, typename XT, typename YT>
 static hipError_t gemv1_q8_t(const int8_t* Q, const uint16_t* D, const XT* x, YT* y, int64_t nout, int K,
-                             int64_t up_off, hipStream_t s) {
+                             int64_t up_off, hipStream_t s, AmaxOut* am) {
     const int kc = (K + 1023) / 1024;
     switch (kc) {
-        case 1: launch_q8_t<1, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s); break;
-        case 2: launch_q8_t<2, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s); break;
-        case 3: launch_q8_t<3, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s); break;
-        case 4: launch_q8_t<4, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s); break;
-        case 5: launch_q8_t<5, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s); break;
-        case 6: launch_q8_t<6, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s); break;
-        case 7: launch_q8_t<7, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s); break;
-        case 8: launch_q8_t<8, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s); break;
+        case 1: launch_q8_t<1, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
+        case 2: launch_q8_t<2, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
+        case 3: launch_q8_t<3, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
+        case 4: launch_q8_t<4, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
+        case 5: launch_q8_t<5, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
+        case 6: launch_q8_t<6, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
+        case 7: launch_q8_t<7, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
+        case 8: launch_q8_t<8, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -980,31 +1046,31 @@ bool gemv1_supported(int qtype, int K, bool gu, int64_t n_rows) {
 }
 
 hipError_t launch_gemv1(const WeightView& w, const void* x, bool xf32, void* y, bool yf32, bool gu, int64_t nout,
-                        int64_t up_off, hipStream_t s) {
+                        int64_t up_off, hipStream_t s, AmaxOut* am) {
     const int K = (int)w.K;
     if (w.qtype == 14) {
-        if (xf32) return launch_generic(w, x, xf32, y, yf32, gu, 1, nout, up_off, s);
-        return launch_gemv1_q6k(w, x, y, yf32, gu, nout, up_off, s);
+        if (xf32) return am ? hipSuccess : launch_generic(w, x, xf32, y, yf32, gu, 1, nout, up_off, s);
+        return launch_gemv1_q6k(w, x, y, yf32, gu, nout, up_off, s, am);
     }
     if (w.qtype == 12) {
         if (gu) {
-            return yf32 ? gemv1_q4k_t<true, false, float>(w.q, x, xf32, (float*)y, nout, K, up_off, s)
-                        : gemv1_q4k_t<true, false, bf16_t>(w.q, x, xf32, (bf16_t*)y, nout, K, up_off, s);
+            return yf32 ? gemv1_q4k_t<true, false, float>(w.q, x, xf32, (float*)y, nout, K, up_off, s, am)
+                        : gemv1_q4k_t<true, false, bf16_t>(w.q, x, xf32, (bf16_t*)y, nout, K, up_off, s, am);
         }
-        return yf32 ? gemv1_q4k_t<false, false, float>(w.q, x, xf32, (float*)y, nout, K, up_off, s)
-                    : gemv1_q4k_t<false, false, bf16_t>(w.q, x, xf32, (bf16_t*)y, nout, K, up_off, s);
+        return yf32 ? gemv1_q4k_t<false, false, float>(w.q, x, xf32, (float*)y, nout, K, up_off, s, am)
+                    : gemv1_q4k_t<false, false, bf16_t>(w.q, x, xf32, (bf16_t*)y, nout, K, up_off, s, am);
     }
     if (w.qtype == 13) {
         if (gu) {
-            return yf32 ? gemv1_q4k_t<true, true, float>(w.q, x, xf32, (float*)y, nout, K, up_off, s)
-                        : gemv1_q4k_t<true, true, bf16_t>(w.q, x, xf32, (bf16_t*)y, nout, K, up_off, s);
+            return yf32 ? gemv1_q4k_t<true, true, float>(w.q, x, xf32, (float*)y, nout, K, up_off, s, am)
+                        : gemv1_q4k_t<true, true, bf16_t>(w.q, x, xf32, (bf16_t*)y, nout, K, up_off, s, am);
         }
-        return yf32 ? gemv1_q4k_t<false, true, float>(w.q, x, xf32, (float*)y, nout, K, up_off, s)
-                    : gemv1_q4k_t<false, true, bf16_t>(w.q, x, xf32, (bf16_t*)y, nout, K, up_off, s);
+        return yf32 ? gemv1_q4k_t<false, true, float>(w.q, x, xf32, (float*)y, nout, K, up_off, s, am)
+                    : gemv1_q4k_t<false, true, bf16_t>(w.q, x, xf32, (bf16_t*)y, nout, K, up_off, s, am);
     }
     const int8_t* Q = reinterpret_cast<const int8_t*>(w.q);
     const uint16_t* D = reinterpret_cast<const uint16_t*>(w.aux);
-#define THQ_Q8(GU_, XT_, YT_) gemv1_q8_t<GU_, XT_, YT_>(Q, D, (const XT_*)x, (YT_*)y, nout, K, up_off, s)
+#define THQ_Q8(GU_, XT_, YT_) gemv1_q8_t<GU_, XT_, YT_>(Q, D, (const XT_*)x, (YT_*)y, nout, K, up_off, s, am)
     if (gu) {
         if (xf32) return yf32 ? THQ_Q8(true, float, float) : THQ_Q8(true, float, bf16_t);
         return yf32 ? THQ_Q8(true, bf16_t, float) : THQ_Q8(true, bf16_t, bf16_t);

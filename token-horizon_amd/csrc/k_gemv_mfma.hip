@@ -45,6 +45,7 @@
 // (deterministic) and applies the epilogue.
 #include "thq_dev.hpp"
 #include "thq_kernels.hpp"
+#include "thq_wave.hpp"
 
 #include <type_traits>
 
@@ -95,7 +96,8 @@ __device__ __forceinline__ float dpp_add(float v) {
 template <int QT, int E, int NX, bool GU, bool SPLIT, typename YT>
 __global__ __launch_bounds__(512, QT != 8 ? 4 : 2) void k_gemv_mfma(const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Wa,
                                                   const bf16_t* X, void* __restrict__ Yv, int M, int K,
-                                                  int64_t nout, int64_t up_off, int64_t nrows, int cpw, int splits) {
+                                                  int64_t nout, int64_t up_off, int64_t nrows, int cpw, int splits,
+                                                  float* __restrict__ amv, uint32_t* __restrict__ ami, int64_t am_ld) {
     // staged activation rows (row stride Kb + 8: rows start 16 B apart in bank
     // order), sub-block sums S[sb][8] and the cross-wave reduction buffer
     __shared__ __attribute__((aligned(16))) bf16_t xs[XS_ELEMS + 8 * 8];
@@ -378,6 +380,27 @@ __global__ __launch_bounds__(512, QT != 8 ? 4 : 2) void k_gemv_mfma(const uint8_
             const int64_t o = (int64_t)tile * 16 + c;
             if (o < nout) store_y<YT>(static_cast<YT*>(Yv) + (int64_t)m * nout + o, silu_mul(gs, us));
         }
+    } else if (amv) {
+        // fused argmax: the tile's 32 outputs per row (summed exactly as the
+        // stored path sums them) reduce across their 32 lanes to (max, lowest
+        // index) without a store; rows are whole half-waves
+        for (int t0 = 0; t0 < 32 * M; t0 += blockDim.x) {
+            const int t = t0 + threadIdx.x;
+            const int c = t & 31, m = t >> 5;
+            const int64_t o = (int64_t)tile * 32 + c;
+            float v = -INFINITY;
+            if (m < M) {
+                float sum = 0.0f;
+                for (int w = 0; w < nw; ++w) sum += red[w][m][c];
+                if (o < nout) v = amax_key(sum);
+            }
+            uint32_t i = (uint32_t)o;
+            amax_row32(v, i);
+            if (m < M && c == 0) {
+                amv[m * am_ld + tile] = v;
+                ami[m * am_ld + tile] = i;
+            }
+        }
     } else {
         for (int t = threadIdx.x; t < 32 * M; t += blockDim.x) {
             const int c = t & 31, m = t >> 5;
@@ -396,16 +419,28 @@ int env_int(const char* name) {
 
 template <int QT, int E, int NX, bool GU, typename YT>
 hipError_t run(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* y, int M, int64_t nout, int64_t up_off,
-               float* ws, hipStream_t s) {
+               float* ws, hipStream_t s, AmaxOut* am) {
     const int64_t tiles = GU ? (nout + 15) / 16 : (nout + 31) / 32;
     const dim3 grid((unsigned)(tiles * p.splits)), block(64 * p.waves);
     if (p.splits == 1) {
+        float* amv = nullptr;
+        uint32_t* ami = nullptr;
+        int64_t ld = 0;
+        if (am) {
+            if (GU || tiles > am->ld) return hipErrorInvalidValue;
+            amv = am->v;
+            ami = am->i;
+            ld = am->ld;
+            am->nb = tiles;
+        }
         hipLaunchKernelGGL((k_gemv_mfma<QT, E, NX, GU, false, YT>), grid, block, 0, s, w.q, w.aux, x, y, M,
-                           (int)w.K, nout, up_off, w.N, p.cpw, 1);
+                           (int)w.K, nout, up_off, w.N, p.cpw, 1, amv, ami, ld);
         return hipGetLastError();
     }
+    if (am) return hipSuccess;  // split-K: no fused epilogue (am->nb stays 0)
     hipLaunchKernelGGL((k_gemv_mfma<QT, E, NX, GU, true, float>), grid, block, 0, s, w.q, w.aux, x, (void*)ws, M,
-                       (int)w.K, nout, up_off, w.N, p.cpw, p.splits);
+                       (int)w.K, nout, up_off, w.N, p.cpw, p.splits, (float*)nullptr, (uint32_t*)nullptr,
+                       (int64_t)0);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     return launch_split_reduce(ws, y, std::is_same<YT, float>::value, GU, M, nout, up_off, w.N, p.splits, s);
@@ -414,21 +449,21 @@ hipError_t run(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* y,
 // staged activation chunks per thread: M * cpw * 256 / 8 / (64 * waves) = M * cpw / 2, rounded up to 1, 2, 4, 8
 template <int QT, int E, bool GU, typename YT>
 hipError_t run_nx(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* y, int M, int64_t nout,
-                  int64_t up_off, float* ws, hipStream_t s) {
+                  int64_t up_off, float* ws, hipStream_t s, AmaxOut* am) {
     const int need = (M * p.cpw + 1) / 2;
-    if (need <= 1) return run<QT, E, 1, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
-    if (need <= 2) return run<QT, E, 2, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
-    if (need <= 4) return run<QT, E, 4, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
-    return run<QT, E, 8, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
+    if (need <= 1) return run<QT, E, 1, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
+    if (need <= 2) return run<QT, E, 2, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
+    if (need <= 4) return run<QT, E, 4, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
+    return run<QT, E, 8, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
 }
 
 template <int QT, bool GU, typename YT>
 hipError_t run_e(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* y, int M, int64_t nout,
-                 int64_t up_off, float* ws, hipStream_t s) {
+                 int64_t up_off, float* ws, hipStream_t s, AmaxOut* am) {
     // live accumulator rows per lane: rows 4g + e < M, e < E
-    if (M == 1) return run_nx<QT, 1, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
-    if (M == 2) return run_nx<QT, 2, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
-    return run_nx<QT, 4, GU, YT>(p, w, x, y, M, nout, up_off, ws, s);
+    if (M == 1) return run_nx<QT, 1, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
+    if (M == 2) return run_nx<QT, 2, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
+    return run_nx<QT, 4, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
 }
 
 }  // namespace
@@ -466,31 +501,31 @@ GemvPlan plan_gemv_mfma(int qtype, int64_t M, int64_t N_rows, int64_t K, bool gu
 }
 
 hipError_t launch_gemv_mfma(const GemvPlan& p, const WeightView& w, const void* x, void* y, bool yf32, bool gu, int M,
-                            int64_t nout, int64_t up_off, float* ws, hipStream_t s) {
+                            int64_t nout, int64_t up_off, float* ws, hipStream_t s, AmaxOut* am) {
     if (!p.waves) return hipErrorInvalidValue;
     const bf16_t* xb = static_cast<const bf16_t*>(x);
     if (w.qtype == 12) {
-        if (gu) return yf32 ? run_e<12, true, float>(p, w, xb, y, M, nout, up_off, ws, s)
-                            : run_e<12, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
-        return yf32 ? run_e<12, false, float>(p, w, xb, y, M, nout, up_off, ws, s)
-                    : run_e<12, false, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
+        if (gu) return yf32 ? run_e<12, true, float>(p, w, xb, y, M, nout, up_off, ws, s, am)
+                            : run_e<12, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s, am);
+        return yf32 ? run_e<12, false, float>(p, w, xb, y, M, nout, up_off, ws, s, am)
+                    : run_e<12, false, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s, am);
     }
     if (w.qtype == 13) {
-        if (gu) return yf32 ? run_e<13, true, float>(p, w, xb, y, M, nout, up_off, ws, s)
-                            : run_e<13, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
-        return yf32 ? run_e<13, false, float>(p, w, xb, y, M, nout, up_off, ws, s)
-                    : run_e<13, false, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
+        if (gu) return yf32 ? run_e<13, true, float>(p, w, xb, y, M, nout, up_off, ws, s, am)
+                            : run_e<13, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s, am);
+        return yf32 ? run_e<13, false, float>(p, w, xb, y, M, nout, up_off, ws, s, am)
+                    : run_e<13, false, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s, am);
     }
     if (w.qtype == 14) {
-        if (gu) return yf32 ? run_e<14, true, float>(p, w, xb, y, M, nout, up_off, ws, s)
-                            : run_e<14, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
-        return yf32 ? run_e<14, false, float>(p, w, xb, y, M, nout, up_off, ws, s)
-                    : run_e<14, false, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
+        if (gu) return yf32 ? run_e<14, true, float>(p, w, xb, y, M, nout, up_off, ws, s, am)
+                            : run_e<14, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s, am);
+        return yf32 ? run_e<14, false, float>(p, w, xb, y, M, nout, up_off, ws, s, am)
+                    : run_e<14, false, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s, am);
     }
-    if (gu) return yf32 ? run_e<8, true, float>(p, w, xb, y, M, nout, up_off, ws, s)
-                        : run_e<8, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
-    return yf32 ? run_e<8, false, float>(p, w, xb, y, M, nout, up_off, ws, s)
-                : run_e<8, false, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s);
+    if (gu) return yf32 ? run_e<8, true, float>(p, w, xb, y, M, nout, up_off, ws, s, am)
+                        : run_e<8, true, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s, am);
+    return yf32 ? run_e<8, false, float>(p, w, xb, y, M, nout, up_off, ws, s, am)
+                : run_e<8, false, bf16_t>(p, w, xb, y, M, nout, up_off, ws, s, am);
 }
 
 }  // namespace thq

@@ -91,7 +91,8 @@ __device__ __forceinline__ float q6_row_dot(const Q6Row& R, const uint32_t (&xq)
 template <int KC, int QPB, bool GU, typename YT>
 __global__ __launch_bounds__(64 * QPB * KC) void k_gemv1_q6k_bf16(Q6Planes P, const bf16_t* x, YT* __restrict__ y,
                                                                  int64_t nout, int K, int64_t up_off,
-                                                                 int64_t ngroups) {
+                                                                 int64_t ngroups, float* __restrict__ amv,
+                                                                 uint32_t* __restrict__ ami) {
     static_assert(QPB == 2 || QPB == 4, "x staging uses two or four pieces per thread");
     extern __shared__ uint4 lds[];  // x (K bf16)
     __shared__ float red[QPB][KC][4];
@@ -156,6 +157,30 @@ __global__ __launch_bounds__(64 * QPB * KC) void k_gemv1_q6k_bf16(Q6Planes P, co
     if (!(lane & 15)) red[qb][c][slot_of_lane<4>(lane)] = tot;
     __syncthreads();
     constexpr int NO = GU ? 2 : 4;  // outputs per row group
+    if (!GU && amv) {
+        // fused argmax: the block's QPB * 4 outputs (summed over chunks exactly
+        // as the stored path) reduce across wave 0's first lanes to one
+        // (max, lowest index) partial
+        static_assert(QPB * 4 <= 16, "one DPP row holds the block's outputs");
+        if (threadIdx.x < 64) {
+            const int64_t o = (int64_t)blockIdx.x * QPB * 4 + threadIdx.x;
+            const bool own = threadIdx.x < QPB * 4;
+            float v = -INFINITY;
+            if (own && o < nout) {
+                float a = 0.0f;
+#pragma unroll
+                for (int k = 0; k < KC; ++k) a += red[threadIdx.x >> 2][k][threadIdx.x & 3];
+                v = amax_key(a);
+            }
+            uint32_t i = own ? (uint32_t)o : 0xFFFFFFFFu;
+            amax_row16(v, i);
+            if (threadIdx.x == 0) {
+                amv[blockIdx.x] = v;
+                ami[blockIdx.x] = i;
+            }
+        }
+        return;
+    }
     if (threadIdx.x < QPB * NO) {
         const int q2 = threadIdx.x / NO, p = threadIdx.x % NO;
         const int64_t o = (int64_t)NO * ((int64_t)blockIdx.x * QPB + q2) + p;
@@ -170,37 +195,47 @@ __global__ __launch_bounds__(64 * QPB * KC) void k_gemv1_q6k_bf16(Q6Planes P, co
 }
 
 template <int KC, int QPB, bool GU, typename YT>
-static void q6_launch(const Q6Planes& P, const bf16_t* x, YT* y, int64_t nout, int K, int64_t up_off, hipStream_t s) {
+static void q6_launch(const Q6Planes& P, const bf16_t* x, YT* y, int64_t nout, int K, int64_t up_off, hipStream_t s,
+                      AmaxOut* am) {
     constexpr int NO = GU ? 2 : 4;
     const int64_t ngroups = (nout + NO - 1) / NO;
-    hipLaunchKernelGGL((k_gemv1_q6k_bf16<KC, QPB, GU, YT>), dim3((unsigned)((ngroups + QPB - 1) / QPB)),
-                       dim3(64 * QPB * KC), (size_t)K * 2, s, P, x, y, nout, K, up_off, ngroups);
+    const int64_t blocks = (ngroups + QPB - 1) / QPB;
+    float* amv = nullptr;
+    uint32_t* ami = nullptr;
+    if (am) {  // one partial per block (M = 1)
+        if (GU || blocks > am->ld) return;
+        amv = am->v;
+        ami = am->i;
+        am->nb = blocks;
+    }
+    hipLaunchKernelGGL((k_gemv1_q6k_bf16<KC, QPB, GU, YT>), dim3((unsigned)blocks), dim3(64 * QPB * KC),
+                       (size_t)K * 2, s, P, x, y, nout, K, up_off, ngroups, amv, ami);
 }
 
 template <bool GU, typename YT>
 static hipError_t q6_dispatch(const Q6Planes& P, const bf16_t* x, YT* y, int64_t nout, int K, int64_t up_off,
-                              hipStream_t s) {
+                              hipStream_t s, AmaxOut* am) {
     switch ((K + 4095) / 4096) {
-        case 1: q6_launch<1, 4, GU, YT>(P, x, y, nout, K, up_off, s); break;
-        case 2: q6_launch<2, 2, GU, YT>(P, x, y, nout, K, up_off, s); break;
-        case 3: q6_launch<3, 2, GU, YT>(P, x, y, nout, K, up_off, s); break;
-        case 4: q6_launch<4, 2, GU, YT>(P, x, y, nout, K, up_off, s); break;
+        case 1: q6_launch<1, 4, GU, YT>(P, x, y, nout, K, up_off, s, am); break;
+        case 2: q6_launch<2, 2, GU, YT>(P, x, y, nout, K, up_off, s, am); break;
+        case 3: q6_launch<3, 2, GU, YT>(P, x, y, nout, K, up_off, s, am); break;
+        case 4: q6_launch<4, 2, GU, YT>(P, x, y, nout, K, up_off, s, am); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
 hipError_t launch_gemv1_q6k(const WeightView& w, const void* x, void* y, bool yf32, bool gu, int64_t nout,
-                            int64_t up_off, hipStream_t s) {
+                            int64_t up_off, hipStream_t s, AmaxOut* am) {
     const int K = (int)w.K;
     if (w.qtype != 14 || K % 256 || K > 4 * 4096 || nout <= 0) return hipErrorInvalidValue;
     const Q6Layout L = q6k_layout(w.N, w.K);
     const Q6Planes P{w.q, w.q + L.qh, w.q + L.sc, reinterpret_cast<const uint16_t*>(w.q + L.d)};
     const bf16_t* xb = static_cast<const bf16_t*>(x);
-    if (gu) return yf32 ? q6_dispatch<true, float>(P, xb, (float*)y, nout, K, up_off, s)
-                        : q6_dispatch<true, bf16_t>(P, xb, (bf16_t*)y, nout, K, up_off, s);
-    return yf32 ? q6_dispatch<false, float>(P, xb, (float*)y, nout, K, up_off, s)
-                : q6_dispatch<false, bf16_t>(P, xb, (bf16_t*)y, nout, K, up_off, s);
+    if (gu) return yf32 ? q6_dispatch<true, float>(P, xb, (float*)y, nout, K, up_off, s, am)
+                        : q6_dispatch<true, bf16_t>(P, xb, (bf16_t*)y, nout, K, up_off, s, am);
+    return yf32 ? q6_dispatch<false, float>(P, xb, (float*)y, nout, K, up_off, s, am)
+                : q6_dispatch<false, bf16_t>(P, xb, (bf16_t*)y, nout, K, up_off, s, am);
 }
 
 }  // namespace thq

@@ -193,9 +193,11 @@ hipError_t dequant_any(const thq_weight* w, void* out, bool bf16, hipStream_t s)
     return thq::launch_dequant_q4k(w->q, out, bf16, w->N, (int)(w->K / 256), s);
 }
 
-// Shared body of matmul / gate_up / argmax-logits.
+// Shared body of matmul / gate_up / argmax-logits.  With `am` (fused argmax,
+// y unused) only a path with the fused epilogue launches; am->nb = 0 reports
+// that this shape / type has none and nothing ran.
 int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t m, void* y, int yt, uint32_t flags,
-               bool gu, void* stream) {
+               bool gu, void* stream, thq::AmaxOut* am = nullptr) {
     if (!ctx || !w) return fail(THQ_EINVAL, "null context or weight");
     if (xt != THQ_ACT_F32 && xt != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad x_type %d", xt);
     if (yt != THQ_ACT_F32 && yt != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad y_type %d", yt);
@@ -204,7 +206,8 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
     if (m > (1 << 24)) return fail(THQ_ESHAPE, "M=%lld too large", (long long)m);
     if (gu && (w->N % 2)) return fail(THQ_ESHAPE, "gate/up weight has an odd row count %lld", (long long)w->N);
     if (m == 0) return THQ_OK;
-    if (!x || !y) return fail(THQ_EINVAL, "null x or y");
+    if (!x || (!y && !am)) return fail(THQ_EINVAL, "null x or y");
+    if (am) am->nb = 0;
     DeviceGuard g(ctx->device);
     hipStream_t s = static_cast<hipStream_t>(stream);
     const thq::WeightView v = view(w);
@@ -213,6 +216,7 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
     const int64_t up_off = gu ? w->N / 2 : 0;
     hipError_t e;
     if (flags & THQ_MODE_Q8ACT) {
+        if (am) return THQ_OK;
         if (w->qtype == THQ_MLX_Q4) return fail(THQ_EDTYPE, "THQ_MODE_Q8ACT applies to GGUF weights only");
         if (w->qtype == THQ_Q6_K) return fail(THQ_EDTYPE, "THQ_MODE_Q8ACT is not implemented for Q6_K weights");
         if (!thq::q8act_supported(w->qtype, w->K))
@@ -235,6 +239,10 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
                                  ? thq::plan_gemv_mfma(v.qtype, m, w->N, w->K, gu)
                                  : thq::GemvPlan{};
     const bool skinny = gp.waves > 0;
+    // Q8_0 at M = 1: the one-row-per-wave VALU kernel reloads x per row; on
+    // large weights the MFMA kernel is faster (LM head 151936 x 4096:
+    // 122.7 vs 208.5 us; 12288 x 4096: 12.9 vs 17.9 us; 3072 x 1024: 11.9 vs 9.1 us)
+    const bool q8_m1_mfma = w->qtype == THQ_Q8_0 && skinny && w->N * w->K >= ((int64_t)1 << 24);
     // the 4-bit tile kernels need whole superblocks (MLX affine K % 256 != 0 runs the generic kernel)
     const bool q4 = w->qtype == THQ_Q4_K || w->qtype == THQ_MLX_Q4;
     // 2..4 bf16 rows of Q4_K / MLX affine at K <= 4096: the VALU row kernel (THQ_GEMV_ROWS=0: MFMA)
@@ -242,17 +250,26 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
         const char* v = getenv("THQ_GEMV_ROWS");
         return !(v && !strcmp(v, "0"));
     }();
-    if (m == 1 && !(m1_mfma && skinny) && aligned16(x) && thq::gemv1_supported(v.qtype, (int)w->K, gu, w->N)) {
-        e = thq::launch_gemv1(v, x, xf32, y, yf32, gu, nout, up_off, s);
+    if (m == 1 && !((m1_mfma || q8_m1_mfma) && skinny) && aligned16(x) &&
+        thq::gemv1_supported(v.qtype, (int)w->K, gu, w->N)) {
+        e = thq::launch_gemv1(v, x, xf32, y, yf32, gu, nout, up_off, s, am);
     } else if (rows_on && !xf32 && aligned16(x) && thq::gemv_rows_supported(v.qtype, (int)m, (int)w->K, gu, w->N)) {
+        if (am) return THQ_OK;
         e = thq::launch_gemv_rows(v, x, y, yf32, gu, (int)m, nout, up_off, s);
     } else if (skinny) {
-        std::lock_guard<std::mutex> lk(ctx->mu);
-        if (gp.workspace_bytes) {
-            int rc = ensure_ws(ctx, gp.workspace_bytes);
-            if (rc) return rc;
+        if (am) {  // the fused epilogue exists on the unsplit plan only (no workspace)
+            e = gp.splits == 1 ? thq::launch_gemv_mfma(gp, v, x, y, yf32, gu, (int)m, nout, up_off, nullptr, s, am)
+                               : hipSuccess;
+        } else {
+            std::lock_guard<std::mutex> lk(ctx->mu);
+            if (gp.workspace_bytes) {
+                int rc = ensure_ws(ctx, gp.workspace_bytes);
+                if (rc) return rc;
+            }
+            e = thq::launch_gemv_mfma(gp, v, x, y, yf32, gu, (int)m, nout, up_off, static_cast<float*>(ctx->ws), s);
         }
-        e = thq::launch_gemv_mfma(gp, v, x, y, yf32, gu, (int)m, nout, up_off, static_cast<float*>(ctx->ws), s);
+    } else if (am) {
+        return THQ_OK;
     } else if (!xf32 && aligned16(x) && !((q4 || q6) && ((flags & THQ_MODE_EXACT_W) || w->K % 256)) &&
                !(q6 && (m <= 8 || thq::q6k_layout(w->N, w->K).total >= (1ull << 32) ||
                         (uint64_t)m * (uint64_t)w->K * 2 >= (1ull << 32)))) {
@@ -668,6 +685,32 @@ int thq_matmul_argmax(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_
     DeviceGuard g(ctx->device);
     hipStream_t s = static_cast<hipStream_t>(stream);
     float* logits = logits_dev;
+    // no logits wanted and THQ_MODE_ARGMAX_FUSED: decode paths with the fused
+    // epilogue write per-tile (max, index) partials instead of logits
+    const bool fused = (flags & THQ_MODE_ARGMAX_FUSED) != 0;
+    flags &= ~THQ_MODE_ARGMAX_FUSED;
+    if (!logits && fused && !(flags & THQ_MODE_Q8ACT) && m <= 8) {
+        const int64_t ld = (w->N + 3) / 4;  // the most partials any fused path writes per row
+        const size_t part = ((size_t)m * (size_t)ld * 8 + 255) & ~(size_t)255;
+        {
+            std::lock_guard<std::mutex> lk(ctx->mu);
+            int rc = ensure_ws(ctx, part + thq::argmax_partials_tmp_bytes(m, ld));
+            if (rc) return rc;
+        }
+        thq::AmaxOut am;
+        am.v = static_cast<float*>(ctx->ws);
+        am.i = reinterpret_cast<uint32_t*>(am.v + m * ld);
+        am.ld = ld;
+        int rc = run_matmul(ctx, w, x_dev, x_type, m, nullptr, THQ_ACT_F32, flags | THQ_MODE_EXACT_W, false, stream, &am);
+        if (rc) return rc;
+        if (am.nb > 0) {
+            hipError_t e = thq::launch_argmax_partials(am.v, am.i, m, am.nb, ld, idx_dev,
+                                                       static_cast<char*>(ctx->ws) + part, s);
+            if (e != hipSuccess) return fail(THQ_EHIP, "argmax: %s", hipGetErrorString(e));
+            return THQ_OK;
+        }
+        // no fused epilogue on this path: logits in the workspace below
+    }
     if (!logits) {
         // logits live at the end of the workspace, after the GEMM / argmax scratch
         const thq::GemmPlan p = thq::plan_gemm(view(w).qtype, true, m, w->N, w->K, false);

@@ -17,6 +17,18 @@ namespace thq {
 //                          144 B (layout in thq_dev.hpp, q4k_group); padding
 //                          rows are zero
 //                    aux = unused
+// Fused greedy-argmax epilogue (LM head without logits in HBM): a decode
+// kernel given `v` writes, per activation row m and output tile b, the tile's
+// (max, index) under the argmax tie rule to v[m*ld + b], i[m*ld + b] instead
+// of storing y; the launcher reports the tile count in nb (0: this path has
+// no fused epilogue, nothing was launched).
+struct AmaxOut {
+    float* v = nullptr;
+    uint32_t* i = nullptr;
+    int64_t ld = 0;
+    int64_t nb = 0;
+};
+
 struct WeightView {
     int qtype;
     int64_t N, K;
@@ -60,9 +72,9 @@ hipError_t launch_gemv_rows(const WeightView& w, const void* x, void* y, bool yf
                             int64_t up_off, hipStream_t s);
 // Q6_K M = 1 with bf16 x (K % 256 == 0, K <= 16384), k_q6k.hip
 hipError_t launch_gemv1_q6k(const WeightView& w, const void* x, void* y, bool yf32, bool gu, int64_t nout,
-                            int64_t up_off, hipStream_t s);
+                            int64_t up_off, hipStream_t s, AmaxOut* am = nullptr);
 hipError_t launch_gemv1(const WeightView& w, const void* x, bool xf32, void* y, bool yf32, bool gu, int64_t nout,
-                        int64_t up_off, hipStream_t s);
+                        int64_t up_off, hipStream_t s, AmaxOut* am = nullptr);
 // decode GEMV on MFMA: 1 <= M <= 8 bf16 activation rows, exact weights
 struct GemvPlan {
     int waves = 0, cpw = 0, splits = 0;  // waves per block, 256-wide chunks per wave, K splits
@@ -70,7 +82,7 @@ struct GemvPlan {
 };
 GemvPlan plan_gemv_mfma(int qtype, int64_t M, int64_t N_rows, int64_t K, bool gu);  // waves == 0: unsupported
 hipError_t launch_gemv_mfma(const GemvPlan& p, const WeightView& w, const void* x, void* y, bool yf32, bool gu, int M,
-                            int64_t nout, int64_t up_off, float* ws, hipStream_t s);
+                            int64_t nout, int64_t up_off, float* ws, hipStream_t s, AmaxOut* am = nullptr);
 // sum split partials P[s][M][ldp] in split order, then the epilogue
 hipError_t launch_split_reduce(const float* P, void* y, bool yf32, bool gu, int M, int64_t nout, int64_t up_off,
                                int64_t ldp, int splits, hipStream_t s);
@@ -95,5 +107,10 @@ hipError_t launch_quantize_act(int qtype, const void* x, bool xf32, int64_t M, i
 // argmax
 size_t argmax_workspace_bytes(int64_t m, int64_t n);
 hipError_t launch_argmax(const float* v, int64_t m, int64_t n, uint32_t* idx, void* ws, hipStream_t s);
+// reduce fused-epilogue partials v / i [m][ld] (nb per row) to idx[m]; tmp
+// holds argmax_partials_tmp_bytes(m, nb)
+size_t argmax_partials_tmp_bytes(int64_t m, int64_t nb);
+hipError_t launch_argmax_partials(const float* v, const uint32_t* i, int64_t m, int64_t nb, int64_t ld,
+                                  uint32_t* idx, void* tmp, hipStream_t s);
 
 }  // namespace thq

@@ -88,4 +88,41 @@ __device__ __forceinline__ int slot_of_lane(int lane) {
     return 0;
 }
 
+// Argmax combine of (value, index) pairs across lanes: larger value, else
+// lower index.  With NaN entered as -inf and every lane holding its own
+// output's index, a butterfly over W lanes equals the strict '>' scan from
+// (-inf, lowest index) over those outputs: NaN is never chosen, and a group
+// of -inf / NaN only yields its lowest index.
+__device__ __forceinline__ float amax_key(float v) { return v != v ? -INFINITY : v; }
+
+template <int CTRL>
+__device__ __forceinline__ void amax_dpp(float& v, uint32_t& i) {
+    const float v2 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+    const uint32_t i2 = (uint32_t)__builtin_amdgcn_mov_dpp((int)i, CTRL, 0xF, 0xF, false);
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+
+// combine over each 16-lane DPP row (the pairings of row16_sum); every lane
+// of the row ends with the row's (max, lowest index)
+__device__ __forceinline__ void amax_row16(float& v, uint32_t& i) {
+    amax_dpp<0xB1>(v, i);   // quad_perm [1,0,3,2]
+    amax_dpp<0x4E>(v, i);   // quad_perm [2,3,0,1]
+    amax_dpp<0x141>(v, i);  // row_half_mirror
+    amax_dpp<0x140>(v, i);  // row_mirror
+}
+
+// the same over 32 lanes (two rows, then one exchange across them)
+__device__ __forceinline__ void amax_row32(float& v, uint32_t& i) {
+    amax_row16(v, i);
+    const float v2 = __shfl_xor(v, 16, 64);
+    const uint32_t i2 = __shfl_xor(i, 16, 64);
+    if (v2 > v || (v2 == v && i2 < i)) {
+        v = v2;
+        i = i2;
+    }
+}
+
 }  // namespace thq

@@ -33,6 +33,7 @@ ACT_BF16 = 1
 MODE_DEQUANT_F32 = 0
 MODE_Q8ACT = 0x1
 MODE_EXACT_W = 0x10
+MODE_ARGMAX_FUSED = 0x20
 
 OK = 0
 EINVAL, ESHAPE, EDTYPE, EALIGN, EHIP, ENOMEM = -1, -2, -3, -4, -5, -6
