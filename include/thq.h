@@ -169,6 +169,26 @@ int thq_dequantize_bf16(thq_ctx* ctx, const thq_weight* w, uint16_t* out_dev, vo
 int thq_quantize_act(thq_ctx* ctx, thq_dtype dot_type, const void* x_dev, thq_act x_type, int64_t m, int64_t k,
                      void* blocks_dev, void* stream);
 
+/* Producer-side activation operand for THQ_MODE_Q8ACT ("presum": the
+ * producer emits what every consumer would otherwise recompute; the engine's
+ * presum blocks, engine/src/quant_kernel.rs:265-321).  candle's default
+ * QMatMul::forward quantizes its input once per call, so projections that
+ * share an input (q / k / v, gate / up) quantize the same rows again.  Here
+ * thq_q8act_prepare quantizes x [M, K] once into an opaque device buffer of
+ * thq_q8act_bytes(dot_type, m, k) bytes (256-byte aligned), and
+ * thq_matmul_q8act / thq_gate_up_silu_q8act consume it for any number of
+ * weights whose dot type it is (THQ_Q8_0 for Q8_0 weights, THQ_Q8_K for
+ * Q4_K) and whose K is k.  Results are bit-identical to thq_matmul /
+ * thq_gate_up_silu with THQ_MODE_Q8ACT on the same x.  Returns 0 for an
+ * unsupported dot type. */
+size_t thq_q8act_bytes(thq_dtype dot_type, int64_t m, int64_t k);
+int thq_q8act_prepare(thq_ctx* ctx, thq_dtype dot_type, const void* x_dev, thq_act x_type, int64_t m, int64_t k,
+                      void* buf_dev, void* stream);
+int thq_matmul_q8act(thq_ctx* ctx, const thq_weight* w, thq_dtype dot_type, const void* buf_dev, int64_t m,
+                     int64_t k, void* y_dev, thq_act y_type, void* stream);
+int thq_gate_up_silu_q8act(thq_ctx* ctx, const thq_weight* fused, thq_dtype dot_type, const void* buf_dev,
+                           int64_t m, int64_t k, void* y_dev, thq_act y_type, void* stream);
+
 /* y[M, N] = x[M, K] . W^T with f32 accumulation.
  * Replaces QMatMul::forward ([ext] candle-core 0.11 quantized/mod.rs, called
  * for every projection by quantized_qwen3) and the engine's routed projection

@@ -65,3 +65,16 @@ def test_init_without_gpu_reports_an_error():
     rc = thq.lib.thq_init(0, C.byref(h))
     assert rc in (thq.EHIP, thq.EINVAL)
     assert thq.last_error()
+
+
+def test_q8act_buffer_sizes_without_a_device():
+    import thq
+    L = thq.lib
+    assert L.thq_q8act_bytes(thq.Q4_K, 1, 4096) == 0          # not a dot type
+    assert L.thq_q8act_bytes(thq.Q8_K, 1, 0) == 0
+    q8k = L.thq_q8act_bytes(thq.Q8_K, 3, 4096)                # i8 plane + f32 d + i16 sums, 256-B aligned parts
+    assert q8k == 12288 + 256 + 768
+    q80 = L.thq_q8act_bytes(thq.Q8_0, 3, 4096)                # i8 plane + f32 d per 32
+    assert q80 == 12288 + 1536
+    assert L.thq_q8act_prepare(None, thq.Q8_K, None, thq.ACT_BF16, 1, 256, None, None) == thq.EINVAL
+

@@ -175,3 +175,47 @@ def test_q8act_errors():
     with pytest.raises(thq.ThqError) as e:
         thq.quantize_act(torch.zeros((1, 1024), device="cuda"), thq.Q4_K)
     assert e.value.code == thq.EDTYPE
+
+
+@pytest.mark.parametrize("dot_type,qtype,shapes", [
+    (thq.Q8_K, O.Q4_K, [(1024, 4096), (256, 4096), (512, 4096)]),   # q / k / v of one input
+    (thq.Q8_0, O.Q8_0, [(3072, 1024), (1000, 1024)]),
+])
+@pytest.mark.parametrize("m", [1, 5, 13])
+def test_q8act_prepared_once_bit_identical(dot_type, qtype, shapes, m):
+    """thq_q8act_prepare quantizes x once; every projection that reads the
+    buffer gives exactly the bits of thq_matmul with THQ_MODE_Q8ACT."""
+    k = shapes[0][1]
+    x = O.bf16_round(activations(m, k, seed=51))
+    xt = torch.from_numpy(x).cuda().to(torch.bfloat16)
+    pre = thq.Q8Act(xt, dot_type)
+    for i, (n, kk) in enumerate(shapes):
+        w = thq.QTensor.from_gguf_bytes(qtype, weight_bytes(qtype, n, kk, seed=60 + i), n, kk)
+        for dt in (torch.float32, torch.bfloat16):
+            want = thq.matmul(w, xt, dt, flags=thq.MODE_Q8ACT)
+            got = pre.matmul(w, dt)
+            assert torch.equal(got.view(torch.int16) if dt == torch.bfloat16 else got.view(torch.int32),
+                               want.view(torch.int16) if dt == torch.bfloat16 else want.view(torch.int32))
+
+
+def test_q8act_prepared_gate_up_and_errors():
+    n, k, m = 1000, 1024, 3
+    both = np.concatenate([weight_bytes(O.Q4_K, n, k, seed=71), weight_bytes(O.Q4_K, n, k, seed=72)])
+    fused = thq.QTensor.from_gguf_bytes(O.Q4_K, both, 2 * n, k)
+    xt = torch.from_numpy(O.bf16_round(activations(m, k, seed=73))).cuda().to(torch.bfloat16)
+    pre = thq.Q8Act(xt, thq.Q8_K)
+    want = thq.gate_up_silu(fused, xt, torch.bfloat16, flags=thq.MODE_Q8ACT)
+    assert torch.equal(pre.gate_up_silu(fused).view(torch.int16), want.view(torch.int16))
+    # a Q8_0 weight needs a Q8_0 buffer; K must match
+    w8 = thq.QTensor.from_gguf_bytes(O.Q8_0, weight_bytes(O.Q8_0, 64, 1024, seed=74), 64, 1024)
+    with pytest.raises(thq.ThqError) as e:
+        pre.matmul(w8)
+    assert e.value.code == thq.EDTYPE
+    w4 = thq.QTensor.from_gguf_bytes(O.Q4_K, weight_bytes(O.Q4_K, 64, 2048, seed=75), 64, 2048)
+    with pytest.raises(thq.ThqError) as e:
+        pre.matmul(w4)
+    assert e.value.code == thq.ESHAPE
+    buf = torch.empty(thq.lib.thq_q8act_bytes(thq.Q8_K, m, k) + 256, dtype=torch.uint8, device="cuda")
+    rc = thq.lib.thq_q8act_prepare(pre.ctx.h, thq.Q8_K, thq._ptr(xt), thq.ACT_BF16, m, k,
+                                   thq.C.c_void_p(buf.data_ptr() + 16), None)
+    assert rc == thq.EALIGN

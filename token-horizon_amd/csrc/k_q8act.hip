@@ -509,12 +509,23 @@ hipError_t launch_quantize_act(int qtype, const void* x, bool xf32, int64_t M, i
                 : quant_act_t<bf16_t>(qtype, static_cast<const bf16_t*>(x), M, K, nullptr, b, s);
 }
 
+hipError_t launch_q8act_prepare(int qtype, const void* x, bool xf32, int64_t M, int64_t K, void* planes,
+                                hipStream_t s) {
+    const ActPlanes a = act_planes(qtype, planes, M, K);
+    return xf32 ? quant_act_t<float>(qtype, static_cast<const float*>(x), M, K, &a, nullptr, s)
+                : quant_act_t<bf16_t>(qtype, static_cast<const bf16_t*>(x), M, K, &a, nullptr, s);
+}
+
 hipError_t launch_q8act(const WeightView& w, const void* x, bool xf32, void* y, bool yf32, bool gu, int M,
                         int64_t nout, int64_t up_off, void* ws, hipStream_t s) {
-    const ActPlanes a = act_planes(w.qtype, ws, M, w.K);
-    hipError_t e = xf32 ? quant_act_t<float>(w.qtype, static_cast<const float*>(x), M, w.K, &a, nullptr, s)
-                        : quant_act_t<bf16_t>(w.qtype, static_cast<const bf16_t*>(x), M, w.K, &a, nullptr, s);
+    hipError_t e = launch_q8act_prepare(w.qtype, x, xf32, M, w.K, ws, s);
     if (e != hipSuccess) return e;
+    return launch_q8act_dot(w, ws, y, yf32, gu, M, nout, up_off, s);
+}
+
+hipError_t launch_q8act_dot(const WeightView& w, const void* planes, void* y, bool yf32, bool gu, int M, int64_t nout,
+                            int64_t up_off, hipStream_t s) {
+    const ActPlanes a = act_planes(w.qtype, const_cast<void*>(planes), M, w.K);
     const int mt = pick_mt(w.qtype, M, (int)w.K);
     if (gu) {
         if (yf32) launch_dot_mt<true, float>(mt, w, a, static_cast<float*>(y), M, nout, up_off, s);

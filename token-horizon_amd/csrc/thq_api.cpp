@@ -652,6 +652,67 @@ int thq_quantize_act(thq_ctx* ctx, thq_dtype dot_type, const void* x_dev, thq_ac
     return THQ_OK;
 }
 
+size_t thq_q8act_bytes(thq_dtype dot_type, int64_t m, int64_t k) {
+    if ((dot_type != THQ_Q8_0 && dot_type != THQ_Q8_K) || m < 0 || k <= 0) return 0;
+    return thq::q8act_workspace_bytes(dot_type == THQ_Q8_0 ? 8 : 12, m, k);
+}
+
+int thq_q8act_prepare(thq_ctx* ctx, thq_dtype dot_type, const void* x_dev, thq_act x_type, int64_t m, int64_t k,
+                      void* buf_dev, void* stream) {
+    if (!ctx || !x_dev || !buf_dev) return fail(THQ_EINVAL, "null argument");
+    if (dot_type != THQ_Q8_0 && dot_type != THQ_Q8_K) return fail(THQ_EDTYPE, "dot type %d (want Q8_0 or Q8_K)", dot_type);
+    if (x_type != THQ_ACT_F32 && x_type != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad x_type %d", x_type);
+    const int qt = dot_type == THQ_Q8_0 ? 8 : 12;
+    const int bs = dot_type == THQ_Q8_0 ? 32 : 256;
+    if (m < 0 || k <= 0 || k % bs) return fail(THQ_ESHAPE, "x [%lld, %lld]: K must be a positive multiple of %d",
+                                               (long long)m, (long long)k, bs);
+    if (!thq::q8act_supported(qt, k)) return fail(THQ_ESHAPE, "K=%lld too large for THQ_MODE_Q8ACT", (long long)k);
+    if (!aligned16(x_dev)) return fail(THQ_EALIGN, "x_dev must be 16-byte aligned");
+    if ((uintptr_t)buf_dev & 255u) return fail(THQ_EALIGN, "buf_dev must be 256-byte aligned");
+    if (m == 0) return THQ_OK;
+    DeviceGuard g(ctx->device);
+    hipError_t e = thq::launch_q8act_prepare(qt, x_dev, x_type == THQ_ACT_F32, m, k, buf_dev,
+                                             static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(THQ_EHIP, "kernel launch: %s", hipGetErrorString(e));
+    return THQ_OK;
+}
+
+namespace {
+
+int run_q8act_dot(thq_ctx* ctx, const thq_weight* w, thq_dtype dot_type, const void* buf, int64_t m, int64_t k,
+                  void* y, int yt, bool gu, void* stream) {
+    if (!ctx || !w || !buf) return fail(THQ_EINVAL, "null argument");
+    if (yt != THQ_ACT_F32 && yt != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad y_type %d", yt);
+    if (w->qtype != THQ_Q8_0 && w->qtype != THQ_Q4_K)
+        return fail(THQ_EDTYPE, "THQ_MODE_Q8ACT applies to Q8_0 and Q4_K weights");
+    const thq_dtype want = w->qtype == THQ_Q8_0 ? THQ_Q8_0 : THQ_Q8_K;
+    if (dot_type != want) return fail(THQ_EDTYPE, "buffer dot type %d, the weight's is %d", dot_type, want);
+    if (k != w->K) return fail(THQ_ESHAPE, "buffer K=%lld, weight K=%lld", (long long)k, (long long)w->K);
+    if (gu && (w->N % 2)) return fail(THQ_ESHAPE, "gate/up weight has an odd row count %lld", (long long)w->N);
+    if (m < 0 || m > (1 << 24)) return fail(THQ_ESHAPE, "M=%lld out of range", (long long)m);
+    if ((uintptr_t)buf & 255u) return fail(THQ_EALIGN, "buf_dev must be 256-byte aligned");
+    if (m == 0) return THQ_OK;
+    if (!y) return fail(THQ_EINVAL, "null y");
+    DeviceGuard g(ctx->device);
+    const int64_t nout = gu ? w->N / 2 : w->N;
+    hipError_t e = thq::launch_q8act_dot(view(w), buf, y, yt == THQ_ACT_F32, gu, (int)m, nout, gu ? nout : 0,
+                                         static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(THQ_EHIP, "kernel launch: %s", hipGetErrorString(e));
+    return THQ_OK;
+}
+
+}  // namespace
+
+int thq_matmul_q8act(thq_ctx* ctx, const thq_weight* w, thq_dtype dot_type, const void* buf_dev, int64_t m, int64_t k,
+                     void* y_dev, thq_act y_type, void* stream) {
+    return run_q8act_dot(ctx, w, dot_type, buf_dev, m, k, y_dev, y_type, false, stream);
+}
+
+int thq_gate_up_silu_q8act(thq_ctx* ctx, const thq_weight* fused, thq_dtype dot_type, const void* buf_dev, int64_t m,
+                           int64_t k, void* y_dev, thq_act y_type, void* stream) {
+    return run_q8act_dot(ctx, fused, dot_type, buf_dev, m, k, y_dev, y_type, true, stream);
+}
+
 int thq_matmul(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m, void* y_dev,
                thq_act y_type, uint32_t flags, void* stream) {
     return run_matmul(ctx, w, x_dev, x_type, m, y_dev, y_type, flags, false, stream);

@@ -100,6 +100,13 @@ bool q8act_supported(int qtype, int64_t K);
 size_t q8act_workspace_bytes(int qtype, int64_t M, int64_t K);
 hipError_t launch_q8act(const WeightView& w, const void* x, bool xf32, void* y, bool yf32, bool gu, int M,
                         int64_t nout, int64_t up_off, void* ws, hipStream_t s);
+// THQ_MODE_Q8ACT in two steps: the activation planes (q8act_workspace_bytes,
+// 256-B aligned) written once by the quantizer, then read by any number of
+// dot launches over weights of the same dot type and K
+hipError_t launch_q8act_prepare(int qtype, const void* x, bool xf32, int64_t M, int64_t K, void* planes,
+                                hipStream_t s);
+hipError_t launch_q8act_dot(const WeightView& w, const void* planes, void* y, bool yf32, bool gu, int M, int64_t nout,
+                            int64_t up_off, hipStream_t s);
 // GGML blocks of the dot type (qtype 8 -> Q8_0 blocks, 12 -> Q8_K blocks)
 hipError_t launch_quantize_act(int qtype, const void* x, bool xf32, int64_t M, int64_t K, void* blocks,
                                hipStream_t s);

@@ -52,7 +52,7 @@ EXPORTS = (
     "thq_gguf_open", "thq_gguf_close", "thq_gguf_version", "thq_gguf_tensor_count", "thq_gguf_metadata_count",
     "thq_gguf_find_tensor", "thq_gguf_tensor_info", "thq_gguf_tensor_data", "thq_gguf_metadata_key",
     "thq_gguf_metadata_u32", "thq_gguf_metadata_f32", "thq_gguf_metadata_str", "thq_gguf_metadata_array",
-    "thq_weight_from_gguf",
+    "thq_weight_from_gguf", "thq_q8act_bytes", "thq_q8act_prepare", "thq_matmul_q8act", "thq_gate_up_silu_q8act",
 )
 
 
@@ -105,6 +105,10 @@ def _load():
         "thq_gguf_metadata_str": ([P, C.c_char_p, C.POINTER(C.c_void_p), C.POINTER(C.c_uint64)], I),
         "thq_gguf_metadata_array": ([P, C.c_char_p, C.POINTER(u32), C.POINTER(C.c_uint64)], I),
         "thq_weight_from_gguf": ([P, P, C.c_char_p, PP], I),
+        "thq_q8act_bytes": ([I, i64, i64], C.c_size_t),
+        "thq_q8act_prepare": ([P, I, P, I, i64, i64, P, P], I),
+        "thq_matmul_q8act": ([P, P, I, P, i64, i64, P, I, P], I),
+        "thq_gate_up_silu_q8act": ([P, P, I, P, i64, i64, P, I, P], I),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -275,6 +279,38 @@ def quantize_act(x: torch.Tensor, dot_type: int, ctx: Context | None = None) -> 
     out = torch.empty((m, (k // BLOCK[dot_type]) * BLOCK_BYTES[dot_type]), dtype=torch.uint8, device=x.device)
     check(lib.thq_quantize_act(ctx.h, dot_type, _ptr(x2), _act(x2), m, k, _ptr(out), _stream()))
     return out
+
+
+class Q8Act:
+    """Activation rows quantized once for THQ_MODE_Q8ACT consumers
+    (thq_q8act_prepare): the producer-side operand several projections of
+    the same input share."""
+
+    def __init__(self, x: torch.Tensor, dot_type: int, ctx: Context | None = None):
+        x2 = x.reshape(-1, x.shape[-1])
+        assert x2.is_contiguous()
+        self.ctx = ctx or Context.get(x.device.index or 0)
+        self.m, self.k = x2.shape
+        self.dot_type = dot_type
+        nbytes = lib.thq_q8act_bytes(dot_type, self.m, self.k)
+        if nbytes == 0:
+            raise ThqError(EDTYPE, f"unsupported dot type {dot_type}")
+        # 256-byte aligned: torch's allocator aligns blocks to 512 bytes
+        self.buf = torch.empty(nbytes, dtype=torch.uint8, device=x.device)
+        check(lib.thq_q8act_prepare(self.ctx.h, dot_type, _ptr(x2), _act(x2), self.m, self.k, _ptr(self.buf),
+                                    _stream()))
+
+    def matmul(self, w: "QTensor", out_dtype=torch.float32) -> torch.Tensor:
+        y = torch.empty((self.m, w.n), dtype=out_dtype, device=self.buf.device)
+        check(lib.thq_matmul_q8act(self.ctx.h, w.h, self.dot_type, _ptr(self.buf), self.m, self.k, _ptr(y),
+                                   _act(y), _stream()))
+        return y
+
+    def gate_up_silu(self, fused: "QTensor", out_dtype=torch.bfloat16) -> torch.Tensor:
+        y = torch.empty((self.m, fused.n // 2), dtype=out_dtype, device=self.buf.device)
+        check(lib.thq_gate_up_silu_q8act(self.ctx.h, fused.h, self.dot_type, _ptr(self.buf), self.m, self.k,
+                                         _ptr(y), _act(y), _stream()))
+        return y
 
 
 def matmul(w: QTensor, x: torch.Tensor, out_dtype=torch.float32, flags: int = 0, out: torch.Tensor | None = None):
