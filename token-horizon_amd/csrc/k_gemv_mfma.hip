@@ -93,8 +93,12 @@ __device__ __forceinline__ float dpp_add(float v) {
 // by the compiler barrier in the staging step.
 // Grid: tiles x splits blocks; block (tile, split) owns the tile's 32 weight
 // rows over K range [split*Kb, (split+1)*Kb), Kb = waves * cpw * 256.
+// Four waves per SIMD for every weight type: two 8-wave blocks per CU (64 KB
+// of LDS each).  The Q8_0 instances with four live rows then spill 28 B per
+// lane, which costs less than halving the resident waves (LM head 151936 x
+// 4096, M = 5: 188 -> 180 us).
 template <int QT, int E, int NX, bool GU, bool SPLIT, typename YT>
-__global__ __launch_bounds__(512, QT != 8 ? 4 : 2) void k_gemv_mfma(const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Wa,
+__global__ __launch_bounds__(512, 4) void k_gemv_mfma(const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Wa,
                                                   const bf16_t* X, void* __restrict__ Yv, int M, int K,
                                                   int64_t nout, int64_t up_off, int64_t nrows, int cpw, int splits,
                                                   float* __restrict__ amv, uint32_t* __restrict__ ami, int64_t am_ld) {
