@@ -214,6 +214,19 @@ def test_q8_0_gemm(m, flags):
         assert_close_elem(f"q8_0 gemm m={m}", y, ref, 2.0 ** -7, floor="rms")
 
 
+@pytest.mark.parametrize("m", [1, 2, 9, 100])
+def test_q8_0_k_odd_multiple_of_32(m):
+    """Q8_0 with K = 32 * odd (K % 64 != 0, allowed by the block size): every
+    M uses all of K (the 64-wide GEMM tiles do not apply to this K)."""
+    n, k = 200, 1056
+    b, w = upload(O.Q8_0, n, k)
+    xf, xb = bf16_x(m, k)
+    y = tonp(thq.matmul(w, xb, torch.float32))
+    ref = O.matmul(O.Q8_0, b, n, k, xf, O.MODE_DEQUANT_F32)
+    assert rel_row_err(y, ref) <= 1e-4
+    assert_close_elem(f"q8_0 k={k} m={m}", y, ref, 2.0 ** -14)
+
+
 @pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K])
 def test_f32_activations_multi_row(qtype):
     n, k = 300, 1024
