@@ -1,0 +1,130 @@
+"""Every routing branch of thq_matmul / thq_gate_up_silu / thq_matmul_argmax
+(run_matmul, token-horizon_amd/csrc/thq_api.cpp) against the oracle, on small
+shapes chosen to reach each kernel's edges: row counts that fill no tile,
+the smallest and unusual K of each block size (including K past the M = 1
+kernels' limits and Q8_0 K that is an odd multiple of 32), M from 1 to past
+the GEMM's 64-row tile, fused gate/up, and f32 activations.
+
+Bars (the tolerances the path is held to everywhere): bf16 x within 1e-2 of
+the row L2 norm, f32 x within 1e-4, argmax equal to the oracle's scan of the
+same call's logits (engine.rs:1891-1898).  Each case prints its parameters
+before it runs.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import activations, q6k_bytes, rand_qlin_fast, rel_row_err, weight_bytes
+
+pytestmark = pytest.mark.gpu
+
+thq = pytest.importorskip("thq")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    torch.cuda.init()
+    yield
+    torch.cuda.synchronize()
+
+
+MS = [1, 2, 3, 5, 8, 9, 33, 65, 130]
+
+# (n, k): rows that fill no 4-row quad / 32-row tile; K at the block size, K
+# between tile sizes, K past the M = 1 kernels' 4096 / 16384 (8192 for Q8_0)
+SHAPES = {
+    O.Q8_0: [(37, 32), (131, 96), (66, 1056), (20, 8224), (34, 4096)],
+    O.Q4_K: [(37, 256), (131, 768), (66, 4352), (10, 16640)],
+    O.Q6_K: [(37, 256), (131, 768), (66, 4352)],
+}
+
+
+def gguf_weight(qtype, n, k, seed):
+    b = q6k_bytes(n, k, seed=seed) if qtype == O.Q6_K else weight_bytes(qtype, n, k, seed=seed)
+    return b, thq.QTensor.from_gguf_bytes(qtype, b, n, k)
+
+
+def run_case(tag, got, want, bar):
+    err = rel_row_err(got, want)
+    assert err <= bar, f"{tag}: max row error {err:.3g} > {bar}"
+
+
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K, O.Q6_K])
+def test_matmul_every_route(qtype):
+    for si, (n, k) in enumerate(SHAPES[qtype]):
+        b, w = gguf_weight(qtype, n, k, seed=100 + si)
+        for m in MS:
+            if m * k > (1 << 21):
+                continue  # keeps the f64 oracle under a second per case
+            print(f"[sweep] qtype={qtype} n={n} k={k} m={m}", flush=True)
+            xf = O.bf16_round(activations(m, k, seed=m))
+            ref = O.matmul(qtype, b, n, k, xf)
+            xb = torch.from_numpy(xf).cuda().to(torch.bfloat16)
+            run_case(f"bf16 q{qtype} {n}x{k} m={m}", thq.matmul(w, xb, torch.float32).cpu().numpy(), ref, 1e-2)
+            if m in (1, 3, 9, 65):
+                xd = torch.from_numpy(xf).cuda()
+                run_case(f"f32 q{qtype} {n}x{k} m={m}", thq.matmul(w, xd, torch.float32).cpu().numpy(), ref, 1e-4)
+
+
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K, O.Q6_K])
+def test_gate_up_every_route(qtype):
+    for si, (h, k) in enumerate(SHAPES[qtype]):
+        b, w = gguf_weight(qtype, 2 * h, k, seed=200 + si)
+        for m in MS:
+            if m * k > (1 << 21):
+                continue
+            print(f"[sweep] gate/up qtype={qtype} h={h} k={k} m={m}", flush=True)
+            xf = O.bf16_round(activations(m, k, seed=m + 7))
+            want = O.bf16_bits_to_f32(O.gate_up_silu(O.matmul(qtype, b, 2 * h, k, xf)))
+            xb = torch.from_numpy(xf).cuda().to(torch.bfloat16)
+            got = thq.gate_up_silu(w, xb, torch.float32).cpu().numpy()
+            run_case(f"gate/up q{qtype} {h}x{k} m={m}", got, want, 1e-2)
+
+
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K, O.Q6_K])
+def test_argmax_every_route(qtype):
+    for si, (n, k) in enumerate(SHAPES[qtype]):
+        b, w = gguf_weight(qtype, n, k, seed=300 + si)
+        for m in (1, 2, 9, 65):
+            if m * k > (1 << 21):
+                continue
+            print(f"[sweep] argmax qtype={qtype} n={n} k={k} m={m}", flush=True)
+            xf = O.bf16_round(activations(m, k, seed=m + 11))
+            xb = torch.from_numpy(xf).cuda().to(torch.bfloat16)
+            logits, idx = thq.matmul_argmax(w, xb)
+            lg = logits.cpu().numpy()
+            run_case(f"argmax logits q{qtype} {n}x{k} m={m}", lg, O.matmul(qtype, b, n, k, xf), 1e-4)
+            assert np.array_equal(idx.cpu().numpy().astype(np.uint32), O.argmax_rows(lg))
+            _, idx2 = thq.matmul_argmax(w, xb, want_logits=False)
+            assert torch.equal(idx, idx2)
+
+
+def test_affine_gate_up_every_route():
+    for si, (h, k) in enumerate([(37, 64), (131, 320), (66, 768)]):
+        wq, sb = rand_qlin_fast(2 * h, k, seed=500 + si)
+        w = thq.QTensor.from_affine(wq, sb, 2 * h, k)
+        for m in MS:
+            print(f"[sweep] affine gate/up h={h} k={k} m={m}", flush=True)
+            xf = O.bf16_round(activations(m, k, seed=m + 17))
+            want = O.bf16_bits_to_f32(O.gate_up_silu(O.affine_matmul(wq, sb, 2 * h, k, xf)))
+            xb = torch.from_numpy(xf).cuda().to(torch.bfloat16)
+            run_case(f"affine gate/up {h}x{k} m={m}", thq.gate_up_silu(w, xb, torch.float32).cpu().numpy(), want, 1e-2)
+
+
+def test_affine_every_route():
+    # K = 64 and 320 are not whole 256-wide tiles (exact generic kernel); 768 is
+    for si, (n, k) in enumerate([(37, 64), (131, 320), (66, 768)]):
+        wq, sb = rand_qlin_fast(n, k, seed=400 + si)
+        w = thq.QTensor.from_affine(wq, sb, n, k)
+        for m in MS:
+            print(f"[sweep] affine n={n} k={k} m={m}", flush=True)
+            xf = O.bf16_round(activations(m, k, seed=m + 13))
+            ref = O.affine_matmul(wq, sb, n, k, xf)
+            xb = torch.from_numpy(xf).cuda().to(torch.bfloat16)
+            run_case(f"affine {n}x{k} m={m}", thq.matmul(w, xb, torch.float32).cpu().numpy(), ref, 1e-2)
+            if m in (1, 9):
+                xd = torch.from_numpy(xf).cuda()
+                run_case(f"affine f32 {n}x{k} m={m}", thq.matmul(w, xd, torch.float32).cpu().numpy(), ref, 1e-4)

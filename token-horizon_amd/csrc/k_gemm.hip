@@ -750,6 +750,14 @@ GemmPlan plan_gemm(int qtype, bool exact, int64_t M, int64_t N_rows, int64_t K, 
     p.tiles_n = gu ? (nout + 63) / 64 : (nout + BN - 1) / BN;
     p.tiles_m = (M + bm - 1) / bm;
     const int kiters = (int)(K / BK);
+    if (kiters < 1) {
+        // K < 64: no GEMM tiles (the router sends such K to the generic
+        // kernel); an empty plan keeps workspace sizing well defined
+        p.kps = 0;
+        p.splits = 1;
+        p.workspace_bytes = 0;
+        return p;
+    }
     int splits = env_int("THQ_GEMM_SPLITS", 0);
     if (splits <= 0) {
         const int64_t blocks = p.tiles_n * p.tiles_m;

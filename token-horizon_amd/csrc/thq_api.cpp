@@ -271,6 +271,10 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
     } else if (am) {
         return THQ_OK;
     } else if (!xf32 && aligned16(x) && w->K % 64 == 0 &&  // the GEMMs step K in 64-wide tiles
+               // gate/up rows of < 256 outputs: the rounded-weight tile's error, seen
+               // through silu(g)*u, is not averaged down by the row norm (the exact
+               // kernel costs nothing at that size)
+               !(gu && nout < 256) &&
                !((q4 || q6) && ((flags & THQ_MODE_EXACT_W) || w->K % 256)) &&
                !(q6 && (m <= 8 || thq::q6k_layout(w->N, w->K).total >= (1ull << 32) ||
                         (uint64_t)m * (uint64_t)w->K * 2 >= (1ull << 32)))) {
