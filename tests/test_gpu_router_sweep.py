@@ -128,3 +128,52 @@ def test_affine_every_route():
             if m in (1, 9):
                 xd = torch.from_numpy(xf).cuda()
                 run_case(f"affine f32 {n}x{k} m={m}", thq.matmul(w, xd, torch.float32).cpu().numpy(), ref, 1e-4)
+
+
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K])
+def test_q8act_every_route(qtype):
+    """THQ_MODE_Q8ACT (candle's default semantics) on the same shapes: within
+    1e-5 of the oracle's Q8ACT matmul, and the quantize-once buffer gives the
+    same bits; K past the mode's limit is an error, not a wrong answer."""
+    dot = thq.Q8_0 if qtype == O.Q8_0 else thq.Q8_K
+    for si, (n, k) in enumerate(SHAPES[qtype]):
+        b, w = gguf_weight(qtype, n, k, seed=600 + si)
+        for m in MS:
+            if m * k > (1 << 21):
+                continue
+            print(f"[sweep] q8act qtype={qtype} n={n} k={k} m={m}", flush=True)
+            xf = O.bf16_round(activations(m, k, seed=m + 19))
+            xb = torch.from_numpy(xf).cuda().to(torch.bfloat16)
+            try:
+                y = thq.matmul(w, xb, torch.float32, flags=thq.MODE_Q8ACT)
+            except thq.ThqError as e:
+                assert e.code == thq.ESHAPE, e
+                continue
+            run_case(f"q8act q{qtype} {n}x{k} m={m}", y.cpu().numpy(), O.matmul(qtype, b, n, k, xf, O.MODE_Q8ACT),
+                     1e-5)
+            pre = thq.Q8Act(xb, dot)
+            assert torch.equal(pre.matmul(w, torch.float32).view(torch.int32), y.view(torch.int32))
+
+
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K, O.Q6_K])
+def test_fused_argmax_every_route(qtype):
+    """THQ_MODE_ARGMAX_FUSED gives the logits path's indices on every decode
+    route (and on the shapes where no fused epilogue exists)."""
+    for si, (n, k) in enumerate(SHAPES[qtype]):
+        b, w = gguf_weight(qtype, n, k, seed=700 + si)
+        for m in (1, 2, 3, 5, 8, 9):
+            print(f"[sweep] fused argmax qtype={qtype} n={n} k={k} m={m}", flush=True)
+            xb = torch.from_numpy(O.bf16_round(activations(m, k, seed=m + 23))).cuda().to(torch.bfloat16)
+            _, fused = thq.matmul_argmax(w, xb, want_logits=False, flags=thq.MODE_ARGMAX_FUSED)
+            logits, idx = thq.matmul_argmax(w, xb)
+            assert torch.equal(fused, idx)
+            assert np.array_equal(idx.cpu().numpy().astype(np.uint32), O.argmax_rows(logits.cpu().numpy()))
+
+
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K, O.Q6_K])
+def test_dequant_every_shape(qtype):
+    for si, (n, k) in enumerate(SHAPES[qtype]):
+        print(f"[sweep] dequant qtype={qtype} n={n} k={k}", flush=True)
+        b, w = gguf_weight(qtype, n, k, seed=800 + si)
+        got = w.dequantize().cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), O.dequantize(qtype, b, n, k).view(np.uint32))
