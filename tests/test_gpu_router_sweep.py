@@ -177,3 +177,26 @@ def test_dequant_every_shape(qtype):
         b, w = gguf_weight(qtype, n, k, seed=800 + si)
         got = w.dequantize().cpu().numpy()
         assert np.array_equal(got.view(np.uint32), O.dequantize(qtype, b, n, k).view(np.uint32))
+
+
+@pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K, O.Q6_K])
+def test_bf16_out_and_f32_gate_up_every_route(qtype):
+    """bf16 outputs (RNE of the f32 accumulator) of thq_matmul, and gate/up
+    with f32 activations, on the same routes."""
+    for si, (n, k) in enumerate(SHAPES[qtype]):
+        b, w = gguf_weight(qtype, n, k, seed=900 + si)
+        h = n // 2
+        for m in (1, 3, 9, 65):
+            if m * k > (1 << 21):
+                continue
+            print(f"[sweep] bf16 out / f32 gate-up qtype={qtype} n={n} k={k} m={m}", flush=True)
+            xf = O.bf16_round(activations(m, k, seed=m + 29))
+            xb = torch.from_numpy(xf).cuda().to(torch.bfloat16)
+            ref = O.matmul(qtype, b, n, k, xf)
+            got = thq.matmul(w, xb, torch.bfloat16).float().cpu().numpy()
+            run_case(f"bf16 out q{qtype} {n}x{k} m={m}", got, ref, 1e-2)
+            if h > 0 and n % 2 == 0:
+                xd = torch.from_numpy(xf).cuda()
+                want = O.bf16_bits_to_f32(O.gate_up_silu(ref))
+                run_case(f"f32 gate/up q{qtype} {h}x{k} m={m}",
+                         thq.gate_up_silu(w, xd, torch.float32).cpu().numpy(), want, 1e-2)
