@@ -247,3 +247,93 @@ def test_missing_file_and_null_handles(tmp_path):
     assert L.thq_gguf_find_tensor(None, b"x") == -1
     assert L.thq_gguf_open(None, None) == thq.EINVAL
     L.thq_gguf_close(None)  # no-op
+
+
+def raw_header(n_tensors: int, n_kv: int, body: bytes = b"") -> bytes:
+    return b"GGUF" + struct.pack("<IQQ", 3, n_tensors, n_kv) + body
+
+
+def raw_tensor_info(name: str, ne, ggml_type: int, offset: int) -> bytes:
+    """one tensor info as GGUF stores it (ne fastest dimension first)"""
+    b = struct.pack("<Q", len(name)) + name.encode() + struct.pack("<I", len(ne))
+    for d in ne:
+        b += struct.pack("<Q", d)
+    return b + struct.pack("<IQ", ggml_type, offset)
+
+
+def test_hostile_counts_and_sizes_fail_cleanly(tmp_path):
+    """Counts and sizes near the integer limits are format errors: the reader
+    neither reserves memory for them nor lets a size or offset wrap."""
+    cases = {
+        "tensor count 2^40": raw_header(1 << 40, 0),
+        "tensor count 2^63": raw_header(1 << 63, 0),
+        "metadata count 2^40": raw_header(0, 1 << 40),
+        "metadata count 2^64-1": raw_header(0, (1 << 64) - 1),
+        "array of 2^62 u8": build_raw_kv(G.ARRAY, struct.pack("<IQ", G.U8, 1 << 62)),
+        "array of 2^40 strings": build_raw_kv(G.ARRAY, struct.pack("<IQ", G.STRING, 1 << 40)),
+        "array of 2^61 u64": build_raw_kv(G.ARRAY, struct.pack("<IQ", G.U64, 1 << 61)),
+        "tensor name length 2^63": raw_header(1, 0, struct.pack("<Q", 1 << 63) + b"w"),
+        "element count overflows": raw_header(1, 0, raw_tensor_info("w", (1 << 33, 1 << 33), 0, 0)),
+        "byte size overflows": raw_header(1, 0, raw_tensor_info("w", (1 << 62,), 0, 0)),
+    }
+    for name, data in cases.items():
+        with pytest.raises(thq.ThqError) as e:
+            thq.GGUFFile(write(tmp_path, "bad.gguf", data))
+        assert e.value.code == thq.EFORMAT, name
+    # an offset that wraps past 2^64 with the tensor's size: no data, never a pointer
+    data = raw_header(1, 0, raw_tensor_info("w", (4,), 0, (1 << 64) - 8))
+    try:
+        f = thq.GGUFFile(write(tmp_path, "off.gguf", data))
+    except thq.ThqError as e:
+        assert e.code == thq.EFORMAT
+    else:
+        with f:
+            with pytest.raises(thq.ThqError) as e:
+                f.tensor_bytes("w")
+            assert e.value.code == thq.EFORMAT
+
+
+def test_random_corruption_never_reads_out_of_bounds(tmp_path):
+    """Bit flips and 8-byte overwrites anywhere in a valid header give either a
+    parse or THQ_EFORMAT; every string and tensor the parse returns lies inside
+    the file (each is read here in full)."""
+    import ctypes as C
+    data, _, _ = G.build(KV, TENSORS)
+    header_end = G.build(KV, TENSORS, data_align=1)[1]
+    rng = np.random.default_rng(11)
+    p = tmp_path / "x.gguf"
+    L = thq.lib
+    opened = 0
+    for trial in range(1500):
+        b = bytearray(data)
+        pos = int(rng.integers(0, header_end))
+        if trial % 3 == 0:
+            b[pos:pos + 8] = rng_bytes(8, trial)[: len(b[pos:pos + 8])]
+        else:
+            b[pos] ^= 1 << int(rng.integers(0, 8))
+        p.write_bytes(bytes(b))
+        h = C.c_void_p()
+        rc = L.thq_gguf_open(str(p).encode(), C.byref(h))
+        if rc != 0:
+            assert rc == thq.EFORMAT, (trial, pos, rc)
+            continue
+        opened += 1
+        try:
+            for i in range(L.thq_gguf_metadata_count(h)):
+                key, vt = C.c_char_p(), C.c_uint32()
+                assert L.thq_gguf_metadata_key(h, i, C.byref(key), C.byref(vt)) == 0
+                if vt.value == G.STRING:
+                    s, n = C.c_void_p(), C.c_uint64()
+                    assert L.thq_gguf_metadata_str(h, key.value, C.byref(s), C.byref(n)) == 0
+                    assert n.value <= len(b)
+                    C.string_at(s.value, n.value) if n.value else b""
+            for i in range(L.thq_gguf_tensor_count(h)):
+                d, n = C.c_void_p(), C.c_uint64()
+                rc = L.thq_gguf_tensor_data(h, i, C.byref(d), C.byref(n))
+                assert rc in (0, thq.EFORMAT, thq.ESHAPE), (trial, rc)  # ESHAPE: elements not whole blocks
+                if rc == 0 and n.value:
+                    assert n.value <= len(b)
+                    C.string_at(d.value, n.value)
+        finally:
+            L.thq_gguf_close(h)
+    assert opened > 0

@@ -110,6 +110,10 @@ int check_dtype_shape(int dtype, int64_t n, int64_t k) {
     if (n <= 0 || k <= 0) return fail(THQ_ESHAPE, "weight shape [%lld, %lld] must be positive", (long long)n, (long long)k);
     if (k % bs) return fail(THQ_ESHAPE, "K=%lld is not a multiple of the block size %d", (long long)k, bs);
     if (k > (int64_t)1 << 30 || n > (int64_t)1 << 40) return fail(THQ_ESHAPE, "weight shape too large");
+    // the packed bytes (at most 34 B per 32 weights) must stay far from any
+    // size or offset wrap: 2^46 B is beyond any device's memory
+    if ((double)n * (double)k * (34.0 / 32.0) > (double)((int64_t)1 << 46))
+        return fail(THQ_ESHAPE, "weight of %lld x %lld elements is too large", (long long)n, (long long)k);
     return THQ_OK;
 }
 

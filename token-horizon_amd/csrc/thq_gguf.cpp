@@ -297,8 +297,11 @@ int parse(thq_gguf* g) {
         t.rel_offset = r.rd<uint64_t>();
         if (r.err) return r.err;
         if (!type_info(t.type).bs) return fail(THQ_EFORMAT, "GGUF: unknown dtype %u for tensor %s", t.type, t.name.c_str());
-        uint64_t e;
+        uint64_t e, nb;
         if (!elems(t, e)) return fail(THQ_EFORMAT, "GGUF: tensor %s has more than 2^64 elements", t.name.c_str());
+        const TypeInfo ti = type_info(t.type);
+        if (__builtin_mul_overflow(e / ti.bs, (uint64_t)ti.ts, &nb))
+            return fail(THQ_EFORMAT, "GGUF: tensor %s has more than 2^64 bytes", t.name.c_str());
         auto it = g->t_index.find(t.name);
         if (it != g->t_index.end()) {
             g->tensors[it->second] = t;
