@@ -100,7 +100,9 @@ const char* thq_version(void);
 
 /* Copy GGUF block bytes (host memory, [N][K/bs] blocks row-major, exactly
  * QTensor::data()) to the device.  The library may repack on device; the
- * handle owns its device memory.  Synchronous.
+ * handle owns its device memory.  Synchronous.  Every weight (any creation
+ * call) has N >= 1, K a positive multiple of the block size, K <= 2^30,
+ * N <= 2^40 and at most 2^46 packed bytes; THQ_ESHAPE otherwise.
  * Replaces candle's QTensor::new / QMatMul::from_arc
  * (reached from engine/src/model.rs:551-562). */
 int thq_weight_upload(thq_ctx* ctx, thq_dtype dtype, const void* host_blocks, int64_t n, int64_t k,
