@@ -740,8 +740,36 @@ static inline int env_int(const char* name, int dflt) {
     return v && *v ? atoi(v) : dflt;
 }
 
-GemmPlan plan_gemm(int qtype, bool exact, int64_t M, int64_t N_rows, int64_t K, bool gu) {
+// K-split count for the 128- and 256-row tiles.  Their blocks hold more than
+// 80 KB of LDS, so one block per CU is resident.  The modeled time is:
+//   rounds of resident blocks x K steps per block x step time
+//   + per split, the partials' round trip through HBM (written once, read
+//     once by k_split_reduce: 8 B per output element) and the reduce launch.
+// Step times were measured on MI355X with every CU busy: 1.25 us for 256-row
+// tiles, 1.1 us for 128-row tiles.  The partials are priced at 5 TB/s.  On
+// the 9 swept Q4_K shapes (M = 128..1024; 12288 x 4096 and 4096 x 12288;
+// counts 1, 2, 3, 4, 8 timed), the model picks the fastest count every time.
+static int pick_splits(int64_t blocks, int kiters, int max_split, int64_t M, int64_t N_rows, int bm, int cus) {
+    const double tstep = bm == 256 ? 1.25 : 1.1;                    // us per K step
+    const double part = (double)M * (double)N_rows * 8.0 / 5.0e6;  // us per split
+    int best = 1;
+    double best_t = 0.0;
+    for (int s = 1; s <= max_split && s <= 64; ++s) {
+        const int kps = (kiters + s - 1) / s;
+        if ((kiters + kps - 1) / kps != s) continue;  // the same plan as a smaller count
+        const int64_t rounds = (blocks * s + cus - 1) / cus;
+        const double t = (double)rounds * kps * tstep + (s > 1 ? s * part + 2.0 : 0.0);
+        if (s == 1 || t < best_t) {
+            best = s;
+            best_t = t;
+        }
+    }
+    return best;
+}
+
+GemmPlan plan_gemm(int qtype, bool exact, int64_t M, int64_t N_rows, int64_t K, bool gu, int cus) {
     GemmPlan p;
+    if (cus < 1) cus = 256;
     int bm = env_int("THQ_GEMM_BM", 0);
     if (bm != 64 && bm != 128 && bm != 256) bm = M <= 64 ? 64 : (M <= 128 ? 128 : 256);
     if (exact && bm > 64) bm = 64;  // the exact tile keeps two accumulator sets
@@ -761,12 +789,17 @@ GemmPlan plan_gemm(int qtype, bool exact, int64_t M, int64_t N_rows, int64_t K, 
     int splits = env_int("THQ_GEMM_SPLITS", 0);
     if (splits <= 0) {
         const int64_t blocks = p.tiles_n * p.tiles_m;
-        const int64_t want = 512;  // two blocks per CU
+        const int max_split = kiters / 2 > 0 ? kiters / 2 : 1;
         splits = 1;
-        if (blocks < want) {
-            splits = (int)((want + blocks - 1) / blocks);
-            const int max_split = kiters / 2 > 0 ? kiters / 2 : 1;
-            if (splits > max_split) splits = max_split;
+        if (bm == 64) {
+            // 64-row tiles (< 80 KB of LDS): two blocks per CU; split until they fill it
+            const int64_t want = 2 * (int64_t)cus;
+            if (blocks < want) {
+                splits = (int)((want + blocks - 1) / blocks);
+                if (splits > max_split) splits = max_split;
+            }
+        } else {
+            splits = pick_splits(blocks, kiters, max_split, M, N_rows, bm, cus);
         }
     }
     if (splits > kiters) splits = kiters;

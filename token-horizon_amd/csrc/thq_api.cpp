@@ -23,6 +23,7 @@
 
 struct thq_ctx {
     int device = 0;
+    int cus = 256;  // compute units (GEMM split planning)
     std::mutex mu;
     void* ws = nullptr;  // workspace: split-K partials, argmax partials, logits
     size_t ws_bytes = 0;
@@ -283,7 +284,7 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
                !(q6 && (m <= 8 || thq::q6k_layout(w->N, w->K).total >= (1ull << 32) ||
                         (uint64_t)m * (uint64_t)w->K * 2 >= (1ull << 32)))) {
         const bool exact = (flags & THQ_MODE_EXACT_W) || (w->qtype == THQ_Q8_0 && m <= 64);
-        thq::GemmPlan p = thq::plan_gemm(v.qtype, exact, m, w->N, w->K, gu);
+        thq::GemmPlan p = thq::plan_gemm(v.qtype, exact, m, w->N, w->K, gu, ctx->cus);
         std::lock_guard<std::mutex> lk(ctx->mu);
         if (p.workspace_bytes) {
             int rc = ensure_ws(ctx, p.workspace_bytes);
@@ -313,6 +314,9 @@ int thq_init(int device, thq_ctx** out) {
     thq_ctx* c = new (std::nothrow) thq_ctx();
     if (!c) return fail(THQ_ENOMEM, "host allocation failed");
     c->device = device;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
+        c->cus = cus;
     *out = c;
     return THQ_OK;
 }
@@ -783,7 +787,7 @@ int thq_matmul_argmax(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_
     }
     if (!logits) {
         // logits live at the end of the workspace, after the GEMM / argmax scratch
-        const thq::GemmPlan p = thq::plan_gemm(view(w).qtype, true, m, w->N, w->K, false);
+        const thq::GemmPlan p = thq::plan_gemm(view(w).qtype, true, m, w->N, w->K, false, ctx->cus);
         size_t scratch = std::max(p.workspace_bytes, thq::argmax_workspace_bytes(m, w->N));
         if (flags & THQ_MODE_Q8ACT) scratch = std::max(scratch, thq::q8act_workspace_bytes(w->qtype, m, w->K));
         const size_t off = (scratch + 255) & ~(size_t)255;

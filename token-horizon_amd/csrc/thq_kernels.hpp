@@ -91,7 +91,8 @@ hipError_t launch_generic(const WeightView& w, const void* x, bool xf32, void* y
                           int64_t nout, int64_t up_off, hipStream_t s);
 
 // MFMA GEMM (bf16 activations)
-GemmPlan plan_gemm(int qtype, bool exact, int64_t M, int64_t N_rows, int64_t K, bool gu);
+// cus: compute units of the device (the split count fills whole rounds of them)
+GemmPlan plan_gemm(int qtype, bool exact, int64_t M, int64_t N_rows, int64_t K, bool gu, int cus);
 hipError_t launch_gemm(const GemmPlan& p, const WeightView& w, const void* x, void* y, bool yf32, bool gu, bool exact,
                        int M, float* ws, hipStream_t s);
 
