@@ -189,7 +189,7 @@ def test_q4k_prefill_gemm(m, n, k):
     assert_close_elem(f"q4k gemm m={m}", got, ref, 2.0 ** -6, floor="rms")
 
 
-@pytest.mark.parametrize("m", [9, 33, 100])
+@pytest.mark.parametrize("m", [9, 17, 33, 100])
 def test_q4k_gemm_ragged_m(m):
     n, k = 1000, 2048  # ragged N tile too
     b, w = upload(O.Q4_K, n, k)
@@ -200,7 +200,7 @@ def test_q4k_gemm_ragged_m(m):
     assert_close_elem(f"q4k ragged m={m}", y, ref, 2.0 ** -7, floor="rms")
 
 
-@pytest.mark.parametrize("m,flags", [(16, 0), (100, 0), (100, thq.MODE_EXACT_W)])
+@pytest.mark.parametrize("m,flags", [(16, 0), (17, 0), (100, 0), (100, thq.MODE_EXACT_W)])
 def test_q8_0_gemm(m, flags):
     n, k = 777, 1024
     b, w = upload(O.Q8_0, n, k)

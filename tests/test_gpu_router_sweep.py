@@ -3,7 +3,8 @@
 shapes chosen to reach each kernel's edges: row counts that fill no tile,
 the smallest and unusual K of each block size (including K past the M = 1
 kernels' limits and Q8_0 K that is an odd multiple of 32), M from 1 to past
-the GEMM's 64-row tile, fused gate/up, and f32 activations.
+the GEMM's 64-row tile (9..16 rows: the MFMA decode GEMV with eight live
+accumulator rows per lane), fused gate/up, and f32 activations.
 
 Bars (the tolerances the path is held to everywhere): bf16 x within 1e-2 of
 the row L2 norm, f32 x within 1e-4, argmax equal to the oracle's scan of the
@@ -31,7 +32,7 @@ def _gpu():
     torch.cuda.synchronize()
 
 
-MS = [1, 2, 3, 5, 8, 9, 33, 65, 130]
+MS = [1, 2, 3, 5, 8, 9, 12, 16, 33, 65, 130]
 
 # (n, k): rows that fill no 4-row quad / 32-row tile; K at the block size, K
 # between tile sizes, K past the M = 1 kernels' 4096 / 16384 (8192 for Q8_0)
@@ -88,7 +89,7 @@ def test_gate_up_every_route(qtype):
 def test_argmax_every_route(qtype):
     for si, (n, k) in enumerate(SHAPES[qtype]):
         b, w = gguf_weight(qtype, n, k, seed=300 + si)
-        for m in (1, 2, 9, 65):
+        for m in (1, 2, 9, 16, 65):
             if m * k > (1 << 21):
                 continue
             print(f"[sweep] argmax qtype={qtype} n={n} k={k} m={m}", flush=True)

@@ -39,8 +39,8 @@
 //         QH bytes 8g..8g+7 (group G in bits 2G).  B = bf16(128 + code), and
 //         per group sum x*w = s*(A - 160*S16), s = d*sc, S16 = sum x over the
 //         group; the block's K range is at most 4096 (256 group sums in LDS).
-// The MFMA output lane holds column n and rows 8*(e/4) + 4*g + e%4; with
-// M <= 8 only e = 0..3 (rows 4g + e) are live.  Each wave accumulates its
+// The MFMA output lane holds column n and rows 8*(e/4) + 4*g + e%4: with
+// M <= 8 only e = 0..3 (rows 4g + e) are live, with M <= 16 e = 0..7.  Each wave accumulates its
 // slice in registers; the block sums the slices in LDS in wave order
 // (deterministic) and applies the epilogue.
 #include "thq_dev.hpp"
@@ -73,6 +73,9 @@ constexpr int MAXW = 8;          // waves per block
 constexpr int XS_ELEMS = 32768;  // staged activations (bf16) per block: M * Kb <= 32768
 constexpr int KB_MAX = 8192;     // K range of one block
 constexpr int XCH = 8;           // staged 16-B activation chunks per thread: M * cpw / 2 <= XCH
+constexpr int MMAX = 16;         // activation rows (E = 8 live accumulator rows per lane)
+// with M > 8, M * cpw <= 2 * XCH leaves one chunk per wave: Kb <= MAXW * 256
+constexpr int KB_MAX_E8 = MAXW * 256;
 
 // Packed weights and scales of one chunk (4 units = one Q4_K superblock) of a
 // wave's K slice.
@@ -104,11 +107,15 @@ __global__ __launch_bounds__(512, 4) void k_gemv_mfma(const uint8_t* __restrict_
                                                   float* __restrict__ amv, uint32_t* __restrict__ ami, int64_t am_ld) {
     // staged activation rows (row stride Kb + 8: rows start 16 B apart in bank
     // order), sub-block sums S[sb][8] and the cross-wave reduction buffer
-    __shared__ __attribute__((aligned(16))) bf16_t xs[XS_ELEMS + 8 * 8];
-    __shared__ __attribute__((aligned(16))) float Ss[QT != 8 ? KB_MAX / 32 : 1][8];  // Q6_K: 16-wide sums, Kb <= 4096
+    __shared__ __attribute__((aligned(16))) bf16_t xs[XS_ELEMS + 8 * MMAX];
+    // Q4_K / affine: 32-wide sums (Kb / 32 <= 256); Q6_K: 16-wide sums (Kb <= 4096);
+    // E = 8 (M <= 16): Kb <= 2048, at most 128 sums of 16 rows
+    constexpr int SR = E > 4 ? MMAX : 8;
+    __shared__ __attribute__((aligned(16))) float Ss[QT == 8 ? 1 : (E > 4 ? KB_MAX_E8 / 16 : KB_MAX / 32)][SR];
     // the cross-wave reduction reuses the staging buffer once all waves are done with it
-    float(*red)[8][32] = reinterpret_cast<float(*)[8][32]>(&xs[0]);
-    static_assert(MAXW * 8 * 32 * 4 <= XS_ELEMS * 2, "reduction buffer exceeds the staging buffer");
+    float(*red)[SR][32] = reinterpret_cast<float(*)[SR][32]>(&xs[0]);
+    static_assert(MAXW * SR * 32 * 4 <= XS_ELEMS * 2, "reduction buffer exceeds the staging buffer");
+    static_assert(E == 1 || E == 2 || E == 4 || E == 8, "live accumulator rows");
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -202,7 +209,7 @@ __global__ __launch_bounds__(512, 4) void k_gemv_mfma(const uint8_t* __restrict_
     __builtin_amdgcn_sched_barrier(0);
     Chunk<QT> B0, B1;
     load(B0, c0);
-    load(B1, cpw > 1 ? c0 + 1 : c0);
+    if constexpr (E <= 4) load(B1, cpw > 1 ? c0 + 1 : c0);  // E = 8 plans give one chunk per wave
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
         const int ch = threadIdx.x + i * blockDim.x;
@@ -245,6 +252,16 @@ __global__ __launch_bounds__(512, 4) void k_gemv_mfma(const uint8_t* __restrict_
 #pragma unroll
     for (int e = 0; e < E; ++e) tot[e] = 0.0f;
 
+    // E = 8: eight live rows per lane; left free, the compiler issues every
+    // unit's MFMAs first and spills their results.  Pinning tot after each
+    // unit (and a scheduling barrier) keeps one unit's MFMAs in flight.
+    auto pin_e8 = [](float(&t)[E]) {
+        if constexpr (E > 4) {
+#pragma unroll
+            for (int e = 0; e < E; ++e) asm volatile("" : "+v"(t[e]));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
     auto compute = [&](const Chunk<QT>& C, int c) {
         if constexpr (QT == 14) {
             const float dd = valid ? f16_to_f32((uint16_t)C.d) : 0.0f;
@@ -266,11 +283,15 @@ __global__ __launch_bounds__(512, 4) void k_gemv_mfma(const uint8_t* __restrict_
 #pragma unroll
                 for (int G = 0; G < 4; ++G) {
                     const uint4 a = *reinterpret_cast<const uint4*>(xa + kl + 16 * G);
-                    const f32x4_t S = *reinterpret_cast<const f32x4_t*>(&Ss[(kl >> 4) + G][4 * g]);
+                    f32x4_t S[E > 4 ? 2 : 1];
+#pragma unroll
+                    for (int h = 0; h < (E > 4 ? 2 : 1); ++h)
+                        S[h] = *reinterpret_cast<const f32x4_t*>(&Ss[(kl >> 4) + G][8 * h + 4 * g]);
                     const float sg = dd * (float)(int)(int8_t)(C.s[u] >> (8 * G));
                     const f32x16_t A = mfma32x16(as_bf16x8(a), nib_bf16x8(lo[G], hi[G]), z16);
 #pragma unroll
-                    for (int e = 0; e < E; ++e) tot[e] = __builtin_fmaf(sg, __builtin_fmaf(-160.0f, S[e], A[e]), tot[e]);
+                    for (int e = 0; e < E; ++e)
+                        tot[e] = __builtin_fmaf(sg, __builtin_fmaf(-160.0f, S[e >> 2][e & 3], A[e]), tot[e]);
                     // the 16 MFMAs of a chunk are independent: left free, the compiler
                     // issues them all first and sinks their FMAs past the next chunk's
                     // loads, keeping every accumulator live; pinning tot here (and a
@@ -296,8 +317,12 @@ __global__ __launch_bounds__(512, 4) void k_gemv_mfma(const uint8_t* __restrict_
             const uint4 a2 = *reinterpret_cast<const uint4*>(xa + kl + 32);
             const uint4 a3 = *reinterpret_cast<const uint4*>(xa + kl + 40);
             if (QT != 8) {
-                const f32x4_t S1 = *reinterpret_cast<const f32x4_t*>(&Ss[kl >> 5][4 * g]);
-                const f32x4_t S2 = *reinterpret_cast<const f32x4_t*>(&Ss[(kl >> 5) + 1][4 * g]);
+                f32x4_t S1[E > 4 ? 2 : 1], S2[E > 4 ? 2 : 1];
+#pragma unroll
+                for (int h = 0; h < (E > 4 ? 2 : 1); ++h) {
+                    S1[h] = *reinterpret_cast<const f32x4_t*>(&Ss[kl >> 5][8 * h + 4 * g]);
+                    S2[h] = *reinterpret_cast<const f32x4_t*>(&Ss[(kl >> 5) + 1][8 * h + 4 * g]);
+                }
                 const uint32_t h = C.s[u];
                 float d1, d2, c1, c2;
                 if constexpr (QT == 13) {  // affine group: w = scale * q + bias
@@ -316,11 +341,14 @@ __global__ __launch_bounds__(512, 4) void k_gemv_mfma(const uint8_t* __restrict_
                 f32x16_t A = mfma32x16(as_bf16x8(a0), nib_bf16x8(q.x & M4, q.y & M4), z16);
                 A = mfma32x16(as_bf16x8(a1), nib_bf16x8(q.z & M4, q.w & M4), A);
 #pragma unroll
-                for (int e = 0; e < E; ++e) tot[e] = __builtin_fmaf(-c1, S1[e], __builtin_fmaf(d1, A[e], tot[e]));
+                for (int e = 0; e < E; ++e)
+                    tot[e] = __builtin_fmaf(-c1, S1[e >> 2][e & 3], __builtin_fmaf(d1, A[e], tot[e]));
                 A = mfma32x16(as_bf16x8(a2), nib_bf16x8((q.x >> 4) & M4, (q.y >> 4) & M4), z16);
                 A = mfma32x16(as_bf16x8(a3), nib_bf16x8((q.z >> 4) & M4, (q.w >> 4) & M4), A);
 #pragma unroll
-                for (int e = 0; e < E; ++e) tot[e] = __builtin_fmaf(-c2, S2[e], __builtin_fmaf(d2, A[e], tot[e]));
+                for (int e = 0; e < E; ++e)
+                    tot[e] = __builtin_fmaf(-c2, S2[e >> 2][e & 3], __builtin_fmaf(d2, A[e], tot[e]));
+                pin_e8(tot);
             } else {
                 float da = f16_to_f32((uint16_t)C.s[u]), db = f16_to_f32((uint16_t)(C.s[u] >> 16));
                 if (!valid) da = db = 0.0f;
@@ -333,12 +361,15 @@ __global__ __launch_bounds__(512, 4) void k_gemv_mfma(const uint8_t* __restrict_
                 A = mfma32x16(as_bf16x8(a3), i8_bf16x8(q1.z, q1.w), A);
 #pragma unroll
                 for (int e = 0; e < E; ++e) tot[e] = __builtin_fmaf(db, A[e], tot[e]);
+                pin_e8(tot);
             }
         }
     };
 
     // two chunk buffers; the chunk after next loads while a chunk computes
-    for (int c = 0; c < cpw; c += 2) {
+    if constexpr (E > 4) {
+        compute(B0, c0);
+    } else for (int c = 0; c < cpw; c += 2) {
         compute(B0, c0 + c);
         if (c + 2 < cpw) load(B0, c0 + c + 2);
         if (c + 1 >= cpw) break;
@@ -350,7 +381,7 @@ __global__ __launch_bounds__(512, 4) void k_gemv_mfma(const uint8_t* __restrict_
     __syncthreads();  // every wave is done reading xs
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-        const int m = 4 * g + e;
+        const int m = 8 * (e >> 2) + 4 * g + (e & 3);
         if (m < M) red[wave][m][n] = tot[e];
     }
     __syncthreads();
@@ -464,17 +495,20 @@ hipError_t run_nx(const GemvPlan& p, const WeightView& w, const bf16_t* x, void*
 template <int QT, bool GU, typename YT>
 hipError_t run_e(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* y, int M, int64_t nout,
                  int64_t up_off, float* ws, hipStream_t s, AmaxOut* am) {
-    // live accumulator rows per lane: rows 4g + e < M, e < E
+    // live accumulator rows per lane: rows 8 * (e / 4) + 4g + e % 4 < M, e < E
     if (M == 1) return run_nx<QT, 1, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
     if (M == 2) return run_nx<QT, 2, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
-    return run_nx<QT, 4, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
+    if (M <= 8) return run_nx<QT, 4, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
+    // M = 9..16: the plan gives one chunk per wave, (M + 1) / 2 <= 8 staged chunks per thread
+    if (p.cpw != 1 || p.waves * 256 > KB_MAX_E8) return hipErrorInvalidValue;
+    return run<QT, 8, 8, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
 }
 
 }  // namespace
 
 GemvPlan plan_gemv_mfma(int qtype, int64_t M, int64_t N_rows, int64_t K, bool gu) {
     GemvPlan p;
-    if (M < 1 || M > 8 || K < 256 || K % 256 || K > (1 << 20)) return p;
+    if (M < 1 || M > MMAX || K < 256 || K % 256 || K > (1 << 20)) return p;
     if (qtype != 8 && qtype != 12 && qtype != 13 && qtype != 14) return p;
     const int64_t nout = gu ? N_rows / 2 : N_rows;
     const int64_t tiles = gu ? (nout + 15) / 16 : (nout + 31) / 32;

@@ -234,13 +234,13 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
         if (e != hipSuccess) return fail(THQ_EHIP, "kernel launch: %s", hipGetErrorString(e));
         return THQ_OK;
     }
-    // M = 1 keeps the VALU GEMV unless THQ_GEMV_M1=mfma; 2..8 bf16 rows go to the MFMA GEMV
+    // M = 1 keeps the VALU GEMV unless THQ_GEMV_M1=mfma; 2..16 bf16 rows go to the MFMA GEMV
     static const bool m1_mfma = [] {
         const char* v = getenv("THQ_GEMV_M1");
         return v && !strcmp(v, "mfma");
     }();
     const bool q6 = w->qtype == THQ_Q6_K;
-    const thq::GemvPlan gp = (!xf32 && aligned16(x) && m <= 8)
+    const thq::GemvPlan gp = (!xf32 && aligned16(x) && m <= 16)
                                  ? thq::plan_gemv_mfma(v.qtype, m, w->N, w->K, gu)
                                  : thq::GemvPlan{};
     const bool skinny = gp.waves > 0;
