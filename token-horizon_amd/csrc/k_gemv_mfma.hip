@@ -498,8 +498,9 @@ hipError_t run_e(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* 
     // live accumulator rows per lane: rows 8 * (e / 4) + 4g + e % 4 < M, e < E
     if (M == 1) return run_nx<QT, 1, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
     if (M == 2) return run_nx<QT, 2, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
-    if (M <= 8) return run_nx<QT, 4, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
-    // M = 9..16: the plan gives one chunk per wave, (M + 1) / 2 <= 8 staged chunks per thread
+    if (M <= 8 && !(QT == 8 && M > 4)) return run_nx<QT, 4, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
+    // M = 9..16 (and Q8_0 from 5 rows): the plan gives one chunk per wave,
+    // (M + 1) / 2 <= 8 staged chunks per thread
     if (p.cpw != 1 || p.waves * 256 > KB_MAX_E8) return hipErrorInvalidValue;
     return run<QT, 8, 8, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
 }
@@ -514,6 +515,11 @@ GemvPlan plan_gemv_mfma(int qtype, int64_t M, int64_t N_rows, int64_t K, bool gu
     const int64_t tiles = gu ? (nout + 15) / 16 : (nout + 31) / 32;
     const int chunks = (int)(K / 256);
     const int fs = env_int("THQ_GEMV_SPLITS"), fw = env_int("THQ_GEMV_WAVES");
+    // the eight-row (E = 8) instances take one chunk per wave.  Q8_0 uses them
+    // from 5 rows: its four-row instances spill 28 B per lane, the single-
+    // buffered E = 8 ones none (12288 x 4096, M = 5 / 6 / 8: 21.5 / 21.6 /
+    // 22.0 -> 19.9 / 19.9 / 19.6 us; Q4_K there is faster with four rows)
+    const bool one_chunk = M > 8 || (qtype == 8 && M > 4);
     // fewest K splits that fit the staged activations and give >= 256 blocks
     // (else the most splits, up to 16, that fit); waves: the most (<= 8) that
     // divide the block's chunks with M * (chunks per wave) <= 2 * XCH
@@ -524,7 +530,7 @@ GemvPlan plan_gemv_mfma(int qtype, int64_t M, int64_t N_rows, int64_t K, bool gu
         const int cps = chunks / s;
         int w = 0;
         for (int c = MAXW; c >= 1; --c)
-            if (cps % c == 0 && (!fw || c == fw) && M * (cps / c) <= 2 * XCH) {
+            if (cps % c == 0 && (!fw || c == fw) && M * (cps / c) <= 2 * XCH && !(one_chunk && cps / c != 1)) {
                 w = c;
                 break;
             }
