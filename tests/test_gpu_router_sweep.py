@@ -32,7 +32,7 @@ def _gpu():
     torch.cuda.synchronize()
 
 
-MS = [1, 2, 3, 5, 8, 9, 12, 16, 33, 65, 130]
+MS = [1, 2, 3, 5, 8, 9, 12, 16, 17, 24, 32, 33, 65, 130]
 
 # (n, k): rows that fill no 4-row quad / 32-row tile; K at the block size, K
 # between tile sizes, K past the M = 1 kernels' 4096 / 16384 (8192 for Q8_0)
