@@ -97,9 +97,8 @@ __device__ __forceinline__ float dpp_add(float v) {
 // Grid: tiles x splits blocks; block (tile, split) owns the tile's 32 weight
 // rows over K range [split*Kb, (split+1)*Kb), Kb = waves * cpw * 256.
 // Four waves per SIMD for every weight type: two 8-wave blocks per CU (64 KB
-// of LDS each).  The Q8_0 instances with four live rows then spill 28 B per
-// lane, which costs less than halving the resident waves (LM head 151936 x
-// 4096, M = 5: 188 -> 180 us).
+// of LDS each).  Q8_0 with four live rows would then spill 28 B per lane, so
+// Q8_0 runs 3..8 rows on the single-buffered eight-row instances instead.
 template <int QT, int E, int NX, bool GU, bool SPLIT, typename YT>
 __global__ __launch_bounds__(512, 4) void k_gemv_mfma(const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Wa,
                                                   const bf16_t* X, void* __restrict__ Yv, int M, int K,
@@ -498,8 +497,10 @@ hipError_t run_e(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* 
     // live accumulator rows per lane: rows 8 * (e / 4) + 4g + e % 4 < M, e < E
     if (M == 1) return run_nx<QT, 1, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
     if (M == 2) return run_nx<QT, 2, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
-    if (M <= 8 && !(QT == 8 && M > 4)) return run_nx<QT, 4, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
-    // M = 9..16 (and Q8_0 from 5 rows): the plan gives one chunk per wave,
+    if constexpr (QT != 8) {
+        if (M <= 8) return run_nx<QT, 4, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
+    }
+    // M = 9..16 (and Q8_0 from 3 rows): the plan gives one chunk per wave,
     // (M + 1) / 2 <= 8 staged chunks per thread
     if (p.cpw != 1 || p.waves * 256 > KB_MAX_E8) return hipErrorInvalidValue;
     return run<QT, 8, 8, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
@@ -516,10 +517,11 @@ GemvPlan plan_gemv_mfma(int qtype, int64_t M, int64_t N_rows, int64_t K, bool gu
     const int chunks = (int)(K / 256);
     const int fs = env_int("THQ_GEMV_SPLITS"), fw = env_int("THQ_GEMV_WAVES");
     // the eight-row (E = 8) instances take one chunk per wave.  Q8_0 uses them
-    // from 5 rows: its four-row instances spill 28 B per lane, the single-
-    // buffered E = 8 ones none (12288 x 4096, M = 5 / 6 / 8: 21.5 / 21.6 /
-    // 22.0 -> 19.9 / 19.9 / 19.6 us; Q4_K there is faster with four rows)
-    const bool one_chunk = M > 8 || (qtype == 8 && M > 4);
+    // from 3 rows: its four-row instances spill 28 B per lane, the single-
+    // buffered E = 8 ones none (12288 x 4096, M = 3 / 4 / 5 / 8: 20.7 / 20.9 /
+    // 21.5 / 22.0 -> 19.4 / 19.6 / 19.9 / 19.6 us; at M = 2 the two-row
+    // instance is faster, 17.0 against 19.6 us, and Q4_K keeps four rows)
+    const bool one_chunk = M > 8 || (qtype == 8 && M > 2);
     // fewest K splits that fit the staged activations and give >= 256 blocks
     // (else the most splits, up to 16, that fit); waves: the most (<= 8) that
     // divide the block's chunks with M * (chunks per wave) <= 2 * XCH
