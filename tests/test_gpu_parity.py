@@ -200,6 +200,32 @@ def test_q4k_gemm_ragged_m(m):
     assert_close_elem(f"q4k ragged m={m}", y, ref, 2.0 ** -7, floor="rms")
 
 
+@pytest.mark.parametrize("m", [128, 512])
+def test_q4k_gemm_split_counts(m, monkeypatch):
+    """The split-K machinery at the counts the planner can pick (up to 32 on
+    small-N shapes): every forced count gives the unsplit result up to f32
+    summation order (the split partials are summed in a fixed order).  The
+    planner's own choice meets the 1e-2 row bar against the exact oracle and
+    is pinned at the f32 accumulation bar to the f64 product with the tile's
+    bf16-rounded weights (its per-element deviation from the exact product is
+    that rounding: up to 0.0105 on rows of rms 1.29 here)."""
+    n, k = 1024, 4096  # 8 column tiles: the planner splits K
+    b, w = upload(O.Q4_K, n, k, seed=3)
+    xf, xb = bf16_x(m, k, seed=4)
+    y = tonp(thq.matmul(w, xb, torch.float32))
+    ref = O.matmul(O.Q4_K, b, n, k, xf, O.MODE_DEQUANT_F32)
+    assert rel_row_err(y, ref) <= 1e-2
+    rounded = xf.astype(np.float64) @ O.bf16_round(O.dequantize(O.Q4_K, b, n, k)).astype(np.float64).T
+    assert rel_row_err(y, rounded) <= 1e-5
+    monkeypatch.setenv("THQ_GEMM_SPLITS", "1")
+    y1 = tonp(thq.matmul(w, xb, torch.float32))
+    for splits in (2, 3, 7, 16, 32):
+        print(f"[split] m={m} splits={splits}", flush=True)
+        monkeypatch.setenv("THQ_GEMM_SPLITS", str(splits))
+        ys = tonp(thq.matmul(w, xb, torch.float32))
+        assert rel_row_err(ys, y1) <= 1e-5, splits
+
+
 @pytest.mark.parametrize("m,flags", [(16, 0), (17, 0), (100, 0), (100, thq.MODE_EXACT_W)])
 def test_q8_0_gemm(m, flags):
     n, k = 777, 1024
