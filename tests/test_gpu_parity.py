@@ -200,6 +200,19 @@ def test_q4k_gemm_ragged_m(m):
     assert_close_elem(f"q4k ragged m={m}", y, ref, 2.0 ** -7, floor="rms")
 
 
+@pytest.mark.parametrize("m", [3, 4])
+def test_q4k_rows_3_4_wide(m):
+    """3..4 bf16 rows over >= 12288 outputs take the MFMA decode GEMV instead
+    of the row kernel (exact weights: the f32 accumulation bar)."""
+    n, k = 12288, 1024
+    b, w = upload(O.Q4_K, 2 * n, k, seed=5)
+    xf, xb = bf16_x(m, k, seed=6)
+    logits = O.matmul(O.Q4_K, b, 2 * n, k, xf, O.MODE_DEQUANT_F32)
+    assert rel_row_err(tonp(thq.matmul(w, xb, torch.float32)), logits) <= 1e-4
+    want = O.bf16_bits_to_f32(O.gate_up_silu(logits))
+    assert rel_row_err(tonp(thq.gate_up_silu(w, xb, torch.float32)), want) <= 1e-2
+
+
 @pytest.mark.parametrize("m", [128, 512])
 def test_q4k_gemm_split_counts(m, monkeypatch):
     """The split-K machinery at the counts the planner can pick (up to 32 on

@@ -258,7 +258,11 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
     if (m == 1 && !((m1_mfma || q8_m1_mfma) && skinny) && aligned16(x) &&
         thq::gemv1_supported(v.qtype, (int)w->K, gu, w->N)) {
         e = thq::launch_gemv1(v, x, xf32, y, yf32, gu, nout, up_off, s, am);
-    } else if (rows_on && !xf32 && aligned16(x) && thq::gemv_rows_supported(v.qtype, (int)m, (int)w->K, gu, w->N)) {
+    } else if (rows_on && !xf32 && aligned16(x) && thq::gemv_rows_supported(v.qtype, (int)m, (int)w->K, gu, w->N) &&
+               // 3..4 rows over >= 12288 outputs: the MFMA GEMV is faster (12288 x 4096,
+               // M = 3 / 4: 13.04 / 13.20 against 13.41 / 13.63 us; gate/up 2 x 12288:
+               // 19.45 against 20.45 us); at 4096 outputs the row kernel is (6.8 against 8.2 us)
+               !(m >= 3 && skinny && nout >= 12288)) {
         if (am) return THQ_OK;
         e = thq::launch_gemv_rows(v, x, y, yf32, gu, (int)m, nout, up_off, s);
     } else if (skinny) {
