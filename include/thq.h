@@ -15,9 +15,18 @@
  *    of the last failure on the calling thread is thq_last_error().  No C++
  *    exception ever crosses the ABI.
  *  - Weights are immutable after creation and may be shared by any number of
- *    concurrent calls.  Calls on distinct streams are re-entrant, except that
- *    calls sharing one context's workspace (see thq_matmul) must be ordered
- *    on one stream.
+ *    concurrent calls.  A weight belongs to its device, not to the context
+ *    that made it: it may be freed before or after that context.
+ *  - Workspace.  Calls whose kernels need device scratch (split-K partials,
+ *    quantized activation planes, argmax partials, LM-head logits without a
+ *    logits buffer) take it from their context's workspace.  Calls on
+ *    distinct streams are re-entrant, except that calls sharing one
+ *    context's workspace must be ordered on one stream.  The workspace grows
+ *    (hipMalloc, no device synchronization) the first time a larger shape
+ *    arrives; the buffer it outgrew stays allocated until thq_destroy, so
+ *    work already enqueued, or captured in a HIP graph, keeps valid memory.
+ *    A call that grows the workspace cannot run under stream capture: warm
+ *    every captured shape once beforehand.
  *  - W is [N, K] row-major (row n = output feature n), exactly the GGUF
  *    tensor layout QTensor::data() returns.  y[m, n] = sum_k x[m, k] * W[n, k].
  */

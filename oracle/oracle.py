@@ -48,7 +48,7 @@ def lib():
                      "o_quantize_q8_k", "o_dequantize_q6_k"):
             getattr(L, name).argtypes = [P, P, i64]
         L.o_get_scale_min_k4.argtypes = [C.c_int, P, P, P]
-        L.o_make_qkx1_quants.argtypes = [C.c_int, C.c_int, P, C.c_int, P, P]
+        L.o_make_qkx1_quants.argtypes = [C.c_int, C.c_int, P, C.c_int, P, P, P]
         L.o_quantize.argtypes = [C.c_int, P, i64, i64, P]
         L.o_dequantize.argtypes = [C.c_int, P, i64, i64, P]
         L.o_vec_dot_q8_0_q8_0.argtypes = [i64, P, P]
@@ -190,6 +190,16 @@ def get_scale_min_k4(j: int, scales12: np.ndarray):
     mn = np.zeros(1, np.uint8)
     lib().o_get_scale_min_k4(j, _p(s), _p(sc), _p(mn))
     return int(sc[0]), int(mn[0])
+
+
+def make_qkx1_quants(nmax: int, ntry: int, x: np.ndarray):
+    """(scale, min, levels) of one sub-block ([ext] utils.rs make_qkx1_quants)."""
+    xs = np.ascontiguousarray(x, dtype=np.float32)
+    sc = np.zeros(1, np.float32)
+    mn = np.zeros(1, np.float32)
+    lv = np.zeros(xs.size, np.uint8)
+    lib().o_make_qkx1_quants(nmax, ntry, _p(xs), xs.size, _p(sc), _p(mn), _p(lv))
+    return sc[0], mn[0], lv
 
 
 def max_threads() -> int:

@@ -213,9 +213,11 @@ void o_get_scale_min_k4(int j, const uint8_t* q, uint8_t* sc, uint8_t* m) {
  * min/max by total order, min clamped to <= 0, iscale = nmax/(max-min),
  * up to ntry refinement passes of (least-squares scale, mean-residual min),
  * stopping early when no level changed. */
-void o_make_qkx1_quants(int nmax, int ntry, const float* x, int n, float* scale_out, float* min_out) {
+void o_make_qkx1_quants(int nmax, int ntry, const float* x, int n, float* scale_out, float* min_out,
+                        uint8_t* levels) {
     uint8_t l[256];
     memset(l, 0, sizeof(l));
+    if (levels) memset(levels, 0, (size_t)n);
     float mn = x[0], mx = x[0];
     for (int i = 1; i < n; ++i) {
         if (x[i] < mn) mn = x[i];
@@ -247,6 +249,7 @@ void o_make_qkx1_quants(int nmax, int ntry, const float* x, int n, float* scale_
     }
     *scale_out = scale;
     *min_out = -min;
+    if (levels) memcpy(levels, l, (size_t)n);
 }
 
 /* [ext] BlockQ4K::from_float: per 32-sub-block make_qkx1_quants(15, 5);
@@ -260,7 +263,7 @@ void o_quantize_q4_k(const float* x, uint8_t* blocks, int64_t k) {
         uint8_t* sc = blk + 4;
         uint8_t* qs = blk + 16;
         float scales[8], mins[8];
-        for (int j = 0; j < 8; ++j) o_make_qkx1_quants(15, 5, xs + 32 * j, 32, &scales[j], &mins[j]);
+        for (int j = 0; j < 8; ++j) o_make_qkx1_quants(15, 5, xs + 32 * j, 32, &scales[j], &mins[j], NULL);
         float max_scale = 0.0f, max_min = 0.0f;
         for (int j = 0; j < 8; ++j) {
             max_scale = (scales[j] > max_scale || max_scale != max_scale) ? scales[j] : max_scale;

@@ -21,9 +21,16 @@
  *   f16 / bf16 conversions      exhaustive round trips, IEEE special cases
  *   Q8_0 quantize / dequant     closed-form KATs (exact-in-f16 scales), error bound
  *   Q4_K dequant                hand-built superblock KATs, scale/min pack round trip
- *   Q4_K quantize               parity unpinned (candle's make_qkx1_quants bits
- *                               need candle itself); checked by invariants only
- *   Q8_K quantize               parity unpinned (exact candle rounding); invariants
+ *   Q4_K quantize               grid-exact sub-blocks (x = s*l - m, s and m powers
+ *                               of two: levels and (s, m) exact); the largest
+ *                               stored 6-bit scale / min is 63; literal bytes
+ *                               and (scale, min, levels) from an independent
+ *                               float32 trace of the published algorithm
+ *                               (tests/golden/make_quant_vectors.py), drawn so
+ *                               that nmax 14, ntry 4 / 6 / 1 or 64/max fail
+ *   Q8_K quantize               KAT at iscale = 1 (x.5 ties round away from
+ *                               zero, clamp to 127, first of equal |x|) and
+ *                               literal blocks from the same trace
  *   vec_dot Q8_0xQ8_0 / Q4_KxQ8_K  exact integer brute force on small inputs;
  *                               f32 accumulation order parity unpinned
  *   matmul DEQUANT_F32          brute force f64 on tiny shapes
@@ -81,7 +88,8 @@ void o_dequantize_q4_k(const uint8_t* blocks, float* y, int64_t k);
 void o_quantize_q8_k(const float* x, uint8_t* blocks, int64_t k);
 void o_dequantize_q6_k(const uint8_t* blocks, float* y, int64_t k);
 void o_get_scale_min_k4(int j, const uint8_t* scales, uint8_t* sc, uint8_t* m);
-void o_make_qkx1_quants(int nmax, int ntry, const float* x, int n, float* scale, float* min_out);
+/* levels (nullable): the n levels of the last refinement pass (0 when max == min) */
+void o_make_qkx1_quants(int nmax, int ntry, const float* x, int n, float* scale, float* min_out, uint8_t* levels);
 
 /* whole matrices [n rows][k] */
 int o_quantize(int type, const float* w, int64_t n, int64_t k, uint8_t* out);

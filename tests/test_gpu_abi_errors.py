@@ -87,6 +87,12 @@ def test_invalid_arguments_every_entry_point():
     odd = thq.QTensor.from_gguf_bytes(thq.Q4_K, weight_bytes(O.Q4_K, 7, 512, seed=4), 7, 512)
     expect(L.thq_gate_up_silu(ctx, odd.h, ptr(x), thq.ACT_BF16, 4, ptr(y), thq.ACT_F32, 0, s), thq.ESHAPE)
     expect(L.thq_matmul_argmax(ctx, w4.h, ptr(x), thq.ACT_BF16, 4, None, None, 0, s), thq.EINVAL)
+    # shape and type checks come before any workspace is reserved
+    expect(L.thq_matmul_argmax(ctx, w4.h, ptr(x), thq.ACT_BF16, -1, None, ptr(idx), 0, s), thq.ESHAPE)
+    expect(L.thq_matmul_argmax(ctx, w4.h, ptr(x), thq.ACT_BF16, -(1 << 40), ptr(y), ptr(idx), 0, s), thq.ESHAPE)
+    expect(L.thq_matmul_argmax(ctx, w4.h, ptr(x), 7, 4, None, ptr(idx), 0, s), thq.EINVAL)
+    expect(L.thq_matmul_argmax(ctx, w4.h, ptr(x), thq.ACT_BF16, 4, None, ptr(idx), 0x40000000, s), thq.EINVAL)
+    expect(L.thq_matmul_argmax(ctx, w4.h, None, thq.ACT_BF16, 4, None, ptr(idx), 0, s), thq.EINVAL)
     expect(L.thq_argmax(ctx, ptr(y), -1, 8, ptr(idx), s), thq.ESHAPE)
     expect(L.thq_argmax(ctx, ptr(y), 1, 1 << 33, ptr(idx), s), thq.ESHAPE)
     expect(L.thq_argmax(ctx, None, 4, 8, ptr(idx), s), thq.EINVAL)

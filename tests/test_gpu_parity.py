@@ -290,18 +290,20 @@ def lm_head():
 
 @pytest.mark.parametrize("m", [5, 40])
 def test_lm_head_verify_argmax(lm_head, m):
+    """Every verify row (5 = one slot's drafted + 1 tokens, 40 = a batch of 8
+    slots): logits within 1e-4 of the oracle's f64 product, and the argmax
+    index of each row equal to the oracle's scan of its own logits."""
     w, b = lm_head
     n, k = w.shape
     xf, xb = bf16_x(m, k, seed=3)
     logits, idx = thq.matmul_argmax(w, xb)
     torch.cuda.synchronize()
-    rows = list(range(m)) if m <= 5 else [0, 1, 2, 17, 39]
-    ref = O.matmul(O.Q8_0, b, n, k, xf[rows], O.MODE_DEQUANT_F32)
+    ref = O.matmul(O.Q8_0, b, n, k, xf, O.MODE_DEQUANT_F32)
     got = tonp(logits)
-    assert rel_row_err(got[rows], ref) <= 1e-4
-    assert_close_elem(f"lm head m={m}", got[rows], ref, 2.0 ** -14)
+    assert rel_row_err(got, ref) <= 1e-4
+    assert_close_elem(f"lm head m={m}", got, ref, 2.0 ** -14)
     want = O.argmax_rows(ref)
-    assert list(idx.cpu().numpy()[rows]) == list(want)
+    assert list(idx.cpu().numpy()) == list(want)
     # the GPU argmax equals the oracle scan of the GPU's own logits for every row
     assert list(idx.cpu().numpy()) == list(O.argmax_rows(got))
     # without a logits buffer the same indices come back

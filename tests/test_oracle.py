@@ -5,7 +5,9 @@ against numpy / torch, hand-computed block vectors, exact integer brute
 force, the reference's own argmax tie vectors (engine/src/engine.rs:3086-3128)
 and the closed form of the gate/up epilogue (engine/src/qwen35.rs:7002-7007).
 """
+import json
 import math
+import os
 
 import numpy as np
 import pytest
@@ -189,9 +191,76 @@ def test_q4_k_dequant_is_exact_f32_formula_for_random_bytes():
             assert np.array_equal(y[r, 32 * sb: 32 * sb + 32], exact.astype(np.float32))
 
 
+GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "quant_vectors.json")))
+
+
+def _h2f(a) -> np.ndarray:
+    return np.array([int(v, 16) for v in a], np.uint32).view(np.float32)
+
+
+@pytest.mark.parametrize("s,m", [(2.0 ** -7, 2.0 ** -5), (2.0 ** -3, 0.0), (1.0, 4.0), (2.0 ** -10, 2.0 ** -6),
+                                 (2.0 ** -6, 2.0 ** -9)])
+def test_make_qkx1_quants_grid_exact(s, m):
+    """x = s*l - m with l covering 0..15 and s, m powers of two: the first pass
+    finds the levels exactly (iscale = 15/(15s) = 1/s), the least-squares
+    scale is s and the mean residual is -m, so the search returns (s, m) and
+    l.  nmax 14 would give other levels, a power-of-two bias in the min other
+    (s, m)."""
+    lv = np.concatenate([np.arange(16), np.arange(16)[::-1]]).astype(np.float32)
+    x = (np.float32(s) * lv - np.float32(m)).astype(np.float32)
+    sc, mn, l = O.make_qkx1_quants(15, 5, x)
+    assert np.array_equal(l, lv.astype(np.uint8))
+    assert sc == np.float32(s) and mn == np.float32(m)
+    # nmax = 14 cannot represent 16 levels
+    assert not np.array_equal(O.make_qkx1_quants(14, 5, x)[2], l)
+
+
+@pytest.mark.parametrize("case", range(len(GOLDEN["qkx1"])))
+def test_make_qkx1_quants_golden(case):
+    """Literal (scale, min, levels) from an independent float32 trace of the
+    published 5-pass refinement (tests/golden/make_quant_vectors.py).  The
+    sub-blocks were drawn so that the levels still change in passes 5 and 6:
+    the fixture's ntry-4, ntry-6, ntry-1 and nmax-14 levels all differ from
+    the ntry-5 answer, so a wrong pass count or level count fails here."""
+    c = GOLDEN["qkx1"][case]
+    x = _h2f(c["x"])
+    sc, mn, l = O.make_qkx1_quants(15, 5, x)
+    assert list(l) == c["levels"]
+    assert int(sc.view(np.uint32)) == int(c["scale"], 16)
+    assert int(mn.view(np.uint32)) == int(c["min"], 16)
+    for other in ("levels_ntry4", "levels_ntry6", "levels_nmax14", "levels_ntry1"):
+        assert c[other] != c["levels"], other
+    assert list(O.make_qkx1_quants(15, 4, x)[2]) == c["levels_ntry4"]
+    assert list(O.make_qkx1_quants(15, 6, x)[2]) == c["levels_ntry6"]
+
+
+@pytest.mark.parametrize("case", range(len(GOLDEN["q4k"])))
+def test_q4_k_quantize_golden(case):
+    """BlockQ4K::from_float byte for byte against the float32 trace: Gaussian,
+    all-positive (min clamped to 0) and a superblock with a constant sub-block
+    and outliers.  The generator checks that 64/max in place of 63/max changes
+    each block."""
+    c = GOLDEN["q4k"][case]
+    blk = O.quantize(O.Q4_K, _h2f(c["x"]).reshape(1, 256))
+    assert blk.tobytes().hex() == c["block"]
+
+
+def test_q4_k_max_scale_and_min_are_63():
+    """6-bit scales are quantized against their maxima (63/max): in every
+    superblock the sub-block with the largest scale stores 63, and so does the
+    one with the largest min whenever some min is positive."""
+    w = O.randn(0, 21, 0.02, (64, 1024))
+    w[3, :256] = np.abs(w[3, :256]) + 0.001  # all-positive superblock: the first pass clamps the min to 0
+    blk = O.quantize(O.Q4_K, w).reshape(-1, 144)
+    for b in range(blk.shape[0]):
+        pairs = [O.get_scale_min_k4(j, blk[b, 4:16]) for j in range(8)]
+        assert max(p[0] for p in pairs) == 63, b
+        mx_m = max(p[1] for p in pairs)
+        dmin = blk[b, 2:4].view(np.float16)[0]
+        assert mx_m == (63 if dmin > 0 else 0), b
+
+
 def test_q4_k_quantize_invariants():
-    # make_qkx1_quants bit-parity with candle is unpinned; check what any
-    # faithful Q4_K quantizer must satisfy
     w = O.randn(0, 9, 0.02, (32, 1024))
     blk = O.quantize(O.Q4_K, w)
     deq = O.dequantize(O.Q4_K, blk, 32, 1024)
@@ -207,23 +276,23 @@ def test_q4_k_quantize_invariants():
     assert not O.dequantize(O.Q4_K, c, 1, 256).any()
 
 
-def test_q8_k_invariants():
-    x = O.randn(0, 11, 1.0, (1024,))
-    x[5] = -7.5  # first element of largest |x|: iscale = -128/x[5], so its level is -128
-    x[6] = 7.5   # same magnitude, other sign: 128 -> clamped to 127
-    blk = O.quantize_q8_k(x).reshape(4, 292)
-    for b in range(4):
-        d = blk[b, 0:4].view(np.float32)[0]
-        qs = blk[b, 4:260].view(np.int8).astype(np.int32)
-        bs = blk[b, 260:292].view(np.int16).astype(np.int32)
-        xs = x[256 * b: 256 * (b + 1)]
-        imax = int(np.argmax(np.abs(xs)))
-        assert qs[imax] == -128
-        assert np.array_equal(bs, qs.reshape(16, 16).sum(axis=1))
-        ok = qs != 127  # a level clamped at 127 may sit one step off
-        assert np.all(np.abs(qs * np.float64(d) - xs)[ok] <= abs(d) * 0.5 + 1e-7)
-    assert blk[0, 4 + 5].view(np.int8) == -128
-    assert blk[0, 4 + 6].view(np.int8) == 127
+def test_q8_k_tie_kat():
+    """BlockQ8K::from_float rounds with f32::round (half away from zero): with
+    max = -128, iscale = -128/max = 1 and d = 1, so x.5 values are exact ties.
+    +-2.5 -> +-3 and +-0.5 -> +-1 (half to even would give +-2 and 0); 126.5 ->
+    127; 128 (same |x| as the max, later) is not the max and clamps to 127."""
+    x = np.zeros(256, np.float32)
+    x[0] = -128.0
+    x[1:8] = [2.5, -2.5, 0.5, -0.5, 126.5, -127.5, 128.0]
+    blk = O.quantize_q8_k(x)
+    assert blk[0:4].view(np.float32)[0] == 1.0
+    assert list(blk[4:12].view(np.int8)) == [-128, 3, -3, 1, -1, 127, -128, 127]
+
+
+@pytest.mark.parametrize("case", range(len(GOLDEN["q8k"])))
+def test_q8_k_quantize_golden(case):
+    c = GOLDEN["q8k"][case]
+    assert O.quantize_q8_k(_h2f(c["x"])).tobytes().hex() == c["block"]
 
 
 # ---------------------------------------------------------------- dots

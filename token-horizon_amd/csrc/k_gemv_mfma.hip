@@ -480,30 +480,58 @@ hipError_t run(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* y,
     return launch_split_reduce(ws, y, std::is_same<YT, float>::value, GU, M, nout, up_off, w.N, p.splits, s);
 }
 
-// staged activation chunks per thread: M * cpw * 256 / 8 / (64 * waves) = M * cpw / 2, rounded up to 1, 2, 4, 8
-template <int QT, int E, bool GU, typename YT>
-hipError_t run_nx(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* y, int M, int64_t nout,
-                  int64_t up_off, float* ws, hipStream_t s, AmaxOut* am) {
-    const int need = (M * p.cpw + 1) / 2;
-    if (need <= 1) return run<QT, E, 1, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
-    if (need <= 2) return run<QT, E, 2, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
-    if (need <= 4) return run<QT, E, 4, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
-    return run<QT, E, 8, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
+}  // namespace
+
+// The instance a plan runs: live accumulator rows per lane E (rows
+// 8 * (e / 4) + 4g + e % 4 < M, e < E) and staged 16-B activation chunks per
+// thread NX (M * cpw * 256 / 8 / (64 * waves) = M * cpw / 2, rounded up to
+// 1, 2, 4, 8).  E = 8 (M = 9..16, and Q8_0 from 3 rows) needs one chunk per
+// wave, (M + 1) / 2 <= 8 staged chunks per thread.  {0, 0}: no instance.
+GemvInstance gemv_mfma_instance(int qtype, int M, const GemvPlan& p) {
+    GemvInstance r;
+    if (!p.waves || M < 1 || M > MMAX) return r;
+    if (M <= 2 || (qtype != 8 && M <= 8)) {
+        r.E = M == 1 ? 1 : (M == 2 ? 2 : 4);
+        const int need = (M * p.cpw + 1) / 2;
+        r.NX = need <= 1 ? 1 : need <= 2 ? 2 : need <= 4 ? 4 : 8;
+        return r;
+    }
+    if (p.cpw != 1 || p.waves * 256 > KB_MAX_E8) return r;
+    r.E = 8;
+    r.NX = 8;
+    return r;
 }
+
+namespace {
 
 template <int QT, bool GU, typename YT>
 hipError_t run_e(const GemvPlan& p, const WeightView& w, const bf16_t* x, void* y, int M, int64_t nout,
                  int64_t up_off, float* ws, hipStream_t s, AmaxOut* am) {
-    // live accumulator rows per lane: rows 8 * (e / 4) + 4g + e % 4 < M, e < E
-    if (M == 1) return run_nx<QT, 1, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
-    if (M == 2) return run_nx<QT, 2, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
+    const GemvInstance in = gemv_mfma_instance(QT, M, p);
+#define THQ_RUN(E_, NX_) run<QT, E_, NX_, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am)
+    if (in.E == 8) return THQ_RUN(8, 8);
     if constexpr (QT != 8) {
-        if (M <= 8) return run_nx<QT, 4, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
+        if (in.E == 4) {
+            if (in.NX == 1) return THQ_RUN(4, 1);
+            if (in.NX == 2) return THQ_RUN(4, 2);
+            if (in.NX == 4) return THQ_RUN(4, 4);
+            return THQ_RUN(4, 8);
+        }
     }
-    // M = 9..16 (and Q8_0 from 3 rows): the plan gives one chunk per wave,
-    // (M + 1) / 2 <= 8 staged chunks per thread
-    if (p.cpw != 1 || p.waves * 256 > KB_MAX_E8) return hipErrorInvalidValue;
-    return run<QT, 8, 8, GU, YT>(p, w, x, y, M, nout, up_off, ws, s, am);
+    if (in.E == 2) {
+        if (in.NX == 1) return THQ_RUN(2, 1);
+        if (in.NX == 2) return THQ_RUN(2, 2);
+        if (in.NX == 4) return THQ_RUN(2, 4);
+        return THQ_RUN(2, 8);
+    }
+    if (in.E == 1) {
+        if (in.NX == 1) return THQ_RUN(1, 1);
+        if (in.NX == 2) return THQ_RUN(1, 2);
+        if (in.NX == 4) return THQ_RUN(1, 4);
+        return THQ_RUN(1, 8);
+    }
+#undef THQ_RUN
+    return hipErrorInvalidValue;
 }
 
 }  // namespace
@@ -544,6 +572,21 @@ GemvPlan plan_gemv_mfma(int qtype, int64_t M, int64_t N_rows, int64_t K, bool gu
         if (fs || tiles * s >= 256) break;
     }
     return p;
+}
+
+GemvLimits gemv_mfma_limits() {
+    GemvLimits l;
+    l.xs_elems = XS_ELEMS;
+    l.xs_pad_elems = 8 * MMAX;
+    l.kb_max = KB_MAX;
+    l.kb_max_e8 = KB_MAX_E8;
+    l.mmax = MMAX;
+    l.max_waves = MAXW;
+    l.sums_rows_e4 = KB_MAX / 32;
+    l.sums_rows_e8 = KB_MAX_E8 / 16;
+    l.sums_cols_e4 = 8;
+    l.sums_cols_e8 = MMAX;
+    return l;
 }
 
 hipError_t launch_gemv_mfma(const GemvPlan& p, const WeightView& w, const void* x, void* y, bool yf32, bool gu, int M,

@@ -18,6 +18,7 @@
 #include <vector>
 
 #include "../../include/thq.h"
+#include "../../include/thq_plan.h"
 #include "thq_dev.hpp"
 #include "thq_kernels.hpp"
 
@@ -27,10 +28,14 @@ struct thq_ctx {
     std::mutex mu;
     void* ws = nullptr;  // workspace: split-K partials, argmax partials, logits
     size_t ws_bytes = 0;
+    // buffers the workspace outgrew: kernels already enqueued (or captured in
+    // a graph) may still use them, so they live until thq_destroy
+    std::vector<void*> retired;
 };
 
 struct thq_weight {
-    thq_ctx* ctx = nullptr;
+    int device = 0;          // the device that holds q / aux (not the context: a
+                             // weight may outlive the context that made it)
     int qtype = 0;           // thq_dtype
     int64_t N = 0, K = 0;
     int gs = 0;              // MLX affine group size
@@ -121,7 +126,7 @@ int check_dtype_shape(int dtype, int64_t n, int64_t k) {
 int alloc_weight(thq_ctx* ctx, int dtype, int64_t n, int64_t k, thq_weight** out) {
     thq_weight* w = new (std::nothrow) thq_weight();
     if (!w) return fail(THQ_ENOMEM, "host allocation failed");
-    w->ctx = ctx;
+    w->device = ctx->device;
     w->qtype = dtype;
     w->N = n;
     w->K = k;
@@ -141,20 +146,24 @@ int alloc_weight(thq_ctx* ctx, int dtype, int64_t n, int64_t k, thq_weight** out
     return THQ_OK;
 }
 
-// Grow the context workspace; growing synchronizes the device first so no
-// in-flight kernel still reads the old buffer.
+// Grow the context workspace (caller holds ctx->mu).  The old buffer is
+// retired, not freed: work already enqueued on any stream, or captured in a
+// graph, may still read or write it, so it lives until thq_destroy.  No
+// device synchronization is needed.
 int ensure_ws(thq_ctx* ctx, size_t bytes) {
     if (bytes <= ctx->ws_bytes) return THQ_OK;
-    HIP_TRY(hipDeviceSynchronize());
-    if (ctx->ws) HIP_TRY(hipFree(ctx->ws));
-    ctx->ws = nullptr;
-    ctx->ws_bytes = 0;
     size_t want = bytes + (bytes >> 3);
-    hipError_t e = hipMalloc(&ctx->ws, want);
+    if (want < 2 * ctx->ws_bytes) want = 2 * ctx->ws_bytes;  // retired bytes stay below the live size
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, want);
     if (e != hipSuccess) return fail(THQ_ENOMEM, "workspace hipMalloc(%zu): %s", want, hipGetErrorString(e));
+    if (ctx->ws) ctx->retired.push_back(ctx->ws);
+    ctx->ws = p;
     ctx->ws_bytes = want;
     return THQ_OK;
 }
+
+size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 struct DeviceGuard {
     int prev = -1;
@@ -198,50 +207,79 @@ hipError_t dequant_any(const thq_weight* w, void* out, bool bf16, hipStream_t s)
     return thq::launch_dequant_q4k(w->q, out, bf16, w->N, (int)(w->K / 256), s);
 }
 
-// Shared body of matmul / gate_up / argmax-logits.  With `am` (fused argmax,
-// y unused) only a path with the fused epilogue launches; am->nb = 0 reports
+// One projection call: the arguments of thq_matmul / thq_gate_up_silu (gu)
+// and of the LM head inside thq_matmul_argmax.  With `am` (fused argmax, y
+// unused) only a path with the fused epilogue launches; am->nb = 0 reports
 // that this shape / type has none and nothing ran.
-int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t m, void* y, int yt, uint32_t flags,
-               bool gu, void* stream, thq::AmaxOut* am = nullptr) {
-    if (!ctx || !w) return fail(THQ_EINVAL, "null context or weight");
-    if (xt != THQ_ACT_F32 && xt != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad x_type %d", xt);
-    if (yt != THQ_ACT_F32 && yt != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad y_type %d", yt);
-    if (flags & ~(THQ_MODE_EXACT_W | THQ_MODE_Q8ACT)) return fail(THQ_EINVAL, "unknown flags 0x%x", flags);
-    if (m < 0) return fail(THQ_ESHAPE, "M=%lld must be >= 0", (long long)m);
-    if (m > (1 << 24)) return fail(THQ_ESHAPE, "M=%lld too large", (long long)m);
-    if (gu && (w->N % 2)) return fail(THQ_ESHAPE, "gate/up weight has an odd row count %lld", (long long)w->N);
-    if (m == 0) return THQ_OK;
-    if (!x || (!y && !am)) return fail(THQ_EINVAL, "null x or y");
-    if (am) am->nb = 0;
-    DeviceGuard g(ctx->device);
-    hipStream_t s = static_cast<hipStream_t>(stream);
+struct Call {
+    thq_ctx* ctx;
+    const thq_weight* w;
+    const void* x;
+    int xt;
+    int64_t m;
+    void* y;
+    int yt;
+    uint32_t flags;
+    bool gu;
+    hipStream_t s;
+    thq::AmaxOut* am;
+};
+
+int check_call(const Call& c) {
+    if (!c.ctx || !c.w) return fail(THQ_EINVAL, "null context or weight");
+    if (c.xt != THQ_ACT_F32 && c.xt != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad x_type %d", c.xt);
+    if (c.yt != THQ_ACT_F32 && c.yt != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad y_type %d", c.yt);
+    if (c.flags & ~(THQ_MODE_EXACT_W | THQ_MODE_Q8ACT)) return fail(THQ_EINVAL, "unknown flags 0x%x", c.flags);
+    if (c.m < 0) return fail(THQ_ESHAPE, "M=%lld must be >= 0", (long long)c.m);
+    if (c.m > (1 << 24)) return fail(THQ_ESHAPE, "M=%lld too large", (long long)c.m);
+    if (c.gu && (c.w->N % 2)) return fail(THQ_ESHAPE, "gate/up weight has an odd row count %lld", (long long)c.w->N);
+    if (c.m == 0) return THQ_OK;
+    if (!c.x || (!c.y && !c.am)) return fail(THQ_EINVAL, "null x or y");
+    if ((c.flags & THQ_MODE_Q8ACT) && !c.am) {
+        if (c.w->qtype == THQ_MLX_Q4) return fail(THQ_EDTYPE, "THQ_MODE_Q8ACT applies to GGUF weights only");
+        if (c.w->qtype == THQ_Q6_K) return fail(THQ_EDTYPE, "THQ_MODE_Q8ACT is not implemented for Q6_K weights");
+        if (!thq::q8act_supported(c.w->qtype, c.w->K))
+            return fail(THQ_ESHAPE, "K=%lld too large for THQ_MODE_Q8ACT", (long long)c.w->K);
+        if (!aligned16(c.x)) return fail(THQ_EALIGN, "THQ_MODE_Q8ACT needs 16-byte aligned x");
+    }
+    return THQ_OK;
+}
+
+// The kernels a call runs, and the device scratch (split-K partials or the
+// quantized activation planes) they use, known before anything launches.
+enum class Kind { NONE, Q8ACT, GEMV1, ROWS, GEMV_MFMA, GEMM, GENERIC };
+struct Route {
+    Kind kind = Kind::NONE;
+    thq::GemvPlan gp;
+    thq::GemmPlan gm;
+    bool exact = false;
+    size_t scratch = 0;
+};
+
+// Routing by rows, as QLin::linear_ps (engine/src/qwen35.rs:398-617).  A
+// validated call with m >= 1.  Kind::NONE: a fused-argmax call whose route
+// has no fused epilogue (nothing to launch).
+Route plan_route(const Call& c) {
+    Route r;
+    const thq_weight* w = c.w;
+    const int64_t m = c.m;
     const thq::WeightView v = view(w);
-    const bool xf32 = xt == THQ_ACT_F32, yf32 = yt == THQ_ACT_F32;
-    const int64_t nout = gu ? w->N / 2 : w->N;
-    const int64_t up_off = gu ? w->N / 2 : 0;
-    hipError_t e;
-    if (flags & THQ_MODE_Q8ACT) {
-        if (am) return THQ_OK;
-        if (w->qtype == THQ_MLX_Q4) return fail(THQ_EDTYPE, "THQ_MODE_Q8ACT applies to GGUF weights only");
-        if (w->qtype == THQ_Q6_K) return fail(THQ_EDTYPE, "THQ_MODE_Q8ACT is not implemented for Q6_K weights");
-        if (!thq::q8act_supported(w->qtype, w->K))
-            return fail(THQ_ESHAPE, "K=%lld too large for THQ_MODE_Q8ACT", (long long)w->K);
-        if (!aligned16(x)) return fail(THQ_EALIGN, "THQ_MODE_Q8ACT needs 16-byte aligned x");
-        std::lock_guard<std::mutex> lk(ctx->mu);
-        int rc = ensure_ws(ctx, thq::q8act_workspace_bytes(w->qtype, m, w->K));
-        if (rc) return rc;
-        e = thq::launch_q8act(v, x, xf32, y, yf32, gu, (int)m, nout, up_off, ctx->ws, s);
-        if (e != hipSuccess) return fail(THQ_EHIP, "kernel launch: %s", hipGetErrorString(e));
-        return THQ_OK;
+    const bool xf32 = c.xt == THQ_ACT_F32;
+    const int64_t nout = c.gu ? w->N / 2 : w->N;
+    if (c.flags & THQ_MODE_Q8ACT) {
+        if (c.am) return r;
+        r.kind = Kind::Q8ACT;
+        r.scratch = thq::q8act_workspace_bytes(w->qtype, m, w->K);
+        return r;
     }
     // M = 1 keeps the VALU GEMV unless THQ_GEMV_M1=mfma; 2..16 bf16 rows go to the MFMA GEMV
     static const bool m1_mfma = [] {
-        const char* v = getenv("THQ_GEMV_M1");
-        return v && !strcmp(v, "mfma");
+        const char* e = getenv("THQ_GEMV_M1");
+        return e && !strcmp(e, "mfma");
     }();
     const bool q6 = w->qtype == THQ_Q6_K;
-    const thq::GemvPlan gp = (!xf32 && aligned16(x) && m <= 16)
-                                 ? thq::plan_gemv_mfma(v.qtype, m, w->N, w->K, gu)
+    const thq::GemvPlan gp = (!xf32 && aligned16(c.x) && m <= 16)
+                                 ? thq::plan_gemv_mfma(v.qtype, m, w->N, w->K, c.gu)
                                  : thq::GemvPlan{};
     const bool skinny = gp.waves > 0;
     // Q8_0 at M = 1: the one-row-per-wave VALU kernel reloads x per row; on
@@ -252,54 +290,88 @@ int run_matmul(thq_ctx* ctx, const thq_weight* w, const void* x, int xt, int64_t
     const bool q4 = w->qtype == THQ_Q4_K || w->qtype == THQ_MLX_Q4;
     // 2..4 bf16 rows of Q4_K / MLX affine at K <= 4096: the VALU row kernel (THQ_GEMV_ROWS=0: MFMA)
     static const bool rows_on = [] {
-        const char* v = getenv("THQ_GEMV_ROWS");
-        return !(v && !strcmp(v, "0"));
+        const char* e = getenv("THQ_GEMV_ROWS");
+        return !(e && !strcmp(e, "0"));
     }();
-    if (m == 1 && !((m1_mfma || q8_m1_mfma) && skinny) && aligned16(x) &&
-        thq::gemv1_supported(v.qtype, (int)w->K, gu, w->N)) {
-        e = thq::launch_gemv1(v, x, xf32, y, yf32, gu, nout, up_off, s, am);
-    } else if (rows_on && !xf32 && aligned16(x) && thq::gemv_rows_supported(v.qtype, (int)m, (int)w->K, gu, w->N) &&
+    if (m == 1 && !((m1_mfma || q8_m1_mfma) && skinny) && aligned16(c.x) &&
+        thq::gemv1_supported(v.qtype, (int)w->K, c.gu, w->N)) {
+        r.kind = Kind::GEMV1;
+    } else if (rows_on && !xf32 && aligned16(c.x) && thq::gemv_rows_supported(v.qtype, (int)m, (int)w->K, c.gu, w->N) &&
                // 3..4 rows over >= 12288 outputs: the MFMA GEMV is faster (12288 x 4096,
                // M = 3 / 4: 13.04 / 13.20 against 13.41 / 13.63 us; gate/up 2 x 12288:
                // 19.45 against 20.45 us); at 4096 outputs the row kernel is (6.8 against 8.2 us)
                !(m >= 3 && skinny && nout >= 12288)) {
-        if (am) return THQ_OK;
-        e = thq::launch_gemv_rows(v, x, y, yf32, gu, (int)m, nout, up_off, s);
+        if (!c.am) r.kind = Kind::ROWS;
     } else if (skinny) {
-        if (am) {  // the fused epilogue exists on the unsplit plan only (no workspace)
-            e = gp.splits == 1 ? thq::launch_gemv_mfma(gp, v, x, y, yf32, gu, (int)m, nout, up_off, nullptr, s, am)
-                               : hipSuccess;
-        } else {
-            std::lock_guard<std::mutex> lk(ctx->mu);
-            if (gp.workspace_bytes) {
-                int rc = ensure_ws(ctx, gp.workspace_bytes);
-                if (rc) return rc;
-            }
-            e = thq::launch_gemv_mfma(gp, v, x, y, yf32, gu, (int)m, nout, up_off, static_cast<float*>(ctx->ws), s);
+        // the fused epilogue exists on the unsplit plan only (no scratch)
+        if (!c.am || gp.splits == 1) {
+            r.kind = Kind::GEMV_MFMA;
+            r.gp = gp;
+            r.scratch = c.am ? 0 : gp.workspace_bytes;
         }
-    } else if (am) {
-        return THQ_OK;
-    } else if (!xf32 && aligned16(x) && w->K % 64 == 0 &&  // the GEMMs step K in 64-wide tiles
+    } else if (c.am) {
+        // no fused epilogue
+    } else if (!xf32 && aligned16(c.x) && w->K % 64 == 0 &&  // the GEMMs step K in 64-wide tiles
                // gate/up rows of < 256 outputs: the rounded-weight tile's error, seen
                // through silu(g)*u, is not averaged down by the row norm (the exact
                // kernel costs nothing at that size)
-               !(gu && nout < 256) &&
-               !((q4 || q6) && ((flags & THQ_MODE_EXACT_W) || w->K % 256)) &&
+               !(c.gu && nout < 256) &&
+               !((q4 || q6) && ((c.flags & THQ_MODE_EXACT_W) || w->K % 256)) &&
                !(q6 && (m <= 8 || thq::q6k_layout(w->N, w->K).total >= (1ull << 32) ||
                         (uint64_t)m * (uint64_t)w->K * 2 >= (1ull << 32)))) {
-        const bool exact = (flags & THQ_MODE_EXACT_W) || (w->qtype == THQ_Q8_0 && m <= 64);
-        thq::GemmPlan p = thq::plan_gemm(v.qtype, exact, m, w->N, w->K, gu, ctx->cus);
-        std::lock_guard<std::mutex> lk(ctx->mu);
-        if (p.workspace_bytes) {
-            int rc = ensure_ws(ctx, p.workspace_bytes);
-            if (rc) return rc;
-        }
-        e = thq::launch_gemm(p, v, x, y, yf32, gu, exact, (int)m, static_cast<float*>(ctx->ws), s);
+        r.kind = Kind::GEMM;
+        r.exact = (c.flags & THQ_MODE_EXACT_W) || (w->qtype == THQ_Q8_0 && m <= 64);
+        r.gm = thq::plan_gemm(v.qtype, r.exact, m, w->N, w->K, c.gu, c.ctx->cus);
+        r.scratch = r.gm.workspace_bytes;
     } else {
-        e = thq::launch_generic(v, x, xf32, y, yf32, gu, (int)m, nout, up_off, s);
+        r.kind = Kind::GENERIC;
+    }
+    return r;
+}
+
+// Launch a planned route; `scratch` holds at least r.scratch bytes.
+int exec_route(const Call& c, const Route& r, void* scratch) {
+    const thq_weight* w = c.w;
+    const thq::WeightView v = view(w);
+    const bool xf32 = c.xt == THQ_ACT_F32, yf32 = c.yt == THQ_ACT_F32;
+    const int64_t nout = c.gu ? w->N / 2 : w->N;
+    const int64_t up_off = c.gu ? w->N / 2 : 0;
+    const int m = (int)c.m;
+    hipError_t e = hipSuccess;
+    switch (r.kind) {
+        case Kind::NONE: return THQ_OK;
+        case Kind::Q8ACT:
+            e = thq::launch_q8act(v, c.x, xf32, c.y, yf32, c.gu, m, nout, up_off, scratch, c.s);
+            break;
+        case Kind::GEMV1: e = thq::launch_gemv1(v, c.x, xf32, c.y, yf32, c.gu, nout, up_off, c.s, c.am); break;
+        case Kind::ROWS: e = thq::launch_gemv_rows(v, c.x, c.y, yf32, c.gu, m, nout, up_off, c.s); break;
+        case Kind::GEMV_MFMA:
+            e = thq::launch_gemv_mfma(r.gp, v, c.x, c.y, yf32, c.gu, m, nout, up_off, static_cast<float*>(scratch),
+                                      c.s, c.am);
+            break;
+        case Kind::GEMM:
+            e = thq::launch_gemm(r.gm, v, c.x, c.y, yf32, c.gu, r.exact, m, static_cast<float*>(scratch), c.s);
+            break;
+        case Kind::GENERIC: e = thq::launch_generic(v, c.x, xf32, c.y, yf32, c.gu, m, nout, up_off, c.s); break;
     }
     if (e != hipSuccess) return fail(THQ_EHIP, "kernel launch: %s", hipGetErrorString(e));
     return THQ_OK;
+}
+
+// Validate, plan and launch one call with the context workspace as scratch.
+int run_matmul(const Call& c) {
+    int rc = check_call(c);
+    if (rc || c.m == 0) return rc;
+    if (c.am) c.am->nb = 0;
+    DeviceGuard g(c.ctx->device);
+    const Route r = plan_route(c);
+    if (r.kind == Kind::NONE) return THQ_OK;
+    std::lock_guard<std::mutex> lk(c.ctx->mu);
+    if (r.scratch) {
+        rc = ensure_ws(c.ctx, r.scratch);
+        if (rc) return rc;
+    }
+    return exec_route(c, r, c.ctx->ws);
 }
 
 }  // namespace
@@ -331,6 +403,7 @@ void thq_destroy(thq_ctx* ctx) {
         DeviceGuard g(ctx->device);
         (void)hipDeviceSynchronize();
         (void)hipFree(ctx->ws);
+        for (void* p : ctx->retired) (void)hipFree(p);
     }
     delete ctx;
 }
@@ -472,7 +545,7 @@ int thq_weight_fuse(thq_ctx* ctx, const thq_weight* const* parts, int nparts, th
 
 void thq_weight_free(thq_weight* w) {
     if (!w) return;
-    DeviceGuard g(w->ctx ? w->ctx->device : 0);
+    DeviceGuard g(w->device);
     if (w->q) (void)hipFree(w->q);
     if (w->aux) (void)hipFree(w->aux);
     delete w;
@@ -490,7 +563,7 @@ int thq_weight_info(const thq_weight* w, thq_dtype* dtype, int64_t* n, int64_t* 
 int thq_weight_download(const thq_weight* w, void* host_blocks) {
     if (!w || !host_blocks) return fail(THQ_EINVAL, "null argument");
     if (w->qtype == THQ_MLX_Q4) return fail(THQ_EDTYPE, "MLX affine weights download with thq_affine_download");
-    DeviceGuard g(w->ctx->device);
+    DeviceGuard g(w->device);
     std::vector<uint8_t> qs(q_plane_bytes(w->qtype, w->N, w->K));
     std::vector<uint8_t> aux(aux_plane_bytes(w->qtype, w->N, w->K));
     HIP_TRY(hipMemcpy(qs.data(), w->q, qs.size(), hipMemcpyDeviceToHost));
@@ -619,7 +692,7 @@ int thq_affine_upload(thq_ctx* ctx, const uint32_t* wq_host, const uint16_t* sb_
 int thq_affine_download(const thq_weight* w, uint32_t* wq_host, uint16_t* sb_host) {
     if (!w || !wq_host || !sb_host) return fail(THQ_EINVAL, "null argument");
     if (w->qtype != THQ_MLX_Q4) return fail(THQ_EDTYPE, "not an MLX affine weight");
-    DeviceGuard g(w->ctx->device);
+    DeviceGuard g(w->device);
     std::vector<uint8_t> qs(q_plane_bytes(w->qtype, w->N, w->K));
     HIP_TRY(hipMemcpy(qs.data(), w->q, qs.size(), hipMemcpyDeviceToHost));
     const int nsb = (int)((w->K + 255) / 256), ng = (int)(w->K / w->gs), per = w->gs / 64;
@@ -732,12 +805,14 @@ int thq_gate_up_silu_q8act(thq_ctx* ctx, const thq_weight* fused, thq_dtype dot_
 
 int thq_matmul(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m, void* y_dev,
                thq_act y_type, uint32_t flags, void* stream) {
-    return run_matmul(ctx, w, x_dev, x_type, m, y_dev, y_type, flags, false, stream);
+    return run_matmul(Call{ctx, w, x_dev, x_type, m, y_dev, y_type, flags, false, static_cast<hipStream_t>(stream),
+                           nullptr});
 }
 
 int thq_gate_up_silu(thq_ctx* ctx, const thq_weight* fused, const void* x_dev, thq_act x_type, int64_t m, void* y_dev,
                      thq_act y_type, uint32_t flags, void* stream) {
-    return run_matmul(ctx, fused, x_dev, x_type, m, y_dev, y_type, flags, true, stream);
+    return run_matmul(Call{ctx, fused, x_dev, x_type, m, y_dev, y_type, flags, true, static_cast<hipStream_t>(stream),
+                           nullptr});
 }
 
 int thq_argmax(thq_ctx* ctx, const float* v_dev, int64_t m, int64_t n, uint32_t* idx_dev, void* stream) {
@@ -757,56 +832,124 @@ int thq_argmax(thq_ctx* ctx, const float* v_dev, int64_t m, int64_t n, uint32_t*
 
 int thq_matmul_argmax(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m,
                       float* logits_dev, uint32_t* idx_dev, uint32_t flags, void* stream) {
-    if (!ctx || !w) return fail(THQ_EINVAL, "null context or weight");
-    if (m == 0) return THQ_OK;
-    if (!idx_dev) return fail(THQ_EINVAL, "null idx_dev");
-    DeviceGuard g(ctx->device);
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    float* logits = logits_dev;
+    if (flags & ~(THQ_MODE_EXACT_W | THQ_MODE_Q8ACT | THQ_MODE_ARGMAX_FUSED))
+        return fail(THQ_EINVAL, "unknown flags 0x%x", flags);
     // no logits wanted and THQ_MODE_ARGMAX_FUSED: decode paths with the fused
     // epilogue write per-tile (max, index) partials instead of logits
     const bool fused = (flags & THQ_MODE_ARGMAX_FUSED) != 0;
-    flags &= ~THQ_MODE_ARGMAX_FUSED;
-    if (!logits && fused && !(flags & THQ_MODE_Q8ACT) && m <= 8) {
-        const int64_t ld = (w->N + 3) / 4;  // the most partials any fused path writes per row
-        const size_t part = ((size_t)m * (size_t)ld * 8 + 255) & ~(size_t)255;
-        {
+    flags = (flags & ~THQ_MODE_ARGMAX_FUSED) | THQ_MODE_EXACT_W;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    // validated as the logits-path call; without logits_dev, idx_dev stands in
+    // for y until the logits are placed in the workspace
+    Call c{ctx, w, x_dev, x_type, m, logits_dev ? static_cast<void*>(logits_dev) : static_cast<void*>(idx_dev),
+           THQ_ACT_F32, flags, false, s, nullptr};
+    int rc = check_call(c);
+    if (rc || m == 0) return rc;
+    if (!idx_dev) return fail(THQ_EINVAL, "null idx_dev");
+    if (w->N > 0xFFFFFFFFll) return fail(THQ_ESHAPE, "N=%lld exceeds u32 indices", (long long)w->N);
+    DeviceGuard g(ctx->device);
+    thq::AmaxOut am;
+    if (!logits_dev && fused && !(flags & THQ_MODE_Q8ACT) && m <= 8) {
+        c.am = &am;
+        const Route r = plan_route(c);
+        if (r.kind != Kind::NONE) {
+            const int64_t ld = (w->N + 3) / 4;  // the most partials any fused path writes per row
+            const size_t part = round256((size_t)m * (size_t)ld * 8);
             std::lock_guard<std::mutex> lk(ctx->mu);
-            int rc = ensure_ws(ctx, part + thq::argmax_partials_tmp_bytes(m, ld));
+            rc = ensure_ws(ctx, part + std::max(r.scratch, thq::argmax_partials_tmp_bytes(m, ld)));
             if (rc) return rc;
-        }
-        thq::AmaxOut am;
-        am.v = static_cast<float*>(ctx->ws);
-        am.i = reinterpret_cast<uint32_t*>(am.v + m * ld);
-        am.ld = ld;
-        int rc = run_matmul(ctx, w, x_dev, x_type, m, nullptr, THQ_ACT_F32, flags | THQ_MODE_EXACT_W, false, stream, &am);
-        if (rc) return rc;
-        if (am.nb > 0) {
-            hipError_t e = thq::launch_argmax_partials(am.v, am.i, m, am.nb, ld, idx_dev,
-                                                       static_cast<char*>(ctx->ws) + part, s);
-            if (e != hipSuccess) return fail(THQ_EHIP, "argmax: %s", hipGetErrorString(e));
-            return THQ_OK;
-        }
-        // no fused epilogue on this path: logits in the workspace below
-    }
-    if (!logits) {
-        // logits live at the end of the workspace, after the GEMM / argmax scratch
-        const thq::GemmPlan p = thq::plan_gemm(view(w).qtype, true, m, w->N, w->K, false, ctx->cus);
-        size_t scratch = std::max(p.workspace_bytes, thq::argmax_workspace_bytes(m, w->N));
-        if (flags & THQ_MODE_Q8ACT) scratch = std::max(scratch, thq::q8act_workspace_bytes(w->qtype, m, w->K));
-        const size_t off = (scratch + 255) & ~(size_t)255;
-        const size_t need = off + (size_t)m * (size_t)w->N * sizeof(float);
-        {
-            std::lock_guard<std::mutex> lk(ctx->mu);
-            int rc = ensure_ws(ctx, need);
+            am.v = static_cast<float*>(ctx->ws);
+            am.i = reinterpret_cast<uint32_t*>(am.v + m * ld);
+            am.ld = ld;
+            am.nb = 0;
+            rc = exec_route(c, r, static_cast<char*>(ctx->ws) + part);
             if (rc) return rc;
+            if (am.nb > 0) {
+                hipError_t e = thq::launch_argmax_partials(am.v, am.i, m, am.nb, ld, idx_dev,
+                                                           static_cast<char*>(ctx->ws) + part, s);
+                if (e != hipSuccess) return fail(THQ_EHIP, "argmax: %s", hipGetErrorString(e));
+                return THQ_OK;
+            }
+            // this launch path has no fused epilogue after all: nothing ran
         }
-        // the matmul and argmax use the workspace head; logits use its tail
-        logits = reinterpret_cast<float*>(static_cast<char*>(ctx->ws) + off);
     }
-    int rc = run_matmul(ctx, w, x_dev, x_type, m, logits, THQ_ACT_F32, flags | THQ_MODE_EXACT_W, false, stream);
+    // logits path.  Without logits_dev the logits take the workspace head and
+    // the route's scratch (split-K partials, quantized activations) and the
+    // argmax scratch follow them: one reservation, sized from the route the
+    // call will take, before any pointer into the workspace is formed
+    c.am = nullptr;
+    const Route r = plan_route(c);
+    const size_t lbytes = logits_dev ? 0 : round256((size_t)m * (size_t)w->N * sizeof(float));
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    rc = ensure_ws(ctx, lbytes + std::max(r.scratch, thq::argmax_workspace_bytes(m, w->N)));
     if (rc) return rc;
-    return thq_argmax(ctx, logits, m, w->N, idx_dev, s);
+    float* logits = logits_dev ? logits_dev : static_cast<float*>(ctx->ws);
+    void* scratch = static_cast<char*>(ctx->ws) + lbytes;
+    c.y = logits;
+    rc = exec_route(c, r, scratch);
+    if (rc) return rc;
+    hipError_t e = thq::launch_argmax(logits, m, w->N, idx_dev, scratch, s);
+    if (e != hipSuccess) return fail(THQ_EHIP, "argmax: %s", hipGetErrorString(e));
+    return THQ_OK;
+}
+
+namespace {
+int kernel_qtype(int dtype) {
+    switch (dtype) {
+        case THQ_Q8_0: return 8;
+        case THQ_Q4_K: return 12;
+        case THQ_Q6_K: return 14;
+        case THQ_MLX_Q4: return 13;
+        default: return 0;
+    }
+}
+}  // namespace
+
+int thq_plan_gemv_mfma(int dtype, int64_t m, int64_t n, int64_t k, int gate_up, thq_gemv_plan_info* out) {
+    const int qt = kernel_qtype(dtype);
+    if (!qt) return fail(THQ_EDTYPE, "dtype %d", dtype);
+    if (!out) return fail(THQ_EINVAL, "null out");
+    if (m < 1 || n < 1 || k < 1) return fail(THQ_ESHAPE, "shape [%lld, %lld, %lld]", (long long)m, (long long)n,
+                                             (long long)k);
+    const thq::GemvPlan p = thq::plan_gemv_mfma(qt, m, n, k, gate_up != 0);
+    const thq::GemvInstance in = thq::gemv_mfma_instance(qt, (int)std::min<int64_t>(m, 1 << 20), p);
+    const thq::GemvLimits l = thq::gemv_mfma_limits();
+    *out = thq_gemv_plan_info{};
+    out->waves = p.waves;
+    out->chunks_per_wave = p.cpw;
+    out->splits = p.splits;
+    out->live_rows = in.E;
+    out->staged_per_thread = in.NX;
+    out->workspace_bytes = (int64_t)p.workspace_bytes;
+    out->xs_elems = l.xs_elems;
+    out->xs_pad_elems = l.xs_pad_elems;
+    out->kb_max = l.kb_max;
+    out->kb_max_e8 = l.kb_max_e8;
+    out->mmax = l.mmax;
+    out->max_waves = l.max_waves;
+    out->sums_rows_e4 = l.sums_rows_e4;
+    out->sums_cols_e4 = l.sums_cols_e4;
+    out->sums_rows_e8 = l.sums_rows_e8;
+    out->sums_cols_e8 = l.sums_cols_e8;
+    return THQ_OK;
+}
+
+int thq_plan_gemm(int dtype, int exact, int64_t m, int64_t n, int64_t k, int gate_up, int cus,
+                  thq_gemm_plan_info* out) {
+    const int qt = kernel_qtype(dtype);
+    if (!qt) return fail(THQ_EDTYPE, "dtype %d", dtype);
+    if (!out) return fail(THQ_EINVAL, "null out");
+    if (m < 1 || n < 1 || k < 1) return fail(THQ_ESHAPE, "shape [%lld, %lld, %lld]", (long long)m, (long long)n,
+                                             (long long)k);
+    const thq::GemmPlan p = thq::plan_gemm(qt, exact != 0, m, n, k, gate_up != 0, cus);
+    *out = thq_gemm_plan_info{};
+    out->bm = p.bm;
+    out->splits = p.splits;
+    out->k_steps = p.kps;
+    out->tiles_n = p.tiles_n;
+    out->tiles_m = p.tiles_m;
+    out->workspace_bytes = (int64_t)p.workspace_bytes;
+    return THQ_OK;
 }
 
 }  // extern "C"

@@ -81,6 +81,18 @@ struct GemvPlan {
     size_t workspace_bytes = 0;          // split partials (f32 [splits][M][N])
 };
 GemvPlan plan_gemv_mfma(int qtype, int64_t M, int64_t N_rows, int64_t K, bool gu);  // waves == 0: unsupported
+// the kernel instance a plan launches (E live accumulator rows per lane, NX
+// staged activation chunks per thread); E == 0: none
+struct GemvInstance {
+    int E = 0, NX = 0;
+};
+GemvInstance gemv_mfma_instance(int qtype, int M, const GemvPlan& p);
+// the kernel's LDS staging limits (bf16 elements / float sums)
+struct GemvLimits {
+    int xs_elems, xs_pad_elems, kb_max, kb_max_e8, mmax, max_waves;
+    int sums_rows_e4, sums_rows_e8, sums_cols_e4, sums_cols_e8;
+};
+GemvLimits gemv_mfma_limits();
 hipError_t launch_gemv_mfma(const GemvPlan& p, const WeightView& w, const void* x, void* y, bool yf32, bool gu, int M,
                             int64_t nout, int64_t up_off, float* ws, hipStream_t s, AmaxOut* am = nullptr);
 // sum split partials P[s][M][ldp] in split order, then the epilogue

@@ -53,6 +53,7 @@ EXPORTS = (
     "thq_gguf_find_tensor", "thq_gguf_tensor_info", "thq_gguf_tensor_data", "thq_gguf_metadata_key",
     "thq_gguf_metadata_u32", "thq_gguf_metadata_f32", "thq_gguf_metadata_str", "thq_gguf_metadata_array",
     "thq_weight_from_gguf", "thq_q8act_bytes", "thq_q8act_prepare", "thq_matmul_q8act", "thq_gate_up_silu_q8act",
+    "thq_plan_gemv_mfma", "thq_plan_gemm",
 )
 
 
@@ -60,6 +61,35 @@ class ThqError(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"thq error {code}: {msg}")
         self.code = code
+
+
+class GemvPlanInfo(C.Structure):
+    """thq_gemv_plan_info (include/thq_plan.h)."""
+    _fields_ = [(n, C.c_int32) for n in ("waves", "chunks_per_wave", "splits", "live_rows", "staged_per_thread")] + [
+        ("workspace_bytes", C.c_int64)] + [(n, C.c_int32) for n in (
+            "xs_elems", "xs_pad_elems", "kb_max", "kb_max_e8", "mmax", "max_waves", "sums_rows_e4", "sums_cols_e4",
+            "sums_rows_e8", "sums_cols_e8")]
+
+
+class GemmPlanInfo(C.Structure):
+    """thq_gemm_plan_info (include/thq_plan.h)."""
+    _fields_ = [("bm", C.c_int32), ("splits", C.c_int32), ("k_steps", C.c_int32), ("tiles_n", C.c_int64),
+                ("tiles_m", C.c_int64), ("workspace_bytes", C.c_int64)]
+
+
+def plan_gemv_mfma(dtype: int, m: int, n: int, k: int, gate_up: bool = False) -> GemvPlanInfo:
+    """The decode GEMV's plan for a shape (host only)."""
+    out = GemvPlanInfo()
+    check(lib.thq_plan_gemv_mfma(dtype, m, n, k, int(gate_up), C.byref(out)))
+    return out
+
+
+def plan_gemm(dtype: int, m: int, n: int, k: int, exact: bool = False, gate_up: bool = False,
+              cus: int = 256) -> GemmPlanInfo:
+    """The GEMM's plan for a shape on a device with `cus` compute units (host only)."""
+    out = GemmPlanInfo()
+    check(lib.thq_plan_gemm(dtype, int(exact), m, n, k, int(gate_up), cus, C.byref(out)))
+    return out
 
 
 def _load():
@@ -109,6 +139,8 @@ def _load():
         "thq_q8act_prepare": ([P, I, P, I, i64, i64, P, P], I),
         "thq_matmul_q8act": ([P, P, I, P, i64, i64, P, I, P], I),
         "thq_gate_up_silu_q8act": ([P, P, I, P, i64, i64, P, I, P], I),
+        "thq_plan_gemv_mfma": ([I, i64, i64, i64, I, C.POINTER(GemvPlanInfo)], I),
+        "thq_plan_gemm": ([I, I, i64, i64, i64, I, I, C.POINTER(GemmPlanInfo)], I),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
