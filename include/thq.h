@@ -224,6 +224,21 @@ int thq_gate_up_silu_q8act(thq_ctx* ctx, const thq_weight* fused, thq_dtype dot_
 int thq_matmul(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m, void* y_dev,
                thq_act y_type, uint32_t flags, void* stream);
 
+/* thq_matmul without any allocation, for callers that cannot call hipMalloc
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * it).  No counterpart in the reference.  Same arguments, routing, kernels
+ * and results as thq_matmul; the scratch those kernels need (split-K
+ * partials, THQ_MODE_Q8ACT activation planes) is a static device array of
+ * thq_noalloc_scratch_bytes() bytes (64 MiB) that each device the library
+ * runs on holds until the process ends, instead of the context workspace.
+ * A call whose route needs more scratch than that fails with THQ_ESHAPE and
+ * launches nothing.  Every call on one device shares that device's array:
+ * calls that overlap on one GPU (concurrent streams, or contexts on the same
+ * device) race, so order them on one stream. */
+int thq_matmul_noalloc(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m,
+                       void* y_dev, thq_act y_type, uint32_t flags, void* stream);
+size_t thq_noalloc_scratch_bytes(void);
+
 /* Fused gate/up projection: `fused` = [gate; up] (2H rows).  y[M, H] =
  * bf16( silu(bf16(g)) * bf16(u) ) with silu in f32, g = x.gate^T, u = x.up^T.
  * Replaces QLin::gate_up_act_ps (engine/src/qwen35.rs:711-884) and its kernel

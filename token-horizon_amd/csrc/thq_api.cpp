@@ -22,8 +22,17 @@
 #include "thq_dev.hpp"
 #include "thq_kernels.hpp"
 
+// Device scratch of thq_matmul_noalloc: split-K partials and quantized
+// activation planes for callers that cannot allocate.  Each device the
+// library runs on holds its own copy until the process ends.  In host code
+// this name is a host-side stand-in, not a device address: kernels get the
+// address hipGetSymbolAddress returns for the current device (thq_ctx::scratch).
+constexpr size_t THQ_NOALLOC_SCRATCH_BYTES = (size_t)64 << 20;
+static __device__ __align__(256) unsigned char scratch[THQ_NOALLOC_SCRATCH_BYTES];
+
 struct thq_ctx {
     int device = 0;
+    void* scratch = nullptr;  // this device's copy of `scratch` (thq_init)
     int cus = 256;  // compute units (GEMM split planning)
     std::mutex mu;
     void* ws = nullptr;  // workspace: split-K partials, argmax partials, logits
@@ -390,6 +399,14 @@ int thq_init(int device, thq_ctx** out) {
     thq_ctx* c = new (std::nothrow) thq_ctx();
     if (!c) return fail(THQ_ENOMEM, "host allocation failed");
     c->device = device;
+    {
+        DeviceGuard g(device);
+        hipError_t e = hipGetSymbolAddress(&c->scratch, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) {
+            delete c;
+            return fail(THQ_EHIP, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        }
+    }
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0)
         c->cus = cus;
@@ -802,6 +819,24 @@ int thq_gate_up_silu_q8act(thq_ctx* ctx, const thq_weight* fused, thq_dtype dot_
                            int64_t k, void* y_dev, thq_act y_type, void* stream) {
     return run_q8act_dot(ctx, fused, dot_type, buf_dev, m, k, y_dev, y_type, true, stream);
 }
+
+int thq_matmul_noalloc(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m, void* y_dev,
+                       thq_act y_type, uint32_t flags, void* stream) {
+    // the kernels of thq_matmul on the device's static scratch: no hipMalloc,
+    // hipFree or allocating library call; the partials each route writes
+    // cover everything its reduce reads, so nothing needs clearing
+    const Call c{ctx, w, x_dev, x_type, m, y_dev, y_type, flags, false, static_cast<hipStream_t>(stream), nullptr};
+    int rc = check_call(c);
+    if (rc || m == 0) return rc;
+    DeviceGuard g(ctx->device);
+    const Route r = plan_route(c);
+    if (r.scratch > THQ_NOALLOC_SCRATCH_BYTES)
+        return fail(THQ_ESHAPE, "this call needs %zu bytes of scratch; thq_matmul_noalloc has %zu (use thq_matmul)",
+                    r.scratch, THQ_NOALLOC_SCRATCH_BYTES);
+    return exec_route(c, r, ctx->scratch);
+}
+
+size_t thq_noalloc_scratch_bytes(void) { return THQ_NOALLOC_SCRATCH_BYTES; }
 
 int thq_matmul(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m, void* y_dev,
                thq_act y_type, uint32_t flags, void* stream) {

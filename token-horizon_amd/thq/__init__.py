@@ -53,7 +53,7 @@ EXPORTS = (
     "thq_gguf_find_tensor", "thq_gguf_tensor_info", "thq_gguf_tensor_data", "thq_gguf_metadata_key",
     "thq_gguf_metadata_u32", "thq_gguf_metadata_f32", "thq_gguf_metadata_str", "thq_gguf_metadata_array",
     "thq_weight_from_gguf", "thq_q8act_bytes", "thq_q8act_prepare", "thq_matmul_q8act", "thq_gate_up_silu_q8act",
-    "thq_plan_gemv_mfma", "thq_plan_gemm",
+    "thq_plan_gemv_mfma", "thq_plan_gemm", "thq_matmul_noalloc", "thq_noalloc_scratch_bytes",
 )
 
 
@@ -139,6 +139,8 @@ def _load():
         "thq_q8act_prepare": ([P, I, P, I, i64, i64, P, P], I),
         "thq_matmul_q8act": ([P, P, I, P, i64, i64, P, I, P], I),
         "thq_gate_up_silu_q8act": ([P, P, I, P, i64, i64, P, I, P], I),
+        "thq_matmul_noalloc": ([P, P, P, I, i64, P, I, u32, P], I),
+        "thq_noalloc_scratch_bytes": ([], C.c_size_t),
         "thq_plan_gemv_mfma": ([I, i64, i64, i64, I, C.POINTER(GemvPlanInfo)], I),
         "thq_plan_gemm": ([I, I, i64, i64, i64, I, I, C.POINTER(GemmPlanInfo)], I),
     }
@@ -356,6 +358,16 @@ def matmul(w: QTensor, x: torch.Tensor, out_dtype=torch.float32, flags: int = 0,
         out = torch.empty((m, w.n), dtype=out_dtype, device=x.device)
     check(lib.thq_matmul(w.ctx.h, w.h, _ptr(x2), _act(x2), m, _ptr(out), _act(out), flags, _stream()))
     return out.reshape(*x.shape[:-1], w.n)
+
+
+def matmul_noalloc(w: QTensor, x: torch.Tensor, out: torch.Tensor, flags: int = 0):
+    """thq_matmul_noalloc: thq_matmul on the device's static scratch (no allocation)."""
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.shape[-1] != w.k:
+        raise ValueError(f"x last dim {x2.shape[-1]} != weight inp {w.k}")
+    check(lib.thq_matmul_noalloc(w.ctx.h, w.h, _ptr(x2), _act(x2), x2.shape[0], _ptr(out), _act(out), flags,
+                                 _stream()))
+    return out
 
 
 def gate_up_silu(w: QTensor, x: torch.Tensor, out_dtype=torch.bfloat16, flags: int = 0,
