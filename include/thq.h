@@ -265,6 +265,24 @@ int thq_gate_up_silu(thq_ctx* ctx, const thq_weight* fused, const void* x_dev, t
 int thq_matmul_argmax(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m,
                       float* logits_dev, uint32_t* idx_dev, uint32_t flags, void* stream);
 
+/* Exact per-row top-k of f32 v_dev [M, N] for sampled verify: vals_dev /
+ * idx_dev [M, k] receive each row's k largest logits in rank order (logit
+ * desc, then id asc), a NaN ranking as -inf and -0.0 as +0.0 (the values
+ * written are those keys).  1 <= k <= 64; with k > N the slots past N hold
+ * (-inf, 0xFFFFFFFF).  Candidates of the reference's sampled acceptance:
+ * ts_topk (engine/src/sample_kernel.rs:725-796, CPU form sorted_row_dist
+ * :326-347) consuming the verify logits in place (engine/src/engine.rs:
+ * 2424-2436); that kernel bounds its candidate pool, this one is exact for
+ * any row. */
+int thq_topk(thq_ctx* ctx, const float* v_dev, int64_t m, int64_t n, int k, float* vals_dev, uint32_t* idx_dev,
+             void* stream);
+
+/* LM head + top-k: thq_matmul_argmax's logits (exact weights; logits_dev
+ * may be NULL, the logits then live in the context workspace) followed by
+ * thq_topk of every row. */
+int thq_matmul_topk(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m, int k,
+                    float* logits_dev, float* vals_dev, uint32_t* idx_dev, uint32_t flags, void* stream);
+
 /* Per-row argmax of an f32 [M, N] device matrix, same tie rule
  * (candle Tensor::argmax(D::Minus1) / engine.rs greedy_argmax). */
 int thq_argmax(thq_ctx* ctx, const float* v_dev, int64_t m, int64_t n, uint32_t* idx_dev, void* stream);

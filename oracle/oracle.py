@@ -61,6 +61,7 @@ def lib():
         L.o_argmax.argtypes = [P, i64]
         L.o_argmax.restype = C.c_uint32
         L.o_argmax_rows.argtypes = [P, i64, i64, P]
+        L.o_topk_rows.argtypes = [P, i64, i64, C.c_int, P, P]
         L.o_bf16_from_f64_half.argtypes = [C.c_double]
         L.o_bf16_from_f64_half.restype = C.c_uint16
         L.o_affine_dequant_bf16.argtypes = [P, P, i64, i64, C.c_int, P]
@@ -182,6 +183,18 @@ def argmax_rows(v: np.ndarray) -> np.ndarray:
     idx = np.empty(m, dtype=np.uint32)
     lib().o_argmax_rows(_p(v), m, n, _p(idx))
     return idx
+
+
+def topk_rows(v: np.ndarray, k: int):
+    """(vals f32 [m, k], idx u32 [m, k]): each row's top k by (key desc, id asc)."""
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    if v.ndim == 1:
+        v = v.reshape(1, -1)
+    m, n = v.shape
+    vals = np.empty((m, k), np.float32)
+    idx = np.empty((m, k), np.uint32)
+    lib().o_topk_rows(_p(v), m, n, k, _p(vals), _p(idx))
+    return vals, idx
 
 
 def get_scale_min_k4(j: int, scales12: np.ndarray):

@@ -551,6 +551,40 @@ void o_argmax_rows(const float* v, int64_t m, int64_t n, uint32_t* idx) {
     for (int64_t r = 0; r < m; ++r) idx[r] = o_argmax(v + r * n, n);
 }
 
+/* engine/src/sample_kernel.rs key (:163-169): NaN ranks as -inf, -0.0 as +0.0. */
+static float topk_key(float v) {
+    if (v != v) return -INFINITY;
+    return v + 0.0f;
+}
+
+typedef struct { float key; uint32_t id; } o_kv;
+
+static int kv_cmp(const void* a, const void* b) {
+    const o_kv* x = (const o_kv*)a;
+    const o_kv* y = (const o_kv*)b;
+    if (x->key != y->key) return x->key > y->key ? -1 : 1;  /* key desc */
+    return x->id < y->id ? -1 : (x->id > y->id);            /* then id asc */
+}
+
+/* sorted_row_dist's candidate order (engine/src/sample_kernel.rs:326-337):
+ * the first k of the row sorted by (key desc, id asc), keys reported as
+ * key(v); slots past n are (-inf, 0xFFFFFFFF) as ts_topk leaves them. */
+void o_topk_rows(const float* v, int64_t m, int64_t n, int k, float* vals, uint32_t* idx) {
+    o_kv* buf = (o_kv*)malloc(sizeof(o_kv) * (size_t)(n > 0 ? n : 1));
+    for (int64_t r = 0; r < m; ++r) {
+        for (int64_t i = 0; i < n; ++i) {
+            buf[i].key = topk_key(v[r * n + i]);
+            buf[i].id = (uint32_t)i;
+        }
+        qsort(buf, (size_t)n, sizeof(o_kv), kv_cmp);
+        for (int j = 0; j < k; ++j) {
+            vals[r * k + j] = j < n ? buf[j].key : -INFINITY;
+            idx[r * k + j] = j < n ? buf[j].id : 0xFFFFFFFFu;
+        }
+    }
+    free(buf);
+}
+
 int o_max_threads(void) {
 #ifdef _OPENMP
     return omp_get_max_threads();

@@ -129,6 +129,10 @@ int o_baseline_matmul(int type, const uint8_t* w, int64_t n, int64_t k, const fl
 int o_baseline_has_avx2(void);
 int o_max_threads(void);
 
+/* Per-row top-k by (key desc, id asc), key(NaN) = -inf, key(-0) = +0
+ * (engine/src/sample_kernel.rs:163-169, 326-347); slots past n: (-inf, 0xFFFFFFFF). */
+void o_topk_rows(const float* v, int64_t m, int64_t n, int k, float* vals, uint32_t* idx);
+
 #ifdef __cplusplus
 }
 #endif

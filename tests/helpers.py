@@ -143,3 +143,39 @@ def rand_qlin_fast(out: int, inp: int, seed: int, gs: int = 64):
     sb = np.concatenate([O.f32_to_bf16_bits(sc.astype(np.float32)), O.f32_to_bf16_bits(bi.astype(np.float32))],
                         axis=1)
     return wq, np.ascontiguousarray(sb, dtype=np.uint16)
+
+
+def ref_rng(state: list) -> float:
+    """The reference tests' xorshift64 uniform (engine/src/sample_kernel.rs:1178-1183);
+    state is a one-element list holding the u64 seed."""
+    s = state[0]
+    s ^= (s << 13) & 0xFFFFFFFFFFFFFFFF
+    s ^= s >> 7
+    s ^= (s << 17) & 0xFFFFFFFFFFFFFFFF
+    state[0] = s
+    return (s >> 11) / float(1 << 53)
+
+
+def lm_row(n: int, state: list, spice: bool) -> np.ndarray:
+    """LM-like logits row of the reference's sampler tests (lm_row,
+    engine/src/sample_kernel.rs:1300-1321): bf16-rounded N(0, 2.5) bulk (exact
+    ties), a few peaked tokens, and with `spice` a NaN, a -inf, a -0.0 and a
+    +0.0 at fixed positions.  half's f64 -> bf16 rounding is the oracle's."""
+    import math
+    out = np.empty(n, np.float32)
+    bf = lambda v: float(O.bf16_bits_to_f32(np.array([O.bf16_from_f64_half(v)], np.uint16))[0])
+    for i in range(n):
+        a, b = max(ref_rng(state), 1e-300), ref_rng(state)
+        g = math.sqrt(-2.0 * math.log(a)) * math.cos(2.0 * math.pi * b)
+        out[i] = bf(g * 2.5)
+    top = int(ref_rng(state) * 4.0) + 1
+    for t in range(top + 24):
+        v = int(ref_rng(state) * n) % n
+        x = 16.0 - t * (0.1 + ref_rng(state) * 0.7) + (3.0 if t < top else 0.0)
+        out[v] = bf(x)
+    if spice:
+        out[n // 2] = np.nan
+        out[n // 3] = -np.inf
+        out[n // 5] = -0.0
+        out[n // 7] = 0.0
+    return out

@@ -1,0 +1,138 @@
+"""Exact per-row top-k for sampled verify (thq_topk, thq_matmul_topk) against
+the oracle's sort by (key desc, id asc), key(NaN) = -inf, key(-0.0) = +0.0
+(engine/src/sample_kernel.rs:163-169, 326-347).  Selection is integer work
+on the logits' bits, so indices and values must be bit-exact.
+
+Rows come from the reference's own test generator (lm_row: bf16-rounded
+logits with exact ties, peaked tokens, NaN / -inf / -0.0 / +0.0), plus rows
+built to stress the tie rule across segment boundaries, all-NaN rows, k
+larger than the row, rows long enough for two merge levels, and more rows
+than one launch's grid holds.  The LM-head variant is checked on the Q8_0
+151936 x 4096 head at the verify shapes M = 5 and 40.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from helpers import activations, lm_row, rel_row_err, weight_bytes
+
+pytestmark = pytest.mark.gpu
+
+thq = pytest.importorskip("thq")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    torch.cuda.init()
+    yield
+    torch.cuda.synchronize()
+
+
+def check(v: np.ndarray, k: int, tag: str):
+    vals, idx = thq.topk(torch.from_numpy(np.ascontiguousarray(v, np.float32)).cuda(), k)
+    torch.cuda.synchronize()
+    wv, wi = O.topk_rows(v, k)
+    got_i = idx.cpu().numpy().view(np.uint32)
+    got_v = vals.cpu().numpy()
+    bad = np.argwhere((got_i != wi).any(axis=1)).ravel()
+    assert bad.size == 0, f"{tag}: row {bad[0]}: got {got_i[bad[0]][:8]} want {wi[bad[0]][:8]}"
+    assert np.array_equal(got_v.view(np.uint32), wv.view(np.uint32)), tag
+
+
+@pytest.fixture(scope="module")
+def ref_rows():
+    state = [0xF00D5EED]
+    return {n: np.stack([lm_row(n, state, r % 2 == 0) for r in range(4)]) for n in (5000, 151936)}
+
+
+@pytest.mark.parametrize("n", [5000, 151936])
+@pytest.mark.parametrize("k", [1, 20, 32, 64])
+def test_topk_reference_generator(ref_rows, n, k):
+    print(f"topk lm_row n={n} k={k}", flush=True)
+    check(ref_rows[n], k, f"lm_row n={n} k={k}")
+
+
+@pytest.mark.parametrize("n", [1, 100, 4095, 4096, 4097, 20011, 300000])
+def test_topk_ties_across_segments(n):
+    """Small-integer rows: the k-th value has copies in many 4096-wide
+    segments, so the lowest ids among them must win across the merge."""
+    rng = np.random.default_rng(n)
+    v = rng.integers(0, 3, (3, n)).astype(np.float32)
+    v[1] = 1.0                       # every element tied: ids 0..k-1
+    v[2, rng.integers(0, n, 5)] = np.nan
+    for k in (1, 7, 64):
+        print(f"topk ties n={n} k={k}", flush=True)
+        check(v, k, f"ties n={n} k={k}")
+
+
+def test_topk_special_rows():
+    n = 9000
+    v = np.zeros((5, n), np.float32)
+    v[0] = np.nan                    # all NaN: keys -inf, ids 0..k-1
+    v[1] = -np.inf
+    v[2, ::2] = -0.0                 # -0.0 ties with +0.0
+    v[3] = np.linspace(-1, 1, n, dtype=np.float32)
+    v[3, 17] = np.inf
+    v[4] = np.nan
+    v[4, 8999] = -5.0                # the only real value ranks first
+    check(v, 64, "special")
+
+
+def test_topk_k_beyond_row():
+    v = np.array([[3.0, 1.0, 2.0, np.nan, 1.0]], np.float32)
+    vals, idx = thq.topk(torch.from_numpy(v).cuda(), 8)
+    assert list(idx.cpu().numpy().view(np.uint32)[0]) == [0, 2, 1, 4, 3] + [0xFFFFFFFF] * 3
+    assert np.all(np.isneginf(vals.cpu().numpy()[0, 4:]))
+    check(v, 8, "k > n")
+
+
+def test_topk_many_rows():
+    """More rows than one launch's grid dimension holds (65535)."""
+    rng = np.random.default_rng(3)
+    v = rng.integers(-4, 5, (70000, 8)).astype(np.float32)
+    check(v, 4, "70000 rows")
+
+
+def test_topk_rejects_bad_k():
+    v = torch.zeros((2, 10), dtype=torch.float32, device="cuda")
+    for k in (0, 65):
+        with pytest.raises(thq.ThqError):
+            thq.topk(v, k)
+
+
+@pytest.fixture(scope="module")
+def lm_head():
+    n, k = 151936, 4096
+    b = weight_bytes(O.Q8_0, n, k, seed=4)
+    return b, thq.QTensor.from_gguf_bytes(thq.Q8_0, b, n, k)
+
+
+@pytest.mark.parametrize("m", [5, 40])
+def test_lm_head_topk(lm_head, m):
+    """LM head + top-32 at the verify shapes: logits within 1e-4 of the
+    oracle's f64 product (exact weights), and the top-k of every row equal
+    to the oracle's top-k of those logits; the workspace-logits path gives
+    the same candidates."""
+    b, w = lm_head
+    n, kdim = w.shape
+    xf = O.bf16_round(activations(m, kdim, seed=8))
+    xb = torch.from_numpy(xf).cuda().to(torch.bfloat16)
+    print(f"lm head topk m={m}", flush=True)
+    logits, vals, idx = thq.matmul_topk(w, xb, 32, want_logits=True)
+    _, vals2, idx2 = thq.matmul_topk(w, xb, 32)
+    torch.cuda.synchronize()
+    lg = logits.cpu().numpy()
+    ref = O.matmul(O.Q8_0, b, n, kdim, xf, O.MODE_DEQUANT_F32)
+    assert rel_row_err(lg, ref) <= 1e-4
+    wv, wi = O.topk_rows(lg, 32)
+    assert np.array_equal(idx.cpu().numpy().view(np.uint32), wi)
+    assert np.array_equal(vals.cpu().numpy(), wv)
+    assert torch.equal(idx, idx2) and torch.equal(vals, vals2)
+    # against the f64 product: the oracle's own top-1 matches wherever it is not a near tie
+    top_ref = O.topk_rows(ref, 2)[1]
+    for r in range(m):
+        if ref[r, top_ref[r, 0]] - ref[r, top_ref[r, 1]] > 1e-3 * np.linalg.norm(ref[r]):
+            assert wi[r, 0] == top_ref[r, 0]

@@ -485,3 +485,41 @@ def test_q6k_matmul_dequant_mode_brute_force():
     y = O.matmul(O.Q6_K, raw, n, k, x)
     ref = x.astype(np.float64) @ _q6k_numpy(raw, k).astype(np.float64).T
     assert np.allclose(y, ref, rtol=1e-6, atol=1e-6)
+
+
+# ---------------------------------------------------------------- top-k
+def _ref_key(v: float) -> float:
+    """engine/src/sample_kernel.rs:163-169: NaN ranks as -inf, -0.0 as +0.0."""
+    return -math.inf if v != v else v + 0.0
+
+
+def test_topk_kat():
+    """Ties broken by the lower id, NaN placed with -inf (by id), -0.0 tied
+    with +0.0, keys reported; slots past n are (-inf, 0xFFFFFFFF)."""
+    v = np.array([1.0, np.nan, 3.0, -0.0, 3.0, 0.0, -np.inf], np.float32)
+    vals, idx = O.topk_rows(v, 9)
+    assert list(idx[0]) == [2, 4, 0, 3, 5, 1, 6, 0xFFFFFFFF, 0xFFFFFFFF]
+    assert list(vals[0][:5]) == [3.0, 3.0, 1.0, 0.0, 0.0]
+    assert not np.signbit(vals[0][3])  # -0.0 reported as its key +0.0
+    assert np.all(np.isneginf(vals[0][5:]))
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_topk_matches_python_sort(seed):
+    """Against Python's sort with the reference's comparator
+    (sorted_row_dist, engine/src/sample_kernel.rs:326-337), on rows with many
+    exact ties (small integers), NaN, +-inf and signed zeros."""
+    rng = np.random.default_rng(seed)
+    n = 3000
+    v = rng.integers(-20, 21, (6, n)).astype(np.float32) * 0.5
+    v[0, rng.integers(0, n, 40)] = np.nan
+    v[1, rng.integers(0, n, 40)] = -0.0
+    v[2, rng.integers(0, n, 10)] = np.inf
+    v[3, :] = np.nan
+    v[4, :] = 7.0
+    for k in (1, 5, 64):
+        vals, idx = O.topk_rows(v, k)
+        for r in range(v.shape[0]):
+            order = sorted(range(n), key=lambda i: (-_ref_key(float(v[r, i])), i))[:k]
+            assert list(idx[r]) == order
+            assert np.array_equal(vals[r], np.array([_ref_key(float(v[r, i])) for i in order], np.float32))

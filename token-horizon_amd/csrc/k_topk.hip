@@ -1,0 +1,296 @@
+// k_topk.hip — exact per-row top-k of verify logits for sampled
+// speculative-decode acceptance.
+//
+// Role: the candidate step of the reference's sampled verify consumer
+// (ts_topk, engine/src/sample_kernel.rs:1-16, 725-796; CPU form
+// sorted_row_dist :326-347 and key :163-169, consumed at
+// engine/src/engine.rs:2436-2442): the top k (k <= 64) logits of each row by
+// (logit desc, id asc), where a NaN ranks as -inf and -0.0 as +0.0.  The
+// reference's kernel pools the elements at or above the k-th largest lane
+// maximum (at most 1024 of them, flagging overflow); this one is exact for
+// any row.
+//
+// Order-preserving keys.  A logit maps to a u32 whose unsigned order is the
+// rank order (sign bit flipped for positives, all bits for negatives); key 0
+// is below every real key and marks an absent element.  The composite
+// order (key desc, id asc) has no ties, so the top-k set is exact.
+//
+// Two levels.  Each block takes a segment of 4096 elements of one row
+// (16 per thread, thread t holding ids base + 16t .. +15, so thread order is
+// id order) and selects its top k: a 4-pass radix select (8 bits a pass,
+// LDS histograms) finds the k-th largest key tau and how many of the
+// elements equal to tau are needed; those are the ones with the lowest ids,
+// found by a block prefix count in id order.  Selected elements are
+// compacted in id order, so a row's per-segment candidates stay in id order
+// for the next level, which runs the same select over them until one
+// segment remains; the last one also sorts its k by rank counting.
+// HBM-bound: one pass over the logits (4 B per logit) and a few KB of
+// candidates per row.
+#include "thq_dev.hpp"
+#include "thq_kernels.hpp"
+
+namespace thq {
+
+namespace {
+
+constexpr int TK_THREADS = 256;
+constexpr int TK_EPT = 16;
+constexpr int TK_SEG = TK_THREADS * TK_EPT;
+constexpr uint32_t TK_ABSENT = 0u;
+
+__device__ __forceinline__ uint32_t topk_key(float v) {
+    uint32_t b = __float_as_uint(v);
+    if ((b & 0x7fffffffu) > 0x7f800000u) b = 0xff800000u;  // NaN ranks as -inf
+    if (b == 0x80000000u) b = 0u;                          // -0.0 ranks as +0.0
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__device__ __forceinline__ float topk_value(uint32_t k) {
+    if (k == TK_ABSENT) return -INFINITY;
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// exclusive prefix of one int per thread over the block (256 threads), and the total
+__device__ __forceinline__ int block_scan(int v, int* lds, int& total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(x, d, 64);
+        if (lane >= d) x += y;
+    }
+    if (lane == 63) lds[wave] = x;
+    __syncthreads();
+    int base = 0;
+#pragma unroll
+    for (int w = 0; w < TK_THREADS / 64; ++w) base += w < wave ? lds[w] : 0;
+    total = lds[0] + lds[1] + lds[2] + lds[3];
+    __syncthreads();  // lds is reused by the next scan
+    return base + x - v;
+}
+
+// Grid: (segments, rows).  Level 0 reads logits rows [m][n] (ids = column);
+// later levels read candidate rows ckey / cid [m][ccount] (kept in id order).
+// Non-final: the segment's k selected (key, id) go to okey / oid at
+// m * ostride + seg * k, in id order, padded with absent entries.  FINAL (a
+// single segment): vals / idx [m][k] in rank order, unused slots -inf /
+// 0xFFFFFFFF.
+template <bool FROM_LOGITS, bool FINAL>
+__global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restrict__ logits, int64_t n,
+                                                           const uint32_t* __restrict__ ckey,
+                                                           const uint32_t* __restrict__ cid, int64_t ccount, int k,
+                                                           uint32_t* __restrict__ okey, uint32_t* __restrict__ oid,
+                                                           int64_t ostride, float* __restrict__ vals,
+                                                           uint32_t* __restrict__ idx) {
+    __shared__ uint32_t stage[TK_SEG];  // level 0: the segment's logits, transposed to thread order
+    __shared__ uint32_t hist[256];
+    __shared__ int scan_lds[TK_THREADS / 64];
+    __shared__ uint32_t sh_prefix;
+    __shared__ int sh_kk;
+    __shared__ uint32_t fkey[64], fid[64];
+
+    const int tid = threadIdx.x;
+    const int64_t m = blockIdx.y;
+    const int64_t seg = blockIdx.x;
+    const int64_t count = FROM_LOGITS ? n : ccount;
+    const int64_t base = seg * TK_SEG;
+
+    uint32_t key[TK_EPT], id[TK_EPT];
+    if constexpr (FROM_LOGITS) {
+        // coalesced loads (position base + e*256 + tid), then thread t takes
+        // positions base + 16t .. +15 out of LDS
+        const float* row = logits + m * n;
+#pragma unroll
+        for (int e = 0; e < TK_EPT; ++e) {
+            const int64_t pos = base + e * TK_THREADS + tid;
+            stage[e * TK_THREADS + tid] = pos < n ? topk_key(row[pos]) : TK_ABSENT;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < TK_EPT; ++e) {
+            key[e] = stage[tid * TK_EPT + e];
+            id[e] = (uint32_t)(base + tid * TK_EPT + e);
+        }
+    } else {
+        const uint32_t* kr = ckey + m * ccount;
+        const uint32_t* ir = cid + m * ccount;
+#pragma unroll
+        for (int e = 0; e < TK_EPT; ++e) {
+            const int64_t pos = base + tid * TK_EPT + e;
+            key[e] = pos < count ? kr[pos] : TK_ABSENT;
+            id[e] = pos < count ? ir[pos] : 0xFFFFFFFFu;
+        }
+    }
+
+    int present = 0;
+#pragma unroll
+    for (int e = 0; e < TK_EPT; ++e) present += key[e] != TK_ABSENT;
+    int P;
+    (void)block_scan(present, scan_lds, P);
+
+    // radix select: tau = the k-th largest present key, need = how many of
+    // the keys equal to tau belong to the top k
+    uint32_t tau = 0u;
+    int need = 0;
+    if (P > k) {
+        uint32_t prefix = 0u, pmask = 0u;
+        int kk = k;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            hist[tid] = 0u;
+            __syncthreads();
+#pragma unroll
+            for (int e = 0; e < TK_EPT; ++e)
+                if (key[e] != TK_ABSENT && (key[e] & pmask) == prefix) atomicAdd(&hist[(key[e] >> shift) & 255u], 1u);
+            __syncthreads();
+            if (tid < 64) {
+                // lane l scans bins 255-4l .. 252-4l (from the top)
+                uint32_t c[4];
+                int s = 0;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    c[i] = hist[255 - 4 * tid - i];
+                    s += (int)c[i];
+                }
+                int incl = s;
+#pragma unroll
+                for (int d = 1; d < 64; d <<= 1) {
+                    const int y = __shfl_up(incl, d, 64);
+                    if (tid >= d) incl += y;
+                }
+                int ex = incl - s;
+                if (ex < kk && kk <= incl) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        if (ex + (int)c[i] >= kk) {
+                            sh_prefix = prefix | ((uint32_t)(255 - 4 * tid - i) << shift);
+                            sh_kk = kk - ex;
+                            break;
+                        }
+                        ex += (int)c[i];
+                    }
+                }
+            }
+            __syncthreads();
+            prefix = sh_prefix;
+            kk = sh_kk;
+            pmask |= 255u << shift;
+        }
+        tau = prefix;
+        need = kk;
+    }
+
+    // select: every key above tau, and the `need` lowest ids among keys equal
+    // to tau (P <= k: every present element)
+    int eq = 0;
+    if (P > k) {
+#pragma unroll
+        for (int e = 0; e < TK_EPT; ++e) eq += key[e] == tau;
+    }
+    int eq_total;
+    int eq_rank = block_scan(eq, scan_lds, eq_total);
+    bool sel[TK_EPT];
+    int nsel = 0;
+#pragma unroll
+    for (int e = 0; e < TK_EPT; ++e) {
+        if (P > k) {
+            const bool is_eq = key[e] == tau;
+            sel[e] = key[e] > tau || (is_eq && eq_rank < need);
+            eq_rank += is_eq;
+        } else {
+            sel[e] = key[e] != TK_ABSENT;
+        }
+        nsel += sel[e];
+    }
+    int total;
+    int pos = block_scan(nsel, scan_lds, total);  // total == min(P, k)
+
+    if constexpr (!FINAL) {
+        uint32_t* ok = okey + m * ostride + seg * k;
+        uint32_t* oi = oid + m * ostride + seg * k;
+#pragma unroll
+        for (int e = 0; e < TK_EPT; ++e)
+            if (sel[e]) {
+                ok[pos] = key[e];
+                oi[pos] = id[e];
+                ++pos;
+            }
+        if (tid >= total && tid < k) {
+            ok[tid] = TK_ABSENT;
+            oi[tid] = 0xFFFFFFFFu;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < TK_EPT; ++e)
+            if (sel[e]) {
+                fkey[pos] = key[e];
+                fid[pos] = id[e];
+                ++pos;
+            }
+        __syncthreads();
+        if (tid < k) {
+            float* vr = vals + m * k;
+            uint32_t* xr = idx + m * k;
+            if (tid < total) {
+                const uint32_t kt = fkey[tid], it = fid[tid];
+                int rank = 0;
+                for (int j = 0; j < total; ++j) rank += fkey[j] > kt || (fkey[j] == kt && fid[j] < it);
+                vr[rank] = topk_value(kt);
+                xr[rank] = it;
+            } else {
+                vr[tid] = -INFINITY;
+                xr[tid] = 0xFFFFFFFFu;
+            }
+        }
+    }
+}
+
+}  // namespace
+
+size_t topk_workspace_bytes(int64_t m, int64_t n, int k) {
+    const int64_t seg0 = (n + TK_SEG - 1) / TK_SEG;
+    if (seg0 <= 1) return 0;
+    // two candidate buffers of [m][seg0 * k] (key, id) pairs, 256-B aligned
+    const size_t one = ((size_t)m * (size_t)seg0 * (size_t)k * 8 + 255) & ~(size_t)255;
+    return 2 * one;
+}
+
+hipError_t launch_topk(const float* v, int64_t m, int64_t n, int k, float* vals, uint32_t* idx, void* ws,
+                       hipStream_t s) {
+    if (k < 1 || k > 64 || m < 0) return hipErrorInvalidValue;
+    if (m == 0) return hipSuccess;
+    for (int64_t r0 = 0; r0 < m; r0 += 65535) {
+        const int64_t rows = m - r0 < 65535 ? m - r0 : 65535;
+        float* vr = vals + r0 * k;
+        uint32_t* ir = idx + r0 * k;
+        if (n <= TK_SEG) {
+            hipLaunchKernelGGL((k_topk_select<true, true>), dim3(1, (unsigned)rows), dim3(TK_THREADS), 0, s,
+                               v + r0 * n, n, (const uint32_t*)nullptr, (const uint32_t*)nullptr, (int64_t)0, k,
+                               (uint32_t*)nullptr, (uint32_t*)nullptr, (int64_t)0, vr, ir);
+            continue;
+        }
+        const int64_t seg0 = (n + TK_SEG - 1) / TK_SEG;
+        const size_t one = ((size_t)m * (size_t)seg0 * (size_t)k * 8 + 255) & ~(size_t)255;
+        uint32_t* buf[2] = {static_cast<uint32_t*>(ws), reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + one)};
+        // each buffer: keys [rows][cnt] then ids [rows][cnt]
+        int64_t cnt = seg0 * k;
+        hipLaunchKernelGGL((k_topk_select<true, false>), dim3((unsigned)seg0, (unsigned)rows), dim3(TK_THREADS), 0, s,
+                           v + r0 * n, n, (const uint32_t*)nullptr, (const uint32_t*)nullptr, (int64_t)0, k, buf[0],
+                           buf[0] + rows * cnt, cnt, (float*)nullptr, (uint32_t*)nullptr);
+        int cur = 0;
+        while (cnt > TK_SEG) {
+            const int64_t segs = (cnt + TK_SEG - 1) / TK_SEG;
+            const int64_t nc = segs * k;
+            hipLaunchKernelGGL((k_topk_select<false, false>), dim3((unsigned)segs, (unsigned)rows), dim3(TK_THREADS),
+                               0, s, (const float*)nullptr, (int64_t)0, buf[cur], buf[cur] + rows * cnt, cnt, k,
+                               buf[cur ^ 1], buf[cur ^ 1] + rows * nc, nc, (float*)nullptr, (uint32_t*)nullptr);
+            cur ^= 1;
+            cnt = nc;
+        }
+        hipLaunchKernelGGL((k_topk_select<false, true>), dim3(1, (unsigned)rows), dim3(TK_THREADS), 0, s,
+                           (const float*)nullptr, (int64_t)0, buf[cur], buf[cur] + rows * cnt, cnt, k,
+                           (uint32_t*)nullptr, (uint32_t*)nullptr, (int64_t)0, vr, ir);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace thq

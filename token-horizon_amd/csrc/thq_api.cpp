@@ -865,6 +865,53 @@ int thq_argmax(thq_ctx* ctx, const float* v_dev, int64_t m, int64_t n, uint32_t*
     return THQ_OK;
 }
 
+int thq_topk(thq_ctx* ctx, const float* v_dev, int64_t m, int64_t n, int k, float* vals_dev, uint32_t* idx_dev,
+             void* stream) {
+    if (!ctx) return fail(THQ_EINVAL, "null context");
+    if (k < 1 || k > 64) return fail(THQ_EINVAL, "k=%d (1..64)", k);
+    if (m < 0 || n < 0) return fail(THQ_ESHAPE, "negative shape");
+    if (n > 0xFFFFFFFFll) return fail(THQ_ESHAPE, "row length exceeds u32 indices");
+    if (m == 0) return THQ_OK;
+    if (!vals_dev || !idx_dev || (n > 0 && !v_dev)) return fail(THQ_EINVAL, "null argument");
+    DeviceGuard g(ctx->device);
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    int rc = ensure_ws(ctx, thq::topk_workspace_bytes(m, n, k));
+    if (rc) return rc;
+    hipError_t e = thq::launch_topk(v_dev, m, n, k, vals_dev, idx_dev, ctx->ws, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(THQ_EHIP, "topk: %s", hipGetErrorString(e));
+    return THQ_OK;
+}
+
+int thq_matmul_topk(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m, int k,
+                    float* logits_dev, float* vals_dev, uint32_t* idx_dev, uint32_t flags, void* stream) {
+    if (flags & ~(THQ_MODE_EXACT_W | THQ_MODE_Q8ACT)) return fail(THQ_EINVAL, "unknown flags 0x%x", flags);
+    if (k < 1 || k > 64) return fail(THQ_EINVAL, "k=%d (1..64)", k);
+    flags |= THQ_MODE_EXACT_W;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    Call c{ctx, w, x_dev, x_type, m, logits_dev ? static_cast<void*>(logits_dev) : static_cast<void*>(vals_dev),
+           THQ_ACT_F32, flags, false, s, nullptr};
+    int rc = check_call(c);
+    if (rc || m == 0) return rc;
+    if (!vals_dev || !idx_dev) return fail(THQ_EINVAL, "null vals_dev or idx_dev");
+    if (w->N > 0xFFFFFFFFll) return fail(THQ_ESHAPE, "N=%lld exceeds u32 indices", (long long)w->N);
+    DeviceGuard g(ctx->device);
+    // logits (workspace head unless the caller gives a buffer), then the
+    // route's scratch and the top-k candidates, reserved in one step
+    const Route r = plan_route(c);
+    const size_t lbytes = logits_dev ? 0 : round256((size_t)m * (size_t)w->N * sizeof(float));
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    rc = ensure_ws(ctx, lbytes + std::max(r.scratch, thq::topk_workspace_bytes(m, w->N, k)));
+    if (rc) return rc;
+    float* logits = logits_dev ? logits_dev : static_cast<float*>(ctx->ws);
+    void* scratch = static_cast<char*>(ctx->ws) + lbytes;
+    c.y = logits;
+    rc = exec_route(c, r, scratch);
+    if (rc) return rc;
+    hipError_t e = thq::launch_topk(logits, m, w->N, k, vals_dev, idx_dev, scratch, s);
+    if (e != hipSuccess) return fail(THQ_EHIP, "topk: %s", hipGetErrorString(e));
+    return THQ_OK;
+}
+
 int thq_matmul_argmax(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m,
                       float* logits_dev, uint32_t* idx_dev, uint32_t flags, void* stream) {
     if (flags & ~(THQ_MODE_EXACT_W | THQ_MODE_Q8ACT | THQ_MODE_ARGMAX_FUSED))

@@ -133,4 +133,9 @@ size_t argmax_partials_tmp_bytes(int64_t m, int64_t nb);
 hipError_t launch_argmax_partials(const float* v, const uint32_t* i, int64_t m, int64_t nb, int64_t ld,
                                   uint32_t* idx, void* tmp, hipStream_t s);
 
+// exact per-row top-k (k <= 64) by (logit desc, id asc), k_topk.hip
+size_t topk_workspace_bytes(int64_t m, int64_t n, int k);
+hipError_t launch_topk(const float* v, int64_t m, int64_t n, int k, float* vals, uint32_t* idx, void* ws,
+                       hipStream_t s);
+
 }  // namespace thq

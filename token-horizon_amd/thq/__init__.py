@@ -54,6 +54,7 @@ EXPORTS = (
     "thq_gguf_metadata_u32", "thq_gguf_metadata_f32", "thq_gguf_metadata_str", "thq_gguf_metadata_array",
     "thq_weight_from_gguf", "thq_q8act_bytes", "thq_q8act_prepare", "thq_matmul_q8act", "thq_gate_up_silu_q8act",
     "thq_plan_gemv_mfma", "thq_plan_gemm", "thq_matmul_noalloc", "thq_noalloc_scratch_bytes",
+    "thq_topk", "thq_matmul_topk",
 )
 
 
@@ -140,6 +141,8 @@ def _load():
         "thq_matmul_q8act": ([P, P, I, P, i64, i64, P, I, P], I),
         "thq_gate_up_silu_q8act": ([P, P, I, P, i64, i64, P, I, P], I),
         "thq_matmul_noalloc": ([P, P, P, I, i64, P, I, u32, P], I),
+        "thq_topk": ([P, P, i64, i64, I, P, P, P], I),
+        "thq_matmul_topk": ([P, P, P, I, i64, I, P, P, P, u32, P], I),
         "thq_noalloc_scratch_bytes": ([], C.c_size_t),
         "thq_plan_gemv_mfma": ([I, i64, i64, i64, I, C.POINTER(GemvPlanInfo)], I),
         "thq_plan_gemm": ([I, I, i64, i64, i64, I, I, C.POINTER(GemmPlanInfo)], I),
@@ -404,6 +407,30 @@ def argmax(v: torch.Tensor, ctx: Context | None = None) -> torch.Tensor:
     idx = torch.empty((m,), dtype=torch.int32, device=v.device)
     check(lib.thq_argmax(ctx.h, _ptr(v2), m, n, _ptr(idx), _stream()))
     return idx
+
+
+def topk(v: torch.Tensor, k: int, ctx: Context | None = None):
+    """Exact per-row top-k (logit desc, id asc); returns (vals f32 [M, k], idx int32 [M, k])."""
+    assert v.dtype == torch.float32 and v.is_contiguous()
+    ctx = ctx or Context.get(v.device.index or 0)
+    v2 = v if v.dim() == 2 else v.reshape(1, -1)
+    m, n = v2.shape
+    vals = torch.empty((m, k), dtype=torch.float32, device=v.device)
+    idx = torch.empty((m, k), dtype=torch.int32, device=v.device)
+    check(lib.thq_topk(ctx.h, _ptr(v2), m, n, k, _ptr(vals), _ptr(idx), _stream()))
+    return vals, idx
+
+
+def matmul_topk(w: QTensor, x: torch.Tensor, k: int, want_logits: bool = False, flags: int = 0):
+    """LM head + exact per-row top-k; returns (logits or None, vals, idx)."""
+    x2 = x.reshape(-1, x.shape[-1])
+    m = x2.shape[0]
+    logits = torch.empty((m, w.n), dtype=torch.float32, device=x.device) if want_logits else None
+    vals = torch.empty((m, k), dtype=torch.float32, device=x.device)
+    idx = torch.empty((m, k), dtype=torch.int32, device=x.device)
+    check(lib.thq_matmul_topk(w.ctx.h, w.h, _ptr(x2), _act(x2), m, k, _ptr(logits), _ptr(vals), _ptr(idx), flags,
+                              _stream()))
+    return logits, vals, idx
 
 
 class QMatMul:
