@@ -200,6 +200,22 @@ int thq_matmul_q8act(thq_ctx* ctx, const thq_weight* w, thq_dtype dot_type, cons
 int thq_gate_up_silu_q8act(thq_ctx* ctx, const thq_weight* fused, thq_dtype dot_type, const void* buf_dev,
                            int64_t m, int64_t k, void* y_dev, thq_act y_type, void* stream);
 
+/* thq_gate_up_silu_q8act that also emits the next projection's operand: the
+ * gate/up producer writes, besides y [M, H], the Q8_K activation buffer of y
+ * into next_buf_dev (thq_q8act_bytes(THQ_Q8_K, m, H) bytes, 256-byte
+ * aligned), byte-identical to thq_q8act_prepare(THQ_Q8_K, y, ...), so the
+ * down projection (thq_matmul_q8act with K = H) needs no quantize launch.
+ * The reference's gate/up tile likewise emits down's presum
+ * (engine/src/quant_kernel.rs:3205-3207; producers :265-274).  Q4_K
+ * [gate; up] weights with H a multiple of 256; y_dev 16-byte aligned.  The
+ * epilogue counts arriving blocks per 256-wide segment in a small counter
+ * buffer the context owns (allocated and zeroed on the first call of a
+ * larger shape; each launch leaves it zero), so such calls on one context
+ * must be ordered on one stream. */
+int thq_gate_up_silu_q8act_emit(thq_ctx* ctx, const thq_weight* fused, thq_dtype dot_type, const void* buf_dev,
+                                int64_t m, int64_t k, void* y_dev, thq_act y_type, void* next_buf_dev,
+                                void* stream);
+
 /* y[M, N] = x[M, K] . W^T with f32 accumulation.
  * Replaces QMatMul::forward ([ext] candle-core 0.11 quantized/mod.rs, called
  * for every projection by quantized_qwen3) and the engine's routed projection

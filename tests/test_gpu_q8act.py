@@ -219,3 +219,75 @@ def test_q8act_prepared_gate_up_and_errors():
     rc = thq.lib.thq_q8act_prepare(pre.ctx.h, thq.Q8_K, thq._ptr(xt), thq.ACT_BF16, m, k,
                                    thq.C.c_void_p(buf.data_ptr() + 16), None)
     assert rc == thq.EALIGN
+
+
+def q8k_planes(buf: torch.Tensor, m: int, k: int):
+    """(xq [m][k] i8, xd [m][k/256] f32, xb [m][k/32] i16) of an activation
+    buffer: the three planes, each starting on a 256-byte boundary."""
+    a = lambda b: (b + 255) // 256 * 256
+    raw = buf.cpu().numpy()
+    o1 = a(m * k)
+    o2 = o1 + a(m * (k // 256) * 4)
+    xq = raw[:m * k].view(np.int8).reshape(m, k)
+    xd = raw[o1:o1 + m * (k // 256) * 4].view(np.float32).reshape(m, k // 256)
+    xb = raw[o2:o2 + m * (k // 32) * 2].view(np.int16).reshape(m, k // 32)
+    return xq, xd, xb
+
+
+@pytest.mark.parametrize("h,k,ms", [(256, 512, (1, 3)), (1024, 1024, (9, 2)), (12288, 4096, (1, 8, 5)),
+                                    (2048, 1024, (40, 17))])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_gate_up_emits_down_operand(h, k, ms, out_dtype):
+    """The emitting gate/up (thq_gate_up_silu_q8act_emit) writes the same y
+    as the plain one and, as the next projection's operand, the Q8_K planes
+    of that y: byte-identical to thq_q8act_prepare(y) and to the oracle's
+    BlockQ8K::from_float of y.  Several M in a row on one context (the
+    arrival counters must come back to zero after each launch), and the down
+    projection consumes the emitted buffer exactly as a prepared one."""
+    fused = thq.QTensor.from_gguf_bytes(
+        thq.Q4_K, np.concatenate([weight_bytes(O.Q4_K, h, k, seed=31), weight_bytes(O.Q4_K, h, k, seed=32)]), 2 * h, k)
+    down = thq.QTensor.from_gguf_bytes(thq.Q4_K, weight_bytes(O.Q4_K, 384, h, seed=33), 384, h)
+    for m in ms:
+        print(f"emit h={h} k={k} m={m} {out_dtype}", flush=True)
+        x = torch.from_numpy(activations(m, k, seed=m)).cuda().to(torch.bfloat16)
+        a = thq.Q8Act(x, thq.Q8_K)
+        y_plain = a.gate_up_silu(fused, out_dtype)
+        y, nxt = a.gate_up_silu_emit(fused, out_dtype)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_plain)
+        prep = thq.Q8Act(y, thq.Q8_K)
+        got = q8k_planes(nxt.buf, m, h)
+        for g, w, name in zip(got, q8k_planes(prep.buf, m, h), ("xq", "xd", "xb")):
+            assert np.array_equal(g.view(np.uint8), w.view(np.uint8)), name
+        blocks = O.quantize_q8_k(y.float().cpu().numpy().ravel()).reshape(m, h // 256, 292)
+        assert np.array_equal(got[0].reshape(m, h // 256, 256).view(np.uint8), blocks[:, :, 4:260])
+        assert np.array_equal(got[1].reshape(m, h // 256), blocks[:, :, 0:4].copy().view(np.float32)[..., 0])
+        bs = blocks[:, :, 260:292].copy().view(np.int16).astype(np.int32).reshape(m, h // 256, 8, 2).sum(axis=3)
+        assert np.array_equal(got[2].reshape(m, h // 256, 8).astype(np.int32), bs)
+        assert torch.equal(nxt.matmul(down), prep.matmul(down))
+
+
+def test_gate_up_emit_errors():
+    L = thq.lib
+    ctx = thq.Context.get(0).h
+    k = 512
+    odd = thq.QTensor.from_gguf_bytes(thq.Q4_K, weight_bytes(O.Q4_K, 2 * 200, k, seed=34), 2 * 200, k)
+    q8 = thq.QTensor.from_gguf_bytes(thq.Q8_0, weight_bytes(O.Q8_0, 512, k, seed=35), 512, k)
+    x = torch.zeros((2, k), dtype=torch.bfloat16, device="cuda")
+    a = thq.Q8Act(x, thq.Q8_K)
+    y = torch.zeros((2, 256), dtype=torch.bfloat16, device="cuda")
+    nb = torch.zeros(1 << 16, dtype=torch.uint8, device="cuda")
+    P = lambda t: t.data_ptr()
+    assert L.thq_gate_up_silu_q8act_emit(ctx, odd.h, thq.Q8_K, P(a.buf), 2, k, P(y), thq.ACT_BF16, P(nb),
+                                         None) == thq.ESHAPE  # 200 outputs: not a multiple of 256
+    assert L.thq_gate_up_silu_q8act_emit(ctx, q8.h, thq.Q8_K, P(a.buf), 2, k, P(y), thq.ACT_BF16, P(nb),
+                                         None) == thq.EDTYPE
+    ok = thq.QTensor.from_gguf_bytes(thq.Q4_K, weight_bytes(O.Q4_K, 2 * 256, k, seed=36), 2 * 256, k)
+    assert L.thq_gate_up_silu_q8act_emit(ctx, ok.h, thq.Q8_K, P(a.buf), 2, k, P(y), thq.ACT_BF16, P(nb) + 16,
+                                         None) == thq.EALIGN
+    assert L.thq_gate_up_silu_q8act_emit(ctx, ok.h, thq.Q8_K, P(a.buf), 2, k, P(y), thq.ACT_BF16, None,
+                                         None) == thq.EINVAL
+    assert L.thq_gate_up_silu_q8act_emit(ctx, ok.h, thq.Q8_0, P(a.buf), 2, k, P(y), thq.ACT_BF16, P(nb),
+                                         None) == thq.EDTYPE  # Q4_K dots with Q8_K activations
+    assert L.thq_gate_up_silu_q8act_emit(ctx, ok.h, thq.Q8_K, P(a.buf), 2, k, P(y), thq.ACT_BF16, P(nb),
+                                         None) == thq.OK

@@ -145,15 +145,15 @@ __global__ __launch_bounds__(256) void k_quant_act_q8_0(const XT* __restrict__ x
 // on equal magnitudes (NaN never wins); amax == 0 gives d = 0 and zero
 // quants; else iscale = -128 / max, q = min(round(iscale * x), 127) as i8,
 // d = 1 / iscale, bsums = sums of 16 quants.
-template <typename XT, bool GGUF>
-__global__ __launch_bounds__(256) void k_quant_act_q8k(const XT* __restrict__ x, int64_t nblk, int8_t* __restrict__ xq,
-                                                       float* __restrict__ xd, int16_t* __restrict__ xb,
-                                                       uint8_t* __restrict__ blk) {
-    const int lane = threadIdx.x & 63;
-    const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (b >= nblk) return;  // the whole wave
-    float v[4];
-    load4(x + b * 256 + 4 * lane, v);
+struct Q8KLane {
+    uint32_t q;  // the lane's four quants (bytes)
+    float d;     // the block's d
+    int s16;     // sum of the 16 quants of lanes 4j .. 4j+3 (every lane of the quad)
+    int s32;     // sum of the 32 quants of lanes 8j .. 8j+7 (every lane of the octet)
+};
+
+// one wave quantizes one 256-wide block, lane l holding values 4l .. 4l+3
+__device__ __forceinline__ Q8KLane q8k_wave(const float (&v)[4], int lane) {
     float key = -1.0f, val = 0.0f;
     int idx = 0;
 #pragma unroll
@@ -175,18 +175,35 @@ __global__ __launch_bounds__(256) void k_quant_act_q8k(const XT* __restrict__ x,
             val = ov;
         }
     }
-    uint32_t q = 0;
-    float d = 0.0f;
+    Q8KLane r;
+    r.q = 0;
+    r.d = 0.0f;
     if (key > 0.0f) {
         const float iscale = -128.0f / val;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) q |= as_i8_bits(fminf(roundf(iscale * v[i]), 127.0f)) << (8 * i);
-        d = 1.0f / iscale;
+        for (int i = 0; i < 4; ++i) r.q |= as_i8_bits(fminf(roundf(iscale * v[i]), 127.0f)) << (8 * i);
+        r.d = 1.0f / iscale;
     }
-    int s = (int)(int8_t)(q & 0xFFu) + (int)(int8_t)((q >> 8) & 0xFFu) + (int)(int8_t)((q >> 16) & 0xFFu) +
-            (int)(int8_t)(q >> 24);
-    s = quad_sum(s);  // 16 quants: lanes 4j .. 4j+3
-    const int s32 = s + __shfl_xor(s, 4, 64);
+    int s = (int)(int8_t)(r.q & 0xFFu) + (int)(int8_t)((r.q >> 8) & 0xFFu) + (int)(int8_t)((r.q >> 16) & 0xFFu) +
+            (int)(int8_t)(r.q >> 24);
+    r.s16 = quad_sum(s);  // 16 quants: lanes 4j .. 4j+3
+    r.s32 = r.s16 + __shfl_xor(r.s16, 4, 64);
+    return r;
+}
+
+template <typename XT, bool GGUF>
+__global__ __launch_bounds__(256) void k_quant_act_q8k(const XT* __restrict__ x, int64_t nblk, int8_t* __restrict__ xq,
+                                                       float* __restrict__ xd, int16_t* __restrict__ xb,
+                                                       uint8_t* __restrict__ blk) {
+    const int lane = threadIdx.x & 63;
+    const int64_t b = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (b >= nblk) return;  // the whole wave
+    float v[4];
+    load4(x + b * 256 + 4 * lane, v);
+    const Q8KLane r = q8k_wave(v, lane);
+    const uint32_t q = r.q;
+    const float d = r.d;
+    const int s = r.s16, s32 = r.s32;
     if constexpr (GGUF) {
         uint8_t* p = blk + b * 292;  // 4-B aligned blocks
         if (lane == 0) *reinterpret_cast<float*>(p) = d;
@@ -242,11 +259,23 @@ __device__ __forceinline__ void q8act_store(float (&acc)[(GU ? 8 : 4) * MT], int
 // LDS: x [MT][K/16] 16-B pieces (piece 4u + t of lane unit u at slot
 // 4u + ((t + u/4) & 3), so a lane's four reads hit distinct banks), the
 // 32-sum pairs [MT][K/64] u32 and d [MT][K/256] f32.
-template <int MT, bool GU, typename YT>
+//
+// EMIT (gate/up, nout a multiple of 256): the producer also writes the
+// next projection's operand, the Q8_K planes of its own output y
+// (xq [M][nout] i8, xd [M][nout/256] f32, xb [M][nout/32] i16, as
+// thq_q8act_prepare writes them for x = y).  A block covers 16 outputs, so
+// 16 blocks share one 256-wide Q8_K block of each row.  Each block stores
+// its outputs, then takes a ticket on the counter of its (row tile,
+// 256-wide segment); the 16th block to arrive reads the segment of y back
+// (device-scope release before the ticket, acquire after it) and quantizes
+// it, one wave per row, then resets the counter to 0 for the next launch.
+// No block waits on another.
+template <int MT, bool GU, typename YT, bool EMIT = false>
 __global__ __launch_bounds__(256) void k_q8act_q4k(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
                                                    const float* __restrict__ xd, const int16_t* __restrict__ xb,
                                                    YT* __restrict__ y, int M, int64_t nout, int K, int64_t up_off,
-                                                   int64_t ldy) {
+                                                   int64_t ldy, uint32_t* __restrict__ cnt, int8_t* __restrict__ oq,
+                                                   float* __restrict__ od, int16_t* __restrict__ ob) {
     constexpr int NR = GU ? 8 : 4;
     extern __shared__ uint4 lds4[];
     const int nsb = K >> 8, nu = K >> 6, npc = K >> 4;
@@ -342,6 +371,32 @@ __global__ __launch_bounds__(256) void k_q8act_q4k(const uint8_t* __restrict__ W
 #pragma unroll
     for (int i = 0; i < NR * MT; ++i) acc[i] = p == 0 ? acc[i] : 0.0f;  // one lane per quad
     q8act_store<MT, GU, YT>(acc, lane, y, o0, nout, m0, mrows, ldy);
+    if constexpr (EMIT) {
+        __shared__ int last;
+        const int64_t seg = blockIdx.x >> 4;  // 256-wide segment of the outputs
+        uint32_t* c = cnt + (int64_t)blockIdx.y * (nout >> 8) + seg;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            __threadfence();  // this block's outputs, before its ticket
+            last = atomicAdd(c, 1u) == 15u;
+        }
+        __syncthreads();
+        if (last) {
+            __threadfence();  // the other 15 blocks' outputs
+            const int wave = threadIdx.x >> 6;
+            const int nsb = (int)(nout >> 8);
+            for (int m = wave; m < mrows; m += 4) {
+                const int64_t row = m0 + m;
+                float v[4];
+                load4(y + row * ldy + seg * 256 + 4 * lane, v);
+                const Q8KLane r = q8k_wave(v, lane);
+                reinterpret_cast<uint32_t*>(oq + row * nout + seg * 256)[lane] = r.q;
+                if (lane == 0) od[row * nsb + seg] = r.d;
+                if ((lane & 7) == 0) ob[row * (nout >> 5) + seg * 8 + (lane >> 3)] = (int16_t)r.s32;
+            }
+            if (threadIdx.x == 0) *c = 0u;  // zero again for the next launch
+        }
+    }
 }
 
 // Q8_0 weights x Q8_0 activations ([ext] BlockQ8_0::vec_dot: per block
@@ -476,7 +531,7 @@ void launch_dot(const WeightView& w, const ActPlanes& a, YT* y, int M, int64_t n
     const size_t lds = lds_bytes(w.qtype, MT, K);
     if (w.qtype == 12)
         hipLaunchKernelGGL((k_q8act_q4k<MT, GU, YT>), grid, dim3(256), lds, s, w.q, a.xq, a.xd, a.xb, y, M, nout, K,
-                           up_off, nout);
+                           up_off, nout, (uint32_t*)nullptr, (int8_t*)nullptr, (float*)nullptr, (int16_t*)nullptr);
     else
         hipLaunchKernelGGL((k_q8act_q8_0<MT, GU, YT>), grid, dim3(256), lds, s, reinterpret_cast<const int8_t*>(w.q),
                            reinterpret_cast<const uint16_t*>(w.aux), a.xq, a.xd, y, M, nout, K, up_off, nout);
@@ -493,7 +548,41 @@ void launch_dot_mt(int mt, const WeightView& w, const ActPlanes& a, YT* y, int M
     }
 }
 
+template <int MT, typename YT>
+void launch_emit(const WeightView& w, const ActPlanes& a, YT* y, int M, int64_t nout, uint32_t* cnt,
+                 const ActPlanes& o, hipStream_t s) {
+    const int K = (int)w.K;
+    const int64_t waves = (nout + 3) / 4;
+    const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)((M + MT - 1) / MT));
+    hipLaunchKernelGGL((k_q8act_q4k<MT, true, YT, true>), grid, dim3(256), lds_bytes(12, MT, K), s, w.q, a.xq, a.xd,
+                       a.xb, y, M, nout, K, nout, nout, cnt, o.xq, o.xd, o.xb);
+}
+
 }  // namespace
+
+size_t q8act_emit_counters(int64_t M, int64_t K, int64_t nout) {
+    const int mt = pick_mt(12, M, (int)K);
+    return (size_t)((M + mt - 1) / mt) * (size_t)(nout / 256);
+}
+
+hipError_t launch_q8act_dot_emit(const WeightView& w, const void* planes, void* y, bool yf32, int M, int64_t nout,
+                                 uint32_t* counters, void* out_planes, hipStream_t s) {
+    if (w.qtype != 12 || nout % 256) return hipErrorInvalidValue;
+    const ActPlanes a = act_planes(12, const_cast<void*>(planes), M, w.K);
+    const ActPlanes o = act_planes(12, out_planes, M, nout);
+    const int mt = pick_mt(12, M, (int)w.K);
+#define THQ_E(MT_)                                                                                                \
+    (yf32 ? launch_emit<MT_, float>(w, a, static_cast<float*>(y), M, nout, counters, o, s)                       \
+          : launch_emit<MT_, bf16_t>(w, a, static_cast<bf16_t*>(y), M, nout, counters, o, s))
+    switch (mt) {
+        case 8: THQ_E(8); break;
+        case 4: THQ_E(4); break;
+        case 2: THQ_E(2); break;
+        default: THQ_E(1); break;
+    }
+#undef THQ_E
+    return hipGetLastError();
+}
 
 bool q8act_supported(int qtype, int64_t K) { return lds_bytes(qtype, 1, (int)K) <= kLdsCap; }
 

@@ -40,6 +40,10 @@ struct thq_ctx {
     // buffers the workspace outgrew: kernels already enqueued (or captured in
     // a graph) may still use them, so they live until thq_destroy
     std::vector<void*> retired;
+    // arrival counters of the emitting gate/up epilogue: zero between launches
+    // (each launch leaves them zero); grown like the workspace
+    uint32_t* emit_cnt = nullptr;
+    size_t emit_cnt_n = 0;
 };
 
 struct thq_weight {
@@ -421,6 +425,11 @@ void thq_destroy(thq_ctx* ctx) {
         (void)hipDeviceSynchronize();
         (void)hipFree(ctx->ws);
         for (void* p : ctx->retired) (void)hipFree(p);
+    }
+    if (ctx->emit_cnt) {
+        DeviceGuard g(ctx->device);
+        (void)hipDeviceSynchronize();
+        (void)hipFree(ctx->emit_cnt);
     }
     delete ctx;
 }
@@ -809,6 +818,48 @@ int run_q8act_dot(thq_ctx* ctx, const thq_weight* w, thq_dtype dot_type, const v
 }
 
 }  // namespace
+
+int thq_gate_up_silu_q8act_emit(thq_ctx* ctx, const thq_weight* fused, thq_dtype dot_type, const void* buf_dev,
+                                int64_t m, int64_t k, void* y_dev, thq_act y_type, void* next_buf_dev, void* stream) {
+    if (!ctx || !fused || !buf_dev || !next_buf_dev) return fail(THQ_EINVAL, "null argument");
+    if (fused->qtype != THQ_Q4_K) return fail(THQ_EDTYPE, "the emitting gate/up takes Q4_K weights");
+    if (fused->N % 512) return fail(THQ_ESHAPE, "gate/up outputs %lld: a multiple of 256 per half is needed",
+                                    (long long)(fused->N / 2));
+    if ((uintptr_t)next_buf_dev & 255u) return fail(THQ_EALIGN, "next_buf_dev must be 256-byte aligned");
+    if ((uintptr_t)y_dev & 15u) return fail(THQ_EALIGN, "y_dev must be 16-byte aligned");
+    const int64_t nout = fused->N / 2;
+    if (!thq::q8act_supported(12, nout)) return fail(THQ_ESHAPE, "the next projection's K=%lld is too large",
+                                                    (long long)nout);
+    // the shared checks (dot type, K, y type, M) of the non-emitting call
+    if (m < 0 || m > (1 << 24)) return fail(THQ_ESHAPE, "M=%lld out of range", (long long)m);
+    if (dot_type != THQ_Q8_K) return fail(THQ_EDTYPE, "buffer dot type %d, the weight's is %d", dot_type, THQ_Q8_K);
+    if (k != fused->K) return fail(THQ_ESHAPE, "buffer K=%lld, weight K=%lld", (long long)k, (long long)fused->K);
+    if (y_type != THQ_ACT_F32 && y_type != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad y_type %d", y_type);
+    if ((uintptr_t)buf_dev & 255u) return fail(THQ_EALIGN, "buf_dev must be 256-byte aligned");
+    if (m == 0) return THQ_OK;
+    if (!y_dev) return fail(THQ_EINVAL, "null y");
+    DeviceGuard g(ctx->device);
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    const size_t need = thq::q8act_emit_counters(m, fused->K, nout);
+    if (need > ctx->emit_cnt_n) {
+        // zeroed once here; every launch leaves them zero again
+        size_t want = std::max(need + need / 8, 2 * ctx->emit_cnt_n);
+        uint32_t* p = nullptr;
+        hipError_t e = hipMalloc((void**)&p, want * sizeof(uint32_t));
+        if (e == hipSuccess) e = hipMemset(p, 0, want * sizeof(uint32_t));
+        if (e != hipSuccess) {
+            if (p) (void)hipFree(p);
+            return fail(THQ_ENOMEM, "emit counters (%zu): %s", want, hipGetErrorString(e));
+        }
+        if (ctx->emit_cnt) ctx->retired.push_back(ctx->emit_cnt);
+        ctx->emit_cnt = p;
+        ctx->emit_cnt_n = want;
+    }
+    hipError_t e = thq::launch_q8act_dot_emit(view(fused), buf_dev, y_dev, y_type == THQ_ACT_F32, (int)m, nout,
+                                              ctx->emit_cnt, next_buf_dev, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return fail(THQ_EHIP, "kernel launch: %s", hipGetErrorString(e));
+    return THQ_OK;
+}
 
 int thq_matmul_q8act(thq_ctx* ctx, const thq_weight* w, thq_dtype dot_type, const void* buf_dev, int64_t m, int64_t k,
                      void* y_dev, thq_act y_type, void* stream) {

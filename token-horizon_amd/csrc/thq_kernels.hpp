@@ -120,6 +120,12 @@ hipError_t launch_q8act_prepare(int qtype, const void* x, bool xf32, int64_t M, 
                                 hipStream_t s);
 hipError_t launch_q8act_dot(const WeightView& w, const void* planes, void* y, bool yf32, bool gu, int M, int64_t nout,
                             int64_t up_off, hipStream_t s);
+// Q4_K gate/up over Q8_K planes that also emits the Q8_K planes of its own
+// output y [M][nout] (nout % 256 == 0) into out_planes; counters: zeroed u32
+// [q8act_emit_counters(M, K, nout)], zero again when the launch completes
+size_t q8act_emit_counters(int64_t M, int64_t K, int64_t nout);
+hipError_t launch_q8act_dot_emit(const WeightView& w, const void* planes, void* y, bool yf32, int M, int64_t nout,
+                                 uint32_t* counters, void* out_planes, hipStream_t s);
 // GGML blocks of the dot type (qtype 8 -> Q8_0 blocks, 12 -> Q8_K blocks)
 hipError_t launch_quantize_act(int qtype, const void* x, bool xf32, int64_t M, int64_t K, void* blocks,
                                hipStream_t s);

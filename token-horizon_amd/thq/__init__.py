@@ -54,7 +54,7 @@ EXPORTS = (
     "thq_gguf_metadata_u32", "thq_gguf_metadata_f32", "thq_gguf_metadata_str", "thq_gguf_metadata_array",
     "thq_weight_from_gguf", "thq_q8act_bytes", "thq_q8act_prepare", "thq_matmul_q8act", "thq_gate_up_silu_q8act",
     "thq_plan_gemv_mfma", "thq_plan_gemm", "thq_matmul_noalloc", "thq_noalloc_scratch_bytes",
-    "thq_topk", "thq_matmul_topk",
+    "thq_topk", "thq_matmul_topk", "thq_gate_up_silu_q8act_emit",
 )
 
 
@@ -142,6 +142,7 @@ def _load():
         "thq_gate_up_silu_q8act": ([P, P, I, P, i64, i64, P, I, P], I),
         "thq_matmul_noalloc": ([P, P, P, I, i64, P, I, u32, P], I),
         "thq_topk": ([P, P, i64, i64, I, P, P, P], I),
+        "thq_gate_up_silu_q8act_emit": ([P, P, I, P, i64, i64, P, I, P, P], I),
         "thq_matmul_topk": ([P, P, P, I, i64, I, P, P, P, u32, P], I),
         "thq_noalloc_scratch_bytes": ([], C.c_size_t),
         "thq_plan_gemv_mfma": ([I, i64, i64, i64, I, C.POINTER(GemvPlanInfo)], I),
@@ -348,6 +349,18 @@ class Q8Act:
         check(lib.thq_gate_up_silu_q8act(self.ctx.h, fused.h, self.dot_type, _ptr(self.buf), self.m, self.k,
                                          _ptr(y), _act(y), _stream()))
         return y
+
+    def gate_up_silu_emit(self, fused: "QTensor", out_dtype=torch.bfloat16):
+        """(y, the Q8Act of y) from one launch (thq_gate_up_silu_q8act_emit):
+        the down projection's operand comes out of the gate/up epilogue."""
+        h = fused.n // 2
+        y = torch.empty((self.m, h), dtype=out_dtype, device=self.buf.device)
+        nxt = Q8Act.__new__(Q8Act)
+        nxt.ctx, nxt.m, nxt.k, nxt.dot_type = self.ctx, self.m, h, Q8_K
+        nxt.buf = torch.empty(lib.thq_q8act_bytes(Q8_K, self.m, h), dtype=torch.uint8, device=self.buf.device)
+        check(lib.thq_gate_up_silu_q8act_emit(self.ctx.h, fused.h, self.dot_type, _ptr(self.buf), self.m, self.k,
+                                              _ptr(y), _act(y), _ptr(nxt.buf), _stream()))
+        return y, nxt
 
 
 def matmul(w: QTensor, x: torch.Tensor, out_dtype=torch.float32, flags: int = 0, out: torch.Tensor | None = None):
