@@ -231,7 +231,20 @@ __device__ __forceinline__ void wave_rows(int64_t (&rows)[GU ? 8 : 4], int64_t o
     }
 }
 
-template <int MT, bool GU, typename YT>
+// y[i] = v with a device-scope (agent) relaxed atomic store: written through
+// to the device's coherence point, so another XCD can read it back with
+// device-scope loads and no cache write-back or invalidation is needed
+template <typename YT>
+__device__ __forceinline__ void store_y_device(YT* p, float v) {
+    if constexpr (sizeof(YT) == 4) {
+        __hip_atomic_store(reinterpret_cast<float*>(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        __hip_atomic_store(reinterpret_cast<uint16_t*>(p), (uint16_t)f32_to_bf16(v), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+template <int MT, bool GU, typename YT, bool COH = false>
 __device__ __forceinline__ void q8act_store(float (&acc)[(GU ? 8 : 4) * MT], int lane, YT* __restrict__ y, int64_t o0,
                                             int64_t nout, int m0, int mrows, int64_t ldy) {
     constexpr int NV = (GU ? 8 : 4) * MT;
@@ -243,7 +256,12 @@ __device__ __forceinline__ void q8act_store(float (&acc)[(GU ? 8 : 4) * MT], int
     if constexpr (GU) {
         const float u = __shfl_xor(tot, 32, 64);  // up slot = gate slot + NV/2
         if ((lane & (SPAN - 1)) || (lane & 32)) return;
-        if (m < mrows && o0 + r < nout) store_y<YT>(y + (int64_t)(m0 + m) * ldy + o0 + r, silu_mul(tot, u));
+        if (m < mrows && o0 + r < nout) {
+            if constexpr (COH)
+                store_y_device<YT>(y + (int64_t)(m0 + m) * ldy + o0 + r, silu_mul(tot, u));
+            else
+                store_y<YT>(y + (int64_t)(m0 + m) * ldy + o0 + r, silu_mul(tot, u));
+        }
     } else {
         if (lane & (SPAN - 1)) return;
         if (m < mrows && o0 + r < nout) store_y<YT>(y + (int64_t)(m0 + m) * ldy + o0 + r, tot);
@@ -265,11 +283,14 @@ __device__ __forceinline__ void q8act_store(float (&acc)[(GU ? 8 : 4) * MT], int
 // (xq [M][nout] i8, xd [M][nout/256] f32, xb [M][nout/32] i16, as
 // thq_q8act_prepare writes them for x = y).  A block covers 16 outputs, so
 // 16 blocks share one 256-wide Q8_K block of each row.  Each block stores
-// its outputs, then takes a ticket on the counter of its (row tile,
-// 256-wide segment); the 16th block to arrive reads the segment of y back
-// (device-scope release before the ticket, acquire after it) and quantizes
+// its outputs with device-scope stores (written through to the coherence
+// point shared by all XCDs), waits for them to complete, then takes a ticket
+// on the counter of its (row tile, 256-wide segment); the 16th block to
+// arrive reads the segment of y back with device-scope loads and quantizes
 // it, one wave per row, then resets the counter to 0 for the next launch.
-// No block waits on another.
+// No block waits on another, and no cache is written back or invalidated
+// (a device-scope fence per block, which writes back the whole L2, made the
+// layer 2.4x slower).
 template <int MT, bool GU, typename YT, bool EMIT = false>
 __global__ __launch_bounds__(256) void k_q8act_q4k(const uint8_t* __restrict__ W, const int8_t* __restrict__ xq,
                                                    const float* __restrict__ xd, const int16_t* __restrict__ xb,
@@ -370,31 +391,45 @@ __global__ __launch_bounds__(256) void k_q8act_q4k(const uint8_t* __restrict__ W
     }
 #pragma unroll
     for (int i = 0; i < NR * MT; ++i) acc[i] = p == 0 ? acc[i] : 0.0f;  // one lane per quad
-    q8act_store<MT, GU, YT>(acc, lane, y, o0, nout, m0, mrows, ldy);
+    q8act_store<MT, GU, YT, EMIT>(acc, lane, y, o0, nout, m0, mrows, ldy);
     if constexpr (EMIT) {
+        // the outputs went out as device-scope stores: once they have
+        // completed (vmcnt 0), the ticket (a device-scope atomic) is ordered
+        // after them, and the last block's device-scope loads see them
         __shared__ int last;
         const int64_t seg = blockIdx.x >> 4;  // 256-wide segment of the outputs
         uint32_t* c = cnt + (int64_t)blockIdx.y * (nout >> 8) + seg;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (threadIdx.x == 0) {
-            __threadfence();  // this block's outputs, before its ticket
-            last = atomicAdd(c, 1u) == 15u;
-        }
+        if (threadIdx.x == 0) last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 15u;
         __syncthreads();
         if (last) {
-            __threadfence();  // the other 15 blocks' outputs
             const int wave = threadIdx.x >> 6;
             const int nsb = (int)(nout >> 8);
             for (int m = wave; m < mrows; m += 4) {
                 const int64_t row = m0 + m;
                 float v[4];
-                load4(y + row * ldy + seg * 256 + 4 * lane, v);
+                const YT* src = y + row * ldy + seg * 256 + 4 * lane;
+                if constexpr (sizeof(YT) == 4) {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        v[i] = __hip_atomic_load(reinterpret_cast<const float*>(src) + i, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) {
+                        const uint32_t t = __hip_atomic_load(reinterpret_cast<const uint32_t*>(src) + i,
+                                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        v[2 * i] = bf16_to_f32(t & 0xFFFFu);
+                        v[2 * i + 1] = bf16_to_f32(t >> 16);
+                    }
+                }
                 const Q8KLane r = q8k_wave(v, lane);
                 reinterpret_cast<uint32_t*>(oq + row * nout + seg * 256)[lane] = r.q;
                 if (lane == 0) od[row * nsb + seg] = r.d;
                 if ((lane & 7) == 0) ob[row * (nout >> 5) + seg * 8 + (lane >> 3)] = (int16_t)r.s32;
             }
-            if (threadIdx.x == 0) *c = 0u;  // zero again for the next launch
+            if (threadIdx.x == 0) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // for the next launch
         }
     }
 }
