@@ -16,7 +16,7 @@ import pytest
 import torch
 
 import oracle as O
-from helpers import activations, q6k_bytes, rand_qlin_fast, rel_row_err, weight_bytes
+from helpers import activations, assert_close_elem, q6k_bytes, rand_qlin_fast, rel_row_err, weight_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -201,3 +201,38 @@ def test_bf16_out_and_f32_gate_up_every_route(qtype):
                 want = O.bf16_bits_to_f32(O.gate_up_silu(ref))
                 run_case(f"f32 gate/up q{qtype} {h}x{k} m={m}",
                          thq.gate_up_silu(w, xd, torch.float32).cpu().numpy(), want, 1e-2)
+
+
+@pytest.mark.parametrize("kind", ["q4_k", "q6_k", "affine"])
+def test_exact_weights_past_sixteen_rows(kind):
+    """THQ_MODE_EXACT_W (the LM head's mode) with 4- / 6-bit weights at
+    M = 17..64: the exact decode GEMV over groups of 16 rows (the GEMMs round
+    these weights to bf16).  Exact weights leave only f32 summation error,
+    so the bar is the f32 one (1e-4 of the row norm); gate/up and argmax
+    through the same route."""
+    n, k = 1000, 1024
+    if kind == "affine":
+        wq, sb = rand_qlin_fast(n, k, seed=301)
+        w = thq.QTensor.from_affine(wq, sb, n, k)
+        ref_of = lambda xf: O.affine_matmul(wq, sb, n, k, xf)
+    else:
+        qtype = O.Q4_K if kind == "q4_k" else O.Q6_K
+        b, w = gguf_weight(qtype, n, k, seed=302)
+        ref_of = lambda xf: O.matmul(qtype, b, n, k, xf)
+    for m in (17, 31, 32, 33, 40, 64):
+        print(f"[sweep] exact {kind} {n}x{k} m={m}", flush=True)
+        xf = O.bf16_round(activations(m, k, seed=400 + m))
+        xb = torch.from_numpy(xf).cuda().to(torch.bfloat16)
+        ref = ref_of(xf)
+        got = thq.matmul(w, xb, torch.float32, flags=thq.MODE_EXACT_W).cpu().numpy()
+        run_case(f"exact {kind} m={m}", got, ref, 1e-4)
+        logits, idx = thq.matmul_argmax(w, xb)
+        torch.cuda.synchronize()
+        lg = logits.cpu().numpy()
+        run_case(f"exact {kind} argmax logits m={m}", lg, ref, 1e-4)
+        assert list(idx.cpu().numpy()) == list(O.argmax_rows(lg))
+        if m in (17, 40):
+            gu = thq.gate_up_silu(w, xb, torch.float32, flags=thq.MODE_EXACT_W).cpu().numpy()
+            want = O.bf16_bits_to_f32(O.gate_up_silu(got))
+            # the epilogue over the route's own (exact) gate/up values: at most one bf16 step apart
+            assert_close_elem(f"gate/up {kind} m={m}", gu, want, 2.0 ** -7)

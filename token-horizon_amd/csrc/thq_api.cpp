@@ -260,10 +260,11 @@ int check_call(const Call& c) {
 
 // The kernels a call runs, and the device scratch (split-K partials or the
 // quantized activation planes) they use, known before anything launches.
-enum class Kind { NONE, Q8ACT, GEMV1, ROWS, GEMV_MFMA, GEMM, GENERIC };
+enum class Kind { NONE, Q8ACT, GEMV1, ROWS, GEMV_MFMA, GEMV_MFMA_GROUPS, GEMM, GENERIC };
 struct Route {
     Kind kind = Kind::NONE;
     thq::GemvPlan gp;
+    thq::GemvPlan gp_last;  // GEMV_MFMA_GROUPS: the plan of the last, partial group of rows
     thq::GemmPlan gm;
     bool exact = false;
     size_t scratch = 0;
@@ -336,6 +337,18 @@ Route plan_route(const Call& c) {
         r.exact = (c.flags & THQ_MODE_EXACT_W) || (w->qtype == THQ_Q8_0 && m <= 64);
         r.gm = thq::plan_gemm(v.qtype, r.exact, m, w->N, w->K, c.gu, c.ctx->cus);
         r.scratch = r.gm.workspace_bytes;
+    } else if (!xf32 && aligned16(c.x) && (q4 || q6) && m > 16 && w->K % 256 == 0 &&
+               thq::plan_gemv_mfma(v.qtype, 16, w->N, w->K, c.gu).waves > 0) {
+        // exact 4- / 6-bit weights past the decode GEMV's 16 rows (the verify
+        // LM head of batched drafts; the GEMMs round these weights to bf16):
+        // the exact decode GEMV over groups of 16 rows, each group streaming
+        // the weights again (Q6_K 151936 x 4096, M = 40: 3 groups against
+        // the generic kernel's 3.4 ms)
+        r.kind = Kind::GEMV_MFMA_GROUPS;
+        r.gp = thq::plan_gemv_mfma(v.qtype, 16, w->N, w->K, c.gu);
+        r.gp_last = (m % 16) ? thq::plan_gemv_mfma(v.qtype, m % 16, w->N, w->K, c.gu) : r.gp;
+        r.scratch = std::max(r.gp.workspace_bytes, r.gp_last.workspace_bytes);
+        if (!r.gp_last.waves) r.kind = Kind::GENERIC;
     } else {
         r.kind = Kind::GENERIC;
     }
@@ -362,6 +375,17 @@ int exec_route(const Call& c, const Route& r, void* scratch) {
             e = thq::launch_gemv_mfma(r.gp, v, c.x, c.y, yf32, c.gu, m, nout, up_off, static_cast<float*>(scratch),
                                       c.s, c.am);
             break;
+        case Kind::GEMV_MFMA_GROUPS: {
+            // groups run in stream order, so they share the scratch
+            const size_t xrow = (size_t)w->K * (xf32 ? 4 : 2), yrow = (size_t)nout * (yf32 ? 4 : 2);
+            for (int r0 = 0; r0 < m && e == hipSuccess; r0 += 16) {
+                const int mm = m - r0 < 16 ? m - r0 : 16;
+                e = thq::launch_gemv_mfma(mm == 16 ? r.gp : r.gp_last, v, static_cast<const char*>(c.x) + r0 * xrow,
+                                          static_cast<char*>(c.y) + r0 * yrow, yf32, c.gu, mm, nout, up_off,
+                                          static_cast<float*>(scratch), c.s, nullptr);
+            }
+            break;
+        }
         case Kind::GEMM:
             e = thq::launch_gemm(r.gm, v, c.x, c.y, yf32, c.gu, r.exact, m, static_cast<float*>(scratch), c.s);
             break;
