@@ -18,6 +18,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "thq.h"
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -54,6 +56,14 @@ typedef struct thq_gemm_plan_info {
 
 int thq_plan_gemm(int dtype, int exact, int64_t m, int64_t n, int64_t k, int gate_up, int cus,
                   thq_gemm_plan_info* out);
+
+/* Measurement aid: read `bytes` (a multiple of 16) of buf_dev (16-byte
+ * aligned) once with 16-B loads from `blocks` blocks of 256 threads, on
+ * `stream`; sink_dev (4 bytes) is written only in the unlikely case the
+ * XOR of the data is a fixed constant.  bench.py times it beside the decode
+ * GEMV, launched the same way over the same byte count: the single-launch
+ * HBM read ceiling that kernel is compared against. */
+int thq_probe_hbm_read(thq_ctx* ctx, const void* buf_dev, size_t bytes, int blocks, uint32_t* sink_dev, void* stream);
 
 #ifdef __cplusplus
 }
