@@ -205,11 +205,11 @@ def test_bf16_out_and_f32_gate_up_every_route(qtype):
 
 @pytest.mark.parametrize("kind", ["q4_k", "q6_k", "affine"])
 def test_exact_weights_past_sixteen_rows(kind):
-    """THQ_MODE_EXACT_W (the LM head's mode) with 4- / 6-bit weights at
-    M = 17..64: the exact decode GEMV over groups of 16 rows (the GEMMs round
-    these weights to bf16).  Exact weights leave only f32 summation error,
-    so the bar is the f32 one (1e-4 of the row norm); gate/up and argmax
-    through the same route."""
+    """THQ_MODE_EXACT_W (the LM head's mode) with 4- / 6-bit weights past 16
+    rows (the GEMMs round these weights to bf16): the wide exact GEMV at
+    M = 17..64, the decode GEMV over groups of 16 rows beyond.  Exact weights
+    leave only f32 summation error, so the bar is the f32 one (1e-4 of the
+    row norm); gate/up and argmax through the same route."""
     n, k = 1000, 1024
     if kind == "affine":
         wq, sb = rand_qlin_fast(n, k, seed=301)
@@ -219,7 +219,7 @@ def test_exact_weights_past_sixteen_rows(kind):
         qtype = O.Q4_K if kind == "q4_k" else O.Q6_K
         b, w = gguf_weight(qtype, n, k, seed=302)
         ref_of = lambda xf: O.matmul(qtype, b, n, k, xf)
-    for m in (17, 31, 32, 33, 40, 64):
+    for m in (17, 31, 32, 33, 40, 64, 65, 80):
         print(f"[sweep] exact {kind} {n}x{k} m={m}", flush=True)
         xf = O.bf16_round(activations(m, k, seed=400 + m))
         xb = torch.from_numpy(xf).cuda().to(torch.bfloat16)
@@ -231,7 +231,7 @@ def test_exact_weights_past_sixteen_rows(kind):
         lg = logits.cpu().numpy()
         run_case(f"exact {kind} argmax logits m={m}", lg, ref, 1e-4)
         assert list(idx.cpu().numpy()) == list(O.argmax_rows(lg))
-        if m in (17, 40):
+        if m in (17, 40, 80):
             gu = thq.gate_up_silu(w, xb, torch.float32, flags=thq.MODE_EXACT_W).cpu().numpy()
             want = O.bf16_bits_to_f32(O.gate_up_silu(got))
             # the epilogue over the route's own (exact) gate/up values: at most one bf16 step apart

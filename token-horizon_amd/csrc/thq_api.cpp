@@ -260,11 +260,12 @@ int check_call(const Call& c) {
 
 // The kernels a call runs, and the device scratch (split-K partials or the
 // quantized activation planes) they use, known before anything launches.
-enum class Kind { NONE, Q8ACT, GEMV1, ROWS, GEMV_MFMA, GEMV_MFMA_GROUPS, GEMM, GENERIC };
+enum class Kind { NONE, Q8ACT, GEMV1, ROWS, GEMV_MFMA, GEMV_MFMA_GROUPS, WIDE, GEMM, GENERIC };
 struct Route {
     Kind kind = Kind::NONE;
     thq::GemvPlan gp;
     thq::GemvPlan gp_last;  // GEMV_MFMA_GROUPS: the plan of the last, partial group of rows
+    thq::WidePlan wp;
     thq::GemmPlan gm;
     bool exact = false;
     size_t scratch = 0;
@@ -307,6 +308,18 @@ Route plan_route(const Call& c) {
         const char* e = getenv("THQ_GEMV_ROWS");
         return !(e && !strcmp(e, "0"));
     }();
+    // 17..64 bf16 rows: the wide exact-weight GEMV where exact weights are
+    // required (Q8_0 up to 64 rows, THQ_MODE_EXACT_W on 4- / 6-bit weights)
+    // and on outputs wide enough to fill the GPU without splitting K (the
+    // verify LM head); THQ_GEMV_WIDE=0 turns it off
+    static const bool wide_on = [] {
+        const char* e = getenv("THQ_GEMV_WIDE");
+        return !(e && !strcmp(e, "0"));
+    }();
+    const thq::WidePlan wp = (wide_on && !xf32 && aligned16(c.x) && m >= 17 && m <= 64)
+                                 ? thq::plan_gemv_wide(v.qtype, m, w->N, w->K, c.ctx->cus)
+                                 : thq::WidePlan{};
+    const bool wide_ok = wp.splits > 0 && (w->qtype == THQ_Q8_0 || (c.flags & THQ_MODE_EXACT_W) || nout >= 65536);
     if (m == 1 && !((m1_mfma || q8_m1_mfma) && skinny) && aligned16(c.x) &&
         thq::gemv1_supported(v.qtype, (int)w->K, c.gu, w->N)) {
         r.kind = Kind::GEMV1;
@@ -322,6 +335,12 @@ Route plan_route(const Call& c) {
             r.kind = Kind::GEMV_MFMA;
             r.gp = gp;
             r.scratch = c.am ? 0 : gp.workspace_bytes;
+        }
+    } else if (wide_ok) {
+        if (!c.am || wp.splits == 1) {
+            r.kind = Kind::WIDE;
+            r.wp = wp;
+            r.scratch = c.am ? 0 : wp.workspace_bytes;
         }
     } else if (c.am) {
         // no fused epilogue
@@ -386,6 +405,10 @@ int exec_route(const Call& c, const Route& r, void* scratch) {
             }
             break;
         }
+        case Kind::WIDE:
+            e = thq::launch_gemv_wide(r.wp, v, c.x, c.y, yf32, c.gu, m, nout, up_off, static_cast<float*>(scratch),
+                                      c.s, c.am);
+            break;
         case Kind::GEMM:
             e = thq::launch_gemm(r.gm, v, c.x, c.y, yf32, c.gu, r.exact, m, static_cast<float*>(scratch), c.s);
             break;
@@ -1006,7 +1029,7 @@ int thq_matmul_argmax(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_
     if (w->N > 0xFFFFFFFFll) return fail(THQ_ESHAPE, "N=%lld exceeds u32 indices", (long long)w->N);
     DeviceGuard g(ctx->device);
     thq::AmaxOut am;
-    if (!logits_dev && fused && !(flags & THQ_MODE_Q8ACT) && m <= 8) {
+    if (!logits_dev && fused && !(flags & THQ_MODE_Q8ACT) && (m <= 8 || (m >= 17 && m <= 64))) {
         c.am = &am;
         const Route r = plan_route(c);
         if (r.kind != Kind::NONE) {

@@ -95,6 +95,15 @@ struct GemvLimits {
 GemvLimits gemv_mfma_limits();
 hipError_t launch_gemv_mfma(const GemvPlan& p, const WeightView& w, const void* x, void* y, bool yf32, bool gu, int M,
                             int64_t nout, int64_t up_off, float* ws, hipStream_t s, AmaxOut* am = nullptr);
+// exact-weight GEMV for 1 <= M <= 64 bf16 rows (16-B aligned), K % 256 == 0,
+// Q8_0 / Q4_K / MLX affine / Q6_K, plain or gate/up (k_gemv_wide.hip)
+struct WidePlan {
+    int splits = 0, cps = 0;      // K splits, 256-wide chunks per split (splits == 0: unsupported)
+    size_t workspace_bytes = 0;   // split partials (f32 [splits][M][N])
+};
+WidePlan plan_gemv_wide(int qtype, int64_t M, int64_t N, int64_t K, int cus);
+hipError_t launch_gemv_wide(const WidePlan& p, const WeightView& w, const void* x, void* y, bool yf32, bool gu,
+                            int M, int64_t nout, int64_t up_off, float* ws, hipStream_t s, AmaxOut* am = nullptr);
 // sum split partials P[s][M][ldp] in split order, then the epilogue
 hipError_t launch_split_reduce(const float* P, void* y, bool yf32, bool gu, int M, int64_t nout, int64_t up_off,
                                int64_t ldp, int splits, hipStream_t s);
