@@ -17,8 +17,10 @@
 //
 // Two levels.  Each block takes a segment of 4096 elements of one row
 // (16 per thread, thread t holding ids base + 16t .. +15, so thread order is
-// id order) and selects its top k: a 4-pass radix select (8 bits a pass,
-// LDS histograms) finds the k-th largest key tau and how many of the
+// id order) and selects its top k: a 3-pass radix select (12, 10, 10 bits,
+// LDS histograms; a first pass over the top 8 bits alone sent nearly every
+// logit to the same few sign / exponent bins, serializing the LDS atomics)
+// finds the k-th largest key tau and how many of the
 // elements equal to tau are needed; those are the ones with the lowest ids,
 // found by a block prefix count in id order.  Selected elements are
 // compacted in id order, so a row's per-segment candidates stay in id order
@@ -83,7 +85,7 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
                                                            int64_t ostride, float* __restrict__ vals,
                                                            uint32_t* __restrict__ idx) {
     __shared__ uint32_t stage[TK_SEG];  // level 0: the segment's logits, transposed to thread order
-    __shared__ uint32_t hist[256];
+    __shared__ uint32_t hist[4096];
     __shared__ int scan_lds[TK_THREADS / 64];
     __shared__ uint32_t sh_prefix;
     __shared__ int sh_kk;
@@ -100,10 +102,23 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
         // coalesced loads (position base + e*256 + tid), then thread t takes
         // positions base + 16t .. +15 out of LDS
         const float* row = logits + m * n;
+        if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && base + TK_SEG <= n) {
+            // a whole segment of a 16-B aligned row: 16-B loads
 #pragma unroll
-        for (int e = 0; e < TK_EPT; ++e) {
-            const int64_t pos = base + e * TK_THREADS + tid;
-            stage[e * TK_THREADS + tid] = pos < n ? topk_key(row[pos]) : TK_ABSENT;
+            for (int e = 0; e < TK_EPT / 4; ++e) {
+                const int o = 4 * (e * TK_THREADS + tid);
+                const float4 v = *reinterpret_cast<const float4*>(row + base + o);
+                stage[o] = topk_key(v.x);
+                stage[o + 1] = topk_key(v.y);
+                stage[o + 2] = topk_key(v.z);
+                stage[o + 3] = topk_key(v.w);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < TK_EPT; ++e) {
+                const int64_t pos = base + e * TK_THREADS + tid;
+                stage[e * TK_THREADS + tid] = pos < n ? topk_key(row[pos]) : TK_ABSENT;
+            }
         }
         __syncthreads();
 #pragma unroll
@@ -135,45 +150,40 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
     if (P > k) {
         uint32_t prefix = 0u, pmask = 0u;
         int kk = k;
-        for (int shift = 24; shift >= 0; shift -= 8) {
-            hist[tid] = 0u;
+#pragma unroll
+        for (int pass = 0; pass < 3; ++pass) {
+            const int width = pass == 0 ? 12 : 10;
+            const int shift = pass == 0 ? 20 : (pass == 1 ? 10 : 0);
+            const int nb = 1 << width, per = nb / TK_THREADS;  // bins per thread: 16 or 4
+            for (int i = tid; i < nb; i += TK_THREADS) hist[i] = 0u;
             __syncthreads();
 #pragma unroll
             for (int e = 0; e < TK_EPT; ++e)
-                if (key[e] != TK_ABSENT && (key[e] & pmask) == prefix) atomicAdd(&hist[(key[e] >> shift) & 255u], 1u);
+                if (key[e] != TK_ABSENT && (key[e] & pmask) == prefix)
+                    atomicAdd(&hist[(key[e] >> shift) & (uint32_t)(nb - 1)], 1u);
             __syncthreads();
-            if (tid < 64) {
-                // lane l scans bins 255-4l .. 252-4l (from the top)
-                uint32_t c[4];
-                int s = 0;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    c[i] = hist[255 - 4 * tid - i];
-                    s += (int)c[i];
-                }
-                int incl = s;
-#pragma unroll
-                for (int d = 1; d < 64; d <<= 1) {
-                    const int y = __shfl_up(incl, d, 64);
-                    if (tid >= d) incl += y;
-                }
-                int ex = incl - s;
-                if (ex < kk && kk <= incl) {
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        if (ex + (int)c[i] >= kk) {
-                            sh_prefix = prefix | ((uint32_t)(255 - 4 * tid - i) << shift);
-                            sh_kk = kk - ex;
-                            break;
-                        }
-                        ex += (int)c[i];
+            // thread t owns bins nb-1-per*t .. nb-per*(t+1) (from the top); the
+            // thread whose range holds the kk-th largest key finds its bin
+            int cnt = 0;
+            for (int j = 0; j < per; ++j) cnt += (int)hist[nb - 1 - per * tid - j];
+            int tot;
+            int ex = block_scan(cnt, scan_lds, tot);
+            if (ex < kk && kk <= ex + cnt) {
+                for (int j = 0; j < per; ++j) {
+                    const int b = nb - 1 - per * tid - j;
+                    const int c = (int)hist[b];
+                    if (ex + c >= kk) {
+                        sh_prefix = prefix | ((uint32_t)b << shift);
+                        sh_kk = kk - ex;
+                        break;
                     }
+                    ex += c;
                 }
             }
             __syncthreads();
             prefix = sh_prefix;
             kk = sh_kk;
-            pmask |= 255u << shift;
+            pmask |= (uint32_t)(nb - 1) << shift;
         }
         tau = prefix;
         need = kk;
