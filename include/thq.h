@@ -224,9 +224,12 @@ int thq_gate_up_silu_q8act_emit(thq_ctx* ctx, const thq_weight* fused, thq_dtype
  *   M = 2..16  bf16 x with K a multiple of 256: matrix-core decode GEMV
  *              (exact weights); Q4_K / MLX affine at M = 2..4 and K <= 4096
  *              use a VALU row GEMV (exact weights) instead
+ *   M = 17..64 bf16 x with K a multiple of 256: for Q8_0, under
+ *              THQ_MODE_EXACT_W, or with >= 65536 outputs (the verify LM
+ *              head), a wide matrix-core GEMV that reads the weights once
+ *              for all rows (exact weights)
  *   larger M   (and the other bf16 shapes with K a multiple of 64) MFMA GEMM;
  *              weights are rounded to bf16 on its tile unless THQ_MODE_EXACT_W
- *              (or Q8_0 with M <= 64)
  *   x f32 with M >= 2 runs an exact f32 path, and so do the remaining shapes
  *   (Q6_K with THQ_MODE_EXACT_W among them).
  * THQ_MODE_Q8ACT instead reproduces candle's default CPU k_quants::matmul:
@@ -267,7 +270,8 @@ int thq_gate_up_silu(thq_ctx* ctx, const thq_weight* fused, const void* x_dev, t
  * logits then live in the context workspace).  With logits_dev NULL and
  * THQ_MODE_ARGMAX_FUSED, the decode kernels that have the fused epilogue
  * (M <= 8: Q8_0, Q6_K and Q4_K / MLX affine at M = 1 with K <= 4096, and
- * the M = 2..8 matrix-core path when it runs unsplit in K) write one (max, index)
+ * the M = 2..8 matrix-core path when it runs unsplit in K; M = 17..64 on the
+ * wide GEMV when it runs unsplit in K) write one (max, index)
  * partial per output tile instead of logits, and one pass reduces them;
  * other shapes take the logits path.  Both give identical indices; on
  * MI355X neither is measurably faster (the logits are ~1% of the weight
