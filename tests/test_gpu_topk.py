@@ -68,6 +68,18 @@ def test_topk_ties_across_segments(n):
         check(v, k, f"ties n={n} k={k}")
 
 
+@pytest.mark.parametrize("n", [3000, 9000])
+def test_topk_every_k(n):
+    """Every k from 1 to 64 on normal and bf16-rounded rows: the fast path's
+    candidate count (keys at or above the threshold) then takes many values,
+    including every remainder of its 8-wide batches."""
+    rng = np.random.default_rng(n)
+    v = rng.normal(0, 3, (3, n)).astype(np.float32)
+    v[2] = O.bf16_round(v[2])          # bf16 logits: exact ties
+    for k in range(1, 65):
+        check(v, k, f"every k n={n} k={k}")
+
+
 def test_topk_special_rows():
     n = 9000
     v = np.zeros((5, n), np.float32)

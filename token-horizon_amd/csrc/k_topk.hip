@@ -17,15 +17,22 @@
 //
 // Two levels.  Each block takes a segment of 4096 elements of one row
 // (16 per thread, thread t holding ids base + 16t .. +15, so thread order is
-// id order) and selects its top k: a 3-pass radix select (12, 10, 10 bits,
-// LDS histograms; a first pass over the top 8 bits alone sent nearly every
-// logit to the same few sign / exponent bins, serializing the LDS atomics)
-// finds the k-th largest key tau and how many of the
-// elements equal to tau are needed; those are the ones with the lowest ids,
-// found by a block prefix count in id order.  Selected elements are
-// compacted in id order, so a row's per-segment candidates stay in id order
-// for the next level, which runs the same select over them until one
-// segment remains; the last one also sorts its k by rank counting.
+// id order) and selects its top k.
+// Fast path: each lane keeps its 4 largest keys, and each wave finds, bit by
+// bit with ballots (no LDS, no barrier), the largest t such that at least k
+// of its lanes' kept keys are >= t; the block threshold T is the largest of
+// the four.  Some wave then holds k keys >= T, so the segment's whole top k
+// is among the keys >= T (usually about k to 2k of them).  Those are
+// compacted and ranked exactly by counting (key desc, id asc).
+// Fallback (more than 256 keys >= T, e.g. long runs of equal logits): a
+// 3-pass radix select (12, 10, 10 bits, LDS histograms) finds the k-th
+// largest key tau and how many of the elements equal to tau are needed;
+// those are the ones with the lowest ids, found by a block prefix count in
+// id order.
+// Either way a segment's selected elements leave in id order, so the next
+// level, which runs the same select over the per-segment candidates until
+// one segment remains, can use the fallback too; the last level writes its
+// k in rank order.
 // HBM-bound: one pass over the logits (4 B per logit) and a few KB of
 // candidates per row.
 #include "thq_dev.hpp"
@@ -39,6 +46,7 @@ constexpr int TK_THREADS = 256;
 constexpr int TK_EPT = 16;
 constexpr int TK_SEG = TK_THREADS * TK_EPT;
 constexpr uint32_t TK_ABSENT = 0u;
+constexpr int TK_CAP = 256;  // candidates the fast path ranks
 
 __device__ __forceinline__ uint32_t topk_key(float v) {
     uint32_t b = __float_as_uint(v);
@@ -84,12 +92,16 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
                                                            uint32_t* __restrict__ okey, uint32_t* __restrict__ oid,
                                                            int64_t ostride, float* __restrict__ vals,
                                                            uint32_t* __restrict__ idx) {
-    __shared__ uint32_t stage[TK_SEG];  // level 0: the segment's logits, transposed to thread order
-    __shared__ uint32_t hist[4096];
+    // level 0 stages the segment's logits here (transposed to thread order);
+    // after the keys are in registers the same bytes hold the fast path's
+    // candidates or the fallback's histograms
+    __shared__ uint32_t stage[TK_SEG];
+    uint32_t* const hist = stage;
     __shared__ int scan_lds[TK_THREADS / 64];
     __shared__ uint32_t sh_prefix;
     __shared__ int sh_kk;
     __shared__ uint32_t fkey[64], fid[64];
+    __shared__ uint32_t wthr[TK_THREADS / 64];
 
     const int tid = threadIdx.x;
     const int64_t m = blockIdx.y;
@@ -127,16 +139,127 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
             id[e] = (uint32_t)(base + tid * TK_EPT + e);
         }
     } else {
+        // the segment's candidates spread over every thread (epv each, in
+        // position order, so thread order stays id order)
         const uint32_t* kr = ckey + m * ccount;
         const uint32_t* ir = cid + m * ccount;
+        const int64_t here = count - base < TK_SEG ? count - base : TK_SEG;
+        const int epv = (int)((here + TK_THREADS - 1) / TK_THREADS);
 #pragma unroll
         for (int e = 0; e < TK_EPT; ++e) {
-            const int64_t pos = base + tid * TK_EPT + e;
-            key[e] = pos < count ? kr[pos] : TK_ABSENT;
-            id[e] = pos < count ? ir[pos] : 0xFFFFFFFFu;
+            const int64_t pos = base + (int64_t)tid * epv + e;
+            const bool ok = e < epv && pos < count;
+            key[e] = ok ? kr[pos] : TK_ABSENT;
+            id[e] = ok ? ir[pos] : 0xFFFFFFFFu;
         }
     }
 
+    // ---- fast path: threshold from the waves' lane maxima
+    {
+        uint32_t v0 = 0u, v1 = 0u, v2 = 0u, v3 = 0u;  // the lane's 4 largest keys, v0 >= v1 >= v2 >= v3
+#pragma unroll
+        for (int e = 0; e < TK_EPT; ++e) {
+            uint32_t x = key[e], t;
+            t = x > v0 ? x : v0; x = x > v0 ? v0 : x; v0 = t;
+            t = x > v1 ? x : v1; x = x > v1 ? v1 : x; v1 = t;
+            t = x > v2 ? x : v2; x = x > v2 ? v2 : x; v2 = t;
+            v3 = x > v3 ? x : v3;
+        }
+        // largest t (to 2^-20 of the key range: a smaller T only admits more
+        // candidates) with >= k kept keys of this wave at or above it
+        uint32_t tw = 0u;
+        for (int b = 31; b >= 12; --b) {
+            const uint32_t c = tw | (1u << b);
+            const int cnt = __popcll(__ballot(v0 >= c)) + __popcll(__ballot(v1 >= c)) +
+                            __popcll(__ballot(v2 >= c)) + __popcll(__ballot(v3 >= c));
+            if (cnt >= k) tw = c;
+        }
+        if ((tid & 63) == 0) wthr[tid >> 6] = tw;
+        __syncthreads();
+        uint32_t T = wthr[0];
+#pragma unroll
+        for (int w = 1; w < TK_THREADS / 64; ++w) T = wthr[w] > T ? wthr[w] : T;
+        if (T == TK_ABSENT) T = 1u;  // present keys only
+        int c = 0;
+#pragma unroll
+        for (int e = 0; e < TK_EPT; ++e) c += key[e] >= T;
+        int nc;
+        int pos = block_scan(c, scan_lds, nc);
+        if (nc <= TK_CAP) {
+            uint2* cand = reinterpret_cast<uint2*>(hist);             // [TK_CAP] (key, id)
+            uint2* sel = cand + TK_CAP;                               // [64] selected, by rank
+            __syncthreads();  // every thread is past its reads of the staged logits
+#pragma unroll
+            for (int e = 0; e < TK_EPT; ++e)
+                if (key[e] >= T) cand[pos++] = make_uint2(key[e], id[e]);
+            // pad to a multiple of 8 with entries that beat nothing
+            if (tid < ((nc + 7) & ~7) - nc) cand[nc + tid] = make_uint2(0u, 0xFFFFFFFFu);
+            __syncthreads();
+            // rank = number of candidates ahead in (key desc, id asc); 8 per
+            // LDS round trip (4 x 16-B broadcast reads)
+            auto ahead = [](uint2 a, uint2 me) { return (int)(a.x > me.x || (a.x == me.x && a.y < me.y)); };
+            int rank = k;  // k: not selected
+            uint2 me = make_uint2(0u, 0u);
+            if (tid < nc) {
+                me = cand[tid];
+                const uint4* c4 = reinterpret_cast<const uint4*>(cand);
+                int r0 = 0, r1 = 0;
+                auto batch = [&](int j) {
+                    const uint4 q0 = c4[j / 2], q1 = c4[j / 2 + 1], q2 = c4[j / 2 + 2], q3 = c4[j / 2 + 3];
+                    r0 += ahead(make_uint2(q0.x, q0.y), me) + ahead(make_uint2(q0.z, q0.w), me) +
+                          ahead(make_uint2(q1.x, q1.y), me) + ahead(make_uint2(q1.z, q1.w), me);
+                    r1 += ahead(make_uint2(q2.x, q2.y), me) + ahead(make_uint2(q2.z, q2.w), me) +
+                          ahead(make_uint2(q3.x, q3.y), me) + ahead(make_uint2(q3.z, q3.w), me);
+                };
+                int j = 0;
+                for (; j + 16 <= nc; j += 16) {  // two batches' reads in flight together
+                    batch(j);
+                    batch(j + 8);
+                }
+                for (; j < nc; j += 8) batch(j);  // the rest (up to 15, in batches of 8)
+                rank = r0 + r1;
+            }
+            const int nsel = nc < k ? nc : k;
+            if constexpr (FINAL) {
+                float* vr = vals + m * k;
+                uint32_t* xr = idx + m * k;
+                if (rank < k) {
+                    vr[rank] = topk_value(me.x);
+                    xr[rank] = me.y;
+                }
+                if (tid >= nsel && tid < k) {
+                    vr[tid] = -INFINITY;
+                    xr[tid] = 0xFFFFFFFFu;
+                }
+            } else {
+                // id-order position among the selected: count smaller ids among them
+                if (rank < k) sel[rank] = me;
+                __syncthreads();
+                uint32_t* ok = okey + m * ostride + seg * k;
+                uint32_t* oi = oid + m * ostride + seg * k;
+                if (tid < nsel) {
+                    const uint2 mine = sel[tid];
+                    const uint4* s4 = reinterpret_cast<const uint4*>(sel);
+                    int opos = 0, j = 0;
+                    for (; j + 8 <= nsel; j += 8) {
+                        const uint4 q0 = s4[j / 2], q1 = s4[j / 2 + 1], q2 = s4[j / 2 + 2], q3 = s4[j / 2 + 3];
+                        opos += (q0.y < mine.y) + (q0.w < mine.y) + (q1.y < mine.y) + (q1.w < mine.y) +
+                                (q2.y < mine.y) + (q2.w < mine.y) + (q3.y < mine.y) + (q3.w < mine.y);
+                    }
+                    for (; j < nsel; ++j) opos += sel[j].y < mine.y;
+                    ok[opos] = mine.x;
+                    oi[opos] = mine.y;
+                }
+                if (tid >= nsel && tid < k) {
+                    ok[tid] = TK_ABSENT;
+                    oi[tid] = 0xFFFFFFFFu;
+                }
+            }
+            return;
+        }
+    }
+
+    // ---- fallback: exact radix select over the whole segment
     int present = 0;
 #pragma unroll
     for (int e = 0; e < TK_EPT; ++e) present += key[e] != TK_ABSENT;
