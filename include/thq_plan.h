@@ -57,6 +57,16 @@ typedef struct thq_gemm_plan_info {
 int thq_plan_gemm(int dtype, int exact, int64_t m, int64_t n, int64_t k, int gate_up, int cus,
                   thq_gemm_plan_info* out);
 
+/* Wide exact-weight GEMV (M = 1..64 bf16 rows, K a multiple of 256), for a
+ * device with `cus` compute units; the router takes it for 17..64 rows. */
+typedef struct thq_wide_plan_info {
+    int32_t splits;           /* K splits (0: the shape has no plan)                */
+    int32_t chunks_per_split; /* 256-wide K chunks per split                        */
+    int64_t workspace_bytes;  /* split partials, f32 [splits][M][N]                 */
+} thq_wide_plan_info;
+
+int thq_plan_gemv_wide(int dtype, int64_t m, int64_t n, int64_t k, int cus, thq_wide_plan_info* out);
+
 /* Measurement aid: read `bytes` (a multiple of 16) of buf_dev (16-byte
  * aligned) once with 16-B loads from `blocks` blocks of 256 threads, on
  * `stream`; sink_dev (4 bytes) is written only in the unlikely case the

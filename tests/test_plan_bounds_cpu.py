@@ -155,3 +155,20 @@ def test_planner_rejects_bad_arguments():
     # unsupported shapes plan nothing
     assert thq.plan_gemv_mfma(thq.Q4_K, 17, 4096, 4096).waves == 0
     assert thq.plan_gemv_mfma(thq.Q4_K, 1, 4096, 4000).waves == 0
+
+
+def test_wide_plans():
+    """The wide GEMV's plan covers K exactly with non-empty splits, and its
+    workspace is the split partials; unsupported shapes plan nothing."""
+    for dt in (thq.Q8_0, thq.Q4_K, thq.Q6_K, thq.MLX_Q4):
+        for m in (1, 17, 40, 64):
+            for n in (300, 4096, 12288, 151936):
+                for k in (256, 1024, 4096, 12288):
+                    p = thq.plan_gemv_wide(dt, m, n, k)
+                    nch = k // 256
+                    assert p.splits >= 1 and p.chunks_per_split >= 1
+                    assert p.splits * p.chunks_per_split >= nch > (p.splits - 1) * p.chunks_per_split
+                    assert p.workspace_bytes == (p.splits * m * n * 4 if p.splits > 1 else 0)
+        assert thq.plan_gemv_wide(dt, 65, 4096, 4096).splits == 0
+        assert thq.plan_gemv_wide(dt, 8, 4096, 1000).splits == 0
+    assert thq.plan_gemv_wide(thq.Q4_K, 40, 151936, 4096).splits == 1

@@ -1124,6 +1124,20 @@ int thq_probe_hbm_read(thq_ctx* ctx, const void* buf_dev, size_t bytes, int bloc
     return THQ_OK;
 }
 
+int thq_plan_gemv_wide(int dtype, int64_t m, int64_t n, int64_t k, int cus, thq_wide_plan_info* out) {
+    const int qt = kernel_qtype(dtype);
+    if (!qt) return fail(THQ_EDTYPE, "dtype %d", dtype);
+    if (!out) return fail(THQ_EINVAL, "null out");
+    if (m < 1 || n < 1 || k < 1) return fail(THQ_ESHAPE, "shape [%lld, %lld, %lld]", (long long)m, (long long)n,
+                                             (long long)k);
+    const thq::WidePlan p = thq::plan_gemv_wide(qt, m, n, k, cus);
+    *out = thq_wide_plan_info{};
+    out->splits = p.splits;
+    out->chunks_per_split = p.cps;
+    out->workspace_bytes = (int64_t)p.workspace_bytes;
+    return THQ_OK;
+}
+
 int thq_plan_gemm(int dtype, int exact, int64_t m, int64_t n, int64_t k, int gate_up, int cus,
                   thq_gemm_plan_info* out) {
     const int qt = kernel_qtype(dtype);

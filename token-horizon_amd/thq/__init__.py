@@ -53,7 +53,7 @@ EXPORTS = (
     "thq_gguf_find_tensor", "thq_gguf_tensor_info", "thq_gguf_tensor_data", "thq_gguf_metadata_key",
     "thq_gguf_metadata_u32", "thq_gguf_metadata_f32", "thq_gguf_metadata_str", "thq_gguf_metadata_array",
     "thq_weight_from_gguf", "thq_q8act_bytes", "thq_q8act_prepare", "thq_matmul_q8act", "thq_gate_up_silu_q8act",
-    "thq_plan_gemv_mfma", "thq_plan_gemm", "thq_matmul_noalloc", "thq_noalloc_scratch_bytes",
+    "thq_plan_gemv_mfma", "thq_plan_gemm", "thq_plan_gemv_wide", "thq_matmul_noalloc", "thq_noalloc_scratch_bytes",
     "thq_topk", "thq_matmul_topk", "thq_gate_up_silu_q8act_emit", "thq_probe_hbm_read",
 )
 
@@ -82,6 +82,17 @@ def plan_gemv_mfma(dtype: int, m: int, n: int, k: int, gate_up: bool = False) ->
     """The decode GEMV's plan for a shape (host only)."""
     out = GemvPlanInfo()
     check(lib.thq_plan_gemv_mfma(dtype, m, n, k, int(gate_up), C.byref(out)))
+    return out
+
+
+class WidePlanInfo(C.Structure):
+    _fields_ = [("splits", C.c_int32), ("chunks_per_split", C.c_int32), ("workspace_bytes", C.c_int64)]
+
+
+def plan_gemv_wide(dtype: int, m: int, n: int, k: int, cus: int = 256) -> WidePlanInfo:
+    """The wide exact-weight GEMV's plan (thq_plan_gemv_wide); splits == 0: no plan."""
+    out = WidePlanInfo()
+    check(lib.thq_plan_gemv_wide(dtype, m, n, k, cus, C.byref(out)))
     return out
 
 
@@ -148,6 +159,7 @@ def _load():
         "thq_noalloc_scratch_bytes": ([], C.c_size_t),
         "thq_plan_gemv_mfma": ([I, i64, i64, i64, I, C.POINTER(GemvPlanInfo)], I),
         "thq_plan_gemm": ([I, I, i64, i64, i64, I, I, C.POINTER(GemmPlanInfo)], I),
+        "thq_plan_gemv_wide": ([I, i64, i64, i64, I, C.POINTER(WidePlanInfo)], I),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
