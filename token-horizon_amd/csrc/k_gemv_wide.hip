@@ -27,8 +27,10 @@
 //   Q4_K    B = bf16(128 + q); per 32-wide sub-block
 //           sum = d1 * A - (128 * d1 + m1) * S,  S = sum of x over it
 //   affine  same with d1 = scale, m1 = -bias (w = scale * q + bias)
-//   Q6_K    B = bf16(128 + code); per 16-wide group sum = s * (A - 160 * S16)
-// The sums S / S16 are taken while a chunk is staged.
+//   Q6_K    B = bf16(128 + code); per 16-wide group a second MFMA against a
+//           constant B of bf16(-160) folds in -160 * (sum of x over the group),
+//           so the group's sum is s * A with A = sum x * (code - 32)
+// The 32-wide sums S (Q4_K, affine) are taken while a chunk is staged.
 // Gate/up (GU): a wave's 32 rows are 16 gate rows and the 16 up rows of the
 // same outputs (a block owns 64 outputs); lanes n and n + 16 exchange their
 // sums for the silu(gate) * up epilogue (engine/src/quant_kernel.rs:2922-2926).
@@ -92,9 +94,9 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
                                                      int64_t am_ld) {
     constexpr int MP = 32 * MH;                 // staged rows (M <= MP)
     constexpr int NXP = MP * (WV_KC / 8) / 256; // 16-B activation pieces per thread per chunk
-    constexpr int NS = QT == 14 ? WV_KC / 16 : WV_KC / 32;  // sums per staged row
+    constexpr int NS = WV_KC / 32;  // 32-wide sums per staged row (Q4_K, affine)
     __shared__ __attribute__((aligned(16))) bf16_t xs[2][MP][WV_XR];
-    __shared__ __attribute__((aligned(16))) float Ss[QT == 8 ? 1 : 2][NS][MP];
+    __shared__ __attribute__((aligned(16))) float Ss[QT == 8 || QT == 14 ? 1 : 2][NS][MP];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -177,9 +179,9 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
             if (m < M) {
                 const uint4 v = xv[j];
                 *reinterpret_cast<uint4*>(&xs[buf][m][8 * i]) = v;
-                if constexpr (QT != 8) {
-                    // a 32-wide sub-block is 4 consecutive pieces (lanes 4j..4j+3),
-                    // a 16-wide group 2 (lanes 2j, 2j+1): whole lane quads share m
+                if constexpr (QT == 12 || QT == 13) {
+                    // a 32-wide sub-block is 4 consecutive pieces (lanes 4j..4j+3,
+                    // a whole lane quad, all of one row m)
                     const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
                     bf16x2_t q[4];
                     __builtin_memcpy(q, &v, 16);
@@ -188,12 +190,8 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
                     t = __builtin_amdgcn_fdot2_f32_bf16(q[2], one, t, false);
                     t = __builtin_amdgcn_fdot2_f32_bf16(q[3], one, t, false);
                     t = wdpp_add<0xB1>(t);  // quad_perm [1,0,3,2]
-                    if constexpr (QT == 14) {
-                        if ((i & 1) == 0) Ss[buf][i >> 1][m] = t;
-                    } else {
-                        t = wdpp_add<0x4E>(t);  // quad_perm [2,3,0,1]
-                        if ((i & 3) == 0) Ss[buf][i >> 2][m] = t;
-                    }
+                    t = wdpp_add<0x4E>(t);  // quad_perm [2,3,0,1]
+                    if ((i & 3) == 0) Ss[buf][i >> 2][m] = t;
                 }
             }
         }
@@ -255,19 +253,20 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
                 hi[2] = ((q.y >> 4) & M4) | (hb.y & 0x30303030u);
                 lo[3] = ((q.z >> 4) & M4) | ((hb.x >> 2) & 0x30303030u);
                 hi[3] = ((q.w >> 4) & M4) | ((hb.y >> 2) & 0x30303030u);
+                // bf16(-160) in every element: the second MFMA adds -160 * sum(x)
+                const uint32_t m160 = 0xC320C320u;
+                const bf16x8_t B160 = as_bf16x8(make_uint4(m160, m160, m160, m160));
 #pragma unroll
                 for (int G = 0; G < 4; ++G) {
                     const float sg = dd * (float)(int)(int8_t)(C.s[u] >> (8 * G));
                     const bf16x8_t B = wnib(lo[G], hi[G]);
 #pragma unroll
                     for (int h = 0; h < MH; ++h) {
-                        const uint4 a = *reinterpret_cast<const uint4*>(&xs[buf][arow[h]][GOFF * g + 64 * u + 16 * G]);
-                        f32x4_t S[4];
-                        sums(buf, 4 * u + G, h, S);
-                        const f32x16_t T = wmfma(as_bf16x8(a), B, z16);
+                        const bf16x8_t a = as_bf16x8(*reinterpret_cast<const uint4*>(&xs[buf][arow[h]][GOFF * g + 64 * u + 16 * G]));
+                        f32x16_t T = wmfma(a, B, z16);
+                        T = wmfma(a, B160, T);
 #pragma unroll
-                        for (int e = 0; e < 16; ++e)
-                            acc[h][e] = __builtin_fmaf(sg, __builtin_fmaf(-160.0f, S[e >> 2][e & 3], T[e]), acc[h][e]);
+                        for (int e = 0; e < 16; ++e) acc[h][e] = __builtin_fmaf(sg, T[e], acc[h][e]);
                     }
                     pin();
                 }
