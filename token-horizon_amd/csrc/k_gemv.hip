@@ -687,94 +687,205 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_f32(const uint8_t* __restrict
 }
 
 // ------------------------------------------------------------------ Q8_0 M=1
-// Planes: qs [N][K] i8, d [N][K/32] f16.  Lane l covers 16 bytes of every
-// 1024-wide K chunk: k = 1024c + 16l (block 32c + l/2).  u = q ^ 0x80 is the
-// unsigned byte q + 128, converted with v_cvt_f32_ubyte; the 128 offset is
-// removed with the lane's sum of x.
-template <int KC, int R, bool GU, typename XT, typename YT>
-__global__ __launch_bounds__(256) void k_gemv1_q8(const int8_t* __restrict__ Q, const uint16_t* __restrict__ D,
-                                                 const XT* __restrict__ x, YT* __restrict__ y, int64_t nout, int K,
-                                                 int64_t up_off, float* __restrict__ amv, uint32_t* __restrict__ ami) {
-    const int lane = threadIdx.x & 63;
-    const int64_t wave = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-    const int64_t base = wave * (GU ? R / 2 : R);
-    if (base >= nout && !amv) return;  // the fused argmax's block barrier needs every wave
-    const int nb = K >> 5;
+// Planes: qs [N][K] i8, d [N][K/32] f16.  A block owns the contiguous output
+// range [o0, o0 + rpb); its four waves take outputs o0 + w, o0 + w + 4, ...
+// and stream them: a wave keeps its slice of x in registers for the whole
+// range and issues the next output's loads before the current one's math, so
+// x is read from L2 once per block (staged in LDS) instead of once per row.
+// Lane l covers 16 bytes of every 1024-wide K chunk, k = 1024c + 16l (block
+// 32c + l/2): one 16-B load per chunk, a whole 1-KB run per wave instruction.
+// The row's f16 scales arrive as one dword per lane (blocks 2l, 2l + 1; a
+// second dword for K > 4096) and reach the lane that uses them through
+// ds_bpermute.  u = q ^ 0x80 is the unsigned byte q + 128; the 128 offset is
+// removed with the lane's sum of x.  bf16 x: u goes to bf16 (exact, 0..255)
+// and pairs meet x pairs in v_dot2_f32_bf16; f32 x: v_cvt_f32_ubyte and f32
+// fma.  Every product is exact in f32 either way.
+template <typename XT>
+struct Q8XSlice;
+template <>
+struct Q8XSlice<bf16_t> {
+    uint32_t v[8];  // 16 bf16 as pairs
+};
+template <>
+struct Q8XSlice<float> {
+    float v[16];
+};
 
-    float xv[KC][16], sx[KC];
+__device__ __forceinline__ float q8_dot16(const uint4& q, const Q8XSlice<bf16_t>& X) {
+    const uint32_t u[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
+    float s = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        s = dot2_bf16(pack_bf16x2(ubyte_f32<0>(u[t]), ubyte_f32<1>(u[t])), X.v[2 * t], s);
+        s = dot2_bf16(pack_bf16x2(ubyte_f32<2>(u[t]), ubyte_f32<3>(u[t])), X.v[2 * t + 1], s);
+    }
+    return s;
+}
+__device__ __forceinline__ float q8_dot16(const uint4& q, const Q8XSlice<float>& X) {
+    const uint32_t u[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
+    float s = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        s = __builtin_fmaf(ubyte_f32<0>(u[t]), X.v[4 * t], s);
+        s = __builtin_fmaf(ubyte_f32<1>(u[t]), X.v[4 * t + 1], s);
+        s = __builtin_fmaf(ubyte_f32<2>(u[t]), X.v[4 * t + 2], s);
+        s = __builtin_fmaf(ubyte_f32<3>(u[t]), X.v[4 * t + 3], s);
+    }
+    return s;
+}
+
+// one weight row's loads: KC 16-B pieces and SD scale dwords per lane
+template <int KC>
+struct Q8Row {
+    uint4 q[KC];
+    uint32_t d[(KC + 3) / 4];
+};
+template <int KC>
+__device__ __forceinline__ void q8_row_load(Q8Row<KC>& R, const int8_t* __restrict__ Q, const uint16_t* __restrict__ D,
+                                            int64_t row, int K, int lane) {
+    const int nb = K >> 5;
 #pragma unroll
     for (int c = 0; c < KC; ++c) {
         const int k0 = 1024 * c + 16 * lane;
-        sx[c] = 0.0f;
-        if (k0 < K) {
+        R.q[c] = k0 < K ? ld_stream16(Q + row * K + k0) : make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
+    }
+    const uint16_t* dr = D + row * nb;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) xv[c][i] = load_x<XT>(x + k0 + i);
+    for (int j = 0; j < (KC + 3) / 4; ++j) {
+        const int b = 2 * (lane + 64 * j);  // first block of this dword
+        uint32_t v = 0;
+        if (b + 1 < nb) {
+            // rows start on a dword boundary when nb is even; otherwise two halves
+            v = (nb & 1) ? ((uint32_t)dr[b] | ((uint32_t)dr[b + 1] << 16))
+                         : *reinterpret_cast<const uint32_t*>(dr + b);
+        } else if (b < nb) {
+            v = dr[b];
+        }
+        R.d[j] = v;
+    }
+}
+// f32 dot of one row with the lane's x slices (before the cross-lane sum)
+template <int KC, typename XT>
+__device__ __forceinline__ float q8_row_dot(const Q8Row<KC>& R, const Q8XSlice<XT> (&xv)[KC], const float (&sx)[KC],
+                                            int lane) {
+    float a = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) sx[c] += xv[c][i];
+    for (int c = 0; c < KC; ++c) {
+        // block 32c + lane/2 sits in dword 16c + lane/4 (lane (16c + lane/4) % 64, register c/4)
+        const int src = ((16 * c + (lane >> 2)) & 63) << 2;
+        const uint32_t dw = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)R.d[c >> 2]);
+        const float d = f16_to_f32((uint16_t)(((lane >> 1) & 1) ? (dw >> 16) : dw));
+        a = __builtin_fmaf(d, __builtin_fmaf(-128.0f, sx[c], q8_dot16(R.q[c], xv[c])), a);
+    }
+    return a;
+}
+
+template <int KC, bool GU, typename XT, typename YT>
+__global__ __launch_bounds__(256) void k_gemv1_q8(const int8_t* __restrict__ Q, const uint16_t* __restrict__ D,
+                                                 const XT* __restrict__ x, YT* __restrict__ y, int64_t nout, int K,
+                                                 int64_t up_off, int rpb, float* __restrict__ amv,
+                                                 uint32_t* __restrict__ ami) {
+    constexpr int R = GU ? 2 : 1;  // weight rows per output
+    __shared__ __attribute__((aligned(16))) XT xs[KC * 1024];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t o0 = (int64_t)blockIdx.x * rpb;
+    const int64_t o1 = o0 + rpb < nout ? o0 + rpb : nout;
+    auto rows_of = [&](int64_t o, int r) { return GU ? o + (r ? up_off : 0) : o; };
+
+    // the first two outputs' loads, then x (its wait covers them; vector-memory
+    // counters drain in order)
+    Q8Row<KC> A[R], B[R], C[R];
+    auto load = [&](Q8Row<KC>(&buf)[R], int64_t oo) {
+        if (oo < o1) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) q8_row_load<KC>(buf[r], Q, D, rows_of(oo, r), K, lane);
+        }
+    };
+    int64_t o = o0 + wave;
+    load(A, o);
+    load(B, o + 4);
+    if (sizeof(XT) == 2 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (K & 7) == 0) {
+        for (int i = 8 * threadIdx.x; i < KC * 1024; i += 8 * 256)
+            *reinterpret_cast<uint4*>(&xs[i]) = i < K ? *reinterpret_cast<const uint4*>(x + i) : make_uint4(0, 0, 0, 0);
+    } else {
+        for (int i = threadIdx.x; i < KC * 1024; i += 256) xs[i] = i < K ? x[i] : XT(0.0f);
+    }
+    __syncthreads();
+    Q8XSlice<XT> xv[KC];
+    float sx[KC];
+#pragma unroll
+    for (int c = 0; c < KC; ++c) {
+        const XT* p = &xs[1024 * c + 16 * lane];
+        float sm = 0.0f;
+        if constexpr (sizeof(XT) == 2) {
+            const uint4 a = *reinterpret_cast<const uint4*>(p);
+            const uint4 b = *reinterpret_cast<const uint4*>(p + 8);
+            const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                xv[c].v[i] = w[i];
+                sm += bf16_to_f32(w[i] & 0xFFFFu);
+                sm += bf16_to_f32(w[i] >> 16);
+            }
         } else {
 #pragma unroll
-            for (int i = 0; i < 16; ++i) xv[c][i] = 0.0f;
-        }
-    }
-    uint4 qv[R][KC];
-    uint16_t dv[R][KC];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        int64_t row = slot_row<R, GU>(base, r, up_off);
-        const bool ok = GU ? (base + (r >> 1) < nout) : (row < nout);
-        if (!ok) row = GU ? up_off * (r & 1) : 0;
-#pragma unroll
-        for (int c = 0; c < KC; ++c) {
-            const int k0 = 1024 * c + 16 * lane;
-            if (k0 < K) {
-                qv[r][c] = ld_stream16(Q + row * K + k0);
-                dv[r][c] = D[row * nb + (k0 >> 5)];
-            } else {
-                qv[r][c] = make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
-                dv[r][c] = 0;
+            for (int i = 0; i < 16; ++i) {
+                xv[c].v[i] = p[i];
+                sm += p[i];
             }
         }
+        sx[c] = sm;
     }
-    float acc[R];
+
+    // outputs o, o + 4, ... with two rows in flight ahead of the one being
+    // reduced: buffers rotate A -> B -> C, each refilled right after its math
+    float bv = -INFINITY;
+    uint32_t bi = 0xFFFFFFFFu;
+    auto finish = [&](const Q8Row<KC>(&buf)[R], int64_t oo) {
+        float acc[R];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        float a = 0.0f;
-#pragma unroll
-        for (int c = 0; c < KC; ++c) {
-            const uint32_t w4[4] = {qv[r][c].x ^ 0x80808080u, qv[r][c].y ^ 0x80808080u, qv[r][c].z ^ 0x80808080u,
-                                    qv[r][c].w ^ 0x80808080u};
-            float s = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                s = __builtin_fmaf(ubyte_f32<0>(w4[t]), xv[c][4 * t], s);
-                s = __builtin_fmaf(ubyte_f32<1>(w4[t]), xv[c][4 * t + 1], s);
-                s = __builtin_fmaf(ubyte_f32<2>(w4[t]), xv[c][4 * t + 2], s);
-                s = __builtin_fmaf(ubyte_f32<3>(w4[t]), xv[c][4 * t + 3], s);
+        for (int r = 0; r < R; ++r) acc[r] = wave_sum(q8_row_dot<KC, XT>(buf[r], xv, sx, lane));
+        if (!GU && amv) {
+            // strict '>' in increasing output order: NaN never wins, ties keep the lower index
+            if (acc[0] > bv) {
+                bv = acc[0];
+                bi = (uint32_t)oo;
             }
-            a = __builtin_fmaf(f16_to_f32(dv[r][c]), s - 128.0f * sx[c], a);
+        } else if (lane == 0) {
+            store_y<YT>(y + oo, GU ? silu_mul(acc[0], acc[R - 1]) : acc[0]);
         }
-        acc[r] = wave_sum(a);
+    };
+    for (; o < o1; o += 12) {
+        load(C, o + 8);
+        finish(A, o);
+        if (o + 4 >= o1) break;
+        load(A, o + 12);
+        finish(B, o + 4);
+        if (o + 8 >= o1) break;
+        load(B, o + 16);
+        finish(C, o + 8);
     }
     if (!GU && amv) {
-        // fused argmax (one row per wave): one (max, lowest index) partial per block
+        // one (max, lowest index) partial per block, as a scan from (-inf, o0)
         __shared__ float amx[4];
-        if (lane == 0) amx[threadIdx.x >> 6] = acc[0];
+        __shared__ uint32_t amn[4];
+        if (lane == 0) {
+            amx[wave] = bv;
+            amn[wave] = bi;
+        }
         __syncthreads();
         if (threadIdx.x == 0) {
-            const int64_t o0 = (int64_t)blockIdx.x * (blockDim.x >> 6);
-            float bv = -INFINITY;
-            uint32_t bi = (uint32_t)o0;
-            for (int w = 0; w < (int)(blockDim.x >> 6) && o0 + w < nout; ++w)
-                if (amx[w] > bv) {
-                    bv = amx[w];
-                    bi = (uint32_t)(o0 + w);
+            float v = -INFINITY;
+            uint32_t i = (uint32_t)o0;
+            for (int w = 0; w < 4; ++w)
+                if (amx[w] > v || (amx[w] == v && amx[w] > -INFINITY && amn[w] < i)) {
+                    v = amx[w];
+                    i = amn[w];
                 }
-            amv[blockIdx.x] = bv;
-            ami[blockIdx.x] = bi;
+            amv[blockIdx.x] = v;
+            ami[blockIdx.x] = i;
         }
-        return;
     }
-    write_rows<R, GU, YT>(y, base, nout, acc);
 }
 
 // ------------------------------------------------------------------ generic exact kernel
@@ -952,22 +1063,40 @@ static hipError_t gemv1_q4k_t(const uint8_t* W, const void* x, bool xf32, YT* y,
     return hipGetLastError();
 }
 
+// outputs per block: about three blocks per CU, at most 32 outputs (8 per
+// wave), a multiple of 4 so every wave of a block streams the same count.
+// Measured on MI355X (bf16 x, 24 rotating weight copies, HIP graph):
+// 151936 x 4096: 32 -> 102 us (8 / 16 / 64 / 128 / 256: 123 / 110 / 107 /
+// 105 / 118); 12288 x 4096: 16 -> 13.2 us (8 / 32 / 64: 15.4 / 14.4 / 18.7);
+// 4096 x 4096: 8 -> 7.3 us (4 / 16: 8.1 / 7.5); 3072 x 1024: 4 -> 3.7 us.
+static int q8_rows_per_block(int64_t nout) {
+    const int forced = env_int("THQ_GEMV_Q8_RPB", 0);  // tuning sweeps: outputs per block (a multiple of 4)
+    if (forced >= 4 && forced % 4 == 0) return forced;
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+    }
+    int64_t rpb = (nout + 3 * (int64_t)cus - 1) / (3 * (int64_t)cus);
+    rpb = (rpb + 3) & ~(int64_t)3;
+    return (int)(rpb < 4 ? 4 : (rpb > 32 ? 32 : rpb));
+}
+
 template <int KC, bool GU, typename XT, typename YT>
 static void launch_q8_t(const int8_t* Q, const uint16_t* D, const XT* x, YT* y, int64_t nout, int K, int64_t up_off,
                         hipStream_t s, AmaxOut* am) {
-    constexpr int R = GU ? 2 : 1;
-    const int64_t waves = nout;
-    const int64_t blocks = (waves + 3) / 4;
+    const int rpb = q8_rows_per_block(nout);
+    const int64_t blocks = (nout + rpb - 1) / rpb;
     float* amv = nullptr;
     uint32_t* ami = nullptr;
-    if (am) {  // one partial per block of 4 rows (M = 1)
+    if (am) {  // one partial per block (M = 1)
         if (GU || blocks > am->ld) return;
         amv = am->v;
         ami = am->i;
         am->nb = blocks;
     }
-    hipLaunchKernelGGL((k_gemv1_q8<KC, R, GU, XT, YT>), dim3((unsigned)blocks), dim3(256), 0, s, Q, D, x, y, nout, K,
-                       up_off, amv, ami);
+    hipLaunchKernelGGL((k_gemv1_q8<KC, GU, XT, YT>), dim3((unsigned)blocks), dim3(256), 0, s, Q, D, x, y, nout, K,
+                       up_off, rpb, amv, ami);
 }
 
 template <bool GU, typename XT, typename YT>

@@ -297,10 +297,6 @@ Route plan_route(const Call& c) {
                                  ? thq::plan_gemv_mfma(v.qtype, m, w->N, w->K, c.gu)
                                  : thq::GemvPlan{};
     const bool skinny = gp.waves > 0;
-    // Q8_0 at M = 1: the one-row-per-wave VALU kernel reloads x per row; on
-    // large weights the MFMA kernel is faster (LM head 151936 x 4096:
-    // 122.7 vs 208.5 us; 12288 x 4096: 12.9 vs 17.9 us; 3072 x 1024: 11.9 vs 9.1 us)
-    const bool q8_m1_mfma = w->qtype == THQ_Q8_0 && skinny && w->N * w->K >= ((int64_t)1 << 24);
     // the 4-bit tile kernels need whole superblocks (MLX affine K % 256 != 0 runs the generic kernel)
     const bool q4 = w->qtype == THQ_Q4_K || w->qtype == THQ_MLX_Q4;
     // 2..4 bf16 rows of Q4_K / MLX affine at K <= 4096: the VALU row kernel (THQ_GEMV_ROWS=0: MFMA)
@@ -320,7 +316,9 @@ Route plan_route(const Call& c) {
                                  ? thq::plan_gemv_wide(v.qtype, m, w->N, w->K, c.ctx->cus)
                                  : thq::WidePlan{};
     const bool wide_ok = wp.splits > 0 && (w->qtype == THQ_Q8_0 || (c.flags & THQ_MODE_EXACT_W) || nout >= 65536);
-    if (m == 1 && !((m1_mfma || q8_m1_mfma) && skinny) && aligned16(c.x) &&
+    // (Q8_0 at M = 1 included: the streaming VALU kernel beats the MFMA GEMV at
+    // every size, LM head 151936 x 4096 102 vs 124 us, 3072 x 1024 3.7 vs 6.8 us)
+    if (m == 1 && !(m1_mfma && skinny) && aligned16(c.x) &&
         thq::gemv1_supported(v.qtype, (int)w->K, c.gu, w->N)) {
         r.kind = Kind::GEMV1;
     } else if (rows_on && !xf32 && aligned16(c.x) && thq::gemv_rows_supported(v.qtype, (int)m, (int)w->K, c.gu, w->N) &&
