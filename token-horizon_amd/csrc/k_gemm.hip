@@ -111,10 +111,10 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ Wq, co
             hdr.w = *reinterpret_cast<const uint32_t*>(Wq + q4k_hdword(wrow, nsb, sidx, 3));
             wr0 = *reinterpret_cast<const uint4*>(Wq + q4k_piece(wrow, nsb, sidx, wh, j));
         } else {
-            const uint4* q = reinterpret_cast<const uint4*>(Wq + wrow * K + k0 + 32 * wh);
-            wr0 = q[0];
-            wr1 = q[1];
-            dq = reinterpret_cast<const uint16_t*>(Wa)[wrow * (K >> 5) + (k0 >> 5) + wh];
+            const int64_t blk = (k0 >> 5) + wh;
+            wr0 = *reinterpret_cast<const uint4*>(Wq + q8t_q(wrow, K >> 5, blk, 0));
+            wr1 = *reinterpret_cast<const uint4*>(Wq + q8t_q(wrow, K >> 5, blk, 1));
+            dq = reinterpret_cast<const uint16_t*>(Wa)[q8t_d(wrow, K >> 5, blk)];
         }
     };
 
@@ -409,7 +409,8 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict
         } else if (QT != 8) {
             noff[i] = (uint32_t)q4k_piece(clamp_row(row), nsb, 0, hc, 0);
         } else {
-            noff[i] = (uint32_t)(clamp_row(row) * K + 32 * (hc >> 1) + 16 * (hc & 1));
+            // Q8_0 tiles: block 2 kit + (hc >> 1), half hc & 1; the step adds 2048 kit
+            noff[i] = (uint32_t)q8t_q(clamp_row(row), K >> 5, hc >> 1, hc & 1);
         }
     }
 #pragma unroll
@@ -424,7 +425,8 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict
         } else if (QT != 8) {
             hoff[i] = (uint32_t)q4k_hdword(clamp_row(j >> 2), nsb, 0, j & 3);
         } else {
-            hoff[i] = (uint32_t)(clamp_row(j) * (K >> 5) * 2);
+            // the dword of blocks 2 kit, 2 kit + 1 in the row's scale chunk kit / 4
+            hoff[i] = (uint32_t)(q8t_d(clamp_row(j), K >> 5, 0) * 2);
         }
     }
     auto xcopy = [&](int kit, int slot) {
@@ -434,8 +436,8 @@ __global__ __launch_bounds__(128 * WM) void k_gemm_dma(const uint8_t* __restrict
     };
     auto wcopy = [&](int kit, int slot) {
         const uint32_t l = wlds + slot * RAW;
-        const uint8_t* nb = Q6 ? Wq : (QT != 8 ? Wq + kit * 16 : Wq + kit * 64);
-        const uint8_t* hb = Q6 ? Wq : (QT != 8 ? Wq + (kit >> 2) * 64 : Wa + kit * 4);
+        const uint8_t* nb = Q6 ? Wq : (QT != 8 ? Wq + kit * 16 : Wq + kit * 2048);
+        const uint8_t* hb = Q6 ? Wq : (QT != 8 ? Wq + (kit >> 2) * 64 : Wa + (kit >> 2) * 512 + (kit & 3) * 4);
 #pragma unroll
         for (int i = 0; i < NI; ++i) {
             const uint32_t off = Q6 ? noff[i] + (uint32_t)kit * nstr[i] : noff[i];

@@ -687,31 +687,45 @@ __global__ __launch_bounds__(256) void k_gemv1_q4k_f32(const uint8_t* __restrict
 }
 
 // ------------------------------------------------------------------ Q8_0 M=1
-// Planes: qs [N][K] i8, d [N][K/32] f16.  A block owns the contiguous output
-// range [o0, o0 + rpb); its four waves take outputs o0 + w, o0 + w + 4, ...
-// and stream them: a wave keeps its slice of x in registers for the whole
-// range and issues the next output's loads before the current one's math, so
-// x is read from L2 once per block (staged in LDS) instead of once per row.
-// Lane l covers 16 bytes of every 1024-wide K chunk, k = 1024c + 16l (block
-// 32c + l/2): one 16-B load per chunk, a whole 1-KB run per wave instruction.
-// The row's f16 scales arrive as one dword per lane (blocks 2l, 2l + 1; a
-// second dword for K > 4096) and reach the lane that uses them through
-// ds_bpermute.  u = q ^ 0x80 is the unsigned byte q + 128; the 128 offset is
-// removed with the lane's sum of x.  bf16 x: u goes to bf16 (exact, 0..255)
-// and pairs meet x pairs in v_dot2_f32_bf16; f32 x: v_cvt_f32_ubyte and f32
-// fma.  Every product is exact in f32 either way.
+// Tile planes (thq_dev.hpp, q8t_q / q8t_d).  A wave takes one 32-row tile
+// (outputs 32t .. 32t + 31; gate/up: the gate rows and the up rows of those
+// outputs) over a range of 256-wide chunks and streams it: per chunk eight
+// contiguous 1-KB loads (block b: lane (n, g) gets row n's bytes 16g ..
+// 16g + 15) and one 16-B load of row n's eight scales.  A block's 4 waves are
+// TPB = 4 / KS tiles x KS ranges of K (KS > 1 when there are too few tiles to
+// fill the GPU); x is staged once per block in LDS with the sums of each
+// 16-value run, and each lane reads its row's 16 values per block (one
+// address per lane half: a broadcast).  u = q ^ 0x80 is the unsigned byte
+// q + 128: bf16 x meets bf16(u) (exact) pairs in v_dot2_f32_bf16, f32 x
+// v_cvt_f32_ubyte values in f32 fma; the 128 offset is removed with the sum.
+// The two lanes of a row and the KS ranges are summed in that order at the
+// end (LDS).  Fused argmax: one (max, lowest index) partial per block.
 template <typename XT>
-struct Q8XSlice;
+struct Q8TX;
 template <>
-struct Q8XSlice<bf16_t> {
-    uint32_t v[8];  // 16 bf16 as pairs
+struct Q8TX<bf16_t> {
+    uint32_t v[8];
 };
 template <>
-struct Q8XSlice<float> {
+struct Q8TX<float> {
     float v[16];
 };
-
-__device__ __forceinline__ float q8_dot16(const uint4& q, const Q8XSlice<bf16_t>& X) {
+template <typename XT>
+__device__ __forceinline__ void q8t_xload(Q8TX<XT>& X, const XT* p) {
+    if constexpr (sizeof(XT) == 2) {
+        const uint4 a = *reinterpret_cast<const uint4*>(p);
+        const uint4 b = *reinterpret_cast<const uint4*>(p + 8);
+        X.v[0] = a.x; X.v[1] = a.y; X.v[2] = a.z; X.v[3] = a.w;
+        X.v[4] = b.x; X.v[5] = b.y; X.v[6] = b.z; X.v[7] = b.w;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 f = *reinterpret_cast<const float4*>(p + 4 * i);
+            X.v[4 * i] = f.x; X.v[4 * i + 1] = f.y; X.v[4 * i + 2] = f.z; X.v[4 * i + 3] = f.w;
+        }
+    }
+}
+__device__ __forceinline__ float q8_dot16(const uint4& q, const Q8TX<bf16_t>& X) {
     const uint32_t u[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
     float s = 0.0f;
 #pragma unroll
@@ -721,7 +735,7 @@ __device__ __forceinline__ float q8_dot16(const uint4& q, const Q8XSlice<bf16_t>
     }
     return s;
 }
-__device__ __forceinline__ float q8_dot16(const uint4& q, const Q8XSlice<float>& X) {
+__device__ __forceinline__ float q8_dot16(const uint4& q, const Q8TX<float>& X) {
     const uint32_t u[4] = {q.x ^ 0x80808080u, q.y ^ 0x80808080u, q.z ^ 0x80808080u, q.w ^ 0x80808080u};
     float s = 0.0f;
 #pragma unroll
@@ -733,159 +747,164 @@ __device__ __forceinline__ float q8_dot16(const uint4& q, const Q8XSlice<float>&
     }
     return s;
 }
-
-// one weight row's loads: KC 16-B pieces and SD scale dwords per lane
-template <int KC>
-struct Q8Row {
-    uint4 q[KC];
-    uint32_t d[(KC + 3) / 4];
+// one chunk of one weight row set: 8 block pieces and the row's 8 scales
+struct Q8TChunk {
+    uint4 q[8];
+    uint4 d;
 };
-template <int KC>
-__device__ __forceinline__ void q8_row_load(Q8Row<KC>& R, const int8_t* __restrict__ Q, const uint16_t* __restrict__ D,
-                                            int64_t row, int K, int lane) {
-    const int nb = K >> 5;
-#pragma unroll
-    for (int c = 0; c < KC; ++c) {
-        const int k0 = 1024 * c + 16 * lane;
-        R.q[c] = k0 < K ? ld_stream16(Q + row * K + k0) : make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
-    }
-    const uint16_t* dr = D + row * nb;
-#pragma unroll
-    for (int j = 0; j < (KC + 3) / 4; ++j) {
-        const int b = 2 * (lane + 64 * j);  // first block of this dword
-        uint32_t v = 0;
-        if (b + 1 < nb) {
-            // rows start on a dword boundary when nb is even; otherwise two halves
-            v = (nb & 1) ? ((uint32_t)dr[b] | ((uint32_t)dr[b + 1] << 16))
-                         : *reinterpret_cast<const uint32_t*>(dr + b);
-        } else if (b < nb) {
-            v = dr[b];
-        }
-        R.d[j] = v;
-    }
-}
-// f32 dot of one row with the lane's x slices (before the cross-lane sum)
-template <int KC, typename XT>
-__device__ __forceinline__ float q8_row_dot(const Q8Row<KC>& R, const Q8XSlice<XT> (&xv)[KC], const float (&sx)[KC],
-                                            int lane) {
-    float a = 0.0f;
-#pragma unroll
-    for (int c = 0; c < KC; ++c) {
-        // block 32c + lane/2 sits in dword 16c + lane/4 (lane (16c + lane/4) % 64, register c/4)
-        const int src = ((16 * c + (lane >> 2)) & 63) << 2;
-        const uint32_t dw = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)R.d[c >> 2]);
-        const float d = f16_to_f32((uint16_t)(((lane >> 1) & 1) ? (dw >> 16) : dw));
-        a = __builtin_fmaf(d, __builtin_fmaf(-128.0f, sx[c], q8_dot16(R.q[c], xv[c])), a);
-    }
-    return a;
-}
 
-template <int KC, bool GU, typename XT, typename YT>
+constexpr int Q8T_KMAX = 8192;  // x staged in LDS: K <= 8192
+
+template <int KS, bool FULL, bool GU, typename XT, typename YT>
 __global__ __launch_bounds__(256) void k_gemv1_q8(const int8_t* __restrict__ Q, const uint16_t* __restrict__ D,
                                                  const XT* __restrict__ x, YT* __restrict__ y, int64_t nout, int K,
-                                                 int64_t up_off, int rpb, float* __restrict__ amv,
-                                                 uint32_t* __restrict__ ami) {
-    constexpr int R = GU ? 2 : 1;  // weight rows per output
-    __shared__ __attribute__((aligned(16))) XT xs[KC * 1024];
+                                                 int64_t up_off, float* __restrict__ amv, uint32_t* __restrict__ ami) {
+    constexpr int TPB = 4 / KS;  // tiles per block
+    constexpr int R = GU ? 2 : 1;
+    __shared__ __attribute__((aligned(16))) XT xs[Q8T_KMAX];
+    __shared__ float s16[Q8T_KMAX / 16];
+    __shared__ float red[KS > 1 ? KS - 1 : 1][TPB][32][R];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t o0 = (int64_t)blockIdx.x * rpb;
-    const int64_t o1 = o0 + rpb < nout ? o0 + rpb : nout;
-    auto rows_of = [&](int64_t o, int r) { return GU ? o + (r ? up_off : 0) : o; };
-
-    // the first two outputs' loads, then x (its wait covers them; vector-memory
-    // counters drain in order)
-    Q8Row<KC> A[R], B[R], C[R];
-    auto load = [&](Q8Row<KC>(&buf)[R], int64_t oo) {
-        if (oo < o1) {
+    const int n = lane & 31, g = lane >> 5;
+    const int ti = wave % TPB, ks = wave / TPB;
+    const int64_t tile = (int64_t)blockIdx.x * TPB + ti;
+    const int64_t o = tile * 32 + n;           // this lane's output
+    const bool live = o < nout;
+    const int64_t nb = K >> 5;
+    const int nch = (int)((nb + 7) >> 3);
+    const int cpk = (nch + KS - 1) / KS;
+    const int c0 = ks * cpk, c1 = c0 + cpk < nch ? c0 + cpk : nch;
+    // rows of this lane (padding rows of the last tile read zero weights)
+    int64_t rows[R];
+    rows[0] = GU ? (live ? o : 0) : o;
+    if constexpr (GU) rows[R - 1] = live ? o + up_off : 0;
+    const int8_t* pq[R];
+    const uint16_t* pd[R];
 #pragma unroll
-            for (int r = 0; r < R; ++r) q8_row_load<KC>(buf[r], Q, D, rows_of(oo, r), K, lane);
+    for (int r = 0; r < R; ++r) {
+        pq[r] = Q + q8t_q(rows[r], nb, 0, g);
+        pd[r] = D + q8t_d(rows[r], nb, 0);
+    }
+    auto load = [&](Q8TChunk (&C)[R], int c) {
+        // blocks in chunk c (FULL: K % 256 == 0, every chunk whole)
+        const int nbc = FULL ? 8 : ((int)(nb - 8 * (int64_t)c) < 8 ? (int)(nb - 8 * (int64_t)c) : 8);
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            C[r].d = *reinterpret_cast<const uint4*>(pd[r] + (int64_t)c * 256);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                C[r].q[j] = j < nbc ? *reinterpret_cast<const uint4*>(pq[r] + ((int64_t)c * 8 + j) * 1024)
+                                    : make_uint4(0x80808080u, 0x80808080u, 0x80808080u, 0x80808080u);
         }
     };
-    int64_t o = o0 + wave;
-    load(A, o);
-    load(B, o + 4);
-    if (sizeof(XT) == 2 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (K & 7) == 0) {
-        for (int i = 8 * threadIdx.x; i < KC * 1024; i += 8 * 256)
-            *reinterpret_cast<uint4*>(&xs[i]) = i < K ? *reinterpret_cast<const uint4*>(x + i) : make_uint4(0, 0, 0, 0);
+    Q8TChunk cur[R];
+    if (c0 < c1) load(cur, c0);
+    // stage x (its loads wait behind the first chunk's: counters drain in order)
+    // and the sum of each 16-value run: 2 (bf16) or 4 (f32) threads' pieces,
+    // combined by DPP within the lane pair / quad (K % 32 == 0 keeps them whole)
+    if constexpr (sizeof(XT) == 2) {
+        for (int i = 8 * threadIdx.x; i < K; i += 8 * 256) {
+            const uint4 v = *reinterpret_cast<const uint4*>(x + i);
+            *reinterpret_cast<uint4*>(&xs[i]) = v;
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            float t = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) t += bf16_to_f32(w[e] & 0xFFFFu) + bf16_to_f32(w[e] >> 16);
+            t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+            if ((threadIdx.x & 1) == 0) s16[i >> 4] = t;
+        }
     } else {
-        for (int i = threadIdx.x; i < KC * 1024; i += 256) xs[i] = i < K ? x[i] : XT(0.0f);
+        for (int i = 4 * threadIdx.x; i < K; i += 4 * 256) {
+            const float4 v = *reinterpret_cast<const float4*>(x + i);
+            *reinterpret_cast<float4*>(&xs[i]) = v;
+            float t = (v.x + v.y) + (v.z + v.w);
+            t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0xB1, 0xF, 0xF, false));  // quad_perm [1,0,3,2]
+            t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x4E, 0xF, 0xF, false));  // quad_perm [2,3,0,1]
+            if ((threadIdx.x & 3) == 0) s16[i >> 4] = t;
+        }
     }
     __syncthreads();
-    Q8XSlice<XT> xv[KC];
-    float sx[KC];
-#pragma unroll
-    for (int c = 0; c < KC; ++c) {
-        const XT* p = &xs[1024 * c + 16 * lane];
-        float sm = 0.0f;
-        if constexpr (sizeof(XT) == 2) {
-            const uint4 a = *reinterpret_cast<const uint4*>(p);
-            const uint4 b = *reinterpret_cast<const uint4*>(p + 8);
-            const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                xv[c].v[i] = w[i];
-                sm += bf16_to_f32(w[i] & 0xFFFFu);
-                sm += bf16_to_f32(w[i] >> 16);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                xv[c].v[i] = p[i];
-                sm += p[i];
-            }
-        }
-        sx[c] = sm;
-    }
 
-    // outputs o, o + 4, ... with two rows in flight ahead of the one being
-    // reduced: buffers rotate A -> B -> C, each refilled right after its math
-    float bv = -INFINITY;
-    uint32_t bi = 0xFFFFFFFFu;
-    auto finish = [&](const Q8Row<KC>(&buf)[R], int64_t oo) {
-        float acc[R];
+    float acc[R];
 #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = wave_sum(q8_row_dot<KC, XT>(buf[r], xv, sx, lane));
-        if (!GU && amv) {
-            // strict '>' in increasing output order: NaN never wins, ties keep the lower index
-            if (acc[0] > bv) {
-                bv = acc[0];
-                bi = (uint32_t)oo;
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    // each chunk's math, then the next chunk's loads into the same registers
+    // (the compiler issues them ahead where registers allow; measured faster
+    // than an explicit second buffer)
+    for (int c = c0; c < c1; ++c) {
+        const int nbc = FULL ? 8 : ((int)(nb - 8 * (int64_t)c) < 8 ? (int)(nb - 8 * (int64_t)c) : 8);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            if (j < nbc) {
+                const int64_t k0 = (8 * (int64_t)c + j) * 32 + 16 * g;
+                Q8TX<XT> X;
+                q8t_xload<XT>(X, &xs[k0]);
+                const float sx = s16[k0 >> 4];
+#pragma unroll
+                for (int r = 0; r < R; ++r) {
+                    const uint32_t dw = j < 2 ? cur[r].d.x : (j < 4 ? cur[r].d.y : (j < 6 ? cur[r].d.z : cur[r].d.w));
+                    const float d = f16_to_f32((uint16_t)((j & 1) ? (dw >> 16) : dw));
+                    acc[r] = __builtin_fmaf(d, __builtin_fmaf(-128.0f, sx, q8_dot16(cur[r].q[j], X)), acc[r]);
+                }
             }
-        } else if (lane == 0) {
-            store_y<YT>(y + oo, GU ? silu_mul(acc[0], acc[R - 1]) : acc[0]);
         }
-    };
-    for (; o < o1; o += 12) {
-        load(C, o + 8);
-        finish(A, o);
-        if (o + 4 >= o1) break;
-        load(A, o + 12);
-        finish(B, o + 4);
-        if (o + 8 >= o1) break;
-        load(B, o + 16);
-        finish(C, o + 8);
+        if (c + 1 < c1) load(cur, c + 1);
+    }
+    // the row's two lane halves, then the K ranges in order
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] += __shfl_xor(acc[r], 32, 64);
+    if constexpr (KS > 1) {
+        if (ks > 0 && g == 0) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) red[ks - 1][ti][n][r] = acc[r];
+        }
+        __syncthreads();
+        if (ks == 0) {
+#pragma unroll
+            for (int k = 0; k < KS - 1; ++k)
+#pragma unroll
+                for (int r = 0; r < R; ++r) acc[r] += red[k][ti][n][r];
+        }
     }
     if (!GU && amv) {
-        // one (max, lowest index) partial per block, as a scan from (-inf, o0)
-        __shared__ float amx[4];
-        __shared__ uint32_t amn[4];
-        if (lane == 0) {
-            amx[wave] = bv;
-            amn[wave] = bi;
+        // one (max, lowest index) partial per block: a scan from (-inf, o0)
+        // over the block's outputs (NaN never wins, ties keep the lower index)
+        __shared__ float amx[TPB];
+        __shared__ uint32_t amn[TPB];
+        float v = live ? acc[0] : -INFINITY;
+        uint32_t i = (uint32_t)o;
+        if (!(v > -INFINITY)) {
+            v = -INFINITY;
+            i = 0xFFFFFFFFu;
+        }
+#pragma unroll
+        for (int off = 16; off >= 1; off >>= 1) {
+            const float v2 = __shfl_xor(v, off, 64);
+            const uint32_t i2 = __shfl_xor(i, off, 64);
+            if (v2 > v || (v2 == v && i2 < i)) {
+                v = v2;
+                i = i2;
+            }
+        }
+        if (ks == 0 && lane == 0) {
+            amx[ti] = v;
+            amn[ti] = i;
         }
         __syncthreads();
         if (threadIdx.x == 0) {
-            float v = -INFINITY;
-            uint32_t i = (uint32_t)o0;
-            for (int w = 0; w < 4; ++w)
-                if (amx[w] > v || (amx[w] == v && amx[w] > -INFINITY && amn[w] < i)) {
-                    v = amx[w];
-                    i = amn[w];
+            float bv = -INFINITY;
+            uint32_t bi = (uint32_t)((int64_t)blockIdx.x * TPB * 32);
+            for (int t = 0; t < TPB; ++t)
+                if (amx[t] > bv || (amx[t] == bv && amx[t] > -INFINITY && amn[t] < bi)) {
+                    bv = amx[t];
+                    bi = amn[t];
                 }
-            amv[blockIdx.x] = v;
-            ami[blockIdx.x] = i;
+            amv[blockIdx.x] = bv;
+            ami[blockIdx.x] = bi;
         }
+        return;
     }
+    if (ks == 0 && g == 0 && live) store_y<YT>(y + o, GU ? silu_mul(acc[0], acc[R - 1]) : acc[0]);
 }
 
 // ------------------------------------------------------------------ generic exact kernel
@@ -954,10 +973,14 @@ __global__ __launch_bounds__(256) void k_gemv_generic(const uint8_t* __restrict_
                     for (int i = 0; i < 16; ++i) wv[16 * hh + i] = d1 * (float)((q[i] >> sh) & 0xF) - m1;
                 }
             } else {
-                const int8_t* q = reinterpret_cast<const int8_t*>(Wq) + row * K + 32 * sbi;
-                const float d = f16_to_f32(reinterpret_cast<const uint16_t*>(Wa)[row * nsub + sbi]);
+                const int8_t* q0 = reinterpret_cast<const int8_t*>(Wq) + q8t_q(row, nsub, sbi, 0);
+                const int8_t* q1 = reinterpret_cast<const int8_t*>(Wq) + q8t_q(row, nsub, sbi, 1);
+                const float d = f16_to_f32(reinterpret_cast<const uint16_t*>(Wa)[q8t_d(row, nsub, sbi)]);
 #pragma unroll
-                for (int i = 0; i < 32; ++i) wv[i] = (float)q[i] * d;
+                for (int i = 0; i < 16; ++i) {
+                    wv[i] = (float)q0[i] * d;
+                    wv[16 + i] = (float)q1[i] * d;
+                }
             }
 #pragma unroll
             for (int m = 0; m < 8; ++m) {
@@ -1063,30 +1086,16 @@ static hipError_t gemv1_q4k_t(const uint8_t* W, const void* x, bool xf32, YT* y,
     return hipGetLastError();
 }
 
-// outputs per block: about three blocks per CU, at most 32 outputs (8 per
-// wave), a multiple of 4 so every wave of a block streams the same count.
-// Measured on MI355X (bf16 x, 24 rotating weight copies, HIP graph):
-// 151936 x 4096: 32 -> 102 us (8 / 16 / 64 / 128 / 256: 123 / 110 / 107 /
-// 105 / 118); 12288 x 4096: 16 -> 13.2 us (8 / 32 / 64: 15.4 / 14.4 / 18.7);
-// 4096 x 4096: 8 -> 7.3 us (4 / 16: 8.1 / 7.5); 3072 x 1024: 4 -> 3.7 us.
-static int q8_rows_per_block(int64_t nout) {
-    const int forced = env_int("THQ_GEMV_Q8_RPB", 0);  // tuning sweeps: outputs per block (a multiple of 4)
-    if (forced >= 4 && forced % 4 == 0) return forced;
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) == hipSuccess) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
-    }
-    int64_t rpb = (nout + 3 * (int64_t)cus - 1) / (3 * (int64_t)cus);
-    rpb = (rpb + 3) & ~(int64_t)3;
-    return (int)(rpb < 4 ? 4 : (rpb > 32 ? 32 : rpb));
-}
-
-template <int KC, bool GU, typename XT, typename YT>
+// K ranges per tile: enough waves for the GPU (LM head: 4748 tiles, one
+// range; 12288 rows: 384 tiles, four ranges)
+template <bool GU, typename XT, typename YT>
 static void launch_q8_t(const int8_t* Q, const uint16_t* D, const XT* x, YT* y, int64_t nout, int K, int64_t up_off,
                         hipStream_t s, AmaxOut* am) {
-    const int rpb = q8_rows_per_block(nout);
-    const int64_t blocks = (nout + rpb - 1) / rpb;
+    const int64_t tiles = (nout + 31) / 32;
+    const int nch = (K / 32 + 7) / 8;
+    const int ks = (tiles >= 2048 || nch < 2) ? 1 : ((tiles >= 1024 || nch < 4) ? 2 : 4);
+    const int tpb = 4 / ks;
+    const int64_t blocks = (tiles + tpb - 1) / tpb;
     float* amv = nullptr;
     uint32_t* ami = nullptr;
     if (am) {  // one partial per block (M = 1)
@@ -1095,25 +1104,26 @@ static void launch_q8_t(const int8_t* Q, const uint16_t* D, const XT* x, YT* y, 
         ami = am->i;
         am->nb = blocks;
     }
-    hipLaunchKernelGGL((k_gemv1_q8<KC, GU, XT, YT>), dim3((unsigned)blocks), dim3(256), 0, s, Q, D, x, y, nout, K,
-                       up_off, rpb, amv, ami);
+#define THQ_Q8T(KS_)                                                                                            \
+    do {                                                                                                        \
+        if (K % 256 == 0)                                                                                       \
+            hipLaunchKernelGGL((k_gemv1_q8<KS_, true, GU, XT, YT>), dim3((unsigned)blocks), dim3(256), 0, s, Q, D, \
+                               x, y, nout, K, up_off, amv, ami);                                                \
+        else                                                                                                    \
+            hipLaunchKernelGGL((k_gemv1_q8<KS_, false, GU, XT, YT>), dim3((unsigned)blocks), dim3(256), 0, s, Q,   \
+                               D, x, y, nout, K, up_off, amv, ami);                                             \
+    } while (0)
+    if (ks == 1) THQ_Q8T(1);
+    else if (ks == 2) THQ_Q8T(2);
+    else THQ_Q8T(4);
+#undef THQ_Q8T
 }
 
 template <bool GU, typename XT, typename YT>
 static hipError_t gemv1_q8_t(const int8_t* Q, const uint16_t* D, const XT* x, YT* y, int64_t nout, int K,
                              int64_t up_off, hipStream_t s, AmaxOut* am) {
-    const int kc = (K + 1023) / 1024;
-    switch (kc) {
-        case 1: launch_q8_t<1, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
-        case 2: launch_q8_t<2, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
-        case 3: launch_q8_t<3, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
-        case 4: launch_q8_t<4, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
-        case 5: launch_q8_t<5, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
-        case 6: launch_q8_t<6, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
-        case 7: launch_q8_t<7, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
-        case 8: launch_q8_t<8, GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am); break;
-        default: return hipErrorInvalidValue;
-    }
+    if (K > Q8T_KMAX || K % 32) return hipErrorInvalidValue;
+    launch_q8_t<GU, XT, YT>(Q, D, x, y, nout, K, up_off, s, am);
     return hipGetLastError();
 }
 

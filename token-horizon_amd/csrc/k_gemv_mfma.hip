@@ -153,8 +153,9 @@ __global__ __launch_bounds__(512, 4) void k_gemv_mfma(const uint8_t* __restrict_
         pw = Wq + q4k_piece(row, nsb, 0, g, 0);
         ps = Wq + q4k_hdword(row, nsb, 0, 0);
     } else {
-        pw = Wq + row * K + 16 * g;
-        ps = Wa + row * (K >> 5) * 2;
+        // Q8_0 tiles: block b of the row at pw + 1024 b, chunk c's 8 scales at ps + 512 c
+        pw = Wq + q8t_q(row, K >> 5, 0, g);
+        ps = Wa + q8t_d(row, K >> 5, 0) * 2;
     }
     auto load = [&](Chunk<QT>& C, int c) {
         if constexpr (QT == 14) {
@@ -181,9 +182,9 @@ __global__ __launch_bounds__(512, 4) void k_gemv_mfma(const uint8_t* __restrict_
         } else {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                C.w[2 * u] = *reinterpret_cast<const uint4*>(pw + (int64_t)c * 256 + u * 64);
-                C.w[2 * u + 1] = *reinterpret_cast<const uint4*>(pw + (int64_t)c * 256 + u * 64 + 32);
-                C.s[u] = *reinterpret_cast<const uint32_t*>(ps + (int64_t)c * 16 + u * 4);
+                C.w[2 * u] = *reinterpret_cast<const uint4*>(pw + (int64_t)c * 8192 + u * 2048);
+                C.w[2 * u + 1] = *reinterpret_cast<const uint4*>(pw + (int64_t)c * 8192 + u * 2048 + 1024);
+                C.s[u] = *reinterpret_cast<const uint32_t*>(ps + (int64_t)c * 512 + u * 4);
             }
         }
     };

@@ -124,8 +124,9 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
         ps = Wq + L.sc + row * (K >> 4);
         pd = reinterpret_cast<const uint16_t*>(Wq + L.d) + row * (K >> 8);
     } else if constexpr (QT == 8) {
-        pw = Wq + row * K + 16 * g;
-        ps = Wa + row * (K >> 4);  // f16 scales: K/32 per row
+        // Q8_0 tiles: block b of the row at pw + 1024 b, chunk c's 8 scales at ps + 512 c
+        pw = Wq + q8t_q(row, K >> 5, 0, g);
+        ps = Wa + q8t_d(row, K >> 5, 0) * 2;
     } else {
         const int nsb = K >> 8;
         pw = Wq + q4k_piece(row, nsb, 0, g, 0);
@@ -146,10 +147,10 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
                 C.h[u] = *reinterpret_cast<const uint2*>(qhc + u * 16);
             }
         } else if constexpr (QT == 8) {
-            const uint4 sv = *reinterpret_cast<const uint4*>(ps + (int64_t)c * 16);
+            const uint4 sv = *reinterpret_cast<const uint4*>(ps + (int64_t)c * 512);
             C.s[0] = sv.x; C.s[1] = sv.y; C.s[2] = sv.z; C.s[3] = sv.w;
 #pragma unroll
-            for (int b = 0; b < 8; ++b) C.w[b] = *reinterpret_cast<const uint4*>(pw + (int64_t)c * 256 + b * 32);
+            for (int b = 0; b < 8; ++b) C.w[b] = *reinterpret_cast<const uint4*>(pw + (int64_t)c * 8192 + b * 1024);
         } else {
 #pragma unroll
             for (int u = 0; u < 4; ++u) {

@@ -435,16 +435,28 @@ __global__ __launch_bounds__(256) void k_q8act_q4k(const uint8_t* __restrict__ W
 }
 
 // Q8_0 weights x Q8_0 activations ([ext] BlockQ8_0::vec_dot: per block
-// (sum q_w q_x) * (d_w * d_x)).  Lane l of a 1024-wide chunk takes 16 bytes
-// (half a block) of each row; the lane pair forms the block's integer dot.
-// LDS: x [MT][K] i8, d [MT][K/32] f32.
-template <int MT, bool GU, typename YT>
+// (sum q_w q_x) * (d_w * d_x)) on the tile planes (thq_dev.hpp, q8t_q /
+// q8t_d).  A wave takes one 32-row tile over a range of 256-wide chunks (a
+// block's four waves: TPB = 4 / KS tiles x KS ranges of K).  Per block of K,
+// one v_mfma_i32_32x32x32_i8 forms every (activation row, weight row) block
+// integer exactly: B = the tile's 1-KB block as loaded (lane (n, g): row n's
+// 16 bytes of half g), A = the x rows' 16 bytes of the same half (LDS; lanes
+// past the call's rows hold zero).  Lane (n, g) then adds
+// (d_w * d_x) * integer for weight row n and activation rows 4g .. 4g + 3 in
+// block order; the K ranges are summed in order in LDS at the end.
+// LDS: x [MT][K] i8, d_x [K/32][8] f32.
+typedef int q8i32x4 __attribute__((ext_vector_type(4)));
+typedef int q8i32x16 __attribute__((ext_vector_type(16)));
+template <int MT, int KS, bool GU, typename YT>
 __global__ __launch_bounds__(256) void k_q8act_q8_0(const int8_t* __restrict__ Q, const uint16_t* __restrict__ D,
                                                     const int8_t* __restrict__ xq, const float* __restrict__ xd,
                                                     YT* __restrict__ y, int M, int64_t nout, int K, int64_t up_off,
                                                     int64_t ldy) {
-    constexpr int NR = GU ? 8 : 4;
+    static_assert(MT >= 1 && MT <= 8, "activation rows 4g .. 4g + 3 of the two lane halves");
+    constexpr int TPB = 4 / KS;
+    constexpr int R = GU ? 2 : 1;
     extern __shared__ uint4 lds4[];
+    __shared__ float red[KS > 1 ? KS - 1 : 1][TPB][64][4 * R];
     const int nb = K >> 5, npc = K >> 4;
     const int m0 = blockIdx.y * MT;
     const int mrows = M - m0 < MT ? M - m0 : MT;
@@ -454,51 +466,96 @@ __global__ __launch_bounds__(256) void k_q8act_q8_0(const int8_t* __restrict__ Q
         const int m = i / npc, P = i - m * npc;
         xs[i] = m < mrows ? reinterpret_cast<const uint4*>(xq + (int64_t)(m0 + m) * K)[P] : make_uint4(0u, 0u, 0u, 0u);
     }
-    for (int i = threadIdx.x; i < MT * nb; i += 256) {
-        const int m = i / nb, b = i - m * nb;
-        dxl[i] = m < mrows ? xd[(int64_t)(m0 + m) * nb + b] : 0.0f;
+    for (int i = threadIdx.x; i < nb * 8; i += 256) {
+        const int bb = i >> 3, m = i & 7;
+        dxl[i] = m < mrows ? xd[(int64_t)(m0 + m) * nb + bb] : 0.0f;
     }
     __syncthreads();
 
-    const int lane = threadIdx.x & 63;
-    const int64_t o0 = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 4;
-    int64_t rows[NR];
-    wave_rows<GU>(rows, o0, nout, up_off);
-    float acc[NR * MT];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = lane & 31, g = lane >> 5;
+    const int ti = wave % TPB, ks = wave / TPB;
+    const int64_t o = ((int64_t)blockIdx.x * TPB + ti) * 32 + n;
+    const bool live = o < nout;
+    int64_t rows[R];
+    rows[0] = GU ? (live ? o : 0) : o;  // padding rows of the last tile hold zero weights
+    if constexpr (GU) rows[R - 1] = live ? o + up_off : 0;
+    const int8_t* pq[R];
+    const uint16_t* pd[R];
 #pragma unroll
-    for (int i = 0; i < NR * MT; ++i) acc[i] = 0.0f;
-    const int nch = (K + 1023) >> 10;
-    for (int c = 0; c < nch; ++c) {
-        const int k0 = 1024 * c + 16 * lane;
-        const bool live = k0 < K;  // K is a multiple of 32: a lane pair is live together
-        const int kk = live ? k0 : K - 16;
-        const int b = kk >> 5;
-        uint4 wq[NR];
-        float dw[NR];
+    for (int r = 0; r < R; ++r) {
+        pq[r] = Q + q8t_q(rows[r], nb, 0, g);
+        pd[r] = D + q8t_d(rows[r], nb, 0);
+    }
+    const bool arow = n < mrows;  // A operand row n = activation row m0 + n
+    const int nch = (nb + 7) >> 3;
+    const int cpk = (nch + KS - 1) / KS;
+    const int c0 = ks * cpk, c1 = c0 + cpk < nch ? c0 + cpk : nch;
+    float acc[R][4];
 #pragma unroll
-        for (int r = 0; r < NR; ++r) {
-            wq[r] = *reinterpret_cast<const uint4*>(Q + rows[r] * K + kk);
-            dw[r] = f16_to_f32(D[rows[r] * nb + b]);
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[r][e] = 0.0f;
+    const q8i32x16 z16 = {};
+    q8i32x4 av = {0, 0, 0, 0};
+    for (int c = c0; c < c1; ++c) {
+        const int nbc = nb - 8 * c < 8 ? nb - 8 * c : 8;
+        uint4 dv[R];
+        uint4 q[R][8];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            dv[r] = *reinterpret_cast<const uint4*>(pd[r] + (int64_t)c * 256);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                q[r][j] = j < nbc ? *reinterpret_cast<const uint4*>(pq[r] + ((int64_t)c * 8 + j) * 1024)
+                                  : make_uint4(0u, 0u, 0u, 0u);
         }
 #pragma unroll
-        for (int m = 0; m < MT; ++m) {
-            const uint4 xv = xs[m * npc + (kk >> 4)];
-            const float dx = dxl[m * nb + b];
+        for (int j = 0; j < 8; ++j) {
+            if (j < nbc) {
+                const int bb = 8 * c + j;
+                if (arow) {
+                    const uint4 xv = xs[n * npc + 2 * bb + g];
+                    av = q8i32x4{(int)xv.x, (int)xv.y, (int)xv.z, (int)xv.w};
+                }
+                const f32x4_t dx = *reinterpret_cast<const f32x4_t*>(&dxl[bb * 8 + 4 * g]);
 #pragma unroll
-            for (int r = 0; r < NR; ++r) {
-                int sacc = sdot4(wq[r].x, xv.x, 0);
-                sacc = sdot4(wq[r].y, xv.y, sacc);
-                sacc = sdot4(wq[r].z, xv.z, sacc);
-                sacc = sdot4(wq[r].w, xv.w, sacc);
-                sacc = pair_sum(sacc);
-                const float a = __builtin_fmaf(dw[r] * dx, (float)sacc, acc[r * MT + m]);
-                acc[r * MT + m] = live ? a : acc[r * MT + m];
+                for (int r = 0; r < R; ++r) {
+                    const uint32_t w = j < 2 ? dv[r].x : (j < 4 ? dv[r].y : (j < 6 ? dv[r].z : dv[r].w));
+                    const float dw = f16_to_f32((uint16_t)((j & 1) ? (w >> 16) : w));
+                    const q8i32x4 bv = {(int)q[r][j].x, (int)q[r][j].y, (int)q[r][j].z, (int)q[r][j].w};
+                    const q8i32x16 C = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, bv, z16, 0, 0, 0);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[r][e] = __builtin_fmaf(dw * dx[e], (float)C[e], acc[r][e]);
+                }
             }
         }
     }
+    if constexpr (KS > 1) {
+        if (ks > 0) {
 #pragma unroll
-    for (int i = 0; i < NR * MT; ++i) acc[i] = (lane & 1) ? 0.0f : acc[i];  // one lane per block
-    q8act_store<MT, GU, YT>(acc, lane, y, o0, nout, m0, mrows, ldy);
+            for (int r = 0; r < R; ++r)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) red[ks - 1][ti][lane][4 * r + e] = acc[r][e];
+        }
+        __syncthreads();
+        if (ks == 0) {
+#pragma unroll
+            for (int k = 0; k < KS - 1; ++k)
+#pragma unroll
+                for (int r = 0; r < R; ++r)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[r][e] += red[k][ti][lane][4 * r + e];
+        }
+    }
+    if (ks == 0 && live) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int m = 4 * g + e;
+            if (m < mrows)
+                store_y<YT>(y + (int64_t)(m0 + m) * ldy + o, GU ? silu_mul(acc[0][e], acc[R - 1][e]) : acc[0][e]);
+        }
+    }
 }
 
 // ------------------------------------------------------------------ host side
@@ -508,7 +565,7 @@ size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 size_t lds_bytes(int qtype, int mt, int K) {
     const size_t x = (size_t)mt * K;
-    return qtype == 12 ? x + (size_t)mt * (K / 64) * 4 + (size_t)mt * (K / 256) * 4 : x + (size_t)mt * (K / 32) * 4;
+    return qtype == 12 ? x + (size_t)mt * (K / 64) * 4 + (size_t)mt * (K / 256) * 4 : x + (size_t)(K / 32) * 8 * 4;
 }
 
 int pick_mt(int qtype, int64_t M, int K) {
@@ -561,15 +618,31 @@ hipError_t quant_act_t(int qtype, const XT* x, int64_t M, int64_t K, const ActPl
 template <int MT, bool GU, typename YT>
 void launch_dot(const WeightView& w, const ActPlanes& a, YT* y, int M, int64_t nout, int64_t up_off, hipStream_t s) {
     const int K = (int)w.K;
-    const int64_t waves = (nout + 3) / 4;
-    const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)((M + MT - 1) / MT));
     const size_t lds = lds_bytes(w.qtype, MT, K);
-    if (w.qtype == 12)
+    if (w.qtype == 12) {
+        const int64_t waves = (nout + 3) / 4;
+        const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)((M + MT - 1) / MT));
         hipLaunchKernelGGL((k_q8act_q4k<MT, GU, YT>), grid, dim3(256), lds, s, w.q, a.xq, a.xd, a.xb, y, M, nout, K,
                            up_off, nout, (uint32_t*)nullptr, (int8_t*)nullptr, (float*)nullptr, (int16_t*)nullptr);
+        return;
+    }
+    // Q8_0 tiles: K ranges per tile as for the M = 1 GEMV (enough waves to fill the GPU)
+    const int64_t tiles = (nout + 31) / 32;
+    const int nch = (K / 32 + 7) / 8;
+    const int ks = (tiles >= 2048 || nch < 2) ? 1 : ((tiles >= 1024 || nch < 4) ? 2 : 4);
+    const int tpb = 4 / ks;
+    const dim3 grid((unsigned)((tiles + tpb - 1) / tpb), (unsigned)((M + MT - 1) / MT));
+    const int8_t* Q = reinterpret_cast<const int8_t*>(w.q);
+    const uint16_t* D = reinterpret_cast<const uint16_t*>(w.aux);
+    if (ks == 1)
+        hipLaunchKernelGGL((k_q8act_q8_0<MT, 1, GU, YT>), grid, dim3(256), lds, s, Q, D, a.xq, a.xd, y, M, nout, K,
+                           up_off, nout);
+    else if (ks == 2)
+        hipLaunchKernelGGL((k_q8act_q8_0<MT, 2, GU, YT>), grid, dim3(256), lds, s, Q, D, a.xq, a.xd, y, M, nout, K,
+                           up_off, nout);
     else
-        hipLaunchKernelGGL((k_q8act_q8_0<MT, GU, YT>), grid, dim3(256), lds, s, reinterpret_cast<const int8_t*>(w.q),
-                           reinterpret_cast<const uint16_t*>(w.aux), a.xq, a.xd, y, M, nout, K, up_off, nout);
+        hipLaunchKernelGGL((k_q8act_q8_0<MT, 4, GU, YT>), grid, dim3(256), lds, s, Q, D, a.xq, a.xd, y, M, nout, K,
+                           up_off, nout);
 }
 
 template <bool GU, typename YT>

@@ -1,6 +1,6 @@
 // k_weights.hip — weight preparation kernels for gfx950:
-//   * repack GGUF Q8_0 blocks (34 B, 2-byte aligned) into an aligned i8 plane
-//     [N][K] plus an f16 scale plane [N][K/32]; GGUF Q4_K blocks into the
+//   * repack GGUF Q8_0 blocks (34 B, 2-byte aligned) into the 32-row tile
+//     layout (thq_dev.hpp, q8t_q / q8t_d); GGUF Q4_K blocks into the
 //     row-quad layout (thq_dev.hpp, q4k_group)
 //   * quantize f32 weights on the device with candle's CPU rounding rules
 //     ([ext] candle-core 0.11.0 k_quants.rs BlockQ8_0/BlockQ4K::from_float,
@@ -15,18 +15,20 @@
 namespace thq {
 
 // ---------------------------------------------------------------- Q8_0 repack
+// one thread per GGUF block b = row * nb + j: scale to the f16 plane, the two
+// 16-B halves to the tile plane (thq_dev.hpp, q8t_q / q8t_d)
 __global__ __launch_bounds__(256) void k_repack_q8_0(const uint8_t* __restrict__ raw, int8_t* __restrict__ qs,
-                                                     uint16_t* __restrict__ dpl, int64_t nblocks) {
+                                                     uint16_t* __restrict__ dpl, int64_t nblocks, int64_t nb) {
     const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
+    const int64_t row = b / nb, j = b - row * nb;
     const uint16_t* src = reinterpret_cast<const uint16_t*>(raw + b * THQ_Q8_0_BYTES);  // 2-B aligned
     uint32_t w[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) w[i] = (uint32_t)src[1 + 2 * i] | ((uint32_t)src[2 + 2 * i] << 16);
-    dpl[b] = src[0];
-    uint4* dst = reinterpret_cast<uint4*>(qs + b * THQ_QK8_0);
-    dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+    dpl[q8t_d(row, nb, j)] = src[0];
+    *reinterpret_cast<uint4*>(qs + q8t_q(row, nb, j, 0)) = make_uint4(w[0], w[1], w[2], w[3]);
+    *reinterpret_cast<uint4*>(qs + q8t_q(row, nb, j, 1)) = make_uint4(w[4], w[5], w[6], w[7]);
 }
 
 // ---------------------------------------------------------------- quantize Q8_0
@@ -37,9 +39,10 @@ __device__ __forceinline__ int8_t sat_i8(float v) {
 }
 
 __global__ __launch_bounds__(256) void k_quantize_q8_0(const float* __restrict__ w, int8_t* __restrict__ qs,
-                                                       uint16_t* __restrict__ dpl, int64_t nblocks) {
+                                                       uint16_t* __restrict__ dpl, int64_t nblocks, int64_t nb) {
     const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
+    const int64_t row = b / nb, j = b - row * nb;
     const float4* src = reinterpret_cast<const float4*>(w + b * THQ_QK8_0);
     float x[32];
 #pragma unroll
@@ -55,18 +58,32 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float* __restrict__
     _Float16 dh = (_Float16)d;
     uint16_t dbits;
     __builtin_memcpy(&dbits, &dh, 2);
-    dpl[b] = dbits;
+    dpl[q8t_d(row, nb, j)] = dbits;
     uint32_t packed[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         uint32_t v = 0;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) v |= ((uint32_t)(uint8_t)sat_i8(roundf(x[4 * i + j] * id))) << (8 * j);
+        for (int t = 0; t < 4; ++t) v |= ((uint32_t)(uint8_t)sat_i8(roundf(x[4 * i + t] * id))) << (8 * t);
         packed[i] = v;
     }
-    uint4* dst = reinterpret_cast<uint4*>(qs + b * THQ_QK8_0);
-    dst[0] = make_uint4(packed[0], packed[1], packed[2], packed[3]);
-    dst[1] = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+    *reinterpret_cast<uint4*>(qs + q8t_q(row, nb, j, 0)) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
+    *reinterpret_cast<uint4*>(qs + q8t_q(row, nb, j, 1)) = make_uint4(packed[4], packed[5], packed[6], packed[7]);
+}
+
+// rows of one tile-layout Q8_0 weight into another (weight fusion): one
+// thread per (source row, block)
+__global__ __launch_bounds__(256) void k_q8_0_copy_rows(const int8_t* __restrict__ sq, const uint16_t* __restrict__ sd,
+                                                        int64_t nsrc, int8_t* __restrict__ dq, uint16_t* __restrict__ dd,
+                                                        int64_t row0, int64_t nb) {
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b >= nsrc * nb) return;
+    const int64_t row = b / nb, j = b - row * nb;
+    dd[q8t_d(row0 + row, nb, j)] = sd[q8t_d(row, nb, j)];
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+        *reinterpret_cast<uint4*>(dq + q8t_q(row0 + row, nb, j, g)) =
+            *reinterpret_cast<const uint4*>(sq + q8t_q(row, nb, j, g));
 }
 
 // ---------------------------------------------------------------- quantize Q4_K
@@ -228,15 +245,15 @@ __device__ __forceinline__ void put4(bf16_t* p, float a, float b, float c, float
 template <typename OT>
 __global__ __launch_bounds__(256) void k_dequant_q8_0(const int8_t* __restrict__ qs,
                                                       const uint16_t* __restrict__ dpl, OT* __restrict__ out,
-                                                      int64_t nblocks) {
+                                                      int64_t nblocks, int64_t nb) {
     const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= nblocks) return;
-    const float d = f16_to_f32(dpl[b]);
-    const uint4* src = reinterpret_cast<const uint4*>(qs + b * THQ_QK8_0);
+    const int64_t row = b / nb, j = b - row * nb;
+    const float d = f16_to_f32(dpl[q8t_d(row, nb, j)]);
     OT* dst = out + b * THQ_QK8_0;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const uint4 v = src[h];
+        const uint4 v = *reinterpret_cast<const uint4*>(qs + q8t_q(row, nb, j, h));
         const uint32_t w[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
         for (int i = 0; i < 4; ++i)
@@ -522,15 +539,25 @@ __global__ __launch_bounds__(256) void k_q4k_copy_rows(const uint8_t* __restrict
 // ---------------------------------------------------------------- launchers
 static inline unsigned grid_for(int64_t n, int bs) { return (unsigned)((n + bs - 1) / bs); }
 
-hipError_t launch_repack_q8_0(const uint8_t* raw, int8_t* qs, uint16_t* d, int64_t nblocks, hipStream_t s) {
+hipError_t launch_repack_q8_0(const uint8_t* raw, int8_t* qs, uint16_t* d, int64_t n, int64_t nb, hipStream_t s) {
+    const int64_t nblocks = n * nb;
     if (nblocks == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_repack_q8_0, dim3(grid_for(nblocks, 256)), dim3(256), 0, s, raw, qs, d, nblocks);
+    hipLaunchKernelGGL(k_repack_q8_0, dim3(grid_for(nblocks, 256)), dim3(256), 0, s, raw, qs, d, nblocks, nb);
     return hipGetLastError();
 }
 
-hipError_t launch_quantize_q8_0(const float* w, int8_t* qs, uint16_t* d, int64_t nblocks, hipStream_t s) {
+hipError_t launch_quantize_q8_0(const float* w, int8_t* qs, uint16_t* d, int64_t n, int64_t nb, hipStream_t s) {
+    const int64_t nblocks = n * nb;
     if (nblocks == 0) return hipSuccess;
-    hipLaunchKernelGGL(k_quantize_q8_0, dim3(grid_for(nblocks, 256)), dim3(256), 0, s, w, qs, d, nblocks);
+    hipLaunchKernelGGL(k_quantize_q8_0, dim3(grid_for(nblocks, 256)), dim3(256), 0, s, w, qs, d, nblocks, nb);
+    return hipGetLastError();
+}
+
+hipError_t launch_q8_0_copy_rows(const int8_t* sq, const uint16_t* sd, int64_t nsrc, int8_t* dq, uint16_t* dd,
+                                 int64_t row0, int64_t nb, hipStream_t s) {
+    if (nsrc * nb == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_q8_0_copy_rows, dim3(grid_for(nsrc * nb, 256)), dim3(256), 0, s, sq, sd, nsrc, dq, dd, row0,
+                       nb);
     return hipGetLastError();
 }
 
@@ -557,15 +584,16 @@ hipError_t launch_q4k_copy_rows(const uint8_t* src, int64_t n, uint8_t* dst, int
     return hipGetLastError();
 }
 
-hipError_t launch_dequant_q8_0(const int8_t* qs, const uint16_t* d, void* out, bool bf16, int64_t nblocks,
+hipError_t launch_dequant_q8_0(const int8_t* qs, const uint16_t* d, void* out, bool bf16, int64_t n, int64_t nb,
                                hipStream_t s) {
+    const int64_t nblocks = n * nb;
     if (nblocks == 0) return hipSuccess;
     if (bf16)
         hipLaunchKernelGGL(k_dequant_q8_0<bf16_t>, dim3(grid_for(nblocks, 256)), dim3(256), 0, s, qs, d,
-                           static_cast<bf16_t*>(out), nblocks);
+                           static_cast<bf16_t*>(out), nblocks, nb);
     else
         hipLaunchKernelGGL(k_dequant_q8_0<float>, dim3(grid_for(nblocks, 256)), dim3(256), 0, s, qs, d,
-                           static_cast<float*>(out), nblocks);
+                           static_cast<float*>(out), nblocks, nb);
     return hipGetLastError();
 }
 

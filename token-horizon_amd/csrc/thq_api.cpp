@@ -110,16 +110,17 @@ thq::WeightView view(const thq_weight* w) {
     return thq::WeightView{w->qtype == THQ_MLX_Q4 ? 13 : w->qtype, w->N, w->K, w->q, w->aux};
 }
 
-// device plane sizes: Q8_0 = i8 plane + f16 scale plane; Q4_K / MLX affine =
-// one row-quad plane (rows padded to a multiple of 4 and, for MLX affine, K
-// to whole superblocks; padding zero); Q6_K = the QL/QH/SC/D planes
+// device plane sizes: Q8_0 = i8 tile plane + f16 scale tile plane (rows
+// padded to a multiple of 32); Q4_K / MLX affine = one row-quad plane (rows
+// padded to a multiple of 4 and, for MLX affine, K to whole superblocks);
+// Q6_K = the QL/QH/SC/D planes.  Padding is zero.
 size_t q_plane_bytes(int qtype, int64_t n, int64_t k) {
-    if (qtype == THQ_Q8_0) return (size_t)n * (size_t)k;
+    if (qtype == THQ_Q8_0) return (size_t)thq::q8t_q_bytes(n, k);
     if (qtype == THQ_Q6_K) return thq::q6k_layout(n, k).total;
     return (size_t)((n + 3) / 4) * (size_t)((k + 255) / 256) * 576;
 }
 size_t aux_plane_bytes(int qtype, int64_t n, int64_t k) {
-    return qtype == THQ_Q8_0 ? (size_t)n * (size_t)(k / 32) * 2 : 0;
+    return qtype == THQ_Q8_0 ? (size_t)thq::q8t_d_bytes(n, k) : 0;
 }
 
 int check_dtype_shape(int dtype, int64_t n, int64_t k) {
@@ -147,8 +148,11 @@ int alloc_weight(thq_ctx* ctx, int dtype, int64_t n, int64_t k, thq_weight** out
     hipError_t e = hipMalloc((void**)&w->q, qb);
     if (e == hipSuccess && (dtype == THQ_Q4_K || dtype == THQ_MLX_Q4) && (n & 3))
         e = hipMemset(w->q, 0, qb);  // zero padding rows
+    if (e == hipSuccess && dtype == THQ_Q8_0 && (n & 31)) e = hipMemset(w->q, 0, qb);
     if (e == hipSuccess && ab) {
         e = hipMalloc((void**)&w->aux, ab);
+        // zero padding rows and the padded tail of each row's last 8-block chunk
+        if (e == hipSuccess && ((n & 31) || ((k / 32) & 7))) e = hipMemset(w->aux, 0, ab);
         if (e != hipSuccess) (void)hipFree(w->q);
     }
     if (e != hipSuccess) {
@@ -214,7 +218,7 @@ void affine_src_bytes(int64_t n, int64_t k, int gs, int tiled, size_t& wq_bytes,
 hipError_t dequant_any(const thq_weight* w, void* out, bool bf16, hipStream_t s) {
     if (w->qtype == THQ_Q8_0)
         return thq::launch_dequant_q8_0(reinterpret_cast<const int8_t*>(w->q), reinterpret_cast<const uint16_t*>(w->aux),
-                                        out, bf16, w->N * (w->K / 32), s);
+                                        out, bf16, w->N, w->K / 32, s);
     if (w->qtype == THQ_MLX_Q4) return thq::launch_dequant_affine(w->q, out, bf16, w->N, (int)w->K, s);
     if (w->qtype == THQ_Q6_K) return thq::launch_dequant_q6k(w->q, out, bf16, w->N, (int)(w->K / 256), s);
     return thq::launch_dequant_q4k(w->q, out, bf16, w->N, (int)(w->K / 256), s);
@@ -316,9 +320,12 @@ Route plan_route(const Call& c) {
                                  ? thq::plan_gemv_wide(v.qtype, m, w->N, w->K, c.ctx->cus)
                                  : thq::WidePlan{};
     const bool wide_ok = wp.splits > 0 && (w->qtype == THQ_Q8_0 || (c.flags & THQ_MODE_EXACT_W) || nout >= 65536);
-    // (Q8_0 at M = 1 included: the streaming VALU kernel beats the MFMA GEMV at
-    // every size, LM head 151936 x 4096 102 vs 124 us, 3072 x 1024 3.7 vs 6.8 us)
-    if (m == 1 && !(m1_mfma && skinny) && aligned16(c.x) &&
+    // Q8_0 at M = 1 from 12288 outputs: the MFMA GEMV on the tile layout beats
+    // the VALU kernel (bf16 x; 12288 / 24576 x 4096: 13.7 / 21.9 vs 14.0 /
+    // 23.1 us; LM head 151936 x 4096: 111 vs 125 us); below, the VALU kernel
+    // (3072 x 1024 / 4096 x 4096 / 6144 x 4096: 3.2 / 7.7 / 8.4 vs 5.7 / 8.2 / 9.7 us)
+    const bool q8_m1_mfma = w->qtype == THQ_Q8_0 && nout >= 12288;
+    if (m == 1 && !((m1_mfma || q8_m1_mfma) && skinny) && aligned16(c.x) &&
         thq::gemv1_supported(v.qtype, (int)w->K, c.gu, w->N)) {
         r.kind = Kind::GEMV1;
     } else if (rows_on && !xf32 && aligned16(c.x) && thq::gemv_rows_supported(v.qtype, (int)m, (int)w->K, c.gu, w->N) &&
@@ -522,8 +529,8 @@ int thq_weight_from_device(thq_ctx* ctx, thq_dtype dtype, const void* dev_blocks
     else if (dtype == THQ_Q6_K)
         e = thq::launch_repack_q6k(src, w->q, n, (int)(k / 256), s);
     else
-        e = thq::launch_repack_q8_0(src, reinterpret_cast<int8_t*>(w->q), reinterpret_cast<uint16_t*>(w->aux),
-                                    n * (k / 32), s);
+        e = thq::launch_repack_q8_0(src, reinterpret_cast<int8_t*>(w->q), reinterpret_cast<uint16_t*>(w->aux), n,
+                                    k / 32, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
         thq_weight_free(w);
@@ -548,7 +555,7 @@ int thq_quantize(thq_ctx* ctx, thq_dtype dtype, const float* w_dev, int64_t n, i
     if (rc) return rc;
     hipError_t e = dtype == THQ_Q8_0
                        ? thq::launch_quantize_q8_0(w_dev, reinterpret_cast<int8_t*>(w->q),
-                                                   reinterpret_cast<uint16_t*>(w->aux), n * (k / 32), s)
+                                                   reinterpret_cast<uint16_t*>(w->aux), n, k / 32, s)
                        : thq::launch_quantize_q4k(w_dev, w->q, n, (int)(k / 256), s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) {
@@ -578,7 +585,6 @@ int thq_weight_fuse(thq_ctx* ctx, const thq_weight* const* parts, int nparts, th
     int rc = alloc_weight(ctx, dtype, n, k, &w);
     if (rc) return rc;
     w->gs = parts[0]->gs;
-    size_t qoff = 0, aoff = 0;
     int64_t row0 = 0;
     for (int i = 0; i < nparts; ++i) {
         hipError_t e = hipSuccess;
@@ -593,11 +599,11 @@ int thq_weight_fuse(thq_ctx* ctx, const thq_weight* const* parts, int nparts, th
         } else if (dtype != THQ_Q8_0) {
             e = thq::launch_q4k_copy_rows(parts[i]->q, parts[i]->N, w->q, row0, (int)((k + 255) / 256), nullptr);
         } else {
-            const size_t qb = q_plane_bytes(dtype, parts[i]->N, k), ab = aux_plane_bytes(dtype, parts[i]->N, k);
-            e = hipMemcpy(w->q + qoff, parts[i]->q, qb, hipMemcpyDeviceToDevice);
-            if (e == hipSuccess) e = hipMemcpy(w->aux + aoff, parts[i]->aux, ab, hipMemcpyDeviceToDevice);
-            qoff += qb;
-            aoff += ab;
+            // tile planes: row by row (a part need not end on a tile boundary)
+            e = thq::launch_q8_0_copy_rows(reinterpret_cast<const int8_t*>(parts[i]->q),
+                                           reinterpret_cast<const uint16_t*>(parts[i]->aux), parts[i]->N,
+                                           reinterpret_cast<int8_t*>(w->q), reinterpret_cast<uint16_t*>(w->aux), row0,
+                                           k / 32, nullptr);
         }
         row0 += parts[i]->N;
         if (e != hipSuccess) {
@@ -687,11 +693,14 @@ int thq_weight_download(const thq_weight* w, void* host_blocks) {
         }
         return THQ_OK;
     }
-    const int64_t nb = w->N * (w->K / 32);
-    for (int64_t b = 0; b < nb; ++b) {
-        std::memcpy(dst + b * 34, aux.data() + 2 * b, 2);
-        std::memcpy(dst + b * 34 + 2, qs.data() + b * 32, 32);
-    }
+    const int64_t nb = w->K / 32;
+    for (int64_t n = 0; n < w->N; ++n)
+        for (int64_t j = 0; j < nb; ++j) {
+            uint8_t* blk = dst + (n * nb + j) * 34;
+            std::memcpy(blk, aux.data() + 2 * thq::q8t_d(n, nb, j), 2);
+            std::memcpy(blk + 2, qs.data() + thq::q8t_q(n, nb, j, 0), 16);
+            std::memcpy(blk + 18, qs.data() + thq::q8t_q(n, nb, j, 1), 16);
+        }
     return THQ_OK;
 }
 

@@ -2,7 +2,7 @@
 //
 // Block formats (GGML, as candle-core's k_quants stores them):
 //   Q8_0: 32 weights / 34 B  = f16 d, i8 qs[32]            (repacked on device
-//         into an i8 plane [N][K] and an f16 scale plane [N][K/32])
+//         into 32-row tiles: see q8t_q and q8t_d below)
 //   Q4_K: 256 weights / 144 B = f16 d, f16 dmin, u8 scales[12], u8 qs[128]
 //         (re-laid on device in row quads, headers re-encoded: see
 //         q4k_hdr_from_gguf and q4k_group below)
@@ -163,6 +163,28 @@ __host__ __device__ __forceinline__ int64_t q4k_piece(int64_t n, int nsb, int s,
 }
 __host__ __device__ __forceinline__ int64_t q4k_hdword(int64_t n, int nsb, int s, int p) {
     return q4k_group(n, nsb) + (int64_t)nsb * 512 + (int64_t)(4 * s + p) * 16 + 4 * (n & 3);
+}
+
+// Q8_0 device layout, tiles of 32 rows (rows padded to a multiple of 32 with
+// zero rows).  nb = K / 32 blocks per row.
+//   i8 plane:  [tile][block b][half g][row n][16 B]: row 32t + n's bytes
+//              16g .. 16g + 15 of block b.  One block of a tile is 1 KB, so a
+//              wave load with lane (n, g) reads it contiguously and each lane
+//              gets the MFMA B-operand piece of its row.
+//   f16 plane: [tile][chunk c = b / 8][row n][8]: the scales of blocks
+//              8c .. 8c + 7 of a row are 16 contiguous bytes (last chunk zero-
+//              padded when nb % 8 != 0).
+// Offsets: q8t_q in bytes of the i8 plane, q8t_d in f16 units.
+__host__ __device__ __forceinline__ int64_t q8t_chunks(int64_t nb) { return (nb + 7) >> 3; }
+__host__ __device__ __forceinline__ int64_t q8t_q(int64_t row, int64_t nb, int64_t b, int g) {
+    return (((row >> 5) * nb + b) << 10) + ((int64_t)(32 * g + (row & 31)) << 4);
+}
+__host__ __device__ __forceinline__ int64_t q8t_d(int64_t row, int64_t nb, int64_t b) {
+    return (((row >> 5) * q8t_chunks(nb) + (b >> 3)) << 8) + ((row & 31) << 3) + (b & 7);
+}
+__host__ __device__ __forceinline__ int64_t q8t_q_bytes(int64_t n, int64_t k) { return (n + 31) / 32 * 32 * k; }
+__host__ __device__ __forceinline__ int64_t q8t_d_bytes(int64_t n, int64_t k) {
+    return (n + 31) / 32 * q8t_chunks(k / 32) * 512;
 }
 
 // Streaming loads of weights that a kernel reads exactly once, where one wave

@@ -7,8 +7,8 @@
 namespace thq {
 
 // A weight as the kernels see it (device layouts; download restores GGUF bytes).
-//   Q8_0 (qtype 8):  q   = i8 plane [N][K]
-//                    aux = f16 scale plane [N][K/32]
+//   Q8_0 (qtype 8):  q   = i8 tile plane, aux = f16 scale tile plane
+//                    (32-row tiles: thq_dev.hpp, q8t_q / q8t_d)
 //   MLX affine 4-bit (qtype 13): q = the same row-quad plane with affine
 //                    headers (thq_dev.hpp, aff_scale); K may be padded to
 //                    whole superblocks (zero groups)
@@ -44,15 +44,18 @@ struct GemmPlan {
 };
 
 // weights
-hipError_t launch_repack_q8_0(const uint8_t* raw, int8_t* qs, uint16_t* d, int64_t nblocks, hipStream_t s);
-hipError_t launch_quantize_q8_0(const float* w, int8_t* qs, uint16_t* d, int64_t nblocks, hipStream_t s);
+// Q8_0: n rows of nb = K / 32 blocks, into / out of the tile planes (thq_dev.hpp, q8t_q / q8t_d)
+hipError_t launch_repack_q8_0(const uint8_t* raw, int8_t* qs, uint16_t* d, int64_t n, int64_t nb, hipStream_t s);
+hipError_t launch_quantize_q8_0(const float* w, int8_t* qs, uint16_t* d, int64_t n, int64_t nb, hipStream_t s);
+hipError_t launch_q8_0_copy_rows(const int8_t* sq, const uint16_t* sd, int64_t nsrc, int8_t* dq, uint16_t* dd,
+                                 int64_t row0, int64_t nb, hipStream_t s);
 hipError_t launch_quantize_q4k(const float* w, uint8_t* dst, int64_t n, int nsb, hipStream_t s);
 // GGUF Q4_K blocks -> row-quad plane (rows dst_row0 ..)
 hipError_t launch_repack_q4k(const uint8_t* gguf, uint8_t* dst, int64_t n, int nsb, hipStream_t s);
 // copy rows between row-quad planes (weight fusion)
 hipError_t launch_q4k_copy_rows(const uint8_t* src, int64_t n, uint8_t* dst, int64_t dst_row0, int nsb, hipStream_t s);
 // dequantization to f32 (bf16 = false) or bf16
-hipError_t launch_dequant_q8_0(const int8_t* qs, const uint16_t* d, void* out, bool bf16, int64_t nblocks,
+hipError_t launch_dequant_q8_0(const int8_t* qs, const uint16_t* d, void* out, bool bf16, int64_t n, int64_t nb,
                                hipStream_t s);
 hipError_t launch_dequant_q4k(const uint8_t* src, void* out, bool bf16, int64_t n, int nsb, hipStream_t s);
 // Q6_K (qtype 14): GGUF blocks -> planes (thq_dev.hpp, q6k_layout), dequantization
