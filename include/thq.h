@@ -132,6 +132,19 @@ int thq_quantize(thq_ctx* ctx, thq_dtype dtype, const float* w_dev, int64_t n, i
  * [gate; up].  Replaces QLin fusion (engine/src/qwen35.rs:1581-1621 fuse_lins). */
 int thq_weight_fuse(thq_ctx* ctx, const thq_weight* const* parts, int nparts, thq_weight** out);
 
+/* Give a Q4_K or MLX affine weight a second, tile-major copy (32-row tiles,
+ * built on the device from the weight's own planes; synchronous).  With it,
+ * thq_matmul runs 3..8 bf16 activation rows of a plain projection on the
+ * tile-plane decode GEMV (exact weights, whole-line loads) instead of the
+ * row-layout kernels; every other call is unchanged.  It doubles the
+ * weight's device memory, which thq_weight_free releases.  Idempotent.  Call
+ * it before the weight is shared with other threads or used by work in
+ * flight (it adds to the weight handle).  A fused weight does not inherit
+ * its parts' tile planes.  THQ_EDTYPE for other dtypes.  Replaces the
+ * engine's tiled weight repack for its few-row kernels (QLin::tiled,
+ * engine/src/qwen35.rs:629-697). */
+int thq_weight_add_tiles(thq_ctx* ctx, thq_weight* w);
+
 void thq_weight_free(thq_weight* w);
 
 /* Shape / dtype / GGUF byte size of a weight. */

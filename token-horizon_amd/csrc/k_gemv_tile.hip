@@ -1,0 +1,330 @@
+// k_gemv_tile.hip — decode GEMV for 3..8 bf16 activation rows over the Q4_K /
+// MLX affine tile plane, with exact (unrounded) weights.
+//
+// Role: the m = 2..8 projections of the reference (AffineQmpp,
+// engine/src/quant_kernel.rs:3188-3738) over a second, tile-major copy of the
+// weight, as the engine keeps its own tiled repack for those kernels
+// (QLin::tiled, engine/src/qwen35.rs:629-697).  The row-quad plane stays the
+// weight's primary copy (the M = 1 GEMV's contiguous 1-KB wave loads need it);
+// thq_weight_add_tiles builds this one on the device.
+//
+// Why a second layout.  The MFMA decode GEMV on the row-quad plane gives each
+// lane one weight row, so one wave load touches 64 cache lines in 16-B pieces
+// (each line is finished by 8 later loads): the memory pipeline backs up and
+// the stream runs at 0.25-0.3 of HBM.  In the tile plane (thq_dev.hpp,
+// q4t_record) a 32-row tile's 64-weight part is 1 KB contiguous in exactly
+// the MFMA B-operand order, so every wave load reads whole lines.
+//
+// Exactness, as in k_gemv_mfma: B = bf16(128 + q) from one v_perm per two
+// nibbles, the MFMA gives A = sum x*(128 + q) per 32-weight sub-block, and
+//   sum x*w = d1*A - (128*d1 + m1)*S         (Q4_K, d1 = d*sc, m1 = dmin*m)
+//   sum x*w = s*A - (128*s - b)*S            (MLX affine, scale s, bias b)
+// with S = sum x over the sub-block, taken while the rows are staged.
+//
+// Block: one 32-row output tile x KW waves.  The block stages rows x[0..M) of
+// its K range (KW * 512 columns) in LDS with the 32-wide sums; wave w owns two
+// superblocks of the range, issues all its weight loads (10 x 16 B per lane)
+// at entry behind the activation loads, and accumulates its rows; the waves'
+// partials are summed in LDS in wave order.  K beyond one block's range is
+// split over blockIdx.y, with f32 partials summed in split order by
+// k_split_reduce (deterministic).
+#include "thq_dev.hpp"
+#include "thq_kernels.hpp"
+
+#include <algorithm>
+#include <atomic>
+
+namespace thq {
+namespace {
+
+constexpr int TL_CPB = 2;  // superblocks per wave
+constexpr int TL_MX = 8;   // activation rows at most
+
+// row-quad plane -> tile plane, one thread per 16-B chunk of the destination
+__global__ __launch_bounds__(256) void k_repack_q4t(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst,
+                                                   int64_t n, int nsb, int64_t chunks) {
+    const int64_t c = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+    if (c >= chunks) return;
+    const int64_t rec = c / 288;
+    const int j = (int)(c % 288);
+    const int64_t t = rec / nsb;
+    const int s = (int)(rec % nsb);
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (j < 256) {
+        const int64_t row = 32 * t + (j & 31);
+        if (row < n) v = *reinterpret_cast<const uint4*>(src + q4k_piece(row, nsb, s, (j >> 5) & 1, j >> 6));
+    } else {
+        const int64_t row = 32 * t + (j - 256);
+        if (row < n) {
+            v.x = *reinterpret_cast<const uint32_t*>(src + q4k_hdword(row, nsb, s, 0));
+            v.y = *reinterpret_cast<const uint32_t*>(src + q4k_hdword(row, nsb, s, 1));
+            v.z = *reinterpret_cast<const uint32_t*>(src + q4k_hdword(row, nsb, s, 2));
+            v.w = *reinterpret_cast<const uint32_t*>(src + q4k_hdword(row, nsb, s, 3));
+        }
+    }
+    reinterpret_cast<uint4*>(dst)[c] = v;
+}
+
+__device__ __forceinline__ f32x16_t tmfma(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+// low nibbles (masked to 4 bits) of the bytes of a, b -> bf16(128 + q) x 8 (exact)
+__device__ __forceinline__ bf16x8_t tnib(uint32_t a, uint32_t b) {
+    const uint32_t C = 0x43434343u;
+    return as_bf16x8(make_uint4(__builtin_amdgcn_perm(C, a, 0x04010400u), __builtin_amdgcn_perm(C, a, 0x04030402u),
+                                __builtin_amdgcn_perm(C, b, 0x04010400u), __builtin_amdgcn_perm(C, b, 0x04030402u)));
+}
+template <int CTRL>
+__device__ __forceinline__ float tdpp_add(float v) {
+    return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+// LDS bytes of a block: x rows, 32-wide sums, the waves' partials
+constexpr size_t tile_lds_bytes(int kw, int m) {
+    return (size_t)m * (kw * TL_CPB * 256 + 8) * 2 + (size_t)kw * TL_CPB * 8 * TL_MX * 4 +
+           (size_t)(kw > 1 ? kw - 1 : 1) * 4 * 64 * 4;
+}
+
+// K: x row stride (columns); nsb: superblocks in the plane (K padded to whole
+// superblocks for MLX affine, whose padding groups are zero); the output row
+// is tile * 32 + n, stored as y[m][nout] or, with SPLIT, as partials
+// P[blockIdx.y][m][ldp].
+template <int KW, bool AFF, typename YT, bool SPLIT>
+__global__ __launch_bounds__(64 * KW) void k_gemv_q4t(const uint8_t* __restrict__ T, const bf16_t* __restrict__ X,
+                                                     void* __restrict__ Yv, int M, int K, int nsb, int64_t nout,
+                                                     int64_t ldp) {
+    constexpr int KR = KW * TL_CPB * 256;  // the block's K range (columns)
+    constexpr int XR = KR + 8;             // LDS row stride (bf16): rows start 16 B apart in bank order
+    extern __shared__ __attribute__((aligned(16))) uint8_t tl_lds[];
+    bf16_t* xs = reinterpret_cast<bf16_t*>(tl_lds);                // [M][XR]
+    float* Ss = reinterpret_cast<float*>(tl_lds + (size_t)M * XR * 2);  // [KR / 32][TL_MX]
+    float* red = Ss + (KR / 32) * TL_MX;                           // [KW - 1][4][64]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 31, g = lane >> 5;
+    const int64_t tile = blockIdx.x;
+    const int sb0 = blockIdx.y * KW * TL_CPB;
+    const int s0 = sb0 + wave * TL_CPB;
+
+    // activation rows first (their loads drain before the weight loads):
+    // thread t holds columns 8t .. 8t+7 of the block's range of each row
+    const int64_t col = (int64_t)sb0 * 256 + 8 * threadIdx.x;
+    uint4 xv[TL_MX];
+#pragma unroll
+    for (int m = 0; m < TL_MX; ++m)
+        if (m < M)
+            xv[m] = col < K ? *reinterpret_cast<const uint4*>(X + (int64_t)m * K + col) : make_uint4(0, 0, 0, 0);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    // the wave's weights: per superblock the 32 rows' headers (lane n) and
+    // the four 1-KB parts (lane (n, g): piece g of row n); superblocks past
+    // the plane read the last one and count as zero
+    uint4 hd[TL_CPB], wq[TL_CPB][4];
+#pragma unroll
+    for (int c = 0; c < TL_CPB; ++c) {
+        const int s = s0 + c < nsb ? s0 + c : nsb - 1;
+        const uint8_t* rb = T + q4t_record(tile, nsb, s);
+        hd[c] = *reinterpret_cast<const uint4*>(rb + 4096 + 16 * n);
+#pragma unroll
+        for (int p = 0; p < 4; ++p) wq[c][p] = *reinterpret_cast<const uint4*>(rb + p * 1024 + 16 * lane);
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    // stage the rows and their 32-wide sums (four threads per group); rows
+    // M .. TL_MX-1 of the sums are zero
+#pragma unroll
+    for (int m = 0; m < TL_MX; ++m) {
+        if (m < M) {
+            const uint4 v = xv[m];
+            *reinterpret_cast<uint4*>(xs + m * XR + 8 * threadIdx.x) = v;
+            const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+            bf16x2_t q[4];
+            __builtin_memcpy(q, &v, 16);
+            float t = __builtin_amdgcn_fdot2_f32_bf16(q[0], one, 0.0f, false);
+            t = __builtin_amdgcn_fdot2_f32_bf16(q[1], one, t, false);
+            t = __builtin_amdgcn_fdot2_f32_bf16(q[2], one, t, false);
+            t = __builtin_amdgcn_fdot2_f32_bf16(q[3], one, t, false);
+            t = tdpp_add<0xB1>(t);  // quad_perm [1,0,3,2]
+            t = tdpp_add<0x4E>(t);  // quad_perm [2,3,0,1]
+            if ((threadIdx.x & 3) == 0) Ss[(threadIdx.x >> 2) * TL_MX + m] = t;
+        } else if ((threadIdx.x & 3) == 0) {
+            Ss[(threadIdx.x >> 2) * TL_MX + m] = 0.0f;
+        }
+    }
+    __syncthreads();
+
+    // A operand: lane (n, g) supplies activation row n (rows >= M are zero);
+    // the output lane holds weight row n and activation rows 4g + e, e < 4
+    const bool arow = n < M;
+    const bf16_t* xa = xs + (arow ? n : 0) * XR + 16 * g + wave * TL_CPB * 256;
+    const int sbase = wave * TL_CPB * 8;
+    const f32x16_t z16 = {};
+    float tot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t M4 = 0x0F0F0F0Fu;
+#pragma unroll
+    for (int c = 0; c < TL_CPB; ++c) {
+        const uint4 hh = hd[c];
+        const bool live = s0 + c < nsb;
+        float d = 0.0f, dm = 0.0f;
+        if constexpr (!AFF) {
+            d = live ? q4k_hdr_d(hh) : 0.0f;
+            dm = live ? q4k_hdr_dmin(hh) : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int kl = c * 256 + u * 64;
+            uint4 a0 = {}, a1 = {}, a2 = {}, a3 = {};
+            if (arow) {
+                a0 = *reinterpret_cast<const uint4*>(xa + kl);
+                a1 = *reinterpret_cast<const uint4*>(xa + kl + 8);
+                a2 = *reinterpret_cast<const uint4*>(xa + kl + 32);
+                a3 = *reinterpret_cast<const uint4*>(xa + kl + 40);
+            }
+            const f32x4_t S1 = *reinterpret_cast<const f32x4_t*>(&Ss[(sbase + (kl >> 5)) * TL_MX + 4 * g]);
+            const f32x4_t S2 = *reinterpret_cast<const f32x4_t*>(&Ss[(sbase + (kl >> 5) + 1) * TL_MX + 4 * g]);
+            const uint32_t hw = u == 0 ? hh.x : (u == 1 ? hh.y : (u == 2 ? hh.z : hh.w));
+            float d1, d2, c1, c2;
+            if constexpr (AFF) {  // one 64-weight group: w = s*q + b = s*(128 + q) - (128*s - b)
+                const float sc = live ? aff_scale(hw) : 0.0f, bi = live ? aff_bias(hw) : 0.0f;
+                d1 = d2 = sc;
+                c1 = c2 = __builtin_fmaf(128.0f, sc, -bi);
+            } else {
+                d1 = d * (float)(hw & 63u);
+                d2 = d * (float)((hw >> 12) & 63u);
+                c1 = __builtin_fmaf(128.0f, d1, dm * (float)((hw >> 6) & 63u));
+                c2 = __builtin_fmaf(128.0f, d2, dm * (float)((hw >> 18) & 63u));
+            }
+            const uint4 q = wq[c][u];
+            f32x16_t A = tmfma(as_bf16x8(a0), tnib(q.x & M4, q.y & M4), z16);
+            f32x16_t B = tmfma(as_bf16x8(a2), tnib((q.x >> 4) & M4, (q.y >> 4) & M4), z16);
+            A = tmfma(as_bf16x8(a1), tnib(q.z & M4, q.w & M4), A);
+            B = tmfma(as_bf16x8(a3), tnib((q.z >> 4) & M4, (q.w >> 4) & M4), B);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                tot[e] = __builtin_fmaf(-c1, S1[e], __builtin_fmaf(d1, A[e], tot[e]));
+                tot[e] = __builtin_fmaf(-c2, S2[e], __builtin_fmaf(d2, B[e], tot[e]));
+            }
+            // one part at a time: left free, the compiler issues every part's
+            // MFMAs first and keeps all their results live
+#pragma unroll
+            for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(tot[e]));
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    if constexpr (KW > 1) {
+        if (wave > 0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) red[((wave - 1) * 4 + e) * 64 + lane] = tot[e];
+        }
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int k = 0; k < KW - 1; ++k)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) tot[e] += red[(k * 4 + e) * 64 + lane];
+        }
+    }
+    if (wave != 0) return;
+    const int64_t row = tile * 32 + n;
+    if (row >= nout) return;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int m = 4 * g + e;
+        if (m >= M) continue;
+        if (SPLIT)
+            static_cast<float*>(Yv)[((int64_t)blockIdx.y * M + m) * ldp + row] = tot[e];
+        else
+            store_y<YT>(static_cast<YT*>(Yv) + (int64_t)m * nout + row, tot[e]);
+    }
+}
+
+template <int KW, bool AFF>
+hipError_t launch_kw(const TilePlan& p, const uint8_t* T, const void* x, void* y, bool yf32, int M, int K, int nsb,
+                     int64_t nout, float* ws, hipStream_t s) {
+    const dim3 grid((unsigned)((nout + 31) / 32), (unsigned)p.splits);
+    const size_t lds = tile_lds_bytes(KW, M);
+    // more than 64 KB of dynamic LDS (8 rows, 8 waves) must be allowed per
+    // kernel and device, once
+    constexpr size_t lds_max = tile_lds_bytes(KW, TL_MX);
+    if constexpr (lds_max > 65536) {
+        static std::atomic<uint64_t> allowed{0};
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+        const uint64_t bit = 1ull << (dev & 63);
+        if (!(allowed.load() & bit)) {
+            const void* fns[3] = {(const void*)k_gemv_q4t<KW, AFF, float, true>,
+                                  (const void*)k_gemv_q4t<KW, AFF, float, false>,
+                                  (const void*)k_gemv_q4t<KW, AFF, bf16_t, false>};
+            for (const void* f : fns) {
+                const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
+                if (e != hipSuccess) return e;
+            }
+            allowed.fetch_or(bit);
+        }
+    }
+    const bf16_t* xb = static_cast<const bf16_t*>(x);
+    if (p.splits > 1) {
+        hipLaunchKernelGGL((k_gemv_q4t<KW, AFF, float, true>), grid, dim3(64 * KW), lds, s, T, xb, (void*)ws, M, K,
+                           nsb, nout, nout);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_split_reduce(ws, y, yf32, false, M, nout, 0, nout, p.splits, s);
+    }
+    if (yf32)
+        hipLaunchKernelGGL((k_gemv_q4t<KW, AFF, float, false>), grid, dim3(64 * KW), lds, s, T, xb, y, M, K, nsb, nout,
+                           nout);
+    else
+        hipLaunchKernelGGL((k_gemv_q4t<KW, AFF, bf16_t, false>), grid, dim3(64 * KW), lds, s, T, xb, y, M, K, nsb,
+                           nout, nout);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t tile_plane_bytes(int64_t n, int64_t k) { return (size_t)q4t_bytes(n, (int)((k + 255) / 256)); }
+
+hipError_t launch_repack_q4t(const uint8_t* rowquad, uint8_t* tiles, int64_t n, int64_t k, hipStream_t s) {
+    const int nsb = (int)((k + 255) / 256);
+    const int64_t chunks = (n + 31) / 32 * nsb * 288;
+    hipLaunchKernelGGL(k_repack_q4t, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, s, rowquad, tiles, n, nsb,
+                       chunks);
+    return hipGetLastError();
+}
+
+// Waves per block and K splits: the largest block (8 waves, 4096 columns)
+// whose grid still holds one block per CU; more splits only when the tiles
+// alone cannot fill the GPU.
+TilePlan plan_gemv_tile(int64_t M, int64_t N, int64_t K, int cus) {
+    TilePlan p;
+    if (M < 1 || M > TL_MX || N < 1 || K < 256) return p;
+    if (cus < 1) cus = 256;
+    const int nsb = (int)((K + 255) / 256);
+    const int64_t tiles = (N + 31) / 32;
+    int kw = 8;
+    while (kw > 1 && tiles * ((nsb + kw * TL_CPB - 1) / (kw * TL_CPB)) < cus) kw >>= 1;
+    // never more waves than superblock pairs in K
+    while (kw > 1 && (kw / 2) * TL_CPB >= nsb) kw >>= 1;
+    p.kw = kw;
+    p.splits = (nsb + kw * TL_CPB - 1) / (kw * TL_CPB);
+    p.workspace_bytes = p.splits > 1 ? (size_t)p.splits * (size_t)M * (size_t)N * sizeof(float) : 0;
+    return p;
+}
+
+hipError_t launch_gemv_tile(const TilePlan& p, const WeightView& w, const uint8_t* tiles, const void* x, void* y,
+                            bool yf32, int M, float* ws, hipStream_t s) {
+    if (p.kw == 0 || (w.qtype != 12 && w.qtype != 13)) return hipErrorInvalidValue;
+    const int nsb = (int)((w.K + 255) / 256);
+    const bool aff = w.qtype == 13;
+    switch (p.kw) {
+        case 8: return aff ? launch_kw<8, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s)
+                           : launch_kw<8, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s);
+        case 4: return aff ? launch_kw<4, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s)
+                           : launch_kw<4, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s);
+        case 2: return aff ? launch_kw<2, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s)
+                           : launch_kw<2, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s);
+        default: return aff ? launch_kw<1, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s)
+                            : launch_kw<1, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s);
+    }
+}
+
+}  // namespace thq

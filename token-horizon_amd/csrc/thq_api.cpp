@@ -54,6 +54,7 @@ struct thq_weight {
     int gs = 0;              // MLX affine group size
     uint8_t* q = nullptr;    // Q8_0 i8 plane / Q4_K and MLX affine row-quad plane / Q6_K planes
     uint8_t* aux = nullptr;  // Q8_0 f16 scale plane
+    uint8_t* tq = nullptr;   // Q4_K / MLX affine tile plane (thq_weight_add_tiles), or null
 };
 
 namespace thq {
@@ -264,12 +265,13 @@ int check_call(const Call& c) {
 
 // The kernels a call runs, and the device scratch (split-K partials or the
 // quantized activation planes) they use, known before anything launches.
-enum class Kind { NONE, Q8ACT, GEMV1, ROWS, GEMV_MFMA, GEMV_MFMA_GROUPS, WIDE, GEMM, GENERIC };
+enum class Kind { NONE, Q8ACT, GEMV1, ROWS, GEMV_TILE, GEMV_MFMA, GEMV_MFMA_GROUPS, WIDE, GEMM, GENERIC };
 struct Route {
     Kind kind = Kind::NONE;
     thq::GemvPlan gp;
     thq::GemvPlan gp_last;  // GEMV_MFMA_GROUPS: the plan of the last, partial group of rows
     thq::WidePlan wp;
+    thq::TilePlan tp;
     thq::GemmPlan gm;
     bool exact = false;
     size_t scratch = 0;
@@ -325,6 +327,23 @@ Route plan_route(const Call& c) {
     // 23.1 us; LM head 151936 x 4096: 111 vs 125 us); below, the VALU kernel
     // (3072 x 1024 / 4096 x 4096 / 6144 x 4096: 3.2 / 7.7 / 8.4 vs 5.7 / 8.2 / 9.7 us)
     const bool q8_m1_mfma = w->qtype == THQ_Q8_0 && nout >= 12288;
+    // a weight with a tile plane: 3..8 bf16 rows of a plain projection take
+    // the tile-plane GEMV (whole-line loads; THQ_TILE_MIN_M moves the lower
+    // bound, 2 makes M = 2 take it instead of the row kernel)
+    static const int tile_min_m = [] {
+        const char* e = getenv("THQ_TILE_MIN_M");
+        const int v = e && *e ? atoi(e) : 3;
+        return v < 1 ? 1 : v;
+    }();
+    const thq::TilePlan tp = (w->tq && q4 && !c.gu && !c.am && !xf32 && aligned16(c.x) && m >= tile_min_m && m <= 8)
+                                 ? thq::plan_gemv_tile(m, w->N, w->K, c.ctx->cus)
+                                 : thq::TilePlan{};
+    if (tp.kw > 0) {
+        r.kind = Kind::GEMV_TILE;
+        r.tp = tp;
+        r.scratch = tp.workspace_bytes;
+        return r;
+    }
     if (m == 1 && !((m1_mfma || q8_m1_mfma) && skinny) && aligned16(c.x) &&
         thq::gemv1_supported(v.qtype, (int)w->K, c.gu, w->N)) {
         r.kind = Kind::GEMV1;
@@ -395,6 +414,9 @@ int exec_route(const Call& c, const Route& r, void* scratch) {
             break;
         case Kind::GEMV1: e = thq::launch_gemv1(v, c.x, xf32, c.y, yf32, c.gu, nout, up_off, c.s, c.am); break;
         case Kind::ROWS: e = thq::launch_gemv_rows(v, c.x, c.y, yf32, c.gu, m, nout, up_off, c.s); break;
+        case Kind::GEMV_TILE:
+            e = thq::launch_gemv_tile(r.tp, v, w->tq, c.x, c.y, yf32, m, static_cast<float*>(scratch), c.s);
+            break;
         case Kind::GEMV_MFMA:
             e = thq::launch_gemv_mfma(r.gp, v, c.x, c.y, yf32, c.gu, m, nout, up_off, static_cast<float*>(scratch),
                                       c.s, c.am);
@@ -620,11 +642,34 @@ int thq_weight_fuse(thq_ctx* ctx, const thq_weight* const* parts, int nparts, th
     return THQ_OK;
 }
 
+int thq_weight_add_tiles(thq_ctx* ctx, thq_weight* w) {
+    if (!ctx || !w) return fail(THQ_EINVAL, "null argument");
+    if (w->qtype != THQ_Q4_K && w->qtype != THQ_MLX_Q4)
+        return fail(THQ_EDTYPE, "tile planes exist for Q4_K and MLX affine weights (dtype %d)", w->qtype);
+    if (w->device != ctx->device)
+        return fail(THQ_EINVAL, "weight on device %d, context on device %d", w->device, ctx->device);
+    if (w->tq) return THQ_OK;
+    DeviceGuard g(ctx->device);
+    const size_t bytes = thq::tile_plane_bytes(w->N, w->K);
+    uint8_t* p = nullptr;
+    hipError_t e = hipMalloc(&p, bytes);
+    if (e != hipSuccess) return fail(THQ_ENOMEM, "tile plane hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+    e = thq::launch_repack_q4t(w->q, p, w->N, w->K, nullptr);
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) {
+        (void)hipFree(p);
+        return fail(THQ_EHIP, "tile plane repack: %s", hipGetErrorString(e));
+    }
+    w->tq = p;
+    return THQ_OK;
+}
+
 void thq_weight_free(thq_weight* w) {
     if (!w) return;
     DeviceGuard g(w->device);
     if (w->q) (void)hipFree(w->q);
     if (w->aux) (void)hipFree(w->aux);
+    if (w->tq) (void)hipFree(w->tq);
     delete w;
 }
 
@@ -1141,6 +1186,19 @@ int thq_plan_gemv_wide(int dtype, int64_t m, int64_t n, int64_t k, int cus, thq_
     *out = thq_wide_plan_info{};
     out->splits = p.splits;
     out->chunks_per_split = p.cps;
+    out->workspace_bytes = (int64_t)p.workspace_bytes;
+    return THQ_OK;
+}
+
+int thq_plan_gemv_tile(int dtype, int64_t m, int64_t n, int64_t k, int cus, thq_tile_plan_info* out) {
+    if (dtype != THQ_Q4_K && dtype != THQ_MLX_Q4) return fail(THQ_EDTYPE, "tile planes: Q4_K or MLX affine (%d)", dtype);
+    if (!out) return fail(THQ_EINVAL, "null out");
+    if (m < 1 || n < 1 || k < 1) return fail(THQ_ESHAPE, "shape [%lld, %lld, %lld]", (long long)m, (long long)n,
+                                             (long long)k);
+    const thq::TilePlan p = thq::plan_gemv_tile(m, n, k, cus);
+    *out = thq_tile_plan_info{};
+    out->waves = p.kw;
+    out->splits = p.splits;
     out->workspace_bytes = (int64_t)p.workspace_bytes;
     return THQ_OK;
 }

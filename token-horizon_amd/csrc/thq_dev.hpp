@@ -165,6 +165,19 @@ __host__ __device__ __forceinline__ int64_t q4k_hdword(int64_t n, int nsb, int s
     return q4k_group(n, nsb) + (int64_t)nsb * 512 + (int64_t)(4 * s + p) * 16 + 4 * (n & 3);
 }
 
+// Q4_K / MLX affine tile plane: an optional second copy of a weight
+// (thq_weight_add_tiles), 32-row tiles for the 2..8-row decode GEMV.  Record
+// (tile t, superblock s) is 4608 contiguous bytes at (t * nsb + s) * 4608:
+//   [p][g][n][16 B]  row 32t + n's nibble bytes 32p + 16g .. + 15 of
+//                    superblock s (row-quad piece (g, s, p)); 4096 B
+//   [n][16 B]        row 32t + n's four on-device header dwords of s; 512 B
+// A wave load of part p (64 lanes x 16 B = 1 KB, lane (n, g)) reads whole
+// lines and gives each lane its MFMA B-operand piece.  Rows past N are zero.
+__host__ __device__ __forceinline__ int64_t q4t_record(int64_t tile, int nsb, int s) {
+    return (tile * nsb + s) * 4608;
+}
+__host__ __device__ __forceinline__ int64_t q4t_bytes(int64_t n, int nsb) { return (n + 31) / 32 * nsb * 4608; }
+
 // Q8_0 device layout, tiles of 32 rows (rows padded to a multiple of 32 with
 // zero rows).  nb = K / 32 blocks per row.
 //   i8 plane:  [tile][block b][half g][row n][16 B]: row 32t + n's bytes

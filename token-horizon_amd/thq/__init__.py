@@ -54,7 +54,7 @@ EXPORTS = (
     "thq_gguf_metadata_u32", "thq_gguf_metadata_f32", "thq_gguf_metadata_str", "thq_gguf_metadata_array",
     "thq_weight_from_gguf", "thq_q8act_bytes", "thq_q8act_prepare", "thq_matmul_q8act", "thq_gate_up_silu_q8act",
     "thq_plan_gemv_mfma", "thq_plan_gemm", "thq_plan_gemv_wide", "thq_matmul_noalloc", "thq_noalloc_scratch_bytes",
-    "thq_topk", "thq_matmul_topk", "thq_gate_up_silu_q8act_emit", "thq_probe_hbm_read",
+    "thq_topk", "thq_matmul_topk", "thq_gate_up_silu_q8act_emit", "thq_probe_hbm_read", "thq_weight_add_tiles", "thq_plan_gemv_tile",
 )
 
 
@@ -96,6 +96,17 @@ def plan_gemv_wide(dtype: int, m: int, n: int, k: int, cus: int = 256) -> WidePl
     return out
 
 
+class TilePlanInfo(C.Structure):
+    _fields_ = [("waves", C.c_int32), ("splits", C.c_int32), ("workspace_bytes", C.c_int64)]
+
+
+def plan_gemv_tile(dtype: int, m: int, n: int, k: int, cus: int = 256) -> TilePlanInfo:
+    """The tile-plane decode GEMV's plan (thq_plan_gemv_tile); waves == 0: no plan."""
+    out = TilePlanInfo()
+    check(lib.thq_plan_gemv_tile(dtype, m, n, k, cus, C.byref(out)))
+    return out
+
+
 def plan_gemm(dtype: int, m: int, n: int, k: int, exact: bool = False, gate_up: bool = False,
               cus: int = 256) -> GemmPlanInfo:
     """The GEMM's plan for a shape on a device with `cus` compute units (host only)."""
@@ -119,6 +130,7 @@ def _load():
         "thq_weight_from_device": ([P, I, P, i64, i64, P, PP], I),
         "thq_quantize": ([P, I, P, i64, i64, P, PP], I),
         "thq_weight_fuse": ([P, PP, I, PP], I),
+        "thq_weight_add_tiles": ([P, P], I),
         "thq_weight_free": ([P], None),
         "thq_weight_info": ([P, C.POINTER(C.c_int), C.POINTER(i64), C.POINTER(i64), C.POINTER(C.c_size_t)], I),
         "thq_weight_download": ([P, P], I),
@@ -160,6 +172,7 @@ def _load():
         "thq_plan_gemv_mfma": ([I, i64, i64, i64, I, C.POINTER(GemvPlanInfo)], I),
         "thq_plan_gemm": ([I, I, i64, i64, i64, I, I, C.POINTER(GemmPlanInfo)], I),
         "thq_plan_gemv_wide": ([I, i64, i64, i64, I, C.POINTER(WidePlanInfo)], I),
+        "thq_plan_gemv_tile": ([I, i64, i64, i64, I, C.POINTER(TilePlanInfo)], I),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
@@ -267,6 +280,13 @@ class QTensor:
         qt = cls(h, parts[0].ctx)
         qt.gs = getattr(parts[0], "gs", 0)
         return qt
+
+    def add_tiles(self) -> "QTensor":
+        """Give this Q4_K / MLX affine weight its 32-row tile plane
+        (thq_weight_add_tiles): 3..8-row plain projections then run the
+        tile-plane decode GEMV.  Returns self."""
+        check(lib.thq_weight_add_tiles(self.ctx.h, self.h))
+        return self
 
     @classmethod
     def from_affine(cls, wq, sb, n: int, k: int, gs: int = 64, tiled: bool = False,
