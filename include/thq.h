@@ -236,7 +236,9 @@ int thq_gate_up_silu_q8act_emit(thq_ctx* ctx, const thq_weight* fused, thq_dtype
  *   M == 1     decode GEMV (exact dequantized weights)
  *   M = 2..16  bf16 x with K a multiple of 256: matrix-core decode GEMV
  *              (exact weights); Q4_K / MLX affine at M = 2..4 and K <= 4096
- *              use a VALU row GEMV (exact weights) instead
+ *              use a VALU row GEMV (exact weights) instead, and a weight
+ *              with a tile plane (thq_weight_add_tiles) runs 3..8 rows of a
+ *              plain projection on the tile-plane GEMV (exact weights)
  *   M = 17..64 bf16 x with K a multiple of 256: for Q8_0, under
  *              THQ_MODE_EXACT_W, or with >= 65536 outputs (the verify LM
  *              head), a wide matrix-core GEMV that reads the weights once
