@@ -116,3 +116,28 @@ def test_tile_wrong_dtype():
     with pytest.raises(thq.ThqError) as e:
         w.add_tiles()
     assert e.value.code == thq.EDTYPE
+
+
+@pytest.mark.parametrize("kind", ["q4_k", "affine"])
+def test_tile_split_reduction_matches_reduce_launch(kind):
+    # K split over blocks: thq_matmul sums the splits in the last block of
+    # each tile (arrival counters), thq_matmul_noalloc with k_split_reduce;
+    # both in split order, so bit for bit, on repeated calls (the counters
+    # return to zero) and a smaller second M, f32 and bf16 outputs
+    n, k = 4096, 12288
+    w, ref_of, _ = make(kind, n, k, seed=1440)
+    w.add_tiles()
+    dtype = O.Q4_K if kind == "q4_k" else thq.MLX_Q4
+    for m in (8, 3, 8):
+        assert thq.plan_gemv_tile(dtype, m, n, k).splits > 1
+        xf = O.bf16_round(activations(m, k, seed=1450 + m))
+        xb = torch.from_numpy(xf).cuda().to(torch.bfloat16)
+        for dt in (torch.float32, torch.bfloat16):
+            print(f"[tile split] {kind} m={m} {dt}", flush=True)
+            got = thq.matmul(w, xb, dt)
+            ref = torch.empty_like(got)
+            thq.matmul_noalloc(w, xb, ref)
+            torch.cuda.synchronize()
+            assert torch.equal(got, ref)
+        err = rel_row_err(got.float().cpu().numpy(), ref_of(xf))
+        assert err <= 1e-2

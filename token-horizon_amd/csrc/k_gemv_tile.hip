@@ -26,8 +26,9 @@
 // superblocks of the range, issues all its weight loads (10 x 16 B per lane)
 // at entry behind the activation loads, and accumulates its rows; the waves'
 // partials are summed in LDS in wave order.  K beyond one block's range is
-// split over blockIdx.y, with f32 partials summed in split order by
-// k_split_reduce (deterministic).
+// split over blockIdx.y: f32 partials, summed in split order (deterministic)
+// by the last block of each tile to arrive, or by k_split_reduce when the
+// caller has no arrival counters.
 #include "thq_dev.hpp"
 #include "thq_kernels.hpp"
 
@@ -87,12 +88,16 @@ constexpr size_t tile_lds_bytes(int kw, int m) {
 
 // K: x row stride (columns); nsb: superblocks in the plane (K padded to whole
 // superblocks for MLX affine, whose padding groups are zero); the output row
-// is tile * 32 + n, stored as y[m][nout] or, with SPLIT, as partials
-// P[blockIdx.y][m][ldp].
+// is tile * 32 + n, stored as y[m][nout].  With SPLIT (K split over
+// blockIdx.y) each block writes f32 partials P[blockIdx.y][m][nout]; with
+// arrival counters (cnt: one per output tile, zero before the launch and
+// left zero) the last block of a tile to arrive sums them in split order
+// into y, else k_split_reduce does.
 template <int KW, bool AFF, typename YT, bool SPLIT>
 __global__ __launch_bounds__(64 * KW) void k_gemv_q4t(const uint8_t* __restrict__ T, const bf16_t* __restrict__ X,
-                                                     void* __restrict__ Yv, int M, int K, int nsb, int64_t nout,
-                                                     int64_t ldp) {
+                                                     YT* __restrict__ Y, float* __restrict__ P,
+                                                     uint32_t* __restrict__ cnt, int M, int K, int nsb,
+                                                     int64_t nout) {
     constexpr int KR = KW * TL_CPB * 256;  // the block's K range (columns)
     constexpr int XR = KR + 8;             // LDS row stride (bf16): rows start 16 B apart in bank order
     extern __shared__ __attribute__((aligned(16))) uint8_t tl_lds[];
@@ -224,25 +229,83 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_q4t(const uint8_t* __restrict_
                 for (int e = 0; e < 4; ++e) tot[e] += red[(k * 4 + e) * 64 + lane];
         }
     }
-    if (wave != 0) return;
     const int64_t row = tile * 32 + n;
-    if (row >= nout) return;
+    if constexpr (!SPLIT) {
+        if (wave != 0 || row >= nout) return;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const int m = 4 * g + e;
-        if (m >= M) continue;
-        if (SPLIT)
-            static_cast<float*>(Yv)[((int64_t)blockIdx.y * M + m) * ldp + row] = tot[e];
-        else
-            store_y<YT>(static_cast<YT*>(Yv) + (int64_t)m * nout + row, tot[e]);
+        for (int e = 0; e < 4; ++e)
+            if (4 * g + e < M) store_y<YT>(Y + (int64_t)(4 * g + e) * nout + row, tot[e]);
+    } else {
+        // partials as device-scope stores (written through to the point all
+        // XCDs share) when the last block sums them: once they have
+        // completed (vmcnt 0) the ticket, a device-scope atomic, is ordered
+        // after them, and the last block's device-scope loads see them
+        if (wave == 0 && row < nout) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int m = 4 * g + e;
+                if (m >= M) continue;
+                float* d = P + ((int64_t)blockIdx.y * M + m) * nout + row;
+                if (cnt)
+                    __hip_atomic_store(d, tot[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                else
+                    *d = tot[e];
+            }
+        }
+        if (!cnt) return;
+        __shared__ int last;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   gridDim.y - 1;
+        __syncthreads();
+        if (!last) return;
+        // the tile's outputs, one per thread: the splits' partials in split
+        // order (k_split_reduce's sum, bit for bit), loads batched 8 deep
+        const int splits = (int)gridDim.y;
+        for (int i = threadIdx.x; i < 32 * M; i += 64 * KW) {
+            const int m = i >> 5;
+            const int64_t r = tile * 32 + (i & 31);
+            if (r >= nout) continue;
+            float acc = 0.0f;
+            for (int s0 = 0; s0 < splits; s0 += 8) {
+                float v[8];
+#pragma unroll
+                for (int b = 0; b < 8; ++b)
+                    v[b] = s0 + b < splits ? __hip_atomic_load(P + ((int64_t)(s0 + b) * M + m) * nout + r,
+                                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                           : 0.0f;
+#pragma unroll
+                for (int b = 0; b < 8; ++b)
+                    if (s0 + b < splits) acc += v[b];
+            }
+            store_y<YT>(Y + (int64_t)m * nout + r, acc);
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+}
+
+template <int KW, bool AFF, typename YT>
+hipError_t launch_kwy(const TilePlan& p, const uint8_t* T, const bf16_t* x, YT* y, int M, int K, int nsb,
+                      int64_t nout, float* ws, uint32_t* cnt, hipStream_t s) {
+    const dim3 grid((unsigned)((nout + 31) / 32), (unsigned)p.splits);
+    const size_t lds = tile_lds_bytes(KW, M);
+    if (p.splits == 1) {
+        hipLaunchKernelGGL((k_gemv_q4t<KW, AFF, YT, false>), grid, dim3(64 * KW), lds, s, T, x, y, (float*)nullptr,
+                           (uint32_t*)nullptr, M, K, nsb, nout);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL((k_gemv_q4t<KW, AFF, YT, true>), grid, dim3(64 * KW), lds, s, T, x, y, ws, cnt, M, K, nsb,
+                       nout);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || cnt) return e;
+    return launch_split_reduce(ws, y, sizeof(YT) == 4, false, M, nout, 0, nout, p.splits, s);
 }
 
 template <int KW, bool AFF>
 hipError_t launch_kw(const TilePlan& p, const uint8_t* T, const void* x, void* y, bool yf32, int M, int K, int nsb,
-                     int64_t nout, float* ws, hipStream_t s) {
-    const dim3 grid((unsigned)((nout + 31) / 32), (unsigned)p.splits);
-    const size_t lds = tile_lds_bytes(KW, M);
+                     int64_t nout, float* ws, uint32_t* cnt, hipStream_t s) {
     // more than 64 KB of dynamic LDS (8 rows, 8 waves) must be allowed per
     // kernel and device, once
     constexpr size_t lds_max = tile_lds_bytes(KW, TL_MX);
@@ -252,8 +315,9 @@ hipError_t launch_kw(const TilePlan& p, const uint8_t* T, const void* x, void* y
         if (hipGetDevice(&dev) != hipSuccess) dev = 0;
         const uint64_t bit = 1ull << (dev & 63);
         if (!(allowed.load() & bit)) {
-            const void* fns[3] = {(const void*)k_gemv_q4t<KW, AFF, float, true>,
+            const void* fns[4] = {(const void*)k_gemv_q4t<KW, AFF, float, true>,
                                   (const void*)k_gemv_q4t<KW, AFF, float, false>,
+                                  (const void*)k_gemv_q4t<KW, AFF, bf16_t, true>,
                                   (const void*)k_gemv_q4t<KW, AFF, bf16_t, false>};
             for (const void* f : fns) {
                 const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
@@ -263,20 +327,8 @@ hipError_t launch_kw(const TilePlan& p, const uint8_t* T, const void* x, void* y
         }
     }
     const bf16_t* xb = static_cast<const bf16_t*>(x);
-    if (p.splits > 1) {
-        hipLaunchKernelGGL((k_gemv_q4t<KW, AFF, float, true>), grid, dim3(64 * KW), lds, s, T, xb, (void*)ws, M, K,
-                           nsb, nout, nout);
-        hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-        return launch_split_reduce(ws, y, yf32, false, M, nout, 0, nout, p.splits, s);
-    }
-    if (yf32)
-        hipLaunchKernelGGL((k_gemv_q4t<KW, AFF, float, false>), grid, dim3(64 * KW), lds, s, T, xb, y, M, K, nsb, nout,
-                           nout);
-    else
-        hipLaunchKernelGGL((k_gemv_q4t<KW, AFF, bf16_t, false>), grid, dim3(64 * KW), lds, s, T, xb, y, M, K, nsb,
-                           nout, nout);
-    return hipGetLastError();
+    if (yf32) return launch_kwy<KW, AFF, float>(p, T, xb, static_cast<float*>(y), M, K, nsb, nout, ws, cnt, s);
+    return launch_kwy<KW, AFF, bf16_t>(p, T, xb, static_cast<bf16_t*>(y), M, K, nsb, nout, ws, cnt, s);
 }
 
 }  // namespace
@@ -311,19 +363,19 @@ TilePlan plan_gemv_tile(int64_t M, int64_t N, int64_t K, int cus) {
 }
 
 hipError_t launch_gemv_tile(const TilePlan& p, const WeightView& w, const uint8_t* tiles, const void* x, void* y,
-                            bool yf32, int M, float* ws, hipStream_t s) {
+                            bool yf32, int M, float* ws, uint32_t* cnt, hipStream_t s) {
     if (p.kw == 0 || (w.qtype != 12 && w.qtype != 13)) return hipErrorInvalidValue;
     const int nsb = (int)((w.K + 255) / 256);
     const bool aff = w.qtype == 13;
     switch (p.kw) {
-        case 8: return aff ? launch_kw<8, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s)
-                           : launch_kw<8, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s);
-        case 4: return aff ? launch_kw<4, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s)
-                           : launch_kw<4, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s);
-        case 2: return aff ? launch_kw<2, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s)
-                           : launch_kw<2, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s);
-        default: return aff ? launch_kw<1, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s)
-                            : launch_kw<1, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, s);
+        case 8: return aff ? launch_kw<8, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s)
+                           : launch_kw<8, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s);
+        case 4: return aff ? launch_kw<4, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s)
+                           : launch_kw<4, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s);
+        case 2: return aff ? launch_kw<2, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s)
+                           : launch_kw<2, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s);
+        default: return aff ? launch_kw<1, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s)
+                            : launch_kw<1, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s);
     }
 }
 

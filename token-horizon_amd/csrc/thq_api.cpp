@@ -44,6 +44,10 @@ struct thq_ctx {
     // (each launch leaves them zero); grown like the workspace
     uint32_t* emit_cnt = nullptr;
     size_t emit_cnt_n = 0;
+    // arrival counters of the tile-plane GEMV's last-block split reduction:
+    // zero between launches; grown like the workspace
+    uint32_t* tile_cnt = nullptr;
+    size_t tile_cnt_n = 0;
 };
 
 struct thq_weight {
@@ -182,6 +186,25 @@ int ensure_ws(thq_ctx* ctx, size_t bytes) {
 }
 
 size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// n zeroed arrival counters of the context (caller holds ctx->mu), grown by
+// a synchronous allocation and clear like the workspace; null if that fails
+// (the caller then takes the path without counters)
+uint32_t* tile_counters(thq_ctx* ctx, int64_t n) {
+    if ((size_t)n <= ctx->tile_cnt_n) return ctx->tile_cnt;
+    const size_t want = std::max((size_t)n + (size_t)n / 8, 2 * ctx->tile_cnt_n);
+    uint32_t* p = nullptr;
+    hipError_t e = hipMalloc((void**)&p, want * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMemset(p, 0, want * sizeof(uint32_t));
+    if (e != hipSuccess) {
+        if (p) (void)hipFree(p);
+        return nullptr;
+    }
+    if (ctx->tile_cnt) ctx->retired.push_back(ctx->tile_cnt);
+    ctx->tile_cnt = p;
+    ctx->tile_cnt_n = want;
+    return p;
+}
 
 struct DeviceGuard {
     int prev = -1;
@@ -398,8 +421,10 @@ Route plan_route(const Call& c) {
     return r;
 }
 
-// Launch a planned route; `scratch` holds at least r.scratch bytes.
-int exec_route(const Call& c, const Route& r, void* scratch) {
+// Launch a planned route; `scratch` holds at least r.scratch bytes; `cnt`:
+// zeroed arrival counters for the routes that reduce K splits in their last
+// block (null: those routes launch a separate reduce).
+int exec_route(const Call& c, const Route& r, void* scratch, uint32_t* cnt = nullptr) {
     const thq_weight* w = c.w;
     const thq::WeightView v = view(w);
     const bool xf32 = c.xt == THQ_ACT_F32, yf32 = c.yt == THQ_ACT_F32;
@@ -415,7 +440,7 @@ int exec_route(const Call& c, const Route& r, void* scratch) {
         case Kind::GEMV1: e = thq::launch_gemv1(v, c.x, xf32, c.y, yf32, c.gu, nout, up_off, c.s, c.am); break;
         case Kind::ROWS: e = thq::launch_gemv_rows(v, c.x, c.y, yf32, c.gu, m, nout, up_off, c.s); break;
         case Kind::GEMV_TILE:
-            e = thq::launch_gemv_tile(r.tp, v, w->tq, c.x, c.y, yf32, m, static_cast<float*>(scratch), c.s);
+            e = thq::launch_gemv_tile(r.tp, v, w->tq, c.x, c.y, yf32, m, static_cast<float*>(scratch), cnt, c.s);
             break;
         case Kind::GEMV_MFMA:
             e = thq::launch_gemv_mfma(r.gp, v, c.x, c.y, yf32, c.gu, m, nout, up_off, static_cast<float*>(scratch),
@@ -458,7 +483,9 @@ int run_matmul(const Call& c) {
         rc = ensure_ws(c.ctx, r.scratch);
         if (rc) return rc;
     }
-    return exec_route(c, r, c.ctx->ws);
+    uint32_t* cnt = nullptr;
+    if (r.kind == Kind::GEMV_TILE && r.tp.splits > 1) cnt = tile_counters(c.ctx, (c.w->N + 31) / 32);
+    return exec_route(c, r, c.ctx->ws, cnt);
 }
 
 }  // namespace
@@ -494,16 +521,13 @@ int thq_init(int device, thq_ctx** out) {
 
 void thq_destroy(thq_ctx* ctx) {
     if (!ctx) return;
-    if (ctx->ws) {
+    if (ctx->ws || ctx->emit_cnt || ctx->tile_cnt || !ctx->retired.empty()) {
         DeviceGuard g(ctx->device);
         (void)hipDeviceSynchronize();
-        (void)hipFree(ctx->ws);
+        if (ctx->ws) (void)hipFree(ctx->ws);
+        if (ctx->emit_cnt) (void)hipFree(ctx->emit_cnt);
+        if (ctx->tile_cnt) (void)hipFree(ctx->tile_cnt);
         for (void* p : ctx->retired) (void)hipFree(p);
-    }
-    if (ctx->emit_cnt) {
-        DeviceGuard g(ctx->device);
-        (void)hipDeviceSynchronize();
-        (void)hipFree(ctx->emit_cnt);
     }
     delete ctx;
 }

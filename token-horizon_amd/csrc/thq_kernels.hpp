@@ -117,8 +117,11 @@ struct TilePlan {
     size_t workspace_bytes = 0;   // split partials (f32 [splits][M][N])
 };
 TilePlan plan_gemv_tile(int64_t M, int64_t N, int64_t K, int cus);
+// cnt: null, or ceil(N / 32) u32 arrival counters that are zero (and stay
+// zero after the launch) for the last-block reduction of K splits;
+// without them a split plan runs k_split_reduce after the kernel
 hipError_t launch_gemv_tile(const TilePlan& p, const WeightView& w, const uint8_t* tiles, const void* x, void* y,
-                            bool yf32, int M, float* ws, hipStream_t s);
+                            bool yf32, int M, float* ws, uint32_t* cnt, hipStream_t s);
 // sum split partials P[s][M][ldp] in split order, then the epilogue
 hipError_t launch_split_reduce(const float* P, void* y, bool yf32, bool gu, int M, int64_t nout, int64_t up_off,
                                int64_t ldp, int splits, hipStream_t s);
