@@ -136,7 +136,9 @@ int thq_weight_fuse(thq_ctx* ctx, const thq_weight* const* parts, int nparts, th
  * built on the device from the weight's own planes; synchronous).  With it,
  * thq_matmul runs 3..8 bf16 activation rows of a plain projection on the
  * tile-plane decode GEMV (exact weights, whole-line loads) instead of the
- * row-layout kernels; every other call is unchanged.  It doubles the
+ * row-layout kernels, and so does thq_gate_up_silu on a fused [gate; up]
+ * weight whose halves are whole 32-row tiles; every other call is
+ * unchanged.  It doubles the
  * weight's device memory, which thq_weight_free releases.  Idempotent.  Call
  * it before the weight is shared with other threads or used by work in
  * flight (it adds to the weight handle).  A fused weight does not inherit
@@ -237,8 +239,8 @@ int thq_gate_up_silu_q8act_emit(thq_ctx* ctx, const thq_weight* fused, thq_dtype
  *   M = 2..16  bf16 x with K a multiple of 256: matrix-core decode GEMV
  *              (exact weights); Q4_K / MLX affine at M = 2..4 and K <= 4096
  *              use a VALU row GEMV (exact weights) instead, and a weight
- *              with a tile plane (thq_weight_add_tiles) runs 3..8 rows of a
- *              plain projection on the tile-plane GEMV (exact weights)
+ *              with a tile plane (thq_weight_add_tiles) runs 3..8 rows on
+ *              the tile-plane GEMV (exact weights)
  *   M = 17..64 bf16 x with K a multiple of 256: for Q8_0, under
  *              THQ_MODE_EXACT_W, or with >= 65536 outputs (the verify LM
  *              head), a wide matrix-core GEMV that reads the weights once

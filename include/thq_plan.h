@@ -69,14 +69,17 @@ int thq_plan_gemv_wide(int dtype, int64_t m, int64_t n, int64_t k, int cus, thq_
 
 /* Tile-plane decode GEMV (3..8 bf16 rows of a Q4_K / MLX affine weight
  * with a tile plane, thq_weight_add_tiles), for a device with `cus` compute
- * units; waves 0 for shapes it does not cover (M outside 1..8, K < 256). */
+ * units; gate_up: the fused [gate; up] weight of thq_gate_up_silu (n rows,
+ * n / 2 outputs).  waves 0 for shapes it does not cover (M outside 1..8,
+ * K < 256, gate/up halves that are not whole 32-row tiles). */
 typedef struct thq_tile_plan_info {
     int32_t waves;            /* waves per block (0: the shape has no plan)        */
     int32_t splits;           /* K splits (partials summed by a reduce launch)      */
     int64_t workspace_bytes;  /* split partials, f32 [splits][M][N]                 */
 } thq_tile_plan_info;
 
-int thq_plan_gemv_tile(int dtype, int64_t m, int64_t n, int64_t k, int cus, thq_tile_plan_info* out);
+int thq_plan_gemv_tile(int dtype, int64_t m, int64_t n, int64_t k, int gate_up, int cus,
+                       thq_tile_plan_info* out);
 
 /* Measurement aid: read `bytes` (a multiple of 16) of buf_dev (16-byte
  * aligned) once with 16-B loads from `blocks` blocks of 256 threads, on

@@ -9,15 +9,17 @@ reduce, K = 12288 (three splits), the one-split 8-wave instance (12288 rows),
 and MLX affine K that is not a multiple of 256 (zero padding groups, x
 masked past K).  The tile route's plan exists for every case and agrees with
 the row-layout kernels to f32 summation order; bf16 output is the f32 result
-rounded once; the weight's GGUF bytes are unchanged; gate/up, 1..2 and 9..16
-rows keep their row-layout routes on the same weight.
+rounded once; the weight's GGUF bytes are unchanged; 1..2 and 9..16 rows and
+gate/up halves that are not whole tiles keep their row-layout routes.  Gate/up
+(silu(g)*u over the [gate; up] weight) on the tile plane matches the oracle's
+epilogue and the row-layout kernels' outputs.
 """
 import numpy as np
 import pytest
 import torch
 
 import oracle as O
-from helpers import activations, rand_qlin_fast, rel_row_err, weight_bytes
+from helpers import activations, assert_close_elem, rand_qlin_fast, rel_row_err, weight_bytes
 
 pytestmark = pytest.mark.gpu
 
@@ -100,14 +102,54 @@ def test_tile_keeps_bytes_and_other_routes():
         got = thq.matmul(w, torch.from_numpy(xf).cuda().to(torch.bfloat16), torch.float32)
         torch.cuda.synchronize()
         assert rel_row_err(got.cpu().numpy(), ref_of(xf)) <= 1e-4, f"m={m}"
-    # gate/up over a fused weight with a tile plane keeps its own kernels
-    bg, bu = weight_bytes(O.Q4_K, 256, k, seed=1420), weight_bytes(O.Q4_K, 256, k, seed=1421)
-    fused = thq.QTensor.from_gguf_bytes(O.Q4_K, np.concatenate([bg, bu]), 512, k)
+    # gate/up halves that are not whole tiles (nout = 200) keep their own kernels
+    bg, bu = weight_bytes(O.Q4_K, 200, k, seed=1420), weight_bytes(O.Q4_K, 200, k, seed=1421)
+    fused = thq.QTensor.from_gguf_bytes(O.Q4_K, np.concatenate([bg, bu]), 400, k)
     fused.add_tiles()
     xf = O.bf16_round(activations(5, k, seed=1422))
     got = thq.gate_up_silu(fused, torch.from_numpy(xf).cuda().to(torch.bfloat16), torch.float32).cpu().numpy()
-    want = O.bf16_bits_to_f32(O.gate_up_silu(O.matmul(O.Q4_K, np.concatenate([bg, bu]), 512, k, xf)))
+    want = O.bf16_bits_to_f32(O.gate_up_silu(O.matmul(O.Q4_K, np.concatenate([bg, bu]), 400, k, xf)))
     assert rel_row_err(got, want) <= 1e-2
+
+
+# gate/up on the tile plane: (outputs per half, K, rows); one split of
+# 4-wave blocks would not fill the GPU at 256 outputs, K = 12288 splits
+GU_CASES = [(256, 2048, (3, 8)), (4096, 4096, (3, 5, 8)), (1024, 12288, (4, 8))]
+
+
+@pytest.mark.parametrize("kind", ["q4_k", "affine"])
+@pytest.mark.parametrize("case", range(len(GU_CASES)))
+def test_tile_gate_up(kind, case):
+    h, k, rows = GU_CASES[case]
+    if kind == "affine":
+        wq, sb = rand_qlin_fast(2 * h, k, seed=1460 + case)
+        fused = thq.QTensor.from_affine(wq, sb, 2 * h, k)
+        ref_of = lambda xf: O.affine_matmul(wq, sb, 2 * h, k, xf)
+    else:
+        b = np.concatenate([weight_bytes(O.Q4_K, h, k, seed=1460 + case), weight_bytes(O.Q4_K, h, k, seed=1470 + case)])
+        fused = thq.QTensor.from_gguf_bytes(O.Q4_K, b, 2 * h, k)
+        ref_of = lambda xf: O.matmul(O.Q4_K, b, 2 * h, k, xf)
+    base = {}
+    for m in rows:
+        xf = O.bf16_round(activations(m, k, seed=1480 + m))
+        base[m] = thq.gate_up_silu(fused, torch.from_numpy(xf).cuda().to(torch.bfloat16), torch.float32)
+    fused.add_tiles()
+    for m in rows:
+        print(f"[tile gate/up] {kind} 2x{h}x{k} m={m}", flush=True)
+        xf = O.bf16_round(activations(m, k, seed=1480 + m))
+        xb = torch.from_numpy(xf).cuda().to(torch.bfloat16)
+        got = thq.gate_up_silu(fused, xb, torch.float32)
+        got16 = thq.gate_up_silu(fused, xb, torch.bfloat16)
+        torch.cuda.synchronize()
+        g = got.cpu().numpy()
+        # the epilogue bf16(silu(bf16 g) * bf16 u) over the oracle's f64 gate / up
+        want = O.bf16_bits_to_f32(O.gate_up_silu(ref_of(xf)))
+        assert rel_row_err(g, want) <= 1e-2, f"{kind} m={m}"
+        # against the row-layout kernels (exact weights too): the bf16-rounded
+        # g and u agree except where f32 summation order crosses a rounding
+        # boundary, one bf16 step of the output at most
+        assert_close_elem(f"{kind} m={m} vs row layout", g, base[m].cpu().numpy(), 2.0 ** -7)
+        assert torch.equal(got16, got.to(torch.bfloat16))
 
 
 def test_tile_wrong_dtype():

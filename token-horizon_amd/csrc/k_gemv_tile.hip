@@ -34,6 +34,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <cstdlib>
 
 namespace thq {
 namespace {
@@ -80,30 +81,35 @@ __device__ __forceinline__ float tdpp_add(float v) {
     return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-// LDS bytes of a block: x rows, 32-wide sums, the waves' partials
-constexpr size_t tile_lds_bytes(int kw, int m) {
+// LDS bytes of a block: x rows, 32-wide sums, the waves' partials (nt tiles)
+constexpr size_t tile_lds_bytes(int kw, int m, int nt) {
     return (size_t)m * (kw * TL_CPB * 256 + 8) * 2 + (size_t)kw * TL_CPB * 8 * TL_MX * 4 +
-           (size_t)(kw > 1 ? kw - 1 : 1) * 4 * 64 * 4;
+           (size_t)(kw > 1 ? kw - 1 : 1) * nt * 4 * 64 * 4;
 }
 
 // K: x row stride (columns); nsb: superblocks in the plane (K padded to whole
-// superblocks for MLX affine, whose padding groups are zero); the output row
-// is tile * 32 + n, stored as y[m][nout].  With SPLIT (K split over
-// blockIdx.y) each block writes f32 partials P[blockIdx.y][m][nout]; with
-// arrival counters (cnt: one per output tile, zero before the launch and
-// left zero) the last block of a tile to arrive sums them in split order
-// into y, else k_split_reduce does.
-template <int KW, bool AFF, typename YT, bool SPLIT>
+// superblocks for MLX affine, whose padding groups are zero).  Plain: block
+// x owns weight rows 32x .. 32x+31 = outputs, stored as y[m][nout].  Gate/up
+// (GU, nout a multiple of 32): block x owns gate rows 32x .. and up rows
+// nout + 32x .. of the [gate; up] weight, and stores silu(g)*u (the
+// epilogue of every kernel, silu_mul) for outputs 32x ...  With SPLIT (K
+// split over blockIdx.y) each block writes f32 partials P[blockIdx.y][m][ldp]
+// (ldp = nout, or 2 nout with the up rows at nout + o); with arrival
+// counters (cnt: one per output tile, zero before the launch and left zero)
+// the last block of a tile to arrive sums them in split order into y, else
+// k_split_reduce does.
+template <int KW, bool AFF, bool GU, typename YT, bool SPLIT>
 __global__ __launch_bounds__(64 * KW) void k_gemv_q4t(const uint8_t* __restrict__ T, const bf16_t* __restrict__ X,
                                                      YT* __restrict__ Y, float* __restrict__ P,
                                                      uint32_t* __restrict__ cnt, int M, int K, int nsb,
                                                      int64_t nout) {
+    constexpr int NT = GU ? 2 : 1;         // weight tiles per block
     constexpr int KR = KW * TL_CPB * 256;  // the block's K range (columns)
     constexpr int XR = KR + 8;             // LDS row stride (bf16): rows start 16 B apart in bank order
     extern __shared__ __attribute__((aligned(16))) uint8_t tl_lds[];
     bf16_t* xs = reinterpret_cast<bf16_t*>(tl_lds);                // [M][XR]
     float* Ss = reinterpret_cast<float*>(tl_lds + (size_t)M * XR * 2);  // [KR / 32][TL_MX]
-    float* red = Ss + (KR / 32) * TL_MX;                           // [KW - 1][4][64]
+    float* red = Ss + (KR / 32) * TL_MX;                           // [KW - 1][NT][4][64]
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int n = lane & 31, g = lane >> 5;
@@ -121,17 +127,21 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_q4t(const uint8_t* __restrict_
             xv[m] = col < K ? *reinterpret_cast<const uint4*>(X + (int64_t)m * K + col) : make_uint4(0, 0, 0, 0);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    // the wave's weights: per superblock the 32 rows' headers (lane n) and
-    // the four 1-KB parts (lane (n, g): piece g of row n); superblocks past
-    // the plane read the last one and count as zero
-    uint4 hd[TL_CPB], wq[TL_CPB][4];
+    // the wave's weights: per tile and superblock the 32 rows' headers (lane
+    // n) and the four 1-KB parts (lane (n, g): piece g of row n); superblocks
+    // past the plane read the last one and count as zero
+    uint4 hd[NT][TL_CPB], wq[NT][TL_CPB][4];
 #pragma unroll
-    for (int c = 0; c < TL_CPB; ++c) {
-        const int s = s0 + c < nsb ? s0 + c : nsb - 1;
-        const uint8_t* rb = T + q4t_record(tile, nsb, s);
-        hd[c] = *reinterpret_cast<const uint4*>(rb + 4096 + 16 * n);
+    for (int t = 0; t < NT; ++t) {
+        const int64_t wt = tile + (t ? nout / 32 : 0);
 #pragma unroll
-        for (int p = 0; p < 4; ++p) wq[c][p] = *reinterpret_cast<const uint4*>(rb + p * 1024 + 16 * lane);
+        for (int c = 0; c < TL_CPB; ++c) {
+            const int s = s0 + c < nsb ? s0 + c : nsb - 1;
+            const uint8_t* rb = T + q4t_record(wt, nsb, s);
+            hd[t][c] = *reinterpret_cast<const uint4*>(rb + 4096 + 16 * n);
+#pragma unroll
+            for (int p = 0; p < 4; ++p) wq[t][c][p] = *reinterpret_cast<const uint4*>(rb + p * 1024 + 16 * lane);
+        }
     }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
@@ -164,16 +174,20 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_q4t(const uint8_t* __restrict_
     const bf16_t* xa = xs + (arow ? n : 0) * XR + 16 * g + wave * TL_CPB * 256;
     const int sbase = wave * TL_CPB * 8;
     const f32x16_t z16 = {};
-    float tot[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float tot[NT][4];
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) tot[t][e] = 0.0f;
     const uint32_t M4 = 0x0F0F0F0Fu;
 #pragma unroll
     for (int c = 0; c < TL_CPB; ++c) {
-        const uint4 hh = hd[c];
         const bool live = s0 + c < nsb;
-        float d = 0.0f, dm = 0.0f;
-        if constexpr (!AFF) {
-            d = live ? q4k_hdr_d(hh) : 0.0f;
-            dm = live ? q4k_hdr_dmin(hh) : 0.0f;
+        float d[NT], dm[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            d[t] = (!AFF && live) ? q4k_hdr_d(hd[t][c]) : 0.0f;
+            dm[t] = (!AFF && live) ? q4k_hdr_dmin(hd[t][c]) : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -187,46 +201,54 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_q4t(const uint8_t* __restrict_
             }
             const f32x4_t S1 = *reinterpret_cast<const f32x4_t*>(&Ss[(sbase + (kl >> 5)) * TL_MX + 4 * g]);
             const f32x4_t S2 = *reinterpret_cast<const f32x4_t*>(&Ss[(sbase + (kl >> 5) + 1) * TL_MX + 4 * g]);
-            const uint32_t hw = u == 0 ? hh.x : (u == 1 ? hh.y : (u == 2 ? hh.z : hh.w));
-            float d1, d2, c1, c2;
-            if constexpr (AFF) {  // one 64-weight group: w = s*q + b = s*(128 + q) - (128*s - b)
-                const float sc = live ? aff_scale(hw) : 0.0f, bi = live ? aff_bias(hw) : 0.0f;
-                d1 = d2 = sc;
-                c1 = c2 = __builtin_fmaf(128.0f, sc, -bi);
-            } else {
-                d1 = d * (float)(hw & 63u);
-                d2 = d * (float)((hw >> 12) & 63u);
-                c1 = __builtin_fmaf(128.0f, d1, dm * (float)((hw >> 6) & 63u));
-                c2 = __builtin_fmaf(128.0f, d2, dm * (float)((hw >> 18) & 63u));
-            }
-            const uint4 q = wq[c][u];
-            f32x16_t A = tmfma(as_bf16x8(a0), tnib(q.x & M4, q.y & M4), z16);
-            f32x16_t B = tmfma(as_bf16x8(a2), tnib((q.x >> 4) & M4, (q.y >> 4) & M4), z16);
-            A = tmfma(as_bf16x8(a1), tnib(q.z & M4, q.w & M4), A);
-            B = tmfma(as_bf16x8(a3), tnib((q.z >> 4) & M4, (q.w >> 4) & M4), B);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                tot[e] = __builtin_fmaf(-c1, S1[e], __builtin_fmaf(d1, A[e], tot[e]));
-                tot[e] = __builtin_fmaf(-c2, S2[e], __builtin_fmaf(d2, B[e], tot[e]));
-            }
-            // one part at a time: left free, the compiler issues every part's
-            // MFMAs first and keeps all their results live
+            for (int t = 0; t < NT; ++t) {
+                const uint4 hh = hd[t][c];
+                const uint32_t hw = u == 0 ? hh.x : (u == 1 ? hh.y : (u == 2 ? hh.z : hh.w));
+                float d1, d2, c1, c2;
+                if constexpr (AFF) {  // one 64-weight group: w = s*q + b = s*(128 + q) - (128*s - b)
+                    const float sc = live ? aff_scale(hw) : 0.0f, bi = live ? aff_bias(hw) : 0.0f;
+                    d1 = d2 = sc;
+                    c1 = c2 = __builtin_fmaf(128.0f, sc, -bi);
+                } else {
+                    d1 = d[t] * (float)(hw & 63u);
+                    d2 = d[t] * (float)((hw >> 12) & 63u);
+                    c1 = __builtin_fmaf(128.0f, d1, dm[t] * (float)((hw >> 6) & 63u));
+                    c2 = __builtin_fmaf(128.0f, d2, dm[t] * (float)((hw >> 18) & 63u));
+                }
+                const uint4 q = wq[t][c][u];
+                f32x16_t A = tmfma(as_bf16x8(a0), tnib(q.x & M4, q.y & M4), z16);
+                f32x16_t B = tmfma(as_bf16x8(a2), tnib((q.x >> 4) & M4, (q.y >> 4) & M4), z16);
+                A = tmfma(as_bf16x8(a1), tnib(q.z & M4, q.w & M4), A);
+                B = tmfma(as_bf16x8(a3), tnib((q.z >> 4) & M4, (q.w >> 4) & M4), B);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(tot[e]));
-            __builtin_amdgcn_sched_barrier(0);
+                for (int e = 0; e < 4; ++e) {
+                    tot[t][e] = __builtin_fmaf(-c1, S1[e], __builtin_fmaf(d1, A[e], tot[t][e]));
+                    tot[t][e] = __builtin_fmaf(-c2, S2[e], __builtin_fmaf(d2, B[e], tot[t][e]));
+                }
+                // one part at a time: left free, the compiler issues every
+                // part's MFMAs first and keeps all their results live
+#pragma unroll
+                for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(tot[t][e]));
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     }
     if constexpr (KW > 1) {
         if (wave > 0) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) red[((wave - 1) * 4 + e) * 64 + lane] = tot[e];
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) red[(((wave - 1) * NT + t) * 4 + e) * 64 + lane] = tot[t][e];
         }
         __syncthreads();
         if (wave == 0) {
 #pragma unroll
             for (int k = 0; k < KW - 1; ++k)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) tot[e] += red[(k * 4 + e) * 64 + lane];
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) tot[t][e] += red[((k * NT + t) * 4 + e) * 64 + lane];
         }
     }
     const int64_t row = tile * 32 + n;
@@ -234,23 +256,27 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_q4t(const uint8_t* __restrict_
         if (wave != 0 || row >= nout) return;
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-            if (4 * g + e < M) store_y<YT>(Y + (int64_t)(4 * g + e) * nout + row, tot[e]);
+            if (4 * g + e < M)
+                store_y<YT>(Y + (int64_t)(4 * g + e) * nout + row, GU ? silu_mul(tot[0][e], tot[NT - 1][e]) : tot[0][e]);
     } else {
         // partials as device-scope stores (written through to the point all
         // XCDs share) when the last block sums them: once they have
         // completed (vmcnt 0) the ticket, a device-scope atomic, is ordered
         // after them, and the last block's device-scope loads see them
+        const int64_t ldp = NT * nout;
         if (wave == 0 && row < nout) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int m = 4 * g + e;
-                if (m >= M) continue;
-                float* d = P + ((int64_t)blockIdx.y * M + m) * nout + row;
-                if (cnt)
-                    __hip_atomic_store(d, tot[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                else
-                    *d = tot[e];
-            }
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = 4 * g + e;
+                    if (m >= M) continue;
+                    float* dst = P + ((int64_t)blockIdx.y * M + m) * ldp + t * nout + row;
+                    if (cnt)
+                        __hip_atomic_store(dst, tot[t][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    else
+                        *dst = tot[t][e];
+                }
         }
         if (!cnt) return;
         __shared__ int last;
@@ -262,63 +288,69 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_q4t(const uint8_t* __restrict_
         __syncthreads();
         if (!last) return;
         // the tile's outputs, one per thread: the splits' partials in split
-        // order (k_split_reduce's sum, bit for bit), loads batched 8 deep
+        // order (k_split_reduce's sums, bit for bit), loads batched 8 deep
         const int splits = (int)gridDim.y;
         for (int i = threadIdx.x; i < 32 * M; i += 64 * KW) {
             const int m = i >> 5;
             const int64_t r = tile * 32 + (i & 31);
             if (r >= nout) continue;
-            float acc = 0.0f;
-            for (int s0 = 0; s0 < splits; s0 += 8) {
-                float v[8];
+            float acc[NT];
 #pragma unroll
-                for (int b = 0; b < 8; ++b)
-                    v[b] = s0 + b < splits ? __hip_atomic_load(P + ((int64_t)(s0 + b) * M + m) * nout + r,
-                                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                           : 0.0f;
+            for (int t = 0; t < NT; ++t) {
+                acc[t] = 0.0f;
+                for (int q0 = 0; q0 < splits; q0 += 8) {
+                    float v[8];
 #pragma unroll
-                for (int b = 0; b < 8; ++b)
-                    if (s0 + b < splits) acc += v[b];
+                    for (int b = 0; b < 8; ++b)
+                        v[b] = q0 + b < splits
+                                   ? __hip_atomic_load(P + ((int64_t)(q0 + b) * M + m) * ldp + t * nout + r,
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                   : 0.0f;
+#pragma unroll
+                    for (int b = 0; b < 8; ++b)
+                        if (q0 + b < splits) acc[t] += v[b];
+                }
             }
-            store_y<YT>(Y + (int64_t)m * nout + r, acc);
+            store_y<YT>(Y + (int64_t)m * nout + r, GU ? silu_mul(acc[0], acc[NT - 1]) : acc[0]);
         }
         if (threadIdx.x == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
-template <int KW, bool AFF, typename YT>
+template <int KW, bool AFF, bool GU, typename YT>
 hipError_t launch_kwy(const TilePlan& p, const uint8_t* T, const bf16_t* x, YT* y, int M, int K, int nsb,
                       int64_t nout, float* ws, uint32_t* cnt, hipStream_t s) {
     const dim3 grid((unsigned)((nout + 31) / 32), (unsigned)p.splits);
-    const size_t lds = tile_lds_bytes(KW, M);
+    const size_t lds = tile_lds_bytes(KW, M, GU ? 2 : 1);
     if (p.splits == 1) {
-        hipLaunchKernelGGL((k_gemv_q4t<KW, AFF, YT, false>), grid, dim3(64 * KW), lds, s, T, x, y, (float*)nullptr,
-                           (uint32_t*)nullptr, M, K, nsb, nout);
+        hipLaunchKernelGGL((k_gemv_q4t<KW, AFF, GU, YT, false>), grid, dim3(64 * KW), lds, s, T, x, y,
+                           (float*)nullptr, (uint32_t*)nullptr, M, K, nsb, nout);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL((k_gemv_q4t<KW, AFF, YT, true>), grid, dim3(64 * KW), lds, s, T, x, y, ws, cnt, M, K, nsb,
+    hipLaunchKernelGGL((k_gemv_q4t<KW, AFF, GU, YT, true>), grid, dim3(64 * KW), lds, s, T, x, y, ws, cnt, M, K, nsb,
                        nout);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess || cnt) return e;
-    return launch_split_reduce(ws, y, sizeof(YT) == 4, false, M, nout, 0, nout, p.splits, s);
+    return launch_split_reduce(ws, y, sizeof(YT) == 4, GU, M, nout, GU ? nout : 0, GU ? 2 * nout : nout, p.splits,
+                               s);
 }
 
-template <int KW, bool AFF>
+template <int KW, bool AFF, bool GU>
 hipError_t launch_kw(const TilePlan& p, const uint8_t* T, const void* x, void* y, bool yf32, int M, int K, int nsb,
                      int64_t nout, float* ws, uint32_t* cnt, hipStream_t s) {
     // more than 64 KB of dynamic LDS (8 rows, 8 waves) must be allowed per
     // kernel and device, once
-    constexpr size_t lds_max = tile_lds_bytes(KW, TL_MX);
+    constexpr size_t lds_max = tile_lds_bytes(KW, TL_MX, GU ? 2 : 1);
     if constexpr (lds_max > 65536) {
         static std::atomic<uint64_t> allowed{0};
         int dev = 0;
         if (hipGetDevice(&dev) != hipSuccess) dev = 0;
         const uint64_t bit = 1ull << (dev & 63);
         if (!(allowed.load() & bit)) {
-            const void* fns[4] = {(const void*)k_gemv_q4t<KW, AFF, float, true>,
-                                  (const void*)k_gemv_q4t<KW, AFF, float, false>,
-                                  (const void*)k_gemv_q4t<KW, AFF, bf16_t, true>,
-                                  (const void*)k_gemv_q4t<KW, AFF, bf16_t, false>};
+            const void* fns[4] = {(const void*)k_gemv_q4t<KW, AFF, GU, float, true>,
+                                  (const void*)k_gemv_q4t<KW, AFF, GU, float, false>,
+                                  (const void*)k_gemv_q4t<KW, AFF, GU, bf16_t, true>,
+                                  (const void*)k_gemv_q4t<KW, AFF, GU, bf16_t, false>};
             for (const void* f : fns) {
                 const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_max);
                 if (e != hipSuccess) return e;
@@ -327,8 +359,19 @@ hipError_t launch_kw(const TilePlan& p, const uint8_t* T, const void* x, void* y
         }
     }
     const bf16_t* xb = static_cast<const bf16_t*>(x);
-    if (yf32) return launch_kwy<KW, AFF, float>(p, T, xb, static_cast<float*>(y), M, K, nsb, nout, ws, cnt, s);
-    return launch_kwy<KW, AFF, bf16_t>(p, T, xb, static_cast<bf16_t*>(y), M, K, nsb, nout, ws, cnt, s);
+    if (yf32) return launch_kwy<KW, AFF, GU, float>(p, T, xb, static_cast<float*>(y), M, K, nsb, nout, ws, cnt, s);
+    return launch_kwy<KW, AFF, GU, bf16_t>(p, T, xb, static_cast<bf16_t*>(y), M, K, nsb, nout, ws, cnt, s);
+}
+
+template <bool AFF, bool GU>
+hipError_t launch_t(const TilePlan& p, const uint8_t* T, const void* x, void* y, bool yf32, int M, int K, int nsb,
+                    int64_t nout, float* ws, uint32_t* cnt, hipStream_t s) {
+    switch (p.kw) {
+        case 8: return launch_kw<8, AFF, GU>(p, T, x, y, yf32, M, K, nsb, nout, ws, cnt, s);
+        case 4: return launch_kw<4, AFF, GU>(p, T, x, y, yf32, M, K, nsb, nout, ws, cnt, s);
+        case 2: return launch_kw<2, AFF, GU>(p, T, x, y, yf32, M, K, nsb, nout, ws, cnt, s);
+        default: return launch_kw<1, AFF, GU>(p, T, x, y, yf32, M, K, nsb, nout, ws, cnt, s);
+    }
 }
 
 }  // namespace
@@ -344,18 +387,35 @@ hipError_t launch_repack_q4t(const uint8_t* rowquad, uint8_t* tiles, int64_t n, 
 }
 
 // Waves per block and K splits: the largest block (8 waves, 4096 columns)
-// whose grid still holds one block per CU; more splits only when the tiles
-// alone cannot fill the GPU.
-TilePlan plan_gemv_tile(int64_t M, int64_t N, int64_t K, int cus) {
+// whose grid still holds one block per CU, 4 waves when K needs splits
+// anyway; more splits only when the tiles alone cannot fill the GPU.
+// Gate/up: nout = N / 2 outputs (a multiple of 32), partials of both halves.
+TilePlan plan_gemv_tile(int64_t M, int64_t N, int64_t K, bool gu, int cus) {
     TilePlan p;
     if (M < 1 || M > TL_MX || N < 1 || K < 256) return p;
+    if (gu && (N % 64)) return p;
     if (cus < 1) cus = 256;
     const int nsb = (int)((K + 255) / 256);
-    const int64_t tiles = (N + 31) / 32;
+    const int64_t nout = gu ? N / 2 : N;
+    const int64_t tiles = (nout + 31) / 32;
     int kw = 8;
     while (kw > 1 && tiles * ((nsb + kw * TL_CPB - 1) / (kw * TL_CPB)) < cus) kw >>= 1;
     // never more waves than superblock pairs in K
     while (kw > 1 && (kw / 2) * TL_CPB >= nsb) kw >>= 1;
+    // a K that needs splits anyway: 4-wave blocks, which spread over the CUs
+    // evenly (4096 x 12288, M = 3..8: 6 splits 11.0-11.9 us against 3 splits
+    // of 8-wave blocks 12.0-13.3 us; 12288 x 4096 keeps one split of 8 waves,
+    // 10.4-11.4 us against 10.8-11.7)
+    if (kw == 8 && nsb > 8 * TL_CPB) kw = 4;
+    // gate/up holds both tiles' weights (156 VGPRs, 3 waves per SIMD): one
+    // 8-wave block per CU would leave a third of the slots idle, three
+    // 4-wave blocks fill them
+    if (gu && kw == 8) kw = 4;
+    // tuning override: THQ_TILE_KW = 1, 2, 4 or 8 waves per block
+    if (const char* e = getenv("THQ_TILE_KW")) {
+        const int v = atoi(e);
+        if (v == 1 || v == 2 || v == 4 || v == 8) kw = v;
+    }
     p.kw = kw;
     p.splits = (nsb + kw * TL_CPB - 1) / (kw * TL_CPB);
     p.workspace_bytes = p.splits > 1 ? (size_t)p.splits * (size_t)M * (size_t)N * sizeof(float) : 0;
@@ -363,20 +423,15 @@ TilePlan plan_gemv_tile(int64_t M, int64_t N, int64_t K, int cus) {
 }
 
 hipError_t launch_gemv_tile(const TilePlan& p, const WeightView& w, const uint8_t* tiles, const void* x, void* y,
-                            bool yf32, int M, float* ws, uint32_t* cnt, hipStream_t s) {
-    if (p.kw == 0 || (w.qtype != 12 && w.qtype != 13)) return hipErrorInvalidValue;
+                            bool yf32, bool gu, int M, float* ws, uint32_t* cnt, hipStream_t s) {
+    if (p.kw == 0 || (w.qtype != 12 && w.qtype != 13) || (gu && (w.N % 64))) return hipErrorInvalidValue;
     const int nsb = (int)((w.K + 255) / 256);
-    const bool aff = w.qtype == 13;
-    switch (p.kw) {
-        case 8: return aff ? launch_kw<8, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s)
-                           : launch_kw<8, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s);
-        case 4: return aff ? launch_kw<4, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s)
-                           : launch_kw<4, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s);
-        case 2: return aff ? launch_kw<2, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s)
-                           : launch_kw<2, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s);
-        default: return aff ? launch_kw<1, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s)
-                            : launch_kw<1, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, w.N, ws, cnt, s);
-    }
+    const int64_t nout = gu ? w.N / 2 : w.N;
+    if (w.qtype == 13)
+        return gu ? launch_t<true, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, nout, ws, cnt, s)
+                  : launch_t<true, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, nout, ws, cnt, s);
+    return gu ? launch_t<false, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, nout, ws, cnt, s)
+              : launch_t<false, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, nout, ws, cnt, s);
 }
 
 }  // namespace thq

@@ -350,16 +350,17 @@ Route plan_route(const Call& c) {
     // 23.1 us; LM head 151936 x 4096: 111 vs 125 us); below, the VALU kernel
     // (3072 x 1024 / 4096 x 4096 / 6144 x 4096: 3.2 / 7.7 / 8.4 vs 5.7 / 8.2 / 9.7 us)
     const bool q8_m1_mfma = w->qtype == THQ_Q8_0 && nout >= 12288;
-    // a weight with a tile plane: 3..8 bf16 rows of a plain projection take
-    // the tile-plane GEMV (whole-line loads; THQ_TILE_MIN_M moves the lower
-    // bound, 2 makes M = 2 take it instead of the row kernel)
+    // a weight with a tile plane: 3..8 bf16 rows take the tile-plane GEMV
+    // (whole-line loads; gate/up when each half is a whole number of tiles;
+    // THQ_TILE_MIN_M moves the lower bound, 2 makes M = 2 take it instead of
+    // the row kernel)
     static const int tile_min_m = [] {
         const char* e = getenv("THQ_TILE_MIN_M");
         const int v = e && *e ? atoi(e) : 3;
         return v < 1 ? 1 : v;
     }();
-    const thq::TilePlan tp = (w->tq && q4 && !c.gu && !c.am && !xf32 && aligned16(c.x) && m >= tile_min_m && m <= 8)
-                                 ? thq::plan_gemv_tile(m, w->N, w->K, c.ctx->cus)
+    const thq::TilePlan tp = (w->tq && q4 && !c.am && !xf32 && aligned16(c.x) && m >= tile_min_m && m <= 8)
+                                 ? thq::plan_gemv_tile(m, w->N, w->K, c.gu, c.ctx->cus)
                                  : thq::TilePlan{};
     if (tp.kw > 0) {
         r.kind = Kind::GEMV_TILE;
@@ -440,7 +441,8 @@ int exec_route(const Call& c, const Route& r, void* scratch, uint32_t* cnt = nul
         case Kind::GEMV1: e = thq::launch_gemv1(v, c.x, xf32, c.y, yf32, c.gu, nout, up_off, c.s, c.am); break;
         case Kind::ROWS: e = thq::launch_gemv_rows(v, c.x, c.y, yf32, c.gu, m, nout, up_off, c.s); break;
         case Kind::GEMV_TILE:
-            e = thq::launch_gemv_tile(r.tp, v, w->tq, c.x, c.y, yf32, m, static_cast<float*>(scratch), cnt, c.s);
+            e = thq::launch_gemv_tile(r.tp, v, w->tq, c.x, c.y, yf32, c.gu, m, static_cast<float*>(scratch), cnt,
+                                      c.s);
             break;
         case Kind::GEMV_MFMA:
             e = thq::launch_gemv_mfma(r.gp, v, c.x, c.y, yf32, c.gu, m, nout, up_off, static_cast<float*>(scratch),
@@ -484,7 +486,7 @@ int run_matmul(const Call& c) {
         if (rc) return rc;
     }
     uint32_t* cnt = nullptr;
-    if (r.kind == Kind::GEMV_TILE && r.tp.splits > 1) cnt = tile_counters(c.ctx, (c.w->N + 31) / 32);
+    if (r.kind == Kind::GEMV_TILE && r.tp.splits > 1) cnt = tile_counters(c.ctx, (c.w->N + 31) / 32);  // >= output tiles
     return exec_route(c, r, c.ctx->ws, cnt);
 }
 
@@ -1214,12 +1216,13 @@ int thq_plan_gemv_wide(int dtype, int64_t m, int64_t n, int64_t k, int cus, thq_
     return THQ_OK;
 }
 
-int thq_plan_gemv_tile(int dtype, int64_t m, int64_t n, int64_t k, int cus, thq_tile_plan_info* out) {
+int thq_plan_gemv_tile(int dtype, int64_t m, int64_t n, int64_t k, int gate_up, int cus,
+                       thq_tile_plan_info* out) {
     if (dtype != THQ_Q4_K && dtype != THQ_MLX_Q4) return fail(THQ_EDTYPE, "tile planes: Q4_K or MLX affine (%d)", dtype);
     if (!out) return fail(THQ_EINVAL, "null out");
     if (m < 1 || n < 1 || k < 1) return fail(THQ_ESHAPE, "shape [%lld, %lld, %lld]", (long long)m, (long long)n,
                                              (long long)k);
-    const thq::TilePlan p = thq::plan_gemv_tile(m, n, k, cus);
+    const thq::TilePlan p = thq::plan_gemv_tile(m, n, k, gate_up != 0, cus);
     *out = thq_tile_plan_info{};
     out->waves = p.kw;
     out->splits = p.splits;

@@ -109,19 +109,20 @@ hipError_t launch_gemv_wide(const WidePlan& p, const WeightView& w, const void* 
                             int M, int64_t nout, int64_t up_off, float* ws, hipStream_t s, AmaxOut* am = nullptr);
 // Q4_K / MLX affine tile plane (thq_dev.hpp, q4t_record), k_gemv_tile.hip:
 // its size, its construction from the row-quad plane, and the 3..8-row
-// decode GEMV over it (bf16 rows, 16-B aligned; plain projections)
+// decode GEMV over it (bf16 rows, 16-B aligned; plain or gate/up)
 size_t tile_plane_bytes(int64_t n, int64_t k);
 hipError_t launch_repack_q4t(const uint8_t* rowquad, uint8_t* tiles, int64_t n, int64_t k, hipStream_t s);
 struct TilePlan {
     int kw = 0, splits = 0;       // waves per block (0: unsupported), K splits
     size_t workspace_bytes = 0;   // split partials (f32 [splits][M][N])
 };
-TilePlan plan_gemv_tile(int64_t M, int64_t N, int64_t K, int cus);
-// cnt: null, or ceil(N / 32) u32 arrival counters that are zero (and stay
+// gu: fused gate/up over a [gate; up] weight (N a multiple of 64)
+TilePlan plan_gemv_tile(int64_t M, int64_t N, int64_t K, bool gu, int cus);
+// cnt: null, or ceil(nout / 32) u32 arrival counters that are zero (and stay
 // zero after the launch) for the last-block reduction of K splits;
 // without them a split plan runs k_split_reduce after the kernel
 hipError_t launch_gemv_tile(const TilePlan& p, const WeightView& w, const uint8_t* tiles, const void* x, void* y,
-                            bool yf32, int M, float* ws, uint32_t* cnt, hipStream_t s);
+                            bool yf32, bool gu, int M, float* ws, uint32_t* cnt, hipStream_t s);
 // sum split partials P[s][M][ldp] in split order, then the epilogue
 hipError_t launch_split_reduce(const float* P, void* y, bool yf32, bool gu, int M, int64_t nout, int64_t up_off,
                                int64_t ldp, int splits, hipStream_t s);

@@ -100,10 +100,10 @@ class TilePlanInfo(C.Structure):
     _fields_ = [("waves", C.c_int32), ("splits", C.c_int32), ("workspace_bytes", C.c_int64)]
 
 
-def plan_gemv_tile(dtype: int, m: int, n: int, k: int, cus: int = 256) -> TilePlanInfo:
+def plan_gemv_tile(dtype: int, m: int, n: int, k: int, gate_up: bool = False, cus: int = 256) -> TilePlanInfo:
     """The tile-plane decode GEMV's plan (thq_plan_gemv_tile); waves == 0: no plan."""
     out = TilePlanInfo()
-    check(lib.thq_plan_gemv_tile(dtype, m, n, k, cus, C.byref(out)))
+    check(lib.thq_plan_gemv_tile(dtype, m, n, k, int(gate_up), cus, C.byref(out)))
     return out
 
 
@@ -172,7 +172,7 @@ def _load():
         "thq_plan_gemv_mfma": ([I, i64, i64, i64, I, C.POINTER(GemvPlanInfo)], I),
         "thq_plan_gemm": ([I, I, i64, i64, i64, I, I, C.POINTER(GemmPlanInfo)], I),
         "thq_plan_gemv_wide": ([I, i64, i64, i64, I, C.POINTER(WidePlanInfo)], I),
-        "thq_plan_gemv_tile": ([I, i64, i64, i64, I, C.POINTER(TilePlanInfo)], I),
+        "thq_plan_gemv_tile": ([I, i64, i64, i64, I, I, C.POINTER(TilePlanInfo)], I),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
