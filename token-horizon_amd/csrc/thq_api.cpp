@@ -264,6 +264,7 @@ struct Call {
     bool gu;
     hipStream_t s;
     thq::AmaxOut* am;
+    size_t scratch_cap = SIZE_MAX;  // routes needing more scratch are not planned
 };
 
 int check_call(const Call& c) {
@@ -288,7 +289,7 @@ int check_call(const Call& c) {
 
 // The kernels a call runs, and the device scratch (split-K partials or the
 // quantized activation planes) they use, known before anything launches.
-enum class Kind { NONE, Q8ACT, GEMV1, ROWS, GEMV_TILE, GEMV_MFMA, GEMV_MFMA_GROUPS, WIDE, GEMM, GENERIC };
+enum class Kind { NONE, Q8ACT, GEMV1, ROWS, GEMV_TILE, GEMV_MFMA, GEMV_MFMA_GROUPS, WIDE, GEMM, GEMM_DQ, GENERIC };
 struct Route {
     Kind kind = Kind::NONE;
     thq::GemvPlan gp;
@@ -404,6 +405,24 @@ Route plan_route(const Call& c) {
         r.exact = (c.flags & THQ_MODE_EXACT_W) || (w->qtype == THQ_Q8_0 && m <= 64);
         r.gm = thq::plan_gemm(v.qtype, r.exact, m, w->N, w->K, c.gu, c.ctx->cus);
         r.scratch = r.gm.workspace_bytes;
+        // many rows of a plain projection: dequantize the weight to bf16 once
+        // and run the bf16 GEMM (the reference's "dequant + bf16 matmul"
+        // prefill route): the tile kernel repeats its dequantization per
+        // 256-row block, and on gfx950 that VALU work adds to the MFMA time
+        // (12288 x 4096 at M = 2048: 214 against 254 us).  Only from 1024
+        // rows and where its 256 x 384 tiles fill every CU (it has no
+        // split-K: 12288 x 4096 at M = 1024, 128 tiles, 184 against 153 us;
+        // 4096 x 12288 at M = 2048, 88 tiles, 415 against 243 us).
+        // THQ_GEMM_DQ: 0 never, 1 wherever supported (tests), unset: that rule
+        const char* dqe = getenv("THQ_GEMM_DQ");
+        const int dq_mode = dqe && *dqe ? atoi(dqe) : -1;
+        const size_t wb_bytes = round256((size_t)w->N * (size_t)w->K * 2);
+        if (!r.exact && !c.gu && dq_mode != 0 && thq::gemm_b16_supported(m, w->N, w->K) &&
+            wb_bytes <= c.scratch_cap &&
+            (dq_mode == 1 || (m >= 1024 && thq::gemm_b16_blocks(m, w->N) >= c.ctx->cus))) {
+            r.kind = Kind::GEMM_DQ;
+            r.scratch = wb_bytes;
+        }
     } else if (!xf32 && aligned16(c.x) && (q4 || q6) && m > 16 && w->K % 256 == 0 &&
                thq::plan_gemv_mfma(v.qtype, 16, w->N, w->K, c.gu).waves > 0) {
         // exact 4- / 6-bit weights past the decode GEMV's 16 rows (the verify
@@ -465,6 +484,11 @@ int exec_route(const Call& c, const Route& r, void* scratch, uint32_t* cnt = nul
             break;
         case Kind::GEMM:
             e = thq::launch_gemm(r.gm, v, c.x, c.y, yf32, c.gu, r.exact, m, static_cast<float*>(scratch), c.s);
+            break;
+        case Kind::GEMM_DQ:
+            // the weight as bf16 [N][K] in the scratch, then x . Wb^T
+            e = dequant_any(w, scratch, true, c.s);
+            if (e == hipSuccess) e = thq::launch_gemm_b16(c.x, scratch, c.y, yf32, m, (int)w->N, (int)w->K, c.s);
             break;
         case Kind::GENERIC: e = thq::launch_generic(v, c.x, xf32, c.y, yf32, c.gu, m, nout, up_off, c.s); break;
     }
@@ -1001,7 +1025,8 @@ int thq_matmul_noalloc(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq
     // the kernels of thq_matmul on the device's static scratch: no hipMalloc,
     // hipFree or allocating library call; the partials each route writes
     // cover everything its reduce reads, so nothing needs clearing
-    const Call c{ctx, w, x_dev, x_type, m, y_dev, y_type, flags, false, static_cast<hipStream_t>(stream), nullptr};
+    Call c{ctx, w, x_dev, x_type, m, y_dev, y_type, flags, false, static_cast<hipStream_t>(stream), nullptr};
+    c.scratch_cap = THQ_NOALLOC_SCRATCH_BYTES;  // e.g. the dequantize-then-GEMM route falls back to the tile GEMM
     int rc = check_call(c);
     if (rc || m == 0) return rc;
     DeviceGuard g(ctx->device);

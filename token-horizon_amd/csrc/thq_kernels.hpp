@@ -136,6 +136,12 @@ GemmPlan plan_gemm(int qtype, bool exact, int64_t M, int64_t N_rows, int64_t K, 
 hipError_t launch_gemm(const GemmPlan& p, const WeightView& w, const void* x, void* y, bool yf32, bool gu, bool exact,
                        int M, float* ws, hipStream_t s);
 
+// bf16 x bf16 GEMM over a weight dequantized to bf16 [N][K] (k_gemm_b16.hip),
+// the dequantize-then-GEMM prefill route: K % 32 == 0, x and Wb below 4 GiB
+bool gemm_b16_supported(int64_t M, int64_t N, int64_t K);
+int64_t gemm_b16_blocks(int64_t M, int64_t N);  // 256 x 384 output tiles
+hipError_t launch_gemm_b16(const void* x, const void* wb, void* y, bool yf32, int M, int N, int K, hipStream_t s);
+
 // THQ_MODE_Q8ACT: activation quantization + exact integer block dots
 bool q8act_supported(int qtype, int64_t K);
 size_t q8act_workspace_bytes(int qtype, int64_t M, int64_t K);
