@@ -246,7 +246,12 @@ int thq_gate_up_silu_q8act_emit(thq_ctx* ctx, const thq_weight* fused, thq_dtype
  *              head), a wide matrix-core GEMV that reads the weights once
  *              for all rows (exact weights)
  *   larger M   (and the other bf16 shapes with K a multiple of 64) MFMA GEMM;
- *              weights are rounded to bf16 on its tile unless THQ_MODE_EXACT_W
+ *              weights are rounded to bf16 on its tile unless THQ_MODE_EXACT_W.
+ *              From M = 1024, where its tiles fill the GPU, a plain
+ *              projection instead dequantizes W to bf16 once into the
+ *              workspace (N * K * 2 bytes, the same rounded weights) and
+ *              runs a bf16 MFMA GEMM on it, the engine's "dequant + bf16
+ *              matmul" prefill route
  *   x f32 with M >= 2 runs an exact f32 path, and so do the remaining shapes
  *   (Q6_K with THQ_MODE_EXACT_W among them).
  * THQ_MODE_Q8ACT instead reproduces candle's default CPU k_quants::matmul:

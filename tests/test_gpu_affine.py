@@ -63,6 +63,29 @@ def test_affine_upload_roundtrip_and_dequant(n, k, gs):
     assert np.array_equal(got32.view(np.uint32), O.affine_dequant_f32(wq, sb, n, k, gs).view(np.uint32))
 
 
+def test_affine_dequant_bf16_every_bit_pattern():
+    """Scales and biases of random 16-bit patterns (NaN, infinities, bf16
+    subnormals, values near the overflow threshold, products that round to
+    f32 subnormals or past the largest finite bf16): the bf16 dequantization
+    equals the oracle's f64 -> bf16 bit for bit wherever the oracle's value is
+    not a NaN, and is a NaN where it is (payloads follow the device's f64 NaN
+    propagation)."""
+    n, k = 64, 1024
+    rng = np.random.default_rng(21)
+    wq = rng.integers(0, 1 << 32, (n, k // 8), dtype=np.uint64).astype(np.uint32)
+    sb = rng.integers(0, 1 << 16, (n, 2 * (k // 64)), dtype=np.uint64).astype(np.uint16)
+    sb[:16] &= 0x81FF  # exponent fields 0..3: bf16 subnormal and tiny normal results
+    w = thq.QTensor.from_affine(wq, sb, n, k)
+    got = w.dequantize_bf16().view(torch.int16).cpu().numpy().view(np.uint16)
+    want = O.affine_dequant_bf16(wq, sb, n, k, 64)
+    nan = lambda b: ((b & 0x7F80) == 0x7F80) & ((b & 0x7F) != 0)
+    assert np.array_equal(nan(got), nan(want))
+    assert np.array_equal(got[~nan(want)], want[~nan(want)])
+    # the draw reaches the rounding routine's slow cases
+    exp = (want >> 7) & 0xFF
+    assert (exp == 0).sum() > 100 and (exp == 0xFF).sum() > 100
+
+
 def test_affine_tiled_upload_equals_row_major():
     n, k = 300, 384   # two 256-row tiles, the second ragged
     wq, sb = rand_qlin(n, k, 5)

@@ -64,6 +64,28 @@ def test_dequant_q4k_random_bytes_bit_exact():
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("qtype,n,k", [(O.Q8_0, 1000, 4096), (O.Q8_0, 40, 800), (O.Q4_K, 1000, 4096),
+                                        (O.Q4_K, 0, 0)])
+def test_dequant_bf16_bit_exact(qtype, n, k):
+    """thq_dequantize_bf16 (the dequantize-then-GEMM route's first step) is the
+    oracle's f32 dequantization rounded to nearest even, bit for bit.  The
+    Q4_K case with n = 0 takes random header and nibble bytes (96 x 2048):
+    every 16-B nibble piece's two halves and both nibbles of each byte."""
+    if n == 0:
+        rng = np.random.default_rng(11)
+        n, k = 96, 2048
+        raw = rng.integers(0, 256, (n, k // 256, 144), dtype=np.uint8)
+        d = (rng.standard_normal((n, k // 256, 2)) * 0.05).astype(np.float16)
+        raw[:, :, 0:4] = d.view(np.uint8).reshape(n, k // 256, 4)
+        raw = raw.reshape(n, -1)
+    else:
+        raw = weight_bytes(qtype, n, k, 3)
+    w = thq.QTensor.from_gguf_bytes(qtype, raw, n, k)
+    got = w.dequantize_bf16().view(torch.int16).cpu().numpy().view(np.uint16)
+    want = O.f32_to_bf16_bits(O.dequantize(qtype, raw, n, k))
+    assert np.array_equal(got, want)
+
+
 @pytest.mark.parametrize("qtype", [O.Q8_0, O.Q4_K])
 def test_upload_download_roundtrip(qtype):
     b, w = upload(qtype, 257, 1024)

@@ -11,8 +11,6 @@
 
 namespace thq {
 
-constexpr int ARGMAX_CHUNK = 4096;
-
 __device__ __forceinline__ void amax_combine(float& v, uint32_t& i, float v2, uint32_t i2) {
     if (v2 > v || (v2 == v && i2 < i)) {
         v = v2;

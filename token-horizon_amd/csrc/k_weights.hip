@@ -262,6 +262,35 @@ __global__ __launch_bounds__(256) void k_dequant_q8_0(const int8_t* __restrict__
     }
 }
 
+// bf16 output: a workgroup covers one 32-row tile x 8 blocks (8 whole 1-KB
+// tile records), lane = 8 * row + block, so each row's 8 lanes write 512
+// contiguous output bytes: two 16-B loads (the block's halves), four 16-B
+// stores.  Values as k_dequant_q8_0.
+__global__ __launch_bounds__(256) void k_dequant_q8_0_b16(const int8_t* __restrict__ qs,
+                                                          const uint16_t* __restrict__ dpl, bf16_t* __restrict__ out,
+                                                          int64_t n, int64_t nb) {
+    const int64_t ngrp = (nb + 7) >> 3;
+    const int64_t tile = blockIdx.x / ngrp;
+    const int64_t j = (blockIdx.x - tile * ngrp) * 8 + (threadIdx.x & 7);
+    const int64_t row = tile * 32 + (threadIdx.x >> 3);
+    if (row >= n || j >= nb) return;
+    const float d = f16_to_f32(dpl[q8t_d(row, nb, j)]);
+    uint4* dst = reinterpret_cast<uint4*>(out + (row * nb + j) * THQ_QK8_0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint4 v = *reinterpret_cast<const uint4*>(qs + q8t_q(row, nb, j, h));
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint32_t o[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            o[2 * i] = pack_bf16x2((float)(int8_t)(w[i] & 0xFF) * d, (float)(int8_t)((w[i] >> 8) & 0xFF) * d);
+            o[2 * i + 1] = pack_bf16x2((float)(int8_t)((w[i] >> 16) & 0xFF) * d, (float)(int8_t)(w[i] >> 24) * d);
+        }
+        dst[2 * h] = make_uint4(o[0], o[1], o[2], o[3]);
+        dst[2 * h + 1] = make_uint4(o[4], o[5], o[6], o[7]);
+    }
+}
+
 // one thread per (superblock, sub-block j): y = d*sc*q - dmin*m
 template <typename OT>
 __global__ __launch_bounds__(256) void k_dequant_q4k(const uint8_t* __restrict__ src, OT* __restrict__ out,
@@ -371,6 +400,41 @@ __global__ __launch_bounds__(256) void k_dequant_q6k(const uint8_t* __restrict__
     }
 }
 
+// bf16 output: one lane per 16 weights 16u .. 16u + 15 of a 64-weight step
+// (4 lanes per step): their low four bits are ql bytes 16 (u & 1) .. + 15 of
+// the step (nibble u >> 1), their high two bits the step's 16 qh bytes (bits
+// 2u, 2u + 1), their scale sc[u]; two 16-B loads, two 16-B stores.  Values
+// as k_dequant_q6k: d * sc * (code - 32) in f32, then bf16 to nearest even.
+__global__ __launch_bounds__(256) void k_dequant_q6k_b16(const uint8_t* __restrict__ src, bf16_t* __restrict__ out,
+                                                         int64_t n, int nsb) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t step = t >> 2;
+    if (step >= n * nsb * 4) return;
+    const int u = (int)t & 3;
+    const int64_t row = step / (4 * nsb);
+    const int j = (int)(step - row * 4 * nsb);
+    const int64_t K = (int64_t)nsb * 256;
+    const Q6Layout L = q6k_layout(n, K);
+    const uint4 ql = *reinterpret_cast<const uint4*>(src + row * (K / 2) + j * 32 + 16 * (u & 1));
+    const uint4 qh = *reinterpret_cast<const uint4*>(src + L.qh + row * (K / 4) + j * 16);
+    const float sc = (float)reinterpret_cast<const int8_t*>(src + L.sc + row * (K / 16) + j * 4)[u];
+    const float d = f16_to_f32(reinterpret_cast<const uint16_t*>(src + L.d)[row * nsb + (j >> 2)]);
+    const float ds = d * sc;
+    const uint32_t l4[4] = {ql.x, ql.y, ql.z, ql.w}, h4[4] = {qh.x, qh.y, qh.z, qh.w};
+    const int sl = 4 * (u >> 1), sh = 2 * u;
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        // four 6-bit codes, one per byte
+        const uint32_t c = ((l4[i] >> sl) & 0x0F0F0F0Fu) | (((h4[i] >> sh) & 0x03030303u) << 4);
+        o[2 * i] = pack_bf16x2(ds * (float)((int)(c & 0xFF) - 32), ds * (float)((int)((c >> 8) & 0xFF) - 32));
+        o[2 * i + 1] = pack_bf16x2(ds * (float)((int)((c >> 16) & 0xFF) - 32), ds * (float)((int)(c >> 24) - 32));
+    }
+    uint4* dst = reinterpret_cast<uint4*>(out + row * K + j * 64 + 16 * u);
+    dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+    dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+}
+
 // ---------------------------------------------------------------- MLX affine 4-bit
 // half 2.7.1 bf16::from_f64 (its f64_to_bf16, the rounding dequant_affine
 // uses, engine/src/qwen35.rs:110-134): the low 32 bits of the f64 mantissa
@@ -398,6 +462,19 @@ __device__ __forceinline__ uint16_t bf16_from_f64_half(double v) {
     }
     const uint32_t r = hs | ((uint32_t)he << 7) | (man >> 13);
     return (uint16_t)(((man & 0x1000u) && (man & 0x2FFFu)) ? r + 1 : r);
+}
+
+// The same rounding where the value is +-0 or its 20-mantissa-bit truncation
+// lies in the normal bf16 range: that truncation is exact in f32, and the
+// f32 -> bf16 round to nearest even (v_cvt_pk_bf16_f32) then sees the same
+// round bit (mantissa bit 12), sticky bits (11..0) and last kept bit (13) as
+// the rule above.  Returns false, with f unused, for subnormal, overflowing,
+// infinite and NaN values.
+__device__ __forceinline__ bool f64_half_fast(double v, float& f) {
+    const uint64_t b = (uint64_t)__double_as_longlong(v) & 0xFFFFFFFF00000000ull;
+    const uint32_t e = (uint32_t)(b >> 52) & 0x7FFu;
+    f = (float)__longlong_as_double((long long)b);
+    return (e >= 1023 - 126 && e <= 1023 + 127) || (b << 1) == 0;
 }
 
 // MLX affine -> row-quad plane.  One thread per (row, 64-weight part of the
@@ -457,11 +534,9 @@ __global__ __launch_bounds__(256) void k_repack_affine(const uint32_t* __restric
     *reinterpret_cast<uint32_t*>(dst + q4k_hdword(row, nsb, s, p)) = hw;
 }
 
-// One thread per (row, 64-weight group): f32 out = fmaf(q, scale, bias) (the
-// product is exact, so one rounding of q*scale + bias); bf16 out = half's
-// f64 -> bf16 of q*scale + bias evaluated in f64, as dequant_affine does.
-template <bool BF16>
-__global__ __launch_bounds__(256) void k_dequant_affine(const uint8_t* __restrict__ src, void* __restrict__ out,
+// One thread per (row, 64-weight group): out = fmaf(q, scale, bias) (the
+// product is exact, so one rounding of q*scale + bias).
+__global__ __launch_bounds__(256) void k_dequant_affine(const uint8_t* __restrict__ src, float* __restrict__ out,
                                                         int64_t n, int K, int nsb) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     const int ng64 = K >> 6;
@@ -471,8 +546,7 @@ __global__ __launch_bounds__(256) void k_dequant_affine(const uint8_t* __restric
     const int s = gp >> 2, p = gp & 3;
     const uint32_t hw = *reinterpret_cast<const uint32_t*>(src + q4k_hdword(row, nsb, s, p));
     const float sc = aff_scale(hw), bi = aff_bias(hw);
-    float* of = static_cast<float*>(out) + row * (int64_t)K + 64 * gp;
-    bf16_t* ob = static_cast<bf16_t*>(out) + row * (int64_t)K + 64 * gp;
+    float* of = out + row * (int64_t)K + 64 * gp;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const uint4 v = *reinterpret_cast<const uint4*>(src + q4k_piece(row, nsb, s, h, p));
@@ -484,20 +558,88 @@ __global__ __launch_bounds__(256) void k_dequant_affine(const uint8_t* __restric
                 float q[4];
 #pragma unroll
                 for (int b = 0; b < 4; ++b) q[b] = (float)((w[i] >> (8 * b + 4 * half)) & 0xFu);
-                const int e = 32 * half + 16 * h + 4 * i;
-                if constexpr (BF16) {
-                    uint16_t r[4];
-#pragma unroll
-                    for (int b = 0; b < 4; ++b) r[b] = bf16_from_f64_half((double)q[b] * (double)sc + (double)bi);
-                    *reinterpret_cast<uint2*>(ob + e) =
-                        make_uint2((uint32_t)r[0] | ((uint32_t)r[1] << 16), (uint32_t)r[2] | ((uint32_t)r[3] << 16));
-                } else {
-                    put4(of + e, __builtin_fmaf(q[0], sc, bi), __builtin_fmaf(q[1], sc, bi),
-                         __builtin_fmaf(q[2], sc, bi), __builtin_fmaf(q[3], sc, bi));
-                }
+                put4(of + 32 * half + 16 * h + 4 * i, __builtin_fmaf(q[0], sc, bi), __builtin_fmaf(q[1], sc, bi),
+                     __builtin_fmaf(q[2], sc, bi), __builtin_fmaf(q[3], sc, bi));
             }
         }
     }
+}
+
+// bf16 output of the row-quad layout (Q4_K and MLX affine: the dequantize-
+// then-GEMM route writes 2 B per weight, 3.6x the bytes it reads).  One lane
+// per 8-byte half k of a 16-B nibble piece (h, s, p), 4 lanes per 64-weight
+// group: the half's low nibbles are elements 64 gp + 16h + 8k .. + 7 of the
+// row (gp = 4s + p) and its high nibbles the same + 32, so each lane makes
+// two 16-B stores and a group's four lanes fill each 64-B run of the output
+// in one store instruction.  Q4_K: d1 * q - m1 in f32 (as k_dequant_q4k),
+// then bf16 to nearest even; affine: half's f64 -> bf16 of q * scale + bias
+// evaluated in f64, as dequant_affine does.
+template <bool AFF>
+__global__ __launch_bounds__(256) void k_dequant_q4_b16(const uint8_t* __restrict__ src, bf16_t* __restrict__ out,
+                                                        int64_t n, int K, int nsb) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int ng64 = K >> 6;
+    const int64_t grp = t >> 2;
+    if (grp >= n * ng64) return;
+    const int64_t row = grp / ng64;
+    const int gp = (int)(grp - row * ng64);
+    const int s = gp >> 2, p = gp & 3, h = (int)(t >> 1) & 1, k = (int)t & 1;
+    const uint2 v = *reinterpret_cast<const uint2*>(src + q4k_piece(row, nsb, s, h, p) + 8 * k);
+    const uint32_t w[2] = {v.x, v.y};
+    uint32_t lo[4], hi[4];
+    if constexpr (AFF) {
+        const uint32_t hw = *reinterpret_cast<const uint32_t*>(src + q4k_hdword(row, nsb, s, p));
+        const double sc = (double)aff_scale(hw), bi = (double)aff_bias(hw);
+        // element e's code: lo half e < 8 from byte e, hi half from its high nibble
+        double v[16];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t byte = (w[e >> 2] >> (8 * (e & 3))) & 0xFFu;
+            v[e] = (double)(float)(byte & 0xF) * sc + bi;
+            v[8 + e] = (double)(float)(byte >> 4) * sc + bi;
+        }
+        float f[16];
+        bool fast = true;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) fast = f64_half_fast(v[e], f[e]) && fast;
+        uint32_t o[8];
+        if (fast) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) o[i] = pack_bf16x2(f[2 * i], f[2 * i + 1]);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                o[i] = (uint32_t)bf16_from_f64_half(v[2 * i]) | ((uint32_t)bf16_from_f64_half(v[2 * i + 1]) << 16);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            lo[i] = o[i];
+            hi[i] = o[4 + i];
+        }
+    } else {
+        uint4 hd;
+        hd.x = *reinterpret_cast<const uint32_t*>(src + q4k_hdword(row, nsb, s, 0));
+        hd.y = *reinterpret_cast<const uint32_t*>(src + q4k_hdword(row, nsb, s, 1));
+        hd.z = *reinterpret_cast<const uint32_t*>(src + q4k_hdword(row, nsb, s, 2));
+        hd.w = *reinterpret_cast<const uint32_t*>(src + q4k_hdword(row, nsb, s, 3));
+        const float d = q4k_hdr_d(hd), dmin = q4k_hdr_dmin(hd);
+        uint32_t sc0, m0, sc1, m1;
+        q4k_hdr_sm(hd, 2 * p, sc0, m0);
+        q4k_hdr_sm(hd, 2 * p + 1, sc1, m1);
+        const float dl = d * (float)sc0, ml = dmin * (float)m0;
+        const float dh = d * (float)sc1, mh = dmin * (float)m1;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const uint32_t x = w[i];
+            lo[2 * i] = pack_bf16x2(dl * (float)(x & 0xF) - ml, dl * (float)((x >> 8) & 0xF) - ml);
+            lo[2 * i + 1] = pack_bf16x2(dl * (float)((x >> 16) & 0xF) - ml, dl * (float)((x >> 24) & 0xF) - ml);
+            hi[2 * i] = pack_bf16x2(dh * (float)((x >> 4) & 0xF) - mh, dh * (float)((x >> 12) & 0xF) - mh);
+            hi[2 * i + 1] = pack_bf16x2(dh * (float)((x >> 20) & 0xF) - mh, dh * (float)(x >> 28) - mh);
+        }
+    }
+    bf16_t* dst = out + row * (int64_t)K + 64 * gp + 16 * h + 8 * k;
+    *reinterpret_cast<uint4*>(dst) = make_uint4(lo[0], lo[1], lo[2], lo[3]);
+    *reinterpret_cast<uint4*>(dst + 32) = make_uint4(hi[0], hi[1], hi[2], hi[3]);
 }
 
 // ---------------------------------------------------------------- Q4_K repack
@@ -589,8 +731,8 @@ hipError_t launch_dequant_q8_0(const int8_t* qs, const uint16_t* d, void* out, b
     const int64_t nblocks = n * nb;
     if (nblocks == 0) return hipSuccess;
     if (bf16)
-        hipLaunchKernelGGL(k_dequant_q8_0<bf16_t>, dim3(grid_for(nblocks, 256)), dim3(256), 0, s, qs, d,
-                           static_cast<bf16_t*>(out), nblocks, nb);
+        hipLaunchKernelGGL(k_dequant_q8_0_b16, dim3((unsigned)(((n + 31) / 32) * ((nb + 7) / 8))), dim3(256), 0, s,
+                           qs, d, static_cast<bf16_t*>(out), n, nb);
     else
         hipLaunchKernelGGL(k_dequant_q8_0<float>, dim3(grid_for(nblocks, 256)), dim3(256), 0, s, qs, d,
                            static_cast<float*>(out), nblocks, nb);
@@ -601,8 +743,8 @@ hipError_t launch_dequant_q4k(const uint8_t* src, void* out, bool bf16, int64_t 
     const int64_t nsuper = n * nsb;
     if (nsuper == 0) return hipSuccess;
     if (bf16)
-        hipLaunchKernelGGL(k_dequant_q4k<bf16_t>, dim3(grid_for(nsuper * 8, 256)), dim3(256), 0, s, src,
-                           static_cast<bf16_t*>(out), nsuper, nsb);
+        hipLaunchKernelGGL(k_dequant_q4_b16<false>, dim3(grid_for(nsuper * 16, 256)), dim3(256), 0, s, src,
+                           static_cast<bf16_t*>(out), n, nsb * 256, nsb);
     else
         hipLaunchKernelGGL(k_dequant_q4k<float>, dim3(grid_for(nsuper * 8, 256)), dim3(256), 0, s, src,
                            static_cast<float*>(out), nsuper, nsb);
@@ -619,8 +761,8 @@ hipError_t launch_dequant_q6k(const uint8_t* src, void* out, bool bf16, int64_t 
     const int64_t t = n * nsb * 4;
     if (t == 0) return hipSuccess;
     if (bf16)
-        hipLaunchKernelGGL(k_dequant_q6k<bf16_t>, dim3(grid_for(t, 256)), dim3(256), 0, s, src, static_cast<bf16_t*>(out),
-                           n, nsb);
+        hipLaunchKernelGGL(k_dequant_q6k_b16, dim3(grid_for(t * 4, 256)), dim3(256), 0, s, src,
+                           static_cast<bf16_t*>(out), n, nsb);
     else
         hipLaunchKernelGGL(k_dequant_q6k<float>, dim3(grid_for(t, 256)), dim3(256), 0, s, src, static_cast<float*>(out),
                            n, nsb);
@@ -642,10 +784,11 @@ hipError_t launch_dequant_affine(const uint8_t* src, void* out, bool bf16, int64
     const int64_t threads = n * (K / 64);
     if (threads == 0) return hipSuccess;
     if (bf16)
-        hipLaunchKernelGGL(k_dequant_affine<true>, dim3(grid_for(threads, 256)), dim3(256), 0, s, src, out, n, K, nsb);
+        hipLaunchKernelGGL(k_dequant_q4_b16<true>, dim3(grid_for(threads * 4, 256)), dim3(256), 0, s, src,
+                           static_cast<bf16_t*>(out), n, K, nsb);
     else
-        hipLaunchKernelGGL(k_dequant_affine<false>, dim3(grid_for(threads, 256)), dim3(256), 0, s, src, out, n, K,
-                           nsb);
+        hipLaunchKernelGGL(k_dequant_affine, dim3(grid_for(threads, 256)), dim3(256), 0, s, src,
+                           static_cast<float*>(out), n, K, nsb);
     return hipGetLastError();
 }
 

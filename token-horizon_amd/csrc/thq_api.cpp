@@ -409,17 +409,22 @@ Route plan_route(const Call& c) {
         // and run the bf16 GEMM (the reference's "dequant + bf16 matmul"
         // prefill route): the tile kernel repeats its dequantization per
         // 256-row block, and on gfx950 that VALU work adds to the MFMA time
-        // (12288 x 4096 at M = 2048: 214 against 254 us).  Only from 1024
-        // rows and where its 256 x 384 tiles fill every CU (it has no
-        // split-K: 12288 x 4096 at M = 1024, 128 tiles, 184 against 153 us;
-        // 4096 x 12288 at M = 2048, 88 tiles, 415 against 243 us).
+        // (12288 x 4096 at M = 2048: Q4_K 203 against 258 us, Q6_K 214 / 274,
+        // MLX affine 207 / 236, Q8_0 221 / 238).  Only from 1024 rows and
+        // where its 256 x 384 tiles fill the GPU, since it has no split-K:
+        // all CUs, or two thirds of them for Q4_K / Q6_K, whose in-tile
+        // dequantization costs the most (4096 x 12288 at M = 4096, 176 tiles:
+        // Q4_K 429 against 449 us, Q6_K 436 / 501, Q8_0 452 / 439, affine
+        // 434 / 429; 12288 x 4096 at M = 1024, 128 tiles: Q4_K 168 / 153).
         // THQ_GEMM_DQ: 0 never, 1 wherever supported (tests), unset: that rule
         const char* dqe = getenv("THQ_GEMM_DQ");
         const int dq_mode = dqe && *dqe ? atoi(dqe) : -1;
         const size_t wb_bytes = round256((size_t)w->N * (size_t)w->K * 2);
+        const int64_t blocks = thq::gemm_b16_blocks(m, w->N), cus = c.ctx->cus;
+        const bool q4k_or_q6k = w->qtype == THQ_Q4_K || w->qtype == THQ_Q6_K;
         if (!r.exact && !c.gu && dq_mode != 0 && thq::gemm_b16_supported(m, w->N, w->K) &&
             wb_bytes <= c.scratch_cap &&
-            (dq_mode == 1 || (m >= 1024 && thq::gemm_b16_blocks(m, w->N) >= c.ctx->cus))) {
+            (dq_mode == 1 || (m >= 1024 && (q4k_or_q6k ? 3 * blocks >= 2 * cus : blocks >= cus)))) {
             r.kind = Kind::GEMM_DQ;
             r.scratch = wb_bytes;
         }
