@@ -246,14 +246,17 @@ int thq_gate_up_silu_q8act_emit(thq_ctx* ctx, const thq_weight* fused, thq_dtype
  *              head), a wide matrix-core GEMV that reads the weights once
  *              for all rows (exact weights)
  *   larger M   (and the other bf16 shapes with K a multiple of 64) MFMA GEMM;
- *              weights are rounded to bf16 on its tile unless THQ_MODE_EXACT_W.
+ *              weights are rounded to bf16 on its tile unless THQ_MODE_EXACT_W
+ *              (Q8_0, Q4_K, MLX affine: an exact tile, (128 + q) through the
+ *              MFMA and each 32-wide block's scale and offset in f32).
  *              From M = 1024, where its tiles fill the GPU, a plain
  *              projection instead dequantizes W to bf16 once into the
  *              workspace (N * K * 2 bytes, the same rounded weights) and
  *              runs a bf16 MFMA GEMM on it, the engine's "dequant + bf16
  *              matmul" prefill route
- *   x f32 with M >= 2 runs an exact f32 path, and so do the remaining shapes
- *   (Q6_K with THQ_MODE_EXACT_W among them).
+ *   Q6_K under THQ_MODE_EXACT_W past 64 rows runs the exact decode GEMV in
+ *   groups of 16 rows.  x f32 with M >= 2 runs an exact f32 path, and so do
+ *   the remaining shapes.
  * THQ_MODE_Q8ACT instead reproduces candle's default CPU k_quants::matmul:
  * x rows are quantized as thq_quantize_act does (into the context
  * workspace), every block dot is exact in integers and scaled in f32; only

@@ -203,6 +203,45 @@ def test_bf16_out_and_f32_gate_up_every_route(qtype):
                          thq.gate_up_silu(w, xd, torch.float32).cpu().numpy(), want, 1e-2)
 
 
+@pytest.mark.parametrize("kind", ["q4_k", "affine"])
+def test_exact_gemm_tile(kind):
+    """THQ_MODE_EXACT_W past 64 rows of Q4_K / MLX affine: k_gemm's exact tile
+    (bf16(128 + q) through the MFMA, each 32-wide sub-block's partial scaled
+    in f32 with its x-row sums) on plans with K splits (4096 x 4096 at
+    M = 300: 3 splits; 777 x 2048 at M = 129: 16, ragged M and N) and without
+    (M = 1000, rows sampled): the f32 bar, 1e-4 of the row norm, and a bf16
+    output and gate/up through the same tile."""
+    for (n, k, m, rows) in ((4096, 4096, 300, None), (777, 2048, 129, None), (4096, 4096, 1000, 24)):
+        print(f"[sweep] exact GEMM {kind} {n}x{k} m={m}", flush=True)
+        if kind == "affine":
+            wq, sb = rand_qlin_fast(n, k, seed=311)
+            w = thq.QTensor.from_affine(wq, sb, n, k)
+            ref_of = lambda xf: O.affine_matmul(wq, sb, n, k, xf)
+        else:
+            b, w = gguf_weight(O.Q4_K, n, k, seed=312)
+            ref_of = lambda xf: O.matmul(O.Q4_K, b, n, k, xf)
+        xf = O.bf16_round(activations(m, k, seed=500 + m))
+        xb = torch.from_numpy(xf).cuda().to(torch.bfloat16)
+        got = thq.matmul(w, xb, torch.float32, flags=thq.MODE_EXACT_W).cpu().numpy()
+        sel = np.arange(m) if rows is None else np.linspace(0, m - 1, rows).astype(np.int64)
+        ref = ref_of(np.ascontiguousarray(xf[sel]))
+        run_case(f"exact GEMM {kind} {n}x{k} m={m}", got[sel], ref, 1e-4)
+        if rows is None and m == 129:
+            got16 = thq.matmul(w, xb, torch.bfloat16, flags=thq.MODE_EXACT_W).float().cpu().numpy()
+            assert np.array_equal(got16.view(np.uint32), O.bf16_round(got).view(np.uint32))
+    n, k, m = 2048, 2048, 200
+    if kind == "affine":
+        wq, sb = rand_qlin_fast(n, k, seed=313)
+        w = thq.QTensor.from_affine(wq, sb, n, k)
+    else:
+        b, w = gguf_weight(O.Q4_K, n, k, seed=314)
+    xf = O.bf16_round(activations(m, k, seed=77))
+    xb = torch.from_numpy(xf).cuda().to(torch.bfloat16)
+    y = thq.matmul(w, xb, torch.float32, flags=thq.MODE_EXACT_W).cpu().numpy()
+    gu = thq.gate_up_silu(w, xb, torch.float32, flags=thq.MODE_EXACT_W).cpu().numpy()
+    assert_close_elem(f"exact GEMM gate/up {kind}", gu, O.bf16_bits_to_f32(O.gate_up_silu(y)), 2.0 ** -7)
+
+
 @pytest.mark.parametrize("kind", ["q4_k", "q6_k", "affine"])
 def test_exact_weights_past_sixteen_rows(kind):
     """THQ_MODE_EXACT_W (the LM head's mode) with 4- / 6-bit weights past 16

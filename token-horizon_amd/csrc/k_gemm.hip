@@ -16,7 +16,12 @@
 //   rounded  W tile = bf16(d*sc*q - dmin*m)         (Q4_K, Q8_0; large M)
 //   exact    W tile = bf16(q) (exact for |q| <= 255) and the f32 block scale
 //            is applied to each 32-wide partial in registers (Q8_0), so the
-//            result carries no weight rounding (LM head / argmax).
+//            result carries no weight rounding (LM head / argmax).  Q4_K and
+//            MLX affine: W tile = bf16(128 + q) (exact), and each 32-wide
+//            sub-block's partial A enters the total as d1*A - c1*S with
+//            c1 = 128*d1 + m1 (Q4_K: d1 = d*sc, m1 = dmin*m; affine:
+//            d1 = scale, m1 = -bias) and S the sub-block's sum of each x row,
+//            taken while x is stored to LDS.
 // Split-K: grid.z splits write f32 partials that k_split_reduce sums in a
 // fixed order (deterministic), applying the same epilogue.
 #include "thq_dev.hpp"
@@ -65,6 +70,11 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ Wq, co
     __shared__ __attribute__((aligned(16))) bf16_t Xs[2][BM][LDK];
     __shared__ __attribute__((aligned(16))) bf16_t Ws[2][BN][LDK];
     __shared__ float Ds[2][BN][2];
+    // exact Q4_K / affine: per W-tile row {d1, c1} of the step's two 32-wide
+    // sub-blocks, and per x row the two sub-block sums (row-contiguous)
+    constexpr bool XQ4 = EXACT && QT != 8;
+    __shared__ float Dq[XQ4 ? 2 : 1][XQ4 ? BN : 1][4];
+    __shared__ __attribute__((aligned(16))) float Sx[XQ4 ? 2 : 1][2][XQ4 ? BM : 4];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -123,6 +133,19 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ Wq, co
         for (int i = 0; i < XCH; ++i) {
             const int c = tid + 256 * i;
             *reinterpret_cast<uint4*>(&Xs[buf][c >> 3][8 * (c & 7)]) = xr[i];
+            if constexpr (XQ4) {
+                // 32-wide sums: four consecutive threads hold one sub-block
+                const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
+                bf16x2_t q2[4];
+                __builtin_memcpy(q2, &xr[i], 16);
+                float t = __builtin_amdgcn_fdot2_f32_bf16(q2[0], one, 0.0f, false);
+                t = __builtin_amdgcn_fdot2_f32_bf16(q2[1], one, t, false);
+                t = __builtin_amdgcn_fdot2_f32_bf16(q2[2], one, t, false);
+                t = __builtin_amdgcn_fdot2_f32_bf16(q2[3], one, t, false);
+                t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0xB1, 0xF, 0xF, false));
+                t += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(t), 0x4E, 0xF, 0xF, false));
+                if ((c & 3) == 0) Sx[buf][(c >> 2) & 1][c >> 3] = t;
+            }
         }
         if (QT != 8) {
             const int j = ((kit * BK) & 255) >> 6;
@@ -143,10 +166,26 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ Wq, co
             }
             const uint32_t q[4] = {wr0.x, wr0.y, wr0.z, wr0.w};
             uint32_t lo[8], hi[8];
+            if constexpr (XQ4) {
+                // bf16(128 + q): the nibble in the low mantissa bits under a 0x43 byte
+                const uint32_t C43 = 0x43434343u;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                deq8_q4(q[t] & 0x0F0F0F0Fu, d1, m1, lo + 2 * t);
-                deq8_q4((q[t] >> 4) & 0x0F0F0F0Fu, d2, m2, hi + 2 * t);
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t l4 = q[t] & 0x0F0F0F0Fu, h4 = (q[t] >> 4) & 0x0F0F0F0Fu;
+                    lo[2 * t] = __builtin_amdgcn_perm(C43, l4, 0x04010400u);
+                    lo[2 * t + 1] = __builtin_amdgcn_perm(C43, l4, 0x04030402u);
+                    hi[2 * t] = __builtin_amdgcn_perm(C43, h4, 0x04010400u);
+                    hi[2 * t + 1] = __builtin_amdgcn_perm(C43, h4, 0x04030402u);
+                }
+                if (wh == 0)
+                    *reinterpret_cast<float4*>(&Dq[buf][wc][0]) = make_float4(
+                        d1, __builtin_fmaf(128.0f, d1, m1), d2, __builtin_fmaf(128.0f, d2, m2));
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    deq8_q4(q[t] & 0x0F0F0F0Fu, d1, m1, lo + 2 * t);
+                    deq8_q4((q[t] >> 4) & 0x0F0F0F0Fu, d2, m2, hi + 2 * t);
+                }
             }
             uint4* dl = reinterpret_cast<uint4*>(&Ws[buf][wc][16 * wh]);
             uint4* dh = reinterpret_cast<uint4*>(&Ws[buf][wc][32 + 16 * wh]);
@@ -212,7 +251,28 @@ __global__ __launch_bounds__(256) void k_gemm(const uint8_t* __restrict__ Wq, co
             for (int i = 0; i < MT; ++i)
 #pragma unroll
                 for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
-            if (EXACT && (kk & 1)) {
+            if (XQ4 && (kk & 1)) {
+                // end of a 32-wide sub-block: tot += d1 * A - c1 * S
+                const int sb = kk >> 1;
+                f32x4_t sv[MT][4];
+#pragma unroll
+                for (int i = 0; i < MT; ++i)
+#pragma unroll
+                    for (int g4 = 0; g4 < 4; ++g4)
+                        sv[i][g4] = *reinterpret_cast<const f32x4_t*>(&Sx[buf][sb][wm * TM + 32 * i + 8 * g4 + 4 * (lane >> 5)]);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const float2 dc = *reinterpret_cast<const float2*>(&Dq[buf][wn * 64 + 32 * j + lr][2 * sb]);
+#pragma unroll
+                    for (int i = 0; i < MT; ++i)
+#pragma unroll
+                        for (int e = 0; e < 16; ++e) {
+                            const float t = __builtin_fmaf(dc.x, acc[i][j][e], tot[i][j][e]);
+                            tot[i][j][e] = __builtin_fmaf(-dc.y, sv[i][e >> 2][e & 3], t);
+                            acc[i][j][e] = 0.0f;
+                        }
+                }
+            } else if (EXACT && (kk & 1)) {
                 // end of a 32-wide block: scale the partial into the total
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
@@ -879,14 +939,24 @@ hipError_t launch_gemm(const GemmPlan& p, const WeightView& w, const void* x, vo
                        int M, float* ws, hipStream_t s) {
     const bf16_t* xb = static_cast<const bf16_t*>(x);
     if (w.qtype == 12) {
-        if (exact) return hipErrorInvalidValue;
+        if (exact) {
+            if (gu) return yf32 ? gemm_bm<12, true, true, float>(p, w, xb, y, M, ws, s)
+                                : gemm_bm<12, true, true, bf16_t>(p, w, xb, y, M, ws, s);
+            return yf32 ? gemm_bm<12, true, false, float>(p, w, xb, y, M, ws, s)
+                        : gemm_bm<12, true, false, bf16_t>(p, w, xb, y, M, ws, s);
+        }
         if (gu) return yf32 ? gemm_bm<12, false, true, float>(p, w, xb, y, M, ws, s)
                             : gemm_bm<12, false, true, bf16_t>(p, w, xb, y, M, ws, s);
         return yf32 ? gemm_bm<12, false, false, float>(p, w, xb, y, M, ws, s)
                     : gemm_bm<12, false, false, bf16_t>(p, w, xb, y, M, ws, s);
     }
     if (w.qtype == 13) {
-        if (exact) return hipErrorInvalidValue;
+        if (exact) {
+            if (gu) return yf32 ? gemm_bm<13, true, true, float>(p, w, xb, y, M, ws, s)
+                                : gemm_bm<13, true, true, bf16_t>(p, w, xb, y, M, ws, s);
+            return yf32 ? gemm_bm<13, true, false, float>(p, w, xb, y, M, ws, s)
+                        : gemm_bm<13, true, false, bf16_t>(p, w, xb, y, M, ws, s);
+        }
         if (gu) return yf32 ? gemm_bm<13, false, true, float>(p, w, xb, y, M, ws, s)
                             : gemm_bm<13, false, true, bf16_t>(p, w, xb, y, M, ws, s);
         return yf32 ? gemm_bm<13, false, false, float>(p, w, xb, y, M, ws, s)

@@ -267,6 +267,12 @@ struct Call {
     size_t scratch_cap = SIZE_MAX;  // routes needing more scratch are not planned
 };
 
+// an environment switch set to "0" (read on every call)
+bool env_flag_off(const char* name) {
+    const char* e = getenv(name);
+    return e && e[0] == '0' && e[1] == 0;
+}
+
 int check_call(const Call& c) {
     if (!c.ctx || !c.w) return fail(THQ_EINVAL, "null context or weight");
     if (c.xt != THQ_ACT_F32 && c.xt != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad x_type %d", c.xt);
@@ -398,7 +404,11 @@ Route plan_route(const Call& c) {
                // through silu(g)*u, is not averaged down by the row norm (the exact
                // kernel costs nothing at that size)
                !(c.gu && nout < 256) &&
-               !((q4 || q6) && ((c.flags & THQ_MODE_EXACT_W) || w->K % 256)) &&
+               // exact Q6_K has no GEMM tile (its exact path is the decode GEMV in
+               // groups of 16 rows); exact Q4_K / MLX affine run k_gemm's exact
+               // tile (THQ_EXACT_GEMM=0: the groups of 16 rows instead)
+               !((q4 || q6) && w->K % 256) &&
+               !((q6 || (q4 && env_flag_off("THQ_EXACT_GEMM"))) && (c.flags & THQ_MODE_EXACT_W)) &&
                !(q6 && (m <= 8 || thq::q6k_layout(w->N, w->K).total >= (1ull << 32) ||
                         (uint64_t)m * (uint64_t)w->K * 2 >= (1ull << 32)))) {
         r.kind = Kind::GEMM;
