@@ -262,32 +262,36 @@ __global__ __launch_bounds__(256) void k_dequant_q8_0(const int8_t* __restrict__
     }
 }
 
-// bf16 output: a workgroup covers one 32-row tile x 8 blocks (8 whole 1-KB
-// tile records), lane = 8 * row + block, so each row's 8 lanes write 512
-// contiguous output bytes: two 16-B loads (the block's halves), four 16-B
-// stores.  Values as k_dequant_q8_0.
-__global__ __launch_bounds__(256) void k_dequant_q8_0_b16(const int8_t* __restrict__ qs,
+// bf16 output: one wave per (row, 2048-weight chunk of K), eight rows per
+// block (a tile record's 128-B lines hold eight rows).  Store instruction i
+// of a wave writes weights 512 i + 8 lane .. + 7 of the chunk: 1 KB
+// contiguous.  A lane loads the 8-B half of its block's 16-B piece and the
+// block's scale.  Values as k_dequant_q8_0.
+__global__ __launch_bounds__(512) void k_dequant_q8_0_b16(const int8_t* __restrict__ qs,
                                                           const uint16_t* __restrict__ dpl, bf16_t* __restrict__ out,
-                                                          int64_t n, int64_t nb) {
-    const int64_t ngrp = (nb + 7) >> 3;
-    const int64_t tile = blockIdx.x / ngrp;
-    const int64_t j = (blockIdx.x - tile * ngrp) * 8 + (threadIdx.x & 7);
-    const int64_t row = tile * 32 + (threadIdx.x >> 3);
-    if (row >= n || j >= nb) return;
-    const float d = f16_to_f32(dpl[q8t_d(row, nb, j)]);
-    uint4* dst = reinterpret_cast<uint4*>(out + (row * nb + j) * THQ_QK8_0);
+                                                          int64_t n, int64_t nb, int64_t nchunks) {
+    const int lane = threadIdx.x & 63;
+    const int64_t grp = (int64_t)blockIdx.x / nchunks, chunk = (int64_t)blockIdx.x - grp * nchunks;
+    const int64_t row = grp * 8 + (threadIdx.x >> 6);
+    if (row >= n) return;
+    const int64_t K = nb * 32;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const uint4 v = *reinterpret_cast<const uint4*>(qs + q8t_q(row, nb, j, h));
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-        uint32_t o[8];
+    for (int i = 0; i < 4; ++i) {
+        const int64_t k = chunk * 2048 + 512 * i + 8 * lane;
+        if (k < K) {
+            const int64_t b = k >> 5;
+            const int off = (int)(k & 31);  // 0, 8, 16, 24: half (off & 8) of piece off / 16
+            const float d = f16_to_f32(dpl[q8t_d(row, nb, b)]);
+            const uint2 v = *reinterpret_cast<const uint2*>(qs + q8t_q(row, nb, b, off >> 4) + (off & 8));
+            const uint32_t w[2] = {v.x, v.y};
+            uint32_t o[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            o[2 * i] = pack_bf16x2((float)(int8_t)(w[i] & 0xFF) * d, (float)(int8_t)((w[i] >> 8) & 0xFF) * d);
-            o[2 * i + 1] = pack_bf16x2((float)(int8_t)((w[i] >> 16) & 0xFF) * d, (float)(int8_t)(w[i] >> 24) * d);
+            for (int t = 0; t < 2; ++t) {
+                o[2 * t] = pack_bf16x2((float)(int8_t)(w[t] & 0xFF) * d, (float)(int8_t)((w[t] >> 8) & 0xFF) * d);
+                o[2 * t + 1] = pack_bf16x2((float)(int8_t)((w[t] >> 16) & 0xFF) * d, (float)(int8_t)(w[t] >> 24) * d);
+            }
+            *reinterpret_cast<uint4*>(out + row * K + k) = make_uint4(o[0], o[1], o[2], o[3]);
         }
-        dst[2 * h] = make_uint4(o[0], o[1], o[2], o[3]);
-        dst[2 * h + 1] = make_uint4(o[4], o[5], o[6], o[7]);
     }
 }
 
@@ -730,12 +734,15 @@ hipError_t launch_dequant_q8_0(const int8_t* qs, const uint16_t* d, void* out, b
                                hipStream_t s) {
     const int64_t nblocks = n * nb;
     if (nblocks == 0) return hipSuccess;
-    if (bf16)
-        hipLaunchKernelGGL(k_dequant_q8_0_b16, dim3((unsigned)(((n + 31) / 32) * ((nb + 7) / 8))), dim3(256), 0, s,
-                           qs, d, static_cast<bf16_t*>(out), n, nb);
-    else
+    if (bf16) {
+        const int64_t nchunks = (nb * 32 + 2047) / 2048, blocks = (n + 7) / 8 * nchunks;
+        if (blocks >= (1ll << 31)) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(k_dequant_q8_0_b16, dim3((unsigned)blocks), dim3(512), 0, s, qs, d,
+                           static_cast<bf16_t*>(out), n, nb, nchunks);
+    } else {
         hipLaunchKernelGGL(k_dequant_q8_0<float>, dim3(grid_for(nblocks, 256)), dim3(256), 0, s, qs, d,
                            static_cast<float*>(out), nblocks, nb);
+    }
     return hipGetLastError();
 }
 

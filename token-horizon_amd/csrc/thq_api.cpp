@@ -420,7 +420,7 @@ Route plan_route(const Call& c) {
         // prefill route): the tile kernel repeats its dequantization per
         // 256-row block, and on gfx950 that VALU work adds to the MFMA time
         // (12288 x 4096 at M = 2048: Q4_K 203 against 258 us, Q6_K 214 / 274,
-        // MLX affine 207 / 236, Q8_0 221 / 238).  Only from 1024 rows and
+        // MLX affine 207 / 236, Q8_0 215 / 241).  Only from 1024 rows and
         // where its 256 x 384 tiles fill the GPU, since it has no split-K:
         // all CUs, or two thirds of them for Q4_K / Q6_K, whose in-tile
         // dequantization costs the most (4096 x 12288 at M = 4096, 176 tiles:
