@@ -21,11 +21,12 @@
 //   sum x*w = s*A - (128*s - b)*S            (MLX affine, scale s, bias b)
 // with S = sum x over the sub-block, taken while the rows are staged.
 //
-// Block: one 32-row output tile x KW waves.  The block stages rows x[0..M) of
-// its K range (KW * 512 columns) in LDS with the 32-wide sums; wave w owns two
-// superblocks of the range, issues all its weight loads (10 x 16 B per lane)
-// at entry behind the activation loads, and accumulates its rows; the waves'
-// partials are summed in LDS in wave order.  K beyond one block's range is
+// Block: one 32-row output tile x KW waves over a K range of KW * 512
+// columns.  Wave w owns two superblocks of the range: it loads rows x[0..M)
+// of its 512 columns, issues all its weight loads (10 x 16 B per lane)
+// behind them, stages its columns in LDS with their 32-wide sums (no block
+// barrier: a wave reads only what it wrote), and accumulates its rows; the
+// waves' partials are summed in LDS in wave order.  K beyond one block's range is
 // split over blockIdx.y: f32 partials, summed in split order (deterministic)
 // by the last block of each tile to arrive, or by k_split_reduce when the
 // caller has no arrival counters.
@@ -118,8 +119,9 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_q4t(const uint8_t* __restrict_
     const int s0 = sb0 + wave * TL_CPB;
 
     // activation rows first (their loads drain before the weight loads):
-    // thread t holds columns 8t .. 8t+7 of the block's range of each row
-    const int64_t col = (int64_t)sb0 * 256 + 8 * threadIdx.x;
+    // each wave reads only its own 512 columns (lane: columns 8 lane ..
+    // 8 lane + 7 of each row), so no block barrier stands before its math
+    const int64_t col = (int64_t)s0 * 256 + 8 * lane;
     uint4 xv[TL_MX];
 #pragma unroll
     for (int m = 0; m < TL_MX; ++m)
@@ -145,13 +147,14 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_q4t(const uint8_t* __restrict_
     }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    // stage the rows and their 32-wide sums (four threads per group); rows
-    // M .. TL_MX-1 of the sums are zero
+    // stage the wave's columns of the rows and their 32-wide sums (four
+    // lanes per group); rows M .. TL_MX-1 of the sums are zero
+    const int wc0 = wave * TL_CPB * 256;  // the wave's first column in the block's range
 #pragma unroll
     for (int m = 0; m < TL_MX; ++m) {
         if (m < M) {
             const uint4 v = xv[m];
-            *reinterpret_cast<uint4*>(xs + m * XR + 8 * threadIdx.x) = v;
+            *reinterpret_cast<uint4*>(xs + m * XR + wc0 + 8 * lane) = v;
             const bf16x2_t one = {(__bf16)1.0f, (__bf16)1.0f};
             bf16x2_t q[4];
             __builtin_memcpy(q, &v, 16);
@@ -161,12 +164,14 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_q4t(const uint8_t* __restrict_
             t = __builtin_amdgcn_fdot2_f32_bf16(q[3], one, t, false);
             t = tdpp_add<0xB1>(t);  // quad_perm [1,0,3,2]
             t = tdpp_add<0x4E>(t);  // quad_perm [2,3,0,1]
-            if ((threadIdx.x & 3) == 0) Ss[(threadIdx.x >> 2) * TL_MX + m] = t;
-        } else if ((threadIdx.x & 3) == 0) {
-            Ss[(threadIdx.x >> 2) * TL_MX + m] = 0.0f;
+            if ((lane & 3) == 0) Ss[((wc0 >> 5) + (lane >> 2)) * TL_MX + m] = t;
+        } else if ((lane & 3) == 0) {
+            Ss[((wc0 >> 5) + (lane >> 2)) * TL_MX + m] = 0.0f;
         }
     }
-    __syncthreads();
+    // the wave reads back only what it wrote: its LDS operations complete in order
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
 
     // A operand: lane (n, g) supplies activation row n (rows >= M are zero);
     // the output lane holds weight row n and activation rows 4g + e, e < 4
