@@ -172,3 +172,35 @@ def test_wide_plans():
         assert thq.plan_gemv_wide(dt, 65, 4096, 4096).splits == 0
         assert thq.plan_gemv_wide(dt, 8, 4096, 1000).splits == 0
     assert thq.plan_gemv_wide(thq.Q4_K, 40, 151936, 4096).splits == 1
+
+
+def tile_lds_bytes(kw: int, m: int, nt: int) -> int:
+    """k_gemv_q4t's LDS (token-horizon_amd/csrc/k_gemv_tile.hip, tile_lds_bytes):
+    x rows of the block's K range with an 8-column pad, the 32-wide sums of 8
+    rows, and the waves' partials for the cross-wave sum."""
+    kr = kw * 2 * 256
+    return m * (kr + 8) * 2 + kw * 2 * 8 * 8 * 4 + max(kw - 1, 1) * nt * 4 * 64 * 4
+
+
+def test_tile_plans():
+    """The tile-plane GEMV's plans (thq_plan_gemv_tile) for 1..8 rows, plain
+    and gate/up: waves per block in {1, 2, 4, 8}; the K splits cover every
+    superblock once with no empty split; the block's LDS fits the CU's
+    160 KB; the workspace is the split partials.  Unsupported shapes plan
+    nothing."""
+    for gu in (False, True):
+        for m in range(1, 9):
+            for n in (64, 1000 if not gu else 2048, 4096, 12288, 24576, 151936):
+                for k in (256, 512, 1024, 2304, 4096, 8192, 12288, 16384):
+                    p = thq.plan_gemv_tile(thq.Q4_K, m, n, k, gate_up=gu)
+                    assert p.waves in (1, 2, 4, 8), (gu, m, n, k, p.waves)
+                    nsb = (k + 255) // 256
+                    per = p.waves * 2
+                    assert p.splits * per >= nsb > (p.splits - 1) * per, (gu, m, n, k, p.waves, p.splits)
+                    nt = 2 if gu else 1
+                    assert tile_lds_bytes(p.waves, m, nt) <= 160 * 1024, (gu, m, k, p.waves)
+                    assert p.workspace_bytes == (p.splits * m * n * 4 if p.splits > 1 else 0), (gu, m, n, k)
+    assert thq.plan_gemv_tile(thq.Q4_K, 9, 4096, 4096).waves == 0
+    assert thq.plan_gemv_tile(thq.Q4_K, 4, 4000, 4096, gate_up=True).waves == 0
+    with pytest.raises(thq.ThqError):
+        thq.plan_gemv_tile(thq.Q8_0, 4, 4096, 4096)
