@@ -137,8 +137,10 @@ int thq_weight_fuse(thq_ctx* ctx, const thq_weight* const* parts, int nparts, th
  * thq_matmul runs 3..8 bf16 activation rows of a plain projection on the
  * tile-plane decode GEMV (exact weights, whole-line loads) instead of the
  * row-layout kernels, and so does thq_gate_up_silu on a fused [gate; up]
- * weight whose halves are whole 32-row tiles; every other call is
- * unchanged.  It doubles the
+ * weight whose halves are whole 32-row tiles.  THQ_MODE_Q8ACT calls and
+ * thq_matmul_q8act / thq_gate_up_silu_q8act on a Q4_K weight with a tile
+ * plane run 2..8 rows on it with int8 matrix-core dots (same results to the
+ * f32 summation order).  Every other call is unchanged.  It doubles the
  * weight's device memory, which thq_weight_free releases.  Idempotent.  Call
  * it before the weight is shared with other threads or used by work in
  * flight (it adds to the weight handle).  A fused weight does not inherit
@@ -260,8 +262,9 @@ int thq_gate_up_silu_q8act_emit(thq_ctx* ctx, const thq_weight* fused, thq_dtype
  * THQ_MODE_Q8ACT instead reproduces candle's default CPU k_quants::matmul:
  * x rows are quantized as thq_quantize_act does (into the context
  * workspace), every block dot is exact in integers and scaled in f32; only
- * the f32 summation order over blocks differs from candle's.  Any M; x must
- * be 16-byte aligned (THQ_EALIGN otherwise).
+ * the f32 summation order over blocks differs from candle's (2..8 rows of
+ * a Q4_K weight with a tile plane take int8 matrix-core dots over it).  Any
+ * M; x must be 16-byte aligned (THQ_EALIGN otherwise).
  * Inputs: x_dev [M, K] of x_type, y_dev [M, N] of y_type, both contiguous.
  * M == 0 is a no-op.  Errors: THQ_ESHAPE for K mismatch, THQ_EINVAL for
  * null pointers. */

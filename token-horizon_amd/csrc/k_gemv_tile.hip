@@ -88,6 +88,98 @@ constexpr size_t tile_lds_bytes(int kw, int m, int nt) {
            (size_t)(kw > 1 ? kw - 1 : 1) * nt * 4 * 64 * 4;
 }
 
+// The end of a tile block (both tile kernels): the waves' partials summed
+// in LDS in wave order by wave 0, then y (silu(g)*u for gate/up) or, with
+// SPLIT, the f32 partials and the split-order sum of the last block to arrive.
+// tot[t][e]: weight row 32 tile + n of tile t, activation row 4g + e.
+template <int KW, int NT, bool GU, typename YT, bool SPLIT>
+__device__ __forceinline__ void tile_finish(float (&tot)[NT][4], float* red, YT* __restrict__ Y, float* __restrict__ P,
+                                            uint32_t* __restrict__ cnt, int M, int64_t nout, int64_t tile, int wave,
+                                            int lane) {
+    const int n = lane & 31, g = lane >> 5;
+    if constexpr (KW > 1) {
+        if (wave > 0) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) red[(((wave - 1) * NT + t) * 4 + e) * 64 + lane] = tot[t][e];
+        }
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int k = 0; k < KW - 1; ++k)
+#pragma unroll
+                for (int t = 0; t < NT; ++t)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) tot[t][e] += red[((k * NT + t) * 4 + e) * 64 + lane];
+        }
+    }
+    const int64_t row = tile * 32 + n;
+    if constexpr (!SPLIT) {
+        if (wave != 0 || row >= nout) return;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (4 * g + e < M)
+                store_y<YT>(Y + (int64_t)(4 * g + e) * nout + row, GU ? silu_mul(tot[0][e], tot[NT - 1][e]) : tot[0][e]);
+    } else {
+        // partials as device-scope stores (written through to the point all
+        // XCDs share) when the last block sums them: once they have
+        // completed (vmcnt 0) the ticket, a device-scope atomic, is ordered
+        // after them, and the last block's device-scope loads see them
+        const int64_t ldp = NT * nout;
+        if (wave == 0 && row < nout) {
+#pragma unroll
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int m = 4 * g + e;
+                    if (m >= M) continue;
+                    float* dst = P + ((int64_t)blockIdx.y * M + m) * ldp + t * nout + row;
+                    if (cnt)
+                        __hip_atomic_store(dst, tot[t][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    else
+                        *dst = tot[t][e];
+                }
+        }
+        if (!cnt) return;
+        __shared__ int last;
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (threadIdx.x == 0)
+            last = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   gridDim.y - 1;
+        __syncthreads();
+        if (!last) return;
+        // the tile's outputs, one per thread: the splits' partials in split
+        // order (k_split_reduce's sums, bit for bit), loads batched 8 deep
+        const int splits = (int)gridDim.y;
+        for (int i = threadIdx.x; i < 32 * M; i += 64 * KW) {
+            const int m = i >> 5;
+            const int64_t r = tile * 32 + (i & 31);
+            if (r >= nout) continue;
+            float acc[NT];
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                acc[t] = 0.0f;
+                for (int q0 = 0; q0 < splits; q0 += 8) {
+                    float v[8];
+#pragma unroll
+                    for (int b = 0; b < 8; ++b)
+                        v[b] = q0 + b < splits
+                                   ? __hip_atomic_load(P + ((int64_t)(q0 + b) * M + m) * ldp + t * nout + r,
+                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                   : 0.0f;
+#pragma unroll
+                    for (int b = 0; b < 8; ++b)
+                        if (q0 + b < splits) acc[t] += v[b];
+                }
+            }
+            store_y<YT>(Y + (int64_t)m * nout + r, GU ? silu_mul(acc[0], acc[NT - 1]) : acc[0]);
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // K: x row stride (columns); nsb: superblocks in the plane (K padded to whole
 // superblocks for MLX affine, whose padding groups are zero).  Plain: block
 // x owns weight rows 32x .. 32x+31 = outputs, stored as y[m][nout].  Gate/up
@@ -239,87 +331,162 @@ __global__ __launch_bounds__(64 * KW) void k_gemv_q4t(const uint8_t* __restrict_
             }
         }
     }
-    if constexpr (KW > 1) {
-        if (wave > 0) {
+    tile_finish<KW, NT, GU, YT, SPLIT>(tot, red, Y, P, cnt, M, nout, tile, wave, lane);
+}
+
+typedef int ti32x4 __attribute__((ext_vector_type(4)));
+typedef int ti32x16 __attribute__((ext_vector_type(16)));
+
+// LDS bytes of a THQ_MODE_Q8ACT tile block: int8 x rows, the 32-quant sums,
+// the rows' Q8_K d, the waves' partials (nt tiles)
+constexpr size_t q8t_lds_bytes(int kw, int m, int nt) {
+    return (size_t)m * (kw * TL_CPB * 256 + 32) + (size_t)kw * TL_CPB * 8 * TL_MX * 4 +
+           (size_t)kw * TL_CPB * TL_MX * 4 + (size_t)(kw > 1 ? kw - 1 : 1) * nt * 4 * 64 * 4;
+}
+
+// THQ_MODE_Q8ACT (candle's k_quants::matmul: Q4_K weights against Q8_K
+// activations, [ext] BlockQ4K::vec_dot) over the tile plane, 1..8 rows.
+// Same block and wave structure as k_gemv_q4t; the activation operand is the
+// Q8_K planes (xq [M][K] i8, xd [M][K/256] f32 d, xb [M][K/32] i16 sums of
+// 32 quants).  Per 32-weight sub-block j one v_mfma_i32_32x32x32_i8 forms
+// every (activation row, weight row) integer (q4 . q8)_j exactly: B = the
+// tile piece's low (sub-block 2p) or high (2p + 1) nibbles as they lie in
+// the loaded 16 B, A = the activation row's 16 quants of the same half.  Per
+// superblock and output the integers
+//   aux = sum_j sc_j * (q4 . q8)_j,   mins = sum_j m_j * xb_j
+// enter the total as (d_w * d_x) * aux - (dmin_w * d_x) * mins, the f32 step
+// of k_q8act_q4k.
+template <int KW, bool GU, typename YT, bool SPLIT>
+__global__ __launch_bounds__(64 * KW) void k_q8act_q4t(const uint8_t* __restrict__ T, const int8_t* __restrict__ XQ,
+                                                      const float* __restrict__ XD, const int16_t* __restrict__ XB,
+                                                      YT* __restrict__ Y, float* __restrict__ P,
+                                                      uint32_t* __restrict__ cnt, int M, int nsb, int64_t nout) {
+    constexpr int NT = GU ? 2 : 1;
+    constexpr int KR = KW * TL_CPB * 256;  // the block's K range (columns)
+    constexpr int XR = KR + 32;            // LDS row stride (bytes): rows start 32 B apart in bank order
+    extern __shared__ __attribute__((aligned(16))) uint8_t tl_lds[];
+    int8_t* xs = reinterpret_cast<int8_t*>(tl_lds);                  // [M][XR]
+    int* Sb = reinterpret_cast<int*>(tl_lds + (size_t)M * XR);        // [KR / 32][TL_MX]
+    float* Dx = reinterpret_cast<float*>(Sb + (KR / 32) * TL_MX);     // [KW * TL_CPB][TL_MX]
+    float* red = Dx + KW * TL_CPB * TL_MX;                            // [KW - 1][NT][4][64]
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n = lane & 31, g = lane >> 5;
+    const int64_t tile = blockIdx.x;
+    const int s0 = blockIdx.y * KW * TL_CPB + wave * TL_CPB;
+    const int64_t K = (int64_t)nsb * 256;
+    const int nsub = nsb * 8;
+
+    // the wave's activation data first: 8 quants per lane and row; the
+    // sums of its 16 sub-blocks (lane: row lane / 8, sub-blocks 2 (lane % 8)
+    // and + 1); d of its two superblocks (lanes 0..15: row lane / 2)
+    const int64_t col = (int64_t)s0 * 256 + 8 * lane;
+    uint2 xv[TL_MX];
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
+    for (int m = 0; m < TL_MX; ++m)
+        if (m < M) xv[m] = col < K ? *reinterpret_cast<const uint2*>(XQ + m * K + col) : make_uint2(0, 0);
+    const int mb = lane >> 3, j2 = lane & 7;
+    const int sub = s0 * 8 + 2 * j2;
+    uint32_t bs = 0;
+    if (mb < M && sub < nsub) bs = *reinterpret_cast<const uint32_t*>(XB + (int64_t)mb * nsub + sub);
+    const int md = (lane >> 1) & (TL_MX - 1), cd = lane & 1;
+    float dxv = 0.0f;
+    if (lane < 2 * TL_MX && md < M && s0 + cd < nsb) dxv = XD[(int64_t)md * nsb + s0 + cd];
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    // the wave's weights, as in k_gemv_q4t
+    uint4 hd[NT][TL_CPB], wq[NT][TL_CPB][4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) red[(((wave - 1) * NT + t) * 4 + e) * 64 + lane] = tot[t][e];
-        }
-        __syncthreads();
-        if (wave == 0) {
+    for (int t = 0; t < NT; ++t) {
+        const int64_t wt = tile + (t ? nout / 32 : 0);
 #pragma unroll
-            for (int k = 0; k < KW - 1; ++k)
+        for (int c = 0; c < TL_CPB; ++c) {
+            const int s = s0 + c < nsb ? s0 + c : nsb - 1;
+            const uint8_t* rb = T + q4t_record(wt, nsb, s);
+            hd[t][c] = *reinterpret_cast<const uint4*>(rb + 4096 + 16 * n);
 #pragma unroll
-                for (int t = 0; t < NT; ++t)
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) tot[t][e] += red[((k * NT + t) * 4 + e) * 64 + lane];
+            for (int p = 0; p < 4; ++p) wq[t][c][p] = *reinterpret_cast<const uint4*>(rb + p * 1024 + 16 * lane);
         }
     }
-    const int64_t row = tile * 32 + n;
-    if constexpr (!SPLIT) {
-        if (wave != 0 || row >= nout) return;
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    // stage (rows M .. TL_MX-1 of the sums and d are zero); the wave reads
+    // back only what it wrote
+    const int wc0 = wave * TL_CPB * 256;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            if (4 * g + e < M)
-                store_y<YT>(Y + (int64_t)(4 * g + e) * nout + row, GU ? silu_mul(tot[0][e], tot[NT - 1][e]) : tot[0][e]);
-    } else {
-        // partials as device-scope stores (written through to the point all
-        // XCDs share) when the last block sums them: once they have
-        // completed (vmcnt 0) the ticket, a device-scope atomic, is ordered
-        // after them, and the last block's device-scope loads see them
-        const int64_t ldp = NT * nout;
-        if (wave == 0 && row < nout) {
+    for (int m = 0; m < TL_MX; ++m)
+        if (m < M) *reinterpret_cast<uint2*>(xs + m * XR + wc0 + 8 * lane) = xv[m];
+    Sb[((wc0 >> 5) + 2 * j2) * TL_MX + mb] = (int)(int16_t)(bs & 0xFFFFu);
+    Sb[((wc0 >> 5) + 2 * j2 + 1) * TL_MX + mb] = (int)(int16_t)(bs >> 16);
+    if (lane < 2 * TL_MX) Dx[(wave * TL_CPB + cd) * TL_MX + md] = dxv;
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_wave_barrier();
+
+    // A operand: lane (n, g) supplies activation row n (rows >= M are zero);
+    // the output lane holds weight row n and activation rows 4g + e, e < 4
+    const bool arow = n < M;
+    const int8_t* xa = xs + (arow ? n : 0) * XR + 16 * g + wc0;
+    const ti32x16 z16 = {};
+    const uint32_t M4 = 0x0F0F0F0Fu;
+    float tot[NT][4];
 #pragma unroll
-            for (int t = 0; t < NT; ++t)
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int m = 4 * g + e;
-                    if (m >= M) continue;
-                    float* dst = P + ((int64_t)blockIdx.y * M + m) * ldp + t * nout + row;
-                    if (cnt)
-                        __hip_atomic_store(dst, tot[t][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    else
-                        *dst = tot[t][e];
-                }
-        }
-        if (!cnt) return;
-        __shared__ int last;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
-        if (threadIdx.x == 0)
-            last = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                   gridDim.y - 1;
-        __syncthreads();
-        if (!last) return;
-        // the tile's outputs, one per thread: the splits' partials in split
-        // order (k_split_reduce's sums, bit for bit), loads batched 8 deep
-        const int splits = (int)gridDim.y;
-        for (int i = threadIdx.x; i < 32 * M; i += 64 * KW) {
-            const int m = i >> 5;
-            const int64_t r = tile * 32 + (i & 31);
-            if (r >= nout) continue;
-            float acc[NT];
+        for (int e = 0; e < 4; ++e) tot[t][e] = 0.0f;
+#pragma unroll
+    for (int c = 0; c < TL_CPB; ++c) {
+        int aux[NT][4], mns[NT][4];
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) aux[t][e] = mns[t][e] = 0;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int kl = c * 256 + u * 64;
+            ti32x4 a0 = {0, 0, 0, 0}, a1 = {0, 0, 0, 0};
+            if (arow) {
+                a0 = *reinterpret_cast<const ti32x4*>(xa + kl);
+                a1 = *reinterpret_cast<const ti32x4*>(xa + kl + 32);
+            }
+            const int jb = (wc0 >> 5) + (kl >> 5);
+            const ti32x4 b0 = *reinterpret_cast<const ti32x4*>(&Sb[jb * TL_MX + 4 * g]);
+            const ti32x4 b1 = *reinterpret_cast<const ti32x4*>(&Sb[(jb + 1) * TL_MX + 4 * g]);
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
-                acc[t] = 0.0f;
-                for (int q0 = 0; q0 < splits; q0 += 8) {
-                    float v[8];
+                const uint4 hh = hd[t][c];
+                const uint32_t hw = u == 0 ? hh.x : (u == 1 ? hh.y : (u == 2 ? hh.z : hh.w));
+                const uint4 q = wq[t][c][u];
+                const ti32x4 lo = {(int)(q.x & M4), (int)(q.y & M4), (int)(q.z & M4), (int)(q.w & M4)};
+                const ti32x4 hi = {(int)((q.x >> 4) & M4), (int)((q.y >> 4) & M4), (int)((q.z >> 4) & M4),
+                                   (int)((q.w >> 4) & M4)};
+                const ti32x16 C0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a0, lo, z16, 0, 0, 0);
+                const ti32x16 C1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a1, hi, z16, 0, 0, 0);
+                const int sc0 = (int)(hw & 63u), mn0 = (int)((hw >> 6) & 63u);
+                const int sc1 = (int)((hw >> 12) & 63u), mn1 = (int)((hw >> 18) & 63u);
 #pragma unroll
-                    for (int b = 0; b < 8; ++b)
-                        v[b] = q0 + b < splits
-                                   ? __hip_atomic_load(P + ((int64_t)(q0 + b) * M + m) * ldp + t * nout + r,
-                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                   : 0.0f;
+                for (int e = 0; e < 4; ++e) {
+                    aux[t][e] += __mul24(sc0, C0[e]) + __mul24(sc1, C1[e]);
+                    mns[t][e] += __mul24(mn0, b0[e]) + __mul24(mn1, b1[e]);
+                }
 #pragma unroll
-                    for (int b = 0; b < 8; ++b)
-                        if (q0 + b < splits) acc[t] += v[b];
+                for (int e = 0; e < 4; ++e) asm volatile("" : "+v"(aux[t][e]), "+v"(mns[t][e]));
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        if (s0 + c < nsb) {
+            const f32x4_t dx = *reinterpret_cast<const f32x4_t*>(&Dx[(wave * TL_CPB + c) * TL_MX + 4 * g]);
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const float dw = q4k_hdr_d(hd[t][c]), dmw = q4k_hdr_dmin(hd[t][c]);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float dd = dw * dx[e], dm = dmw * dx[e];
+                    tot[t][e] = __builtin_fmaf(-dm, (float)mns[t][e], __builtin_fmaf(dd, (float)aux[t][e], tot[t][e]));
                 }
             }
-            store_y<YT>(Y + (int64_t)m * nout + r, GU ? silu_mul(acc[0], acc[NT - 1]) : acc[0]);
         }
-        if (threadIdx.x == 0) __hip_atomic_store(cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    tile_finish<KW, NT, GU, YT, SPLIT>(tot, red, Y, P, cnt, M, nout, tile, wave, lane);
 }
 
 template <int KW, bool AFF, bool GU, typename YT>
@@ -376,6 +543,36 @@ hipError_t launch_t(const TilePlan& p, const uint8_t* T, const void* x, void* y,
         case 4: return launch_kw<4, AFF, GU>(p, T, x, y, yf32, M, K, nsb, nout, ws, cnt, s);
         case 2: return launch_kw<2, AFF, GU>(p, T, x, y, yf32, M, K, nsb, nout, ws, cnt, s);
         default: return launch_kw<1, AFF, GU>(p, T, x, y, yf32, M, K, nsb, nout, ws, cnt, s);
+    }
+}
+
+template <int KW, bool GU, typename YT>
+hipError_t launch_q8t_kwy(const TilePlan& p, const uint8_t* T, const int8_t* xq, const float* xd, const int16_t* xb,
+                          YT* y, int M, int nsb, int64_t nout, float* ws, uint32_t* cnt, hipStream_t s) {
+    static_assert(q8t_lds_bytes(KW, TL_MX, GU ? 2 : 1) <= 65536, "Q8ACT tile block beyond 64 KB of LDS");
+    const dim3 grid((unsigned)((nout + 31) / 32), (unsigned)p.splits);
+    const size_t lds = q8t_lds_bytes(KW, M, GU ? 2 : 1);
+    if (p.splits == 1) {
+        hipLaunchKernelGGL((k_q8act_q4t<KW, GU, YT, false>), grid, dim3(64 * KW), lds, s, T, xq, xd, xb, y,
+                           (float*)nullptr, (uint32_t*)nullptr, M, nsb, nout);
+        return hipGetLastError();
+    }
+    hipLaunchKernelGGL((k_q8act_q4t<KW, GU, YT, true>), grid, dim3(64 * KW), lds, s, T, xq, xd, xb, y, ws, cnt, M,
+                       nsb, nout);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || cnt) return e;
+    return launch_split_reduce(ws, y, sizeof(YT) == 4, GU, M, nout, GU ? nout : 0, GU ? 2 * nout : nout, p.splits,
+                               s);
+}
+
+template <bool GU, typename YT>
+hipError_t launch_q8t(const TilePlan& p, const uint8_t* T, const int8_t* xq, const float* xd, const int16_t* xb, YT* y,
+                      int M, int nsb, int64_t nout, float* ws, uint32_t* cnt, hipStream_t s) {
+    switch (p.kw) {
+        case 8: return launch_q8t_kwy<8, GU, YT>(p, T, xq, xd, xb, y, M, nsb, nout, ws, cnt, s);
+        case 4: return launch_q8t_kwy<4, GU, YT>(p, T, xq, xd, xb, y, M, nsb, nout, ws, cnt, s);
+        case 2: return launch_q8t_kwy<2, GU, YT>(p, T, xq, xd, xb, y, M, nsb, nout, ws, cnt, s);
+        default: return launch_q8t_kwy<1, GU, YT>(p, T, xq, xd, xb, y, M, nsb, nout, ws, cnt, s);
     }
 }
 
@@ -437,6 +634,20 @@ hipError_t launch_gemv_tile(const TilePlan& p, const WeightView& w, const uint8_
                   : launch_t<true, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, nout, ws, cnt, s);
     return gu ? launch_t<false, true>(p, tiles, x, y, yf32, M, (int)w.K, nsb, nout, ws, cnt, s)
               : launch_t<false, false>(p, tiles, x, y, yf32, M, (int)w.K, nsb, nout, ws, cnt, s);
+}
+
+hipError_t launch_q8act_tile(const TilePlan& p, const WeightView& w, const uint8_t* tiles, const int8_t* xq,
+                             const float* xd, const int16_t* xb, void* y, bool yf32, bool gu, int M, float* ws,
+                             uint32_t* cnt, hipStream_t s) {
+    if (p.kw == 0 || w.qtype != 12 || w.K % 256 || M < 1 || M > TL_MX || (gu && (w.N % 64)))
+        return hipErrorInvalidValue;
+    const int nsb = (int)(w.K / 256);
+    const int64_t nout = gu ? w.N / 2 : w.N;
+    if (yf32)
+        return gu ? launch_q8t<true, float>(p, tiles, xq, xd, xb, static_cast<float*>(y), M, nsb, nout, ws, cnt, s)
+                  : launch_q8t<false, float>(p, tiles, xq, xd, xb, static_cast<float*>(y), M, nsb, nout, ws, cnt, s);
+    return gu ? launch_q8t<true, bf16_t>(p, tiles, xq, xd, xb, static_cast<bf16_t*>(y), M, nsb, nout, ws, cnt, s)
+              : launch_q8t<false, bf16_t>(p, tiles, xq, xd, xb, static_cast<bf16_t*>(y), M, nsb, nout, ws, cnt, s);
 }
 
 }  // namespace thq

@@ -720,6 +720,20 @@ hipError_t launch_q8act(const WeightView& w, const void* x, bool xf32, void* y, 
     return launch_q8act_dot(w, ws, y, yf32, gu, M, nout, up_off, s);
 }
 
+hipError_t launch_q8act_dot_tile(const TilePlan& p, const WeightView& w, const uint8_t* tiles, const void* planes,
+                                 void* y, bool yf32, bool gu, int M, float* ws, uint32_t* cnt, hipStream_t s) {
+    const ActPlanes a = act_planes(12, const_cast<void*>(planes), M, w.K);
+    return launch_q8act_tile(p, w, tiles, a.xq, a.xd, a.xb, y, yf32, gu, M, ws, cnt, s);
+}
+
+hipError_t launch_q8act_tiled(const TilePlan& p, const WeightView& w, const uint8_t* tiles, const void* x, bool xf32,
+                              void* y, bool yf32, bool gu, int M, void* planes, float* ws, uint32_t* cnt,
+                              hipStream_t s) {
+    hipError_t e = launch_q8act_prepare(12, x, xf32, M, w.K, planes, s);
+    if (e != hipSuccess) return e;
+    return launch_q8act_dot_tile(p, w, tiles, planes, y, yf32, gu, M, ws, cnt, s);
+}
+
 hipError_t launch_q8act_dot(const WeightView& w, const void* planes, void* y, bool yf32, bool gu, int M, int64_t nout,
                             int64_t up_off, hipStream_t s) {
     const ActPlanes a = act_planes(w.qtype, const_cast<void*>(planes), M, w.K);

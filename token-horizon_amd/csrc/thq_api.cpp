@@ -295,7 +295,7 @@ int check_call(const Call& c) {
 
 // The kernels a call runs, and the device scratch (split-K partials or the
 // quantized activation planes) they use, known before anything launches.
-enum class Kind { NONE, Q8ACT, GEMV1, ROWS, GEMV_TILE, GEMV_MFMA, GEMV_MFMA_GROUPS, WIDE, GEMM, GEMM_DQ, GENERIC };
+enum class Kind { NONE, Q8ACT, Q8ACT_TILE, GEMV1, ROWS, GEMV_TILE, GEMV_MFMA, GEMV_MFMA_GROUPS, WIDE, GEMM, GEMM_DQ, GENERIC };
 struct Route {
     Kind kind = Kind::NONE;
     thq::GemvPlan gp;
@@ -306,6 +306,16 @@ struct Route {
     bool exact = false;
     size_t scratch = 0;
 };
+
+size_t align_up(size_t b, size_t a) { return (b + a - 1) / a * a; }
+
+// THQ_MODE_Q8ACT on a Q4_K weight with a tile plane: 2..8 rows take the
+// int8-MFMA tile kernel (THQ_Q8ACT_TILE=0: the row-quad kernel)
+thq::TilePlan q8act_tile_plan(const thq_ctx* ctx, const thq_weight* w, int64_t m, bool gu) {
+    static const bool on = !env_flag_off("THQ_Q8ACT_TILE");
+    if (!on || !w->tq || w->qtype != THQ_Q4_K || m < 2 || m > 8) return thq::TilePlan{};
+    return thq::plan_gemv_tile(m, w->N, w->K, gu, ctx->cus);
+}
 
 // Routing by rows, as QLin::linear_ps (engine/src/qwen35.rs:398-617).  A
 // validated call with m >= 1.  Kind::NONE: a fused-argmax call whose route
@@ -321,6 +331,13 @@ Route plan_route(const Call& c) {
         if (c.am) return r;
         r.kind = Kind::Q8ACT;
         r.scratch = thq::q8act_workspace_bytes(w->qtype, m, w->K);
+        const thq::TilePlan tp = q8act_tile_plan(c.ctx, w, m, c.gu);
+        if (tp.kw > 0) {
+            // the Q8_K planes, then the split partials
+            r.kind = Kind::Q8ACT_TILE;
+            r.tp = tp;
+            r.scratch = align_up(r.scratch, 256) + tp.workspace_bytes;
+        }
         return r;
     }
     // M = 1 keeps the VALU GEMV unless THQ_GEMV_M1=mfma; 2..16 bf16 rows go to the MFMA GEMV
@@ -472,6 +489,12 @@ int exec_route(const Call& c, const Route& r, void* scratch, uint32_t* cnt = nul
         case Kind::Q8ACT:
             e = thq::launch_q8act(v, c.x, xf32, c.y, yf32, c.gu, m, nout, up_off, scratch, c.s);
             break;
+        case Kind::Q8ACT_TILE: {
+            char* planes = static_cast<char*>(scratch);
+            float* part = reinterpret_cast<float*>(planes + align_up(thq::q8act_workspace_bytes(w->qtype, m, w->K), 256));
+            e = thq::launch_q8act_tiled(r.tp, v, w->tq, c.x, xf32, c.y, yf32, c.gu, m, planes, part, cnt, c.s);
+            break;
+        }
         case Kind::GEMV1: e = thq::launch_gemv1(v, c.x, xf32, c.y, yf32, c.gu, nout, up_off, c.s, c.am); break;
         case Kind::ROWS: e = thq::launch_gemv_rows(v, c.x, c.y, yf32, c.gu, m, nout, up_off, c.s); break;
         case Kind::GEMV_TILE:
@@ -525,7 +548,8 @@ int run_matmul(const Call& c) {
         if (rc) return rc;
     }
     uint32_t* cnt = nullptr;
-    if (r.kind == Kind::GEMV_TILE && r.tp.splits > 1) cnt = tile_counters(c.ctx, (c.w->N + 31) / 32);  // >= output tiles
+    if ((r.kind == Kind::GEMV_TILE || r.kind == Kind::Q8ACT_TILE) && r.tp.splits > 1)
+        cnt = tile_counters(c.ctx, (c.w->N + 31) / 32);  // >= output tiles
     return exec_route(c, r, c.ctx->ws, cnt);
 }
 
@@ -975,8 +999,23 @@ int run_q8act_dot(thq_ctx* ctx, const thq_weight* w, thq_dtype dot_type, const v
     if (!y) return fail(THQ_EINVAL, "null y");
     DeviceGuard g(ctx->device);
     const int64_t nout = gu ? w->N / 2 : w->N;
-    hipError_t e = thq::launch_q8act_dot(view(w), buf, y, yt == THQ_ACT_F32, gu, (int)m, nout, gu ? nout : 0,
-                                         static_cast<hipStream_t>(stream));
+    const thq::TilePlan tp = q8act_tile_plan(ctx, w, m, gu);
+    hipError_t e;
+    if (tp.kw > 0) {
+        // the tile kernel; its K splits sum in the context workspace
+        std::lock_guard<std::mutex> lk(ctx->mu);
+        uint32_t* cnt = nullptr;
+        if (tp.splits > 1) {
+            const int rc = ensure_ws(ctx, tp.workspace_bytes);
+            if (rc) return rc;
+            cnt = tile_counters(ctx, (w->N + 31) / 32);
+        }
+        e = thq::launch_q8act_dot_tile(tp, view(w), w->tq, buf, y, yt == THQ_ACT_F32, gu, (int)m,
+                                       static_cast<float*>(ctx->ws), cnt, static_cast<hipStream_t>(stream));
+    } else {
+        e = thq::launch_q8act_dot(view(w), buf, y, yt == THQ_ACT_F32, gu, (int)m, nout, gu ? nout : 0,
+                                  static_cast<hipStream_t>(stream));
+    }
     if (e != hipSuccess) return fail(THQ_EHIP, "kernel launch: %s", hipGetErrorString(e));
     return THQ_OK;
 }

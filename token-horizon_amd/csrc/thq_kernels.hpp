@@ -123,6 +123,12 @@ TilePlan plan_gemv_tile(int64_t M, int64_t N, int64_t K, bool gu, int cus);
 // without them a split plan runs k_split_reduce after the kernel
 hipError_t launch_gemv_tile(const TilePlan& p, const WeightView& w, const uint8_t* tiles, const void* x, void* y,
                             bool yf32, bool gu, int M, float* ws, uint32_t* cnt, hipStream_t s);
+// THQ_MODE_Q8ACT over the Q4_K tile plane (1..8 rows): the Q8_K planes xq
+// [M][K] i8, xd [M][K/256] f32, xb [M][K/32] i16 against the weight with
+// int8 MFMAs; plan, partials and counters as launch_gemv_tile
+hipError_t launch_q8act_tile(const TilePlan& p, const WeightView& w, const uint8_t* tiles, const int8_t* xq,
+                             const float* xd, const int16_t* xb, void* y, bool yf32, bool gu, int M, float* ws,
+                             uint32_t* cnt, hipStream_t s);
 // sum split partials P[s][M][ldp] in split order, then the epilogue
 hipError_t launch_split_reduce(const float* P, void* y, bool yf32, bool gu, int M, int64_t nout, int64_t up_off,
                                int64_t ldp, int splits, hipStream_t s);
@@ -154,6 +160,13 @@ hipError_t launch_q8act_prepare(int qtype, const void* x, bool xf32, int64_t M, 
                                 hipStream_t s);
 hipError_t launch_q8act_dot(const WeightView& w, const void* planes, void* y, bool yf32, bool gu, int M, int64_t nout,
                             int64_t up_off, hipStream_t s);
+// the same dot over the weight's tile plane (Q4_K, 1..8 rows), and the
+// quantize + tile dot in one call (the planes at `planes`, split partials at ws)
+hipError_t launch_q8act_dot_tile(const TilePlan& p, const WeightView& w, const uint8_t* tiles, const void* planes,
+                                 void* y, bool yf32, bool gu, int M, float* ws, uint32_t* cnt, hipStream_t s);
+hipError_t launch_q8act_tiled(const TilePlan& p, const WeightView& w, const uint8_t* tiles, const void* x, bool xf32,
+                              void* y, bool yf32, bool gu, int M, void* planes, float* ws, uint32_t* cnt,
+                              hipStream_t s);
 // Q4_K gate/up over Q8_K planes that also emits the Q8_K planes of its own
 // output y [M][nout] (nout % 256 == 0) into out_planes; counters: zeroed u32
 // [q8act_emit_counters(M, K, nout)], zero again when the launch completes
