@@ -60,8 +60,10 @@ def xin(m, k, seed, act):
 # (n, k, rows): one split of 8-wave blocks; ragged last tile with many splits
 # (10 tiles x 24 splits); 11 superblocks (the last wave's second superblock
 # is past K); 64 superblocks; the decode shapes of a Qwen3-8B-class layer
+# and 2-wave blocks over a ragged last tile
 CASES = [
     (1024, 4096, (2, 3, 8)),
+    (9000, 1024, (2, 8)),
     (301, 12288, (4,)),
     (130, 2816, (2, 7)),
     (66, 16384, (5,)),

@@ -44,8 +44,10 @@ def make(kind, n, k, seed):
 
 
 # (n, k, rows): ragged last tile, 4 K splits; 2 splits; long K (3 splits);
-# the 8-wave one-split instance
-CASES = [(1000, 1024, (3, 5, 8)), (4096, 4096, (3, 4, 8)), (300, 12288, (3, 8)), (12288, 4096, (3, 8))]
+# the 8-wave one-split instance; 2-wave blocks over a ragged last tile
+# (9000 = 281.25 tiles)
+CASES = [(1000, 1024, (3, 5, 8)), (4096, 4096, (3, 4, 8)), (300, 12288, (3, 8)), (12288, 4096, (3, 8)),
+         (9000, 1024, (3, 8))]
 
 
 @pytest.mark.parametrize("kind", ["q4_k", "affine"])
