@@ -65,6 +65,18 @@ __device__ __forceinline__ uint32_t quad_lane(uint32_t v) {  // lane P of each q
 __device__ __forceinline__ int pair_sum(int v) {  // lanes 2i, 2i+1
     return v + __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);
 }
+// DPP moves within a row of 16 lanes (no LDS traffic, unlike __shfl_xor's
+// ds_bpermute): quad_perm [1,0,3,2] = 0xB1, [2,3,0,1] = 0x4E, row_half_mirror
+// (lane i <-> 7 - i of each 8) = 0x141, row_mirror (i <-> 15 - i) = 0x140
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+
 __device__ __forceinline__ int quad_sum(int v) {
     v += __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
     return v + __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
@@ -117,9 +129,10 @@ __global__ __launch_bounds__(256) void k_quant_act_q8_0(const XT* __restrict__ x
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) amax = fmaxf(amax, fabsf(v[i]));
-    amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
-    amax = fmaxf(amax, __shfl_xor(amax, 4, 64));
+    // the 8 lanes of the block: the two quads, then the half-row mirror
+    amax = fmaxf(amax, dpp_f<0xB1>(amax));
+    amax = fmaxf(amax, dpp_f<0x4E>(amax));
+    amax = fmaxf(amax, dpp_f<0x141>(amax));
     const float d = amax / 127.0f;
     const float id = d != 0.0f ? 1.0f / d : 0.0f;
     uint32_t q = 0;
@@ -152,7 +165,8 @@ struct Q8KLane {
     int s32;     // sum of the 32 quants of lanes 8j .. 8j+7 (every lane of the octet)
 };
 
-// one wave quantizes one 256-wide block, lane l holding values 4l .. 4l+3
+// one wave quantizes one 256-wide block, lane l holding values 4l .. 4l+3;
+// all 64 lanes active (the cross-lane steps read every lane)
 __device__ __forceinline__ Q8KLane q8k_wave(const float (&v)[4], int lane) {
     float key = -1.0f, val = 0.0f;
     int idx = 0;
@@ -165,15 +179,31 @@ __device__ __forceinline__ Q8KLane q8k_wave(const float (&v)[4], int lane) {
             val = v[i];
         }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ok = __shfl_xor(key, off, 64), ov = __shfl_xor(val, off, 64);
-        const int oi = __shfl_xor(idx, off, 64);
-        if (ok > key || (ok == key && oi < idx)) {
-            key = ok;
-            idx = oi;
-            val = ov;
+    // (largest magnitude, then lowest index) is a selection of one element,
+    // so any combine order gives the same one: DPP within each row of 16
+    // lanes (quads, half rows, rows), then the four rows' winners read out
+    auto comb = [](float& ck, int& ci, float& cv, float ok, int oi, float ov) {
+        if (ok > ck || (ok == ck && oi < ci)) {
+            ck = ok;
+            ci = oi;
+            cv = ov;
         }
+    };
+    comb(key, idx, val, dpp_f<0xB1>(key), dpp_i<0xB1>(idx), dpp_f<0xB1>(val));
+    comb(key, idx, val, dpp_f<0x4E>(key), dpp_i<0x4E>(idx), dpp_f<0x4E>(val));
+    comb(key, idx, val, dpp_f<0x141>(key), dpp_i<0x141>(idx), dpp_f<0x141>(val));
+    comb(key, idx, val, dpp_f<0x140>(key), dpp_i<0x140>(idx), dpp_f<0x140>(val));
+    {
+        float bk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(key), 0));
+        int bi = __builtin_amdgcn_readlane(idx, 0);
+        float bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(val), 0));
+#pragma unroll
+        for (int r = 16; r < 64; r += 16)
+            comb(bk, bi, bv, __int_as_float(__builtin_amdgcn_readlane(__float_as_int(key), r)),
+                 __builtin_amdgcn_readlane(idx, r), __int_as_float(__builtin_amdgcn_readlane(__float_as_int(val), r)));
+        key = bk;
+        idx = bi;
+        val = bv;
     }
     Q8KLane r;
     r.q = 0;
@@ -187,7 +217,7 @@ __device__ __forceinline__ Q8KLane q8k_wave(const float (&v)[4], int lane) {
     int s = (int)(int8_t)(r.q & 0xFFu) + (int)(int8_t)((r.q >> 8) & 0xFFu) + (int)(int8_t)((r.q >> 16) & 0xFFu) +
             (int)(int8_t)(r.q >> 24);
     r.s16 = quad_sum(s);  // 16 quants: lanes 4j .. 4j+3
-    r.s32 = r.s16 + __shfl_xor(r.s16, 4, 64);
+    r.s32 = r.s16 + dpp_i<0x141>(r.s16);  // the other quad of the 8
     return r;
 }
 
