@@ -228,7 +228,9 @@ int thq_gate_up_silu_q8act(thq_ctx* ctx, const thq_weight* fused, thq_dtype dot_
  * epilogue counts arriving blocks per 256-wide segment in a small counter
  * buffer the context owns (allocated and zeroed on the first call of a
  * larger shape; each launch leaves it zero), so such calls on one context
- * must be ordered on one stream. */
+ * must be ordered on one stream.  A weight with a tile plane
+ * (thq_weight_add_tiles) at 2..8 rows instead runs its int8 tile kernel and
+ * then quantizes y in a second launch: the same bytes, faster there. */
 int thq_gate_up_silu_q8act_emit(thq_ctx* ctx, const thq_weight* fused, thq_dtype dot_type, const void* buf_dev,
                                 int64_t m, int64_t k, void* y_dev, thq_act y_type, void* next_buf_dev,
                                 void* stream);

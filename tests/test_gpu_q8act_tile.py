@@ -147,3 +147,36 @@ def test_q8act_tile_prepared_and_noalloc(n, k, m):
     thq.matmul_noalloc(wt, xt, y, flags=thq.MODE_Q8ACT)
     assert torch.equal(y.view(torch.int32), want.view(torch.int32))
     assert rel_row_err(tonp(want), O.matmul(O.Q4_K, b, n, k, x, O.MODE_Q8ACT)) <= 1e-5
+
+
+@pytest.mark.parametrize("h,k,m", [(1024, 1024, 3), (12288, 4096, 8), (512, 12288, 5)])
+def test_q8act_tile_gate_up_emit(h, k, m):
+    """thq_gate_up_silu_q8act_emit on a [gate; up] weight with a tile plane:
+    y equals the tile kernel's thq_gate_up_silu_q8act output bit for bit, and
+    the emitted buffer is byte-identical to thq_q8act_prepare of that y
+    (K = 12288: split partials in the context workspace)."""
+    both = np.concatenate([weight_bytes(O.Q4_K, h, k, seed=1900), weight_bytes(O.Q4_K, h, k, seed=1901)])
+    fused = thq.QTensor.from_gguf_bytes(O.Q4_K, both, 2 * h, k).add_tiles()
+    xb = torch.from_numpy(O.bf16_round(activations(m, k, seed=1902))).cuda().to(torch.bfloat16)
+    pre = thq.Q8Act(xb, thq.Q8_K)
+    for dt in (torch.bfloat16, torch.float32):
+        want_y = pre.gate_up_silu(fused, dt)
+        y, nxt = pre.gate_up_silu_emit(fused, dt)
+        torch.cuda.synchronize()
+        iv = torch.int16 if dt == torch.bfloat16 else torch.int32
+        assert torch.equal(y.view(iv), want_y.view(iv))
+        want = q8k_planes(thq.Q8Act(y, thq.Q8_K).buf, m, h)
+        for got_p, want_p in zip(q8k_planes(nxt.buf, m, h), want):
+            assert np.array_equal(got_p, want_p)
+
+
+def q8k_planes(buf: torch.Tensor, m: int, k: int):
+    """(xq [m][k] i8, xd [m][k/256] f32 bits, xb [m][k/32] i16) of a Q8_K
+    activation buffer, each plane starting on a 256-byte boundary (the
+    padding between them is not part of the operand)."""
+    a = lambda b: (b + 255) // 256 * 256
+    raw = buf.cpu().numpy()
+    o1 = a(m * k)
+    o2 = o1 + a(m * (k // 256) * 4)
+    return (raw[:m * k].view(np.int8), raw[o1:o1 + m * (k // 256) * 4].view(np.uint32),
+            raw[o2:o2 + m * (k // 32) * 2].view(np.int16))

@@ -1043,6 +1043,25 @@ int thq_gate_up_silu_q8act_emit(thq_ctx* ctx, const thq_weight* fused, thq_dtype
     if (!y_dev) return fail(THQ_EINVAL, "null y");
     DeviceGuard g(ctx->device);
     std::lock_guard<std::mutex> lk(ctx->mu);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const thq::TilePlan tp = q8act_tile_plan(ctx, fused, m, true);
+    if (tp.kw > 0) {
+        // a weight with a tile plane (2..8 rows): its int8 tile kernel, then
+        // the next projection's planes quantized from y (the bytes
+        // thq_q8act_prepare writes for y, by construction)
+        uint32_t* cnt = nullptr;
+        if (tp.splits > 1) {
+            const int rc = ensure_ws(ctx, tp.workspace_bytes);
+            if (rc) return rc;
+            cnt = tile_counters(ctx, (fused->N + 31) / 32);
+        }
+        hipError_t e = thq::launch_q8act_dot_tile(tp, view(fused), fused->tq, buf_dev, y_dev, y_type == THQ_ACT_F32,
+                                                  true, (int)m, static_cast<float*>(ctx->ws), cnt, s);
+        if (e == hipSuccess)
+            e = thq::launch_q8act_prepare(12, y_dev, y_type == THQ_ACT_F32, m, nout, next_buf_dev, s);
+        if (e != hipSuccess) return fail(THQ_EHIP, "kernel launch: %s", hipGetErrorString(e));
+        return THQ_OK;
+    }
     const size_t need = thq::q8act_emit_counters(m, fused->K, nout);
     if (need > ctx->emit_cnt_n) {
         // zeroed once here; every launch leaves them zero again
@@ -1059,7 +1078,7 @@ int thq_gate_up_silu_q8act_emit(thq_ctx* ctx, const thq_weight* fused, thq_dtype
         ctx->emit_cnt_n = want;
     }
     hipError_t e = thq::launch_q8act_dot_emit(view(fused), buf_dev, y_dev, y_type == THQ_ACT_F32, (int)m, nout,
-                                              ctx->emit_cnt, next_buf_dev, static_cast<hipStream_t>(stream));
+                                              ctx->emit_cnt, next_buf_dev, s);
     if (e != hipSuccess) return fail(THQ_EHIP, "kernel launch: %s", hipGetErrorString(e));
     return THQ_OK;
 }
