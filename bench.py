@@ -6,12 +6,19 @@ A "step" is one GEMV call (M=1, bf16 x, f32 y) on the next of 24 distinct
 weight copies (680 MB in rotation, so weights stream from HBM, not from the
 256 MB MALL).  Steps are launched back to back from a captured HIP graph so
 host launch cost is not on the GPU timeline: --warmup untimed steps, then
-HIP events on the launch stream bracket exactly --steps steps.
+HIP events on the launch stream bracket exactly --steps steps.  The timed
+graph is uploaded to the device (hipGraphUpload) before the start event, so
+its one-time setup is not in the timed region.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline] [--no-configs]
 
-Prints one JSON line.  Inputs are synthetic: W ~ N(0, 0.02) quantized to Q4_K
-on the device, x ~ N(0, 1) in bf16, generated by torch's seeded generator.
+Prints one JSON line: the headline GEMV and the M=2048 GEMM, each with its
+roofline, the single-launch read ceilings of the GEMV's byte count, a
+`configs` object timing every benchmark configuration of the path (Q8_0
+3072x1024 with f32 x; Q4_K decode M=1,2,4,8 and prefill M=128,512,2048 on both
+MLP shapes; the Q8_0 LM head with argmax at M=5,40; the decoder layer at
+M=1,256), and the CPU baseline.  Inputs are synthetic: W ~ N(0, 0.02)
+quantized on the device, x ~ N(0, 1) in bf16, from torch's seeded generator.
 """
 from __future__ import annotations
 
@@ -27,6 +34,35 @@ sys.path.insert(0, os.path.join(ROOT, "token-horizon_amd"))
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA
 Q4K_BYTES_PER_256 = 144
+GEMM_ROUTE = ("the weight dequantized to bf16 once per call (k_dequant_q4_b16), then the bf16 MFMA GEMM "
+              "(k_gemm_b16); us_per_call covers both launches")
+
+
+PROBE_LIB = os.path.join(ROOT, "token-horizon_amd", "libthq_probe.so")
+
+
+def load_probe():
+    """The read-ceiling probes (libthq_probe.so, built beside libthq.so by
+    token-horizon_amd/build.py; not part of the product library)."""
+    import ctypes as C
+    lib = C.CDLL(PROBE_LIB)
+    for name in ("thqp_hbm_read", "thqp_hbm_read_x4"):
+        getattr(lib, name).argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.c_void_p, C.c_void_p]
+        getattr(lib, name).restype = C.c_int
+    lib.thqp_gemv_loads.argtypes = [C.c_void_p, C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_void_p]
+    lib.thqp_gemv_loads.restype = C.c_int
+    return lib
+
+
+def graph_upload(gt, stream):
+    """hipGraphUpload of a captured graph's executable on `stream`: the
+    graph's one-time device setup happens here, not at its first replay."""
+    import ctypes as C
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipGraphUpload.argtypes = [C.c_void_p, C.c_void_p]
+    rc = hip.hipGraphUpload(C.c_void_p(gt.raw_cuda_graph_exec()), C.c_void_p(stream.cuda_stream))
+    if rc != 0:
+        raise RuntimeError(f"hipGraphUpload failed: {rc}")
 
 
 def log(msg: str):
@@ -54,10 +90,11 @@ def time_graph(torch, fn_list, steps, warmup, start=0):
     (fn_list cycled, all of one shape, the timed calls continuing the
     rotation after the warmup ones).  The first warmup call runs eagerly, so
     that any workspace the shape needs exists before capture; the other
-    warmup calls and the timed calls are captured in a HIP graph each.  A
-    GPU sleep before the start event keeps the host's graph submission out
-    of the timed region.  Returns seconds for the `steps` calls (HIP events
-    on the launch stream)."""
+    warmup calls and the timed calls are captured in a HIP graph each.  The
+    timed graph is uploaded (hipGraphUpload) before the start event, and a
+    GPU sleep before that event keeps the host's graph submission out of the
+    timed region.  Returns seconds for the `steps` calls (HIP events on the
+    launch stream)."""
     s = torch.cuda.Stream()  # capture needs a non-default stream; everything runs on s
     n = len(fn_list)
     torch.cuda.synchronize()
@@ -75,6 +112,7 @@ def time_graph(torch, fn_list, steps, warmup, start=0):
         with torch.cuda.graph(gt, stream=s):
             for i in range(steps):
                 fn_list[(start + warmup + i) % n]()
+        graph_upload(gt, s)
         if gw is not None:
             gw.replay()
         s.synchronize()
@@ -168,6 +206,48 @@ def cpu_baseline(thq_w, n, k, budget_s=10.0):
     }
 
 
+def ceilings(torch, probe, ws, x1, steps, warmup):
+    """Single-launch read ceilings of the GEMV's byte count, rotated and
+    graph-timed exactly like the GEMV: a grid-stride read with one 16-B load
+    per lane per iteration (2048 and 4096 blocks), the same with four loads
+    in flight per lane, and the GEMV's own load pattern (its grid, x first,
+    nine 1-KB loads per wave, no math).  Returns (the fastest grid-stride
+    time, the load-pattern time, every figure)."""
+    N, K = ws[0].shape
+    wbytes = q4k_bytes(N, K)
+    copies = len(ws)
+    bufs = [torch.full((wbytes,), i, dtype=torch.uint8, device="cuda") for i in range(copies)]
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    cur = lambda: torch.cuda.current_stream().cuda_stream
+
+    def chk(rc):
+        if rc != 0:
+            raise RuntimeError(f"probe launch failed: {rc}")
+
+    out = {}
+    best = None
+    for blocks in (2048, 4096):
+        pf = [lambda b=b, nb=blocks: chk(probe.thqp_hbm_read(b.data_ptr(), wbytes, nb, sink.data_ptr(), cur()))
+              for b in bufs]
+        t = time_graph(torch, pf, steps, warmup) / steps
+        out[f"grid_stride_1x16B_{blocks}blk_us"] = round(t * 1e6, 3)
+        best = t if best is None else min(best, t)
+    pf = [lambda b=b: chk(probe.thqp_hbm_read_x4(b.data_ptr(), wbytes, 2048, sink.data_ptr(), cur())) for b in bufs]
+    t4 = time_graph(torch, pf, steps, warmup) / steps
+    out["grid_stride_4x16B_2048blk_us"] = round(t4 * 1e6, 3)
+    best = min(best, t4)
+    # the GEMV's own loads over buffers of its row-quad plane's size (N/4
+    # quads x K/256 superblocks x 576 B = the weight bytes) and x
+    nquads = (N + 3) // 4
+    assert nquads * (K // 256) * 576 == wbytes
+    pf = [lambda b=b: chk(probe.thqp_gemv_loads(b.data_ptr(), x1.data_ptr(), nquads, K // 256, sink.data_ptr(), cur()))
+          for b in bufs]
+    tl = time_graph(torch, pf, steps, warmup) / steps
+    out["gemv_load_pattern_us"] = round(tl * 1e6, 3)
+    del bufs
+    return best, tl, out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -178,9 +258,12 @@ def main():
     ap.add_argument("--gemm-warmup", type=int, default=30,
                     help="untimed GEMM calls before the timed ones (the first few milliseconds of sustained "
                          "MFMA load run 5-10 %% slower than the steady state)")
+    ap.add_argument("--gemm-copies", type=int, default=12,
+                    help="weight copies the GEMM calls rotate over (12 x 28.3 MB = 340 MB, more than the 256 MB MALL)")
     ap.add_argument("--eager", action="store_true", help="launch from Python instead of a HIP graph")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--extra", action="store_true", help="also time the other configurations")
+    ap.add_argument("--no-configs", action="store_true", help="skip the per-configuration object")
+    ap.add_argument("--extra", action="store_true", help="also time the other workloads (formats, modes, layers)")
     ap.add_argument("--only", default=None,
                     help="with --extra: only the sections whose name contains this (gemv_q8_0, q4k, affine, q6k, "
                          "lm_head_q6k, lm_head_q8_0, topk, decoder), e.g. for a profile of one workload")
@@ -204,8 +287,8 @@ def main():
     N, K = 12288, 4096
     copies = args.copies
     steps = args.steps
-    if steps < 1 or args.warmup < 0:
-        print("--steps must be >= 1 and --warmup >= 0", file=sys.stderr)
+    if steps < 1 or args.warmup < 0 or args.gemm_copies < 1 or args.gemm_copies > copies:
+        print("--steps must be >= 1, --warmup >= 0, 1 <= --gemm-copies <= --copies", file=sys.stderr)
         sys.exit(2)
     log(f"quantizing {copies} copies of Q4_K {N}x{K} ({copies * q4k_bytes(N, K) / 1e6:.0f} MB)")
     ws = make_weights(thq, torch, N, K, copies)
@@ -223,27 +306,20 @@ def main():
     gbs = gemv_bytes / per / 1e9
     log(f"GEMV M=1: {per * 1e6:.2f} us/call, {gbs:.0f} GB/s")
 
-    # the single-launch HBM read ceiling: a kernel that only reads the same
-    # weight bytes, launched, rotated and timed exactly like the GEMV
+    # single-launch read ceilings of the same byte count, launched, rotated
+    # and timed exactly like the GEMV
     wbytes = q4k_bytes(N, K)
-    bufs = [torch.full((wbytes,), i, dtype=torch.uint8, device="cuda") for i in range(copies)]
-    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
-    ceil_t, ceil_blocks = None, 0
-    for blocks in (2048, 4096):
-        pf = [lambda b=b, nb=blocks: thq.probe_hbm_read(b, sink, nb) for b in bufs]
-        t = time_graph(torch, pf, steps, args.warmup) / steps
-        if ceil_t is None or t < ceil_t:
-            ceil_t, ceil_blocks = t, blocks
-    del bufs
-    log(f"HBM read of the same {wbytes} B: {ceil_t * 1e6:.2f} us/launch ({wbytes / ceil_t / 1e9:.0f} GB/s)")
+    ceil_t, load_t, ceil_detail = ceilings(torch, load_probe(), ws, x1, steps, args.warmup)
+    log(f"HBM read of the same {wbytes} B: {ceil_t * 1e6:.2f} us/launch ({wbytes / ceil_t / 1e9:.0f} GB/s); "
+        f"the GEMV's load pattern alone: {load_t * 1e6:.2f} us")
 
-    # prefill GEMM M=2048 (bf16 out)
+    # prefill GEMM M=2048 (bf16 out), rotating --gemm-copies weight copies
     M = 2048
     xg = torch.randn((M, K), generator=g, device="cuda").to(torch.bfloat16)
     yg = torch.empty((M, N), dtype=torch.bfloat16, device="cuda")
-    gfns = [lambda w=w: thq.matmul(w, xg, out=yg) for w in ws[:3]]
+    gfns = [lambda w=w: thq.matmul(w, xg, out=yg) for w in ws[:args.gemm_copies]]
     it = args.gemm_iters
-    log(f"GEMM M={M}: {it} iterations")
+    log(f"GEMM M={M}: {it} iterations over {args.gemm_copies} weight copies")
     dtg = time_eager(torch, gfns, it, args.gemm_warmup)  # untimed calls stated in "gemm"
     flops = 2.0 * M * N * K
     tflops = flops / (dtg / it) / 1e12
@@ -255,9 +331,12 @@ def main():
     wbt = wbf.t()
     vend = time_eager(torch, [lambda: torch.matmul(xg, wbt, out=yg)], it, args.gemm_warmup)
     vend_tf = flops / (vend / it) / 1e12
-    del wbf, wbt
+    del wbf, wbt, xg, yg
     log(f"vendor bf16 GEMM (unquantized weights) M={M}: {vend / it * 1e6:.1f} us/call, {vend_tf:.1f} TFLOP/s")
 
+    configs = None
+    if not args.no_configs:
+        configs = run_configs(torch, thq, g, ws)
     extra = {}
     if args.extra:
         extra = run_extra(torch, thq, g, args.only)
@@ -282,23 +361,26 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "q4_k x bf16 -> f32 (f32 accumulate)",
-        "data": "synthetic: W ~ N(0,0.02) quantized to Q4_K on device, x ~ N(0,1) bf16 (torch seeded)",
+        "data": "synthetic: W ~ N(0,0.02) quantized on device, x ~ N(0,1) bf16 (torch seeded)",
         "config": {"workload": "Q4_K decode GEMV M=1, N=12288, K=4096 (Qwen3-8B-class gate/up projection)",
-                   "rotating_weight_copies": copies, "launch": "eager" if args.eager else "hip-graph",
+                   "rotating_weight_copies": copies, "launch": "eager" if args.eager else "hip-graph, uploaded before timing",
                    "algorithmic_bytes_per_call": gemv_bytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic.get("gemv"),
                      "traffic_profile": os.path.relpath(TRAFFIC_FILE, ROOT),
                      "single_launch_read_ceiling": {
-                         "kernel": f"k_hbm_read, {ceil_blocks} x 256 threads, 16-B loads of the same "
-                                   f"{wbytes} weight bytes, same rotation and graph timing",
+                         "kernels": "libthq_probe.so (bench-only): grid-stride 16-B reads of the same "
+                                    f"{wbytes} weight bytes, one or four loads in flight per lane; and the "
+                                    "GEMV's own load pattern with no math; same rotation and graph timing",
+                         **ceil_detail,
                          "us": round(ceil_t * 1e6, 3), "GBs": round(wbytes / ceil_t / 1e9, 1),
                          "frac_of_peak": round(wbytes / ceil_t / 1e9 / HBM_PEAK_GBS, 4),
-                         "gemv_time_over_ceiling": round(per / ceil_t, 3)}},
+                         "gemv_time_over_ceiling": round(per / ceil_t, 3),
+                         "gemv_time_over_load_pattern": round(per / load_t, 3)}},
         "gemm": {"workload": "Q4_K prefill GEMM M=2048, N=12288, K=4096, bf16 x -> bf16 y",
-                 "route": "the weight dequantized to bf16 once per call (k_dequant_q4_b16), then the bf16 MFMA GEMM "
-                          "(k_gemm_b16); us_per_call covers both launches",
-                 "tflops": round(tflops, 1), "us_per_call": round(dtg / it * 1e6, 1), "iters": it, "warmup": args.gemm_warmup,
+                 "route": GEMM_ROUTE,
+                 "tflops": round(tflops, 1), "us_per_call": round(dtg / it * 1e6, 1), "iters": it,
+                 "warmup": args.gemm_warmup, "rotating_weight_copies": args.gemm_copies,
                  "roofline": {"bound": "mfma", "achieved": round(tflops, 1), "peak": BF16_PEAK_TFLOPS,
                               "unit": "TFLOP/s", "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
                               "traffic": traffic.get("gemm")},
@@ -308,12 +390,128 @@ def main():
                      "frac_of_peak": round(vend_tf / BF16_PEAK_TFLOPS, 4),
                      "quantized_time_over_vendor": round(dtg / vend, 3)}},
     }
+    if configs:
+        out["configs"] = configs
     if extra:
         out["extra"] = extra
     if not args.no_cpu_baseline:
         log("CPU baseline (oracle AVX2 Q8-activation GEMV), ~10 s")
         out["cpu_baseline"] = cpu_baseline(ws[0], N, K)
     print(json.dumps(out), flush=True)
+
+
+def line(us, work, unit, peak):
+    """One configuration's entry: time per call, rate and roofline fraction."""
+    rate = work / (us * 1e-6) / (1e9 if unit == "GB/s" else 1e12)
+    return {"us": round(us, 2), unit: round(rate, 1), "frac": round(rate / peak, 4)}
+
+
+def run_configs(torch, thq, g, ws_gu):
+    """Every benchmark configuration of the path, on synthetic inputs of its
+    shapes, weights rotated beyond the MALL.  Decode lines (HBM-bound, a few
+    microseconds per call) run from an uploaded HIP graph; GEMM, LM-head and
+    prefill-layer lines are eager (each call far above launch cost)."""
+    res = {}
+    HB, MF = HBM_PEAK_GBS, BF16_PEAK_TFLOPS
+
+    def graph_us(fns, steps=240):
+        return time_graph(torch, fns, steps, 16) / steps * 1e6
+
+    def eager_us(fns, it, warm):
+        return time_eager(torch, fns, it, warm) / it * 1e6
+
+    # 1: Q8_0 3072 x 1024 with f32 activations, M = 1 (96 copies: 322 MB)
+    log("configs: Q8_0 3072x1024, f32 x")
+    n, k = 3072, 1024
+    base = make_q8_0(thq, torch, n, k, seed=0)
+    raw = torch.from_numpy(base.data().ravel().copy()).cuda()
+    w8 = [base] + [thq.QTensor.from_gguf_bytes(thq.Q8_0, raw, n, k) for _ in range(95)]
+    del raw
+    x = torch.randn((1, k), generator=g, device="cuda")
+    y = torch.empty((1, n), dtype=torch.float32, device="cuda")
+    us = graph_us([lambda w=w: thq.matmul(w, x, out=y) for w in w8])
+    res["c1_q8_0_n3072_k1024_m1_f32x"] = line(us, n * (k // 32) * 34 + 4 * k + 4 * n, "GB/s", HB)
+    del w8
+    # 2 and 3: Q4_K gate/up shape (the headline copies) and down shape
+    log("configs: Q4_K decode M=1,2,4,8 and prefill M=128,512,2048 on both shapes")
+    for (n, k) in [(12288, 4096), (4096, 12288)]:
+        ws = ws_gu if n == 12288 else make_weights(thq, torch, n, k, 24, seed=5 + n)
+        for m in (1, 2, 4, 8):
+            x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
+            y = torch.empty((m, n), dtype=torch.float32, device="cuda")
+            us = graph_us([lambda w=w, x=x, y=y: thq.matmul(w, x, out=y) for w in ws])
+            res[f"c2_q4k_n{n}_k{k}_m{m}"] = line(us, q4k_bytes(n, k) + m * (2 * k + 4 * n), "GB/s", HB)
+        for m in (128, 512, 2048):
+            x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
+            y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
+            it = 40 if m < 2048 else 24
+            us = eager_us([lambda w=w, x=x, y=y: thq.matmul(w, x, out=y) for w in ws[:12]], it, 12)
+            res[f"c3_q4k_n{n}_k{k}_m{m}"] = line(us, 2.0 * m * n * k, "TFLOP/s", MF)
+        if ws is not ws_gu:
+            del ws
+    # 4: verify LM head, Q8_0 151936 x 4096 (661 MB, beyond the MALL), logits + argmax
+    log("configs: Q8_0 LM head 151936x4096 + argmax, M=5,40")
+    V, H = 151936, 4096
+    wl = make_q8_0(thq, torch, V, H, seed=11)
+    for m in (5, 40):
+        x = torch.randn((m, H), generator=g, device="cuda").to(torch.bfloat16)
+        lg = torch.empty((m, V), dtype=torch.float32, device="cuda")
+        ix = torch.empty((m,), dtype=torch.int32, device="cuda")
+        us = eager_us([lambda x=x, lg=lg, ix=ix: thq.matmul_argmax(wl, x, logits=lg, idx=ix)], 30, 4)
+        res[f"c4_lm_head_q8_0_m{m}"] = line(us, V * (H // 32) * 34 + m * (2 * H + 4 * V), "GB/s", HB)
+    del wl
+    # 5: decoder layer (QKV, o, gate/up + SiLU, down), 4 layers rotating (434 MB)
+    log("configs: Q4_K decoder layer M=1,256")
+    layers = make_layers(thq, torch, 4)
+    layer_bytes = q4k_bytes(6144, 4096) + q4k_bytes(4096, 4096) + q4k_bytes(24576, 4096) + q4k_bytes(4096, 12288)
+    for m in (1, 256):
+        fns = layer_fns(torch, thq, g, layers, m)
+        if m == 1:
+            us = graph_us(fns, 96)
+            res["c5_decoder_layer_q4k_m1"] = line(us, layer_bytes + 4 * (2 * 4096) + 2 * 12288, "GB/s", HB)
+        else:
+            us = eager_us(fns, 24, 4)
+            flops = 2.0 * m * (6144 + 4096 + 24576) * 4096 + 2.0 * m * 4096 * 12288
+            res["c5_decoder_layer_q4k_m256"] = line(us, flops, "TFLOP/s", MF)
+    del layers
+    torch.cuda.synchronize()
+    return res
+
+
+def make_layers(thq, torch, count):
+    """Qwen3-8B-class decoder layers of Q4_K weights: (QKV 6144x4096, o
+    4096x4096, fused gate/up 2x12288x4096, down 4096x12288)."""
+    layers = []
+    for i in range(count):
+        def q(n, k, s):
+            gg = torch.Generator(device="cuda").manual_seed(100 + 10 * i + s)
+            wf = torch.randn((n, k), generator=gg, device="cuda", dtype=torch.float32) * 0.02
+            w = thq.QTensor.quantize(wf, thq.Q4_K)
+            del wf
+            return w
+        gate, up = q(12288, 4096, 2), q(12288, 4096, 3)
+        layers.append((q(6144, 4096, 0), q(4096, 4096, 1), thq.QTensor.fuse([gate, up]), q(4096, 12288, 4)))
+        del gate, up
+    torch.cuda.synchronize()
+    return layers
+
+
+def layer_fns(torch, thq, g, layers, m):
+    """One call per layer: the four projections back to back on one stream
+    (bf16 outputs; down reads the gate/up output)."""
+    x = torch.randn((m, 4096), generator=g, device="cuda").to(torch.bfloat16)
+    qkv = torch.empty((m, 6144), dtype=torch.bfloat16, device="cuda")
+    o = torch.empty((m, 4096), dtype=torch.bfloat16, device="cuda")
+    h = torch.empty((m, 12288), dtype=torch.bfloat16, device="cuda")
+    d = torch.empty((m, 4096), dtype=torch.bfloat16, device="cuda")
+
+    def layer(L):
+        thq.matmul(L[0], x, out=qkv)
+        thq.matmul(L[1], x, out=o)
+        thq.gate_up_silu(L[2], x, out=h)
+        thq.matmul(L[3], h, out=d)
+
+    return [lambda L=L: layer(L) for L in layers]
 
 
 def make_q8_0(thq, torch, n, k, seed):
@@ -406,7 +604,7 @@ def run_extra(torch, thq, g, only=None):
         for m in (128, 512, 2048):
             x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
             y = torch.empty((m, n), dtype=torch.bfloat16, device="cuda")
-            fns = [lambda w=w, x=x, y=y: thq.matmul(w, x, out=y) for w in ws[:3]]
+            fns = [lambda w=w, x=x, y=y: thq.matmul(w, x, out=y) for w in ws[:12]]
             it = 30 if m >= 512 else 120
             dt = time_eager(torch, fns, it, 6) / it
             res[f"gemm_q4k_n{n}_k{k}_m{m}"] = {"us": round(dt * 1e6, 1),
@@ -460,7 +658,7 @@ def run_affine(torch, thq, g, res, gemv_line):
         res[f"gemv_affine_n{n}_k{k}_m{m}"] = gemv_line(fns, q4k_bytes(n, k) + m * (2 * k + 4 * n))
     x = torch.randn((2048, k), generator=g, device="cuda").to(torch.bfloat16)
     y = torch.empty((2048, n), dtype=torch.bfloat16, device="cuda")
-    fns = [lambda w=w, x=x, y=y: thq.matmul(w, x, out=y) for w in ws[:3]]
+    fns = [lambda w=w, x=x, y=y: thq.matmul(w, x, out=y) for w in ws[:12]]
     dt = time_eager(torch, fns, 30, 6) / 30
     res[f"gemm_affine_n{n}_k{k}_m2048"] = {"us": round(dt * 1e6, 1), "TFLOPs": round(2.0 * 2048 * n * k / dt / 1e12, 1)}
     del ws
@@ -476,7 +674,7 @@ def run_q6k(torch, thq, g, res, gemv_line):
         res[f"gemv_q6k_n{n}_k{k}_m1"] = gemv_line(fns, q6k_bytes(n, k) + 2 * k + 4 * n)
         x = torch.randn((2048, k), generator=g, device="cuda").to(torch.bfloat16)
         y = torch.empty((2048, n), dtype=torch.bfloat16, device="cuda")
-        fns = [lambda w=w, x=x, y=y: thq.matmul(w, x, out=y) for w in ws[:3]]
+        fns = [lambda w=w, x=x, y=y: thq.matmul(w, x, out=y) for w in ws[:12]]
         dt = time_eager(torch, fns, 30, 6) / 30
         res[f"gemm_q6k_n{n}_k{k}_m2048"] = {"us": round(dt * 1e6, 1), "TFLOPs": round(2.0 * 2048 * n * k / dt / 1e12, 1)}
         del ws
@@ -546,18 +744,7 @@ def run_topk(torch, thq, g, res):
 
 def run_decoder(torch, thq, g, res):
     log("extra: decoder layer (QKV, o, fused gate/up + silu, down), 4 layers rotating")
-    layers = []
-    for i in range(4):
-        def q(n, k, s):
-            gg = torch.Generator(device="cuda").manual_seed(100 + 10 * i + s)
-            wf = torch.randn((n, k), generator=gg, device="cuda", dtype=torch.float32) * 0.02
-            w = thq.QTensor.quantize(wf, thq.Q4_K)
-            del wf
-            return w
-        gate, up = q(12288, 4096, 2), q(12288, 4096, 3)
-        layers.append((q(6144, 4096, 0), q(4096, 4096, 1), thq.QTensor.fuse([gate, up]), q(4096, 12288, 4)))
-        del gate, up
-    torch.cuda.synchronize()
+    layers = make_layers(thq, torch, 4)
     layer_bytes = q4k_bytes(6144, 4096) + q4k_bytes(4096, 4096) + q4k_bytes(24576, 4096) + q4k_bytes(4096, 12288)
     # M = 5: one speculative-verify step (4 drafted tokens + 1), with and
     # without the weights' tile planes

@@ -81,14 +81,6 @@ typedef struct thq_tile_plan_info {
 int thq_plan_gemv_tile(int dtype, int64_t m, int64_t n, int64_t k, int gate_up, int cus,
                        thq_tile_plan_info* out);
 
-/* Measurement aid: read `bytes` (a multiple of 16) of buf_dev (16-byte
- * aligned) once with 16-B loads from `blocks` blocks of 256 threads, on
- * `stream`; sink_dev (4 bytes) is written only in the unlikely case the
- * XOR of the data is a fixed constant.  bench.py times it beside the decode
- * GEMV, launched the same way over the same byte count: the single-launch
- * HBM read ceiling that kernel is compared against. */
-int thq_probe_hbm_read(thq_ctx* ctx, const void* buf_dev, size_t bytes, int blocks, uint32_t* sink_dev, void* stream);
-
 #ifdef __cplusplus
 }
 #endif

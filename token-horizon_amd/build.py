@@ -1,6 +1,7 @@
 """Build libthq.so (gfx950 HIP kernels + the C ABI) in-tree.
 
     python token-horizon_amd/build.py          # builds token-horizon_amd/libthq.so
+                                               # and libthq_probe.so (bench.py's read probes)
 
 Each source compiles separately with hipcc (in parallel) into _build/, then
 links into one shared library next to this file.  Flags:
@@ -23,11 +24,14 @@ CSRC = os.path.join(HERE, "csrc")
 HOST = os.path.join(HERE, "host")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libthq.so")
+# measurement aids for bench.py only, kept out of the product library's ABI
+PROBE_SOURCES = ["k_probe.hip"]
+PROBE_LIB = os.path.join(HERE, "libthq_probe.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 SOURCES = [
     "thq_api.cpp", "k_weights.hip", "k_gemv.hip", "k_gemv_mfma.hip", "k_gemm.hip", "k_argmax.hip", "k_q8act.hip",
-    "k_q6k.hip", "k_topk.hip", "k_probe.hip", "k_gemv_wide.hip", "k_gemv_tile.hip", "k_gemm_b16.hip",
+    "k_q6k.hip", "k_topk.hip", "k_gemv_wide.hip", "k_gemv_tile.hip", "k_gemm_b16.hip",
     "thq_gguf.cpp",
 ]
 FLAGS = [
@@ -54,19 +58,24 @@ def _compile(src: str) -> str:
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = True) -> str:
-    os.makedirs(BUILD, exist_ok=True)
-    jobs = jobs or min(8, len(SOURCES))
-    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB + ".tmp"
+def _link(objs: list[str], lib: str) -> None:
+    tmp = lib + ".tmp"
     cmd = [HIPCC, "-shared", "-fPIC", "--offload-arch=gfx950", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed: {' '.join(cmd)}\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(jobs: int | None = None, verbose: bool = True) -> str:
+    os.makedirs(BUILD, exist_ok=True)
+    jobs = jobs or min(8, len(SOURCES) + len(PROBE_SOURCES))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+        objs = list(ex.map(_compile, SOURCES + PROBE_SOURCES))
+    _link(objs[:len(SOURCES)], LIB)
+    _link(objs[len(SOURCES):], PROBE_LIB)
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {PROBE_LIB}")
     return LIB
 
 

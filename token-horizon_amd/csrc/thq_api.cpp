@@ -1290,16 +1290,6 @@ int thq_plan_gemv_mfma(int dtype, int64_t m, int64_t n, int64_t k, int gate_up, 
     return THQ_OK;
 }
 
-int thq_probe_hbm_read(thq_ctx* ctx, const void* buf_dev, size_t bytes, int blocks, uint32_t* sink_dev, void* stream) {
-    if (!ctx || !buf_dev || !sink_dev) return fail(THQ_EINVAL, "null argument");
-    if (bytes % 16 || blocks < 1 || blocks > (1 << 20)) return fail(THQ_ESHAPE, "bytes %zu / blocks %d", bytes, blocks);
-    if (!aligned16(buf_dev)) return fail(THQ_EALIGN, "buf_dev must be 16-byte aligned");
-    DeviceGuard g(ctx->device);
-    hipError_t e = thq::launch_hbm_read(buf_dev, bytes, blocks, sink_dev, static_cast<hipStream_t>(stream));
-    if (e != hipSuccess) return fail(THQ_EHIP, "kernel launch: %s", hipGetErrorString(e));
-    return THQ_OK;
-}
-
 int thq_plan_gemv_wide(int dtype, int64_t m, int64_t n, int64_t k, int cus, thq_wide_plan_info* out) {
     const int qt = kernel_qtype(dtype);
     if (!qt) return fail(THQ_EDTYPE, "dtype %d", dtype);

@@ -186,9 +186,6 @@ size_t argmax_partials_tmp_bytes(int64_t m, int64_t nb);
 hipError_t launch_argmax_partials(const float* v, const uint32_t* i, int64_t m, int64_t nb, int64_t ld,
                                   uint32_t* idx, void* tmp, hipStream_t s);
 
-// measurement aid: one pass of 16-B reads over bytes (a multiple of 16), k_probe.hip
-hipError_t launch_hbm_read(const void* buf, size_t bytes, int blocks, uint32_t* sink, hipStream_t s);
-
 // exact per-row top-k (k <= 64) by (logit desc, id asc), k_topk.hip
 size_t topk_workspace_bytes(int64_t m, int64_t n, int k);
 hipError_t launch_topk(const float* v, int64_t m, int64_t n, int k, float* vals, uint32_t* idx, void* ws,

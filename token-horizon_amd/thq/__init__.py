@@ -54,7 +54,7 @@ EXPORTS = (
     "thq_gguf_metadata_u32", "thq_gguf_metadata_f32", "thq_gguf_metadata_str", "thq_gguf_metadata_array",
     "thq_weight_from_gguf", "thq_q8act_bytes", "thq_q8act_prepare", "thq_matmul_q8act", "thq_gate_up_silu_q8act",
     "thq_plan_gemv_mfma", "thq_plan_gemm", "thq_plan_gemv_wide", "thq_matmul_noalloc", "thq_noalloc_scratch_bytes",
-    "thq_topk", "thq_matmul_topk", "thq_gate_up_silu_q8act_emit", "thq_probe_hbm_read", "thq_weight_add_tiles", "thq_plan_gemv_tile",
+    "thq_topk", "thq_matmul_topk", "thq_gate_up_silu_q8act_emit", "thq_weight_add_tiles", "thq_plan_gemv_tile",
 )
 
 
@@ -165,7 +165,6 @@ def _load():
         "thq_gate_up_silu_q8act": ([P, P, I, P, i64, i64, P, I, P], I),
         "thq_matmul_noalloc": ([P, P, P, I, i64, P, I, u32, P], I),
         "thq_topk": ([P, P, i64, i64, I, P, P, P], I),
-        "thq_probe_hbm_read": ([P, P, C.c_size_t, I, P, P], I),
         "thq_gate_up_silu_q8act_emit": ([P, P, I, P, i64, i64, P, I, P, P], I),
         "thq_matmul_topk": ([P, P, P, I, i64, I, P, P, P, u32, P], I),
         "thq_noalloc_scratch_bytes": ([], C.c_size_t),
@@ -465,12 +464,6 @@ def topk(v: torch.Tensor, k: int, ctx: Context | None = None):
     idx = torch.empty((m, k), dtype=torch.int32, device=v.device)
     check(lib.thq_topk(ctx.h, _ptr(v2), m, n, k, _ptr(vals), _ptr(idx), _stream()))
     return vals, idx
-
-
-def probe_hbm_read(buf: torch.Tensor, sink: torch.Tensor, blocks: int = 4096, ctx: Context | None = None):
-    """One pass of 16-B reads over a device buffer (measurement aid)."""
-    ctx = ctx or Context.get(buf.device.index or 0)
-    check(lib.thq_probe_hbm_read(ctx.h, _ptr(buf), buf.numel() * buf.element_size(), blocks, _ptr(sink), _stream()))
 
 
 def matmul_topk(w: QTensor, x: torch.Tensor, k: int, want_logits: bool = False, flags: int = 0):
