@@ -5,21 +5,24 @@
 // Role: the reference router's "dequant + bf16 matmul" prefill route
 // (pf_route, engine/src/quant_kernel.rs:5117-5300, with AffineDequant
 // :1035-1040 writing the bf16 scratch).  For large M this beats
-// dequantizing inside the GEMM tile: on gfx950 the tile's dequantization
-// VALU does not overlap the MFMAs, and a 256-row tile repeats it once per
-// row block (8 times at M = 2048), while one pass over the weights costs
-// about 20 us.
+// dequantizing inside the GEMM tile (k_gemm_fq.hip): a 512-row tile repeats
+// the conversion once per row block (4 times at M = 2048), about 62 VALU
+// instructions per wave per 32-wide K step that the MFMAs do not fully
+// hide, while one pass over the weights costs about 25 us.
 //
-// Tiling: block tile 256 (M) x 384 (N) x 32 (K), 8 waves (two per SIMD) as
-// 2 (M) x 4 (N), wave tile 128 x 96 of v_mfma_f32_32x32x16_bf16 (96 f32
+// Tiling: block tile 256 (M) x 384 (N) x 64 (K), 8 waves (two per SIMD) as
+// 2 (M) x 4 (N), wave tile 128 x 96 of v_mfma_f32_32x32x16_bf16 (192 f32
 // accumulators per lane).  Each wave reads one set of fragments per 16-wide
-// K step and runs its 12 MFMAs; the SIMD's other wave covers the LDS
-// latency.  Operands come in by direct-to-LDS copies (global_load_lds_
-// dwordx4) into a 3-slot ring, two K steps ahead, with 64-B LDS rows whose
-// 16-B chunks are XOR-swizzled (chunk c of row r at slot c ^ ((r >> 2) & 3):
-// any 16 consecutive rows at one chunk hit 16 distinct bank groups).  One
-// block barrier per K step.  Blocks are dealt to the 8 XCDs round-robin; the
-// grid is renumbered so each XCD runs a contiguous range of tiles, 8 row
+// k group and runs its 12 MFMAs, 48 per K step; the SIMD's other wave
+// covers the LDS latency.  Operands come in by direct-to-LDS copies
+// (global_load_lds_dwordx4) into 2 slots (160 KB), the next K step's copies
+// issued right after the barrier that frees their slot, with 128-B LDS rows
+// whose 16-B chunks are XOR-swizzled (chunk c of row r at slot
+// c ^ ((r >> 1) & 7): any 16 consecutive rows at one chunk hit 16 distinct
+// bank groups).  One block barrier per 64-wide K step (a 32-wide step with a
+// 3-slot ring, one barrier per 32: 2048 x 12288 x 4096 in 211 against 174 us,
+// 4096 x 12288 x 4096 356 against 322 us, weights streamed from HBM).
+// Blocks are dealt to the 8 XCDs round-robin; the grid is renumbered so each XCD runs a contiguous range of tiles, 8 row
 // blocks x all column blocks at a time: at M = 2048 an XCD's 32 tiles are
 // all 8 row blocks of 4 column blocks, so each bf16 weight byte leaves HBM
 // once (x, 6x smaller, once per XCD; 4 row blocks x 8 column blocks fetched
@@ -32,7 +35,7 @@
 namespace thq {
 namespace {
 
-constexpr int GB_BM = 256, GB_BN = 384, GB_BK = 32, GB_NS = 3;
+constexpr int GB_BM = 256, GB_BN = 384, GB_BK = 64, GB_NS = 2;
 
 __device__ __forceinline__ uint32_t gb_lds(const void* p) {
     return (uint32_t)(size_t)(__attribute__((address_space(3))) const void*)p;
@@ -47,7 +50,7 @@ template <int N>
 __device__ __forceinline__ void gb_wait_vm() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
-__device__ __forceinline__ int gb_slot(int r, int c) { return c ^ ((r >> 2) & 3); }
+__device__ __forceinline__ int gb_slot(int r, int c) { return c ^ ((r >> 1) & 7); }
 __device__ __forceinline__ int gb_swz(int r, int c) { return r * GB_BK + (gb_slot(r, c) << 3); }
 __device__ __forceinline__ f32x16_t gb_mfma(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -74,9 +77,8 @@ __global__ __launch_bounds__(512) void k_gemm_b16(const bf16_t* __restrict__ X, 
                                                  int tiles_m) {
     constexpr int TM = 128, TN = 96, MT = 4, NT = 3;
     constexpr int WNV = GB_BN / TN;         // 4 waves along N
-    constexpr int XI = GB_BM * 4 / 512;     // X copies per wave per step (16-B chunks / 64 lanes / 8 waves)
-    constexpr int WI = GB_BN * 4 / 512;     // W copies per wave per step
-    constexpr int PS = XI + WI;
+    constexpr int XI = GB_BM * 8 / 512;     // X copies per wave per step (16-B chunks / 64 lanes / 8 waves)
+    constexpr int WI = GB_BN * 8 / 512;     // W copies per wave per step
     __shared__ __attribute__((aligned(16))) bf16_t Xs[GB_NS][GB_BM * GB_BK];
     __shared__ __attribute__((aligned(16))) bf16_t Ws[GB_NS][GB_BN * GB_BK];
     const int lane = threadIdx.x & 63;
@@ -86,22 +88,22 @@ __global__ __launch_bounds__(512) void k_gemm_b16(const bf16_t* __restrict__ X, 
     gb_tile(tiles_n, tiles_m, tn, tm);
     const int m0 = tm * GB_BM, n0 = tn * GB_BN;
     const int T = K / GB_BK;
-    // copy descriptors: instruction i of this wave covers 16 rows; lane ->
-    // row lane / 4, LDS slot lane % 4, which holds chunk gb_slot(row, slot)
+    // copy descriptors: instruction i of this wave covers 8 rows; lane ->
+    // row lane / 8, LDS slot lane % 8, which holds chunk gb_slot(row, slot)
     uint32_t xoff[XI], woff[WI];
 #pragma unroll
     for (int i = 0; i < XI; ++i) {
-        const int r = wave * (GB_BM / 8) + 16 * i + (lane >> 2);
+        const int r = wave * (GB_BM / 8) + 8 * i + (lane >> 3);
         int m = m0 + r;
         if (m >= M) m = M - 1;
-        xoff[i] = (uint32_t)(((int64_t)m * K + 8 * gb_slot(r, lane & 3)) * 2);
+        xoff[i] = (uint32_t)(((int64_t)m * K + 8 * gb_slot(r, lane & 7)) * 2);
     }
 #pragma unroll
     for (int i = 0; i < WI; ++i) {
-        const int r = wave * (GB_BN / 8) + 16 * i + (lane >> 2);
+        const int r = wave * (GB_BN / 8) + 8 * i + (lane >> 3);
         int n = n0 + r;
         if (n >= N) n = N - 1;
-        woff[i] = (uint32_t)(((int64_t)n * K + 8 * gb_slot(r, lane & 3)) * 2);
+        woff[i] = (uint32_t)(((int64_t)n * K + 8 * gb_slot(r, lane & 7)) * 2);
     }
     const uint32_t xl = gb_lds(&Xs[0][0]) + wave * (GB_BM / 8) * GB_BK * 2;
     const uint32_t wl = gb_lds(&Ws[0][0]) + wave * (GB_BN / 8) * GB_BK * 2;
@@ -120,20 +122,18 @@ __global__ __launch_bounds__(512) void k_gemm_b16(const bf16_t* __restrict__ X, 
         for (int j = 0; j < NT; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-#pragma unroll
-    for (int p = 0; p < GB_NS - 1; ++p)
-        if (p < T) copy(p);
+    if (T > 0) copy(0);
     for (int t = 0; t < T; ++t) {
-        // step t's copies have landed (the next step's may stay in flight),
-        // for every wave: then slot (t - 1) % 3 is free for step t + 2
-        if (t + 1 < T) gb_wait_vm<PS>();
-        else gb_wait_vm<0>();
+        // step t's copies have landed, for every wave (they are the only ones
+        // in flight); after the barrier every wave is past step t - 1, so
+        // slot (t + 1) % 2 is free for step t + 1
+        gb_wait_vm<0>();
         __syncthreads();
-        if (t + GB_NS - 1 < T) copy(t + GB_NS - 1);
+        if (t + 1 < T) copy(t + 1);
         const bf16_t* xs = &Xs[t % GB_NS][0];
         const bf16_t* ws = &Ws[t % GB_NS][0];
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+        for (int kk = 0; kk < 4; ++kk) {
             const int ch = 2 * kk + lh;
             bf16x8_t a[MT], b[NT];
 #pragma unroll

@@ -295,7 +295,7 @@ int check_call(const Call& c) {
 
 // The kernels a call runs, and the device scratch (split-K partials or the
 // quantized activation planes) they use, known before anything launches.
-enum class Kind { NONE, Q8ACT, Q8ACT_TILE, GEMV1, ROWS, GEMV_TILE, GEMV_MFMA, GEMV_MFMA_GROUPS, WIDE, GEMM, GEMM_DQ, GENERIC };
+enum class Kind { NONE, Q8ACT, Q8ACT_TILE, GEMV1, ROWS, GEMV_TILE, GEMV_MFMA, GEMV_MFMA_GROUPS, WIDE, GEMM, GEMM_DQ, GEMM_FQ, GENERIC };
 struct Route {
     Kind kind = Kind::NONE;
     thq::GemvPlan gp;
@@ -303,6 +303,7 @@ struct Route {
     thq::WidePlan wp;
     thq::TilePlan tp;
     thq::GemmPlan gm;
+    thq::FqPlan fq;
     bool exact = false;
     size_t scratch = 0;
 };
@@ -455,6 +456,19 @@ Route plan_route(const Call& c) {
             r.kind = Kind::GEMM_DQ;
             r.scratch = wb_bytes;
         }
+        // Q4_K / MLX affine with rounded weights: the GEMM that dequantizes
+        // its weight tiles into LDS (k_gemm_fq).  THQ_GEMM_FQ: 0 never,
+        // 1 wherever supported, unset: off
+        const char* fqe = getenv("THQ_GEMM_FQ");
+        const int fq_mode = fqe && *fqe ? atoi(fqe) : 0;
+        if (q4 && !r.exact && fq_mode == 1 && thq::gemm_fq_supported(m, w->N, w->K, c.gu)) {
+            const thq::FqPlan fp = thq::plan_gemm_fq(m, w->N, w->K, c.gu, c.ctx->cus);
+            if (fp.workspace_bytes <= c.scratch_cap) {
+                r.kind = Kind::GEMM_FQ;
+                r.fq = fp;
+                r.scratch = fp.workspace_bytes;
+            }
+        }
     } else if (!xf32 && aligned16(c.x) && (q4 || q6) && m > 16 && w->K % 256 == 0 &&
                thq::plan_gemv_mfma(v.qtype, 16, w->N, w->K, c.gu).waves > 0) {
         // exact 4- / 6-bit weights past the decode GEMV's 16 rows (the verify
@@ -522,6 +536,10 @@ int exec_route(const Call& c, const Route& r, void* scratch, uint32_t* cnt = nul
             break;
         case Kind::GEMM:
             e = thq::launch_gemm(r.gm, v, c.x, c.y, yf32, c.gu, r.exact, m, static_cast<float*>(scratch), c.s);
+            break;
+        case Kind::GEMM_FQ:
+            e = thq::launch_gemm_fq(r.fq, w->qtype == THQ_MLX_Q4, w->q, c.x, c.y, yf32, c.gu, m, w->N, (int)w->K,
+                                    static_cast<float*>(scratch), c.s);
             break;
         case Kind::GEMM_DQ:
             // the weight as bf16 [N][K] in the scratch, then x . Wb^T

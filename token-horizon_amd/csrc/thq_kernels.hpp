@@ -132,6 +132,18 @@ hipError_t launch_q8act_tile(const TilePlan& p, const WeightView& w, const uint8
 // sum split partials P[s][M][ldp] in split order, then the epilogue
 hipError_t launch_split_reduce(const float* P, void* y, bool yf32, bool gu, int M, int64_t nout, int64_t up_off,
                                int64_t ldp, int splits, hipStream_t s);
+// prefill GEMM with the Q4_K / MLX affine weight dequantized into LDS
+// (k_gemm_fq.hip): geometry (block tile), grid and K splits of a call
+struct FqPlan {
+    int geom = 1;  // 1: 256 x 256 (gate/up: always), 2: 128 x 256, 3: 512 x 192
+    int tiles_m = 0, tiles_n = 0;
+    int kps = 0, splits = 1;  // 32-wide K steps per split
+    size_t workspace_bytes = 0;  // split partials, f32 [splits][M][N rows]
+};
+bool gemm_fq_supported(int64_t M, int64_t N_rows, int64_t K, bool gu);
+FqPlan plan_gemm_fq(int64_t M, int64_t N_rows, int64_t K, bool gu, int cus);
+hipError_t launch_gemm_fq(const FqPlan& p, bool aff, const uint8_t* wq, const void* x, void* y, bool yf32, bool gu,
+                          int M, int64_t N_rows, int K, float* ws, hipStream_t s);
 // exact generic kernel, any M, scalar activation loads
 hipError_t launch_generic(const WeightView& w, const void* x, bool xf32, void* y, bool yf32, bool gu, int M,
                           int64_t nout, int64_t up_off, hipStream_t s);
