@@ -288,6 +288,23 @@ int thq_matmul_noalloc(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq
                        void* y_dev, thq_act y_type, uint32_t flags, void* stream);
 size_t thq_noalloc_scratch_bytes(void);
 
+/* Workspace planning for callers that capture thq calls in a HIP graph (or
+ * must not allocate later).  No counterpart in the reference (its Metal
+ * pipelines size their scratch inside each op).  thq_call_scratch_bytes
+ * plans the route one thq_matmul (gate_up = 0) or thq_gate_up_silu
+ * (gate_up = 1) call of M rows would take, on the host, and returns the
+ * context workspace bytes it needs (0 for routes with no scratch); no device
+ * work.  thq_reserve grows the context workspace to at least
+ * workspace_bytes and the context's zeroed split-K arrival counters to at
+ * least `counters` entries (one per 32-row output tile of the widest
+ * weight), synchronously (hipMalloc, hipMemset, device synchronize); calls
+ * whose needs fit then allocate nothing.  thq_workspace_bytes returns the
+ * current workspace size. */
+int thq_call_scratch_bytes(thq_ctx* ctx, const thq_weight* w, int64_t m, thq_act x_type, uint32_t flags,
+                           int gate_up, size_t* bytes);
+int thq_reserve(thq_ctx* ctx, size_t workspace_bytes, int64_t counters);
+size_t thq_workspace_bytes(const thq_ctx* ctx);
+
 /* Fused gate/up projection: `fused` = [gate; up] (2H rows).  y[M, H] =
  * bf16( silu(bf16(g)) * bf16(u) ) with silu in f32, g = x.gate^T, u = x.up^T.
  * Replaces QLin::gate_up_act_ps (engine/src/qwen35.rs:711-884) and its kernel

@@ -122,10 +122,9 @@ __device__ __forceinline__ void tile_finish(float (&tot)[NT][4], float* red, YT*
             if (4 * g + e < M)
                 store_y<YT>(Y + (int64_t)(4 * g + e) * nout + row, GU ? silu_mul(tot[0][e], tot[NT - 1][e]) : tot[0][e]);
     } else {
-        // partials as device-scope stores (written through to the point all
-        // XCDs share) when the last block sums them: once they have
-        // completed (vmcnt 0) the ticket, a device-scope atomic, is ordered
-        // after them, and the last block's device-scope loads see them
+        // partials as device-scope stores when the last block sums them; a
+        // release fence orders them before the ticket (device-scope acq_rel)
+        // and the last block's acquire fence orders its loads after it
         const int64_t ldp = NT * nout;
         if (wave == 0 && row < nout) {
 #pragma unroll
@@ -143,13 +142,12 @@ __device__ __forceinline__ void tile_finish(float (&tot)[NT][4], float* red, YT*
         }
         if (!cnt) return;
         __shared__ int last;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        ticket_release();
         __syncthreads();
-        if (threadIdx.x == 0)
-            last = __hip_atomic_fetch_add(cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                   gridDim.y - 1;
+        if (threadIdx.x == 0) last = ticket_draw(cnt + tile) == gridDim.y - 1;
         __syncthreads();
         if (!last) return;
+        ticket_acquire();
         // the tile's outputs, one per thread: the splits' partials in split
         // order (k_split_reduce's sums, bit for bit), loads batched 8 deep
         const int splits = (int)gridDim.y;

@@ -423,17 +423,18 @@ __global__ __launch_bounds__(256) void k_q8act_q4k(const uint8_t* __restrict__ W
     for (int i = 0; i < NR * MT; ++i) acc[i] = p == 0 ? acc[i] : 0.0f;  // one lane per quad
     q8act_store<MT, GU, YT, EMIT>(acc, lane, y, o0, nout, m0, mrows, ldy);
     if constexpr (EMIT) {
-        // the outputs went out as device-scope stores: once they have
-        // completed (vmcnt 0), the ticket (a device-scope atomic) is ordered
-        // after them, and the last block's device-scope loads see them
+        // the outputs went out as device-scope stores; a release fence orders
+        // them before the ticket (device-scope acq_rel) and the last block's
+        // acquire fence orders its loads after it
         __shared__ int last;
         const int64_t seg = blockIdx.x >> 4;  // 256-wide segment of the outputs
         uint32_t* c = cnt + (int64_t)blockIdx.y * (nout >> 8) + seg;
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        ticket_release();
         __syncthreads();
-        if (threadIdx.x == 0) last = __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 15u;
+        if (threadIdx.x == 0) last = ticket_draw(c) == 15u;
         __syncthreads();
         if (last) {
+            ticket_acquire();
             const int wave = threadIdx.x >> 6;
             const int nsb = (int)(nout >> 8);
             for (int m = wave; m < mrows; m += 4) {
@@ -622,6 +623,19 @@ ActPlanes act_planes(int qtype, void* ws, int64_t M, int64_t K) {
     return a;
 }
 
+// the planes of rows r0.. of a plane set with rows of K activations
+ActPlanes act_rows(const ActPlanes& a, int qtype, int64_t K, int64_t r0) {
+    ActPlanes r;
+    r.xq = a.xq + r0 * K;
+    r.xd = a.xd + r0 * (K / (qtype == 12 ? 256 : 32));
+    r.xb = a.xb + r0 * (K / 32);
+    return r;
+}
+
+// Row tiles go in grid.y, at most 65535 per launch: larger M runs as
+// several launches over row chunks (stream-ordered).
+constexpr int64_t kMaxGridY = 65535;
+
 template <typename XT>
 hipError_t quant_act_t(int qtype, const XT* x, int64_t M, int64_t K, const ActPlanes* pl, uint8_t* blocks,
                        hipStream_t s) {
@@ -646,7 +660,8 @@ hipError_t quant_act_t(int qtype, const XT* x, int64_t M, int64_t K, const ActPl
 }
 
 template <int MT, bool GU, typename YT>
-void launch_dot(const WeightView& w, const ActPlanes& a, YT* y, int M, int64_t nout, int64_t up_off, hipStream_t s) {
+void launch_dot_rows(const WeightView& w, const ActPlanes& a, YT* y, int M, int64_t nout, int64_t up_off,
+                     hipStream_t s) {
     const int K = (int)w.K;
     const size_t lds = lds_bytes(w.qtype, MT, K);
     if (w.qtype == 12) {
@@ -675,6 +690,14 @@ void launch_dot(const WeightView& w, const ActPlanes& a, YT* y, int M, int64_t n
                            up_off, nout);
 }
 
+template <int MT, bool GU, typename YT>
+void launch_dot(const WeightView& w, const ActPlanes& a, YT* y, int M, int64_t nout, int64_t up_off, hipStream_t s) {
+    for (int64_t r0 = 0; r0 < M; r0 += kMaxGridY * MT) {
+        const int mr = (int)(M - r0 < kMaxGridY * MT ? M - r0 : kMaxGridY * MT);
+        launch_dot_rows<MT, GU, YT>(w, act_rows(a, w.qtype, w.K, r0), y + r0 * nout, mr, nout, up_off, s);
+    }
+}
+
 template <bool GU, typename YT>
 void launch_dot_mt(int mt, const WeightView& w, const ActPlanes& a, YT* y, int M, int64_t nout, int64_t up_off,
                    hipStream_t s) {
@@ -686,14 +709,20 @@ void launch_dot_mt(int mt, const WeightView& w, const ActPlanes& a, YT* y, int M
     }
 }
 
+// the emitting gate/up; the arrival counters of a row chunk are left zero by
+// its last blocks, so the next chunk reuses them
 template <int MT, typename YT>
 void launch_emit(const WeightView& w, const ActPlanes& a, YT* y, int M, int64_t nout, uint32_t* cnt,
                  const ActPlanes& o, hipStream_t s) {
     const int K = (int)w.K;
     const int64_t waves = (nout + 3) / 4;
-    const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)((M + MT - 1) / MT));
-    hipLaunchKernelGGL((k_q8act_q4k<MT, true, YT, true>), grid, dim3(256), lds_bytes(12, MT, K), s, w.q, a.xq, a.xd,
-                       a.xb, y, M, nout, K, nout, nout, cnt, o.xq, o.xd, o.xb);
+    for (int64_t r0 = 0; r0 < M; r0 += kMaxGridY * MT) {
+        const int mr = (int)(M - r0 < kMaxGridY * MT ? M - r0 : kMaxGridY * MT);
+        const ActPlanes ac = act_rows(a, 12, K, r0), oc = act_rows(o, 12, nout, r0);
+        const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)((mr + MT - 1) / MT));
+        hipLaunchKernelGGL((k_q8act_q4k<MT, true, YT, true>), grid, dim3(256), lds_bytes(12, MT, K), s, w.q, ac.xq,
+                           ac.xd, ac.xb, y + r0 * nout, mr, nout, K, nout, nout, cnt, oc.xq, oc.xd, oc.xb);
+    }
 }
 
 }  // namespace

@@ -273,6 +273,11 @@ bool env_flag_off(const char* name) {
     return e && e[0] == '0' && e[1] == 0;
 }
 
+// K-split routes sum their partials in the last block of each output tile
+// (arrival counters); THQ_TILE_TICKET=0 takes the counter-free path instead
+// (partials summed by a separate k_split_reduce launch, bit for bit the same)
+bool tickets_on() { return !env_flag_off("THQ_TILE_TICKET"); }
+
 int check_call(const Call& c) {
     if (!c.ctx || !c.w) return fail(THQ_EINVAL, "null context or weight");
     if (c.xt != THQ_ACT_F32 && c.xt != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad x_type %d", c.xt);
@@ -448,10 +453,15 @@ Route plan_route(const Call& c) {
         const char* dqe = getenv("THQ_GEMM_DQ");
         const int dq_mode = dqe && *dqe ? atoi(dqe) : -1;
         const size_t wb_bytes = round256((size_t)w->N * (size_t)w->K * 2);
+        // the bf16 weight lives in the context workspace, which keeps its size
+        // until thq_destroy: weights above THQ_DQ_MAX_MB (default 512 MiB of
+        // bf16, e.g. a 151936 x 4096 LM head at 1.2 GiB) stay on the tile GEMM
+        const char* dqm = getenv("THQ_DQ_MAX_MB");
+        const size_t dq_cap = (size_t)(dqm && *dqm ? atoll(dqm) : 512) << 20;
         const int64_t blocks = thq::gemm_b16_blocks(m, w->N), cus = c.ctx->cus;
         const bool q4k_or_q6k = w->qtype == THQ_Q4_K || w->qtype == THQ_Q6_K;
         if (!r.exact && !c.gu && dq_mode != 0 && thq::gemm_b16_supported(m, w->N, w->K) &&
-            wb_bytes <= c.scratch_cap &&
+            wb_bytes <= c.scratch_cap && wb_bytes <= dq_cap &&
             (dq_mode == 1 || (m >= 1024 && (q4k_or_q6k ? 3 * blocks >= 2 * cus : blocks >= cus)))) {
             r.kind = Kind::GEMM_DQ;
             r.scratch = wb_bytes;
@@ -566,7 +576,7 @@ int run_matmul(const Call& c) {
         if (rc) return rc;
     }
     uint32_t* cnt = nullptr;
-    if ((r.kind == Kind::GEMV_TILE || r.kind == Kind::Q8ACT_TILE) && r.tp.splits > 1)
+    if ((r.kind == Kind::GEMV_TILE || r.kind == Kind::Q8ACT_TILE) && r.tp.splits > 1 && tickets_on())
         cnt = tile_counters(c.ctx, (c.w->N + 31) / 32);  // >= output tiles
     return exec_route(c, r, c.ctx->ws, cnt);
 }
@@ -1026,7 +1036,7 @@ int run_q8act_dot(thq_ctx* ctx, const thq_weight* w, thq_dtype dot_type, const v
         if (tp.splits > 1) {
             const int rc = ensure_ws(ctx, tp.workspace_bytes);
             if (rc) return rc;
-            cnt = tile_counters(ctx, (w->N + 31) / 32);
+            if (tickets_on()) cnt = tile_counters(ctx, (w->N + 31) / 32);
         }
         e = thq::launch_q8act_dot_tile(tp, view(w), w->tq, buf, y, yt == THQ_ACT_F32, gu, (int)m,
                                        static_cast<float*>(ctx->ws), cnt, static_cast<hipStream_t>(stream));
@@ -1071,7 +1081,7 @@ int thq_gate_up_silu_q8act_emit(thq_ctx* ctx, const thq_weight* fused, thq_dtype
         if (tp.splits > 1) {
             const int rc = ensure_ws(ctx, tp.workspace_bytes);
             if (rc) return rc;
-            cnt = tile_counters(ctx, (fused->N + 31) / 32);
+            if (tickets_on()) cnt = tile_counters(ctx, (fused->N + 31) / 32);
         }
         hipError_t e = thq::launch_q8act_dot_tile(tp, view(fused), fused->tq, buf_dev, y_dev, y_type == THQ_ACT_F32,
                                                   true, (int)m, static_cast<float*>(ctx->ws), cnt, s);
@@ -1129,6 +1139,40 @@ int thq_matmul_noalloc(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq
 }
 
 size_t thq_noalloc_scratch_bytes(void) { return THQ_NOALLOC_SCRATCH_BYTES; }
+
+int thq_call_scratch_bytes(thq_ctx* ctx, const thq_weight* w, int64_t m, thq_act x_type, uint32_t flags,
+                           int gate_up, size_t* bytes) {
+    if (!bytes) return fail(THQ_EINVAL, "null bytes");
+    *bytes = 0;
+    // the route depends on the operands' alignment only: plan with aligned
+    // placeholders (nothing is dereferenced or launched)
+    const uintptr_t ph = 256;
+    Call c{ctx, w, reinterpret_cast<const void*>(ph), x_type, m, reinterpret_cast<void*>(ph), THQ_ACT_F32, flags,
+           gate_up != 0, nullptr, nullptr};
+    int rc = check_call(c);
+    if (rc || m == 0) return rc;
+    *bytes = plan_route(c).scratch;
+    return THQ_OK;
+}
+
+int thq_reserve(thq_ctx* ctx, size_t workspace_bytes, int64_t counters) {
+    if (!ctx) return fail(THQ_EINVAL, "null context");
+    if (counters < 0 || counters > ((int64_t)1 << 32)) return fail(THQ_ESHAPE, "counters %lld out of range", (long long)counters);
+    DeviceGuard g(ctx->device);
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    int rc = ensure_ws(ctx, workspace_bytes);
+    if (rc) return rc;
+    if (counters > 0 && !tile_counters(ctx, counters))
+        return fail(THQ_ENOMEM, "arrival counters (%lld entries) could not be allocated", (long long)counters);
+    HIP_TRY(hipDeviceSynchronize());
+    return THQ_OK;
+}
+
+size_t thq_workspace_bytes(const thq_ctx* ctx) {
+    if (!ctx) return 0;
+    std::lock_guard<std::mutex> lk(const_cast<thq_ctx*>(ctx)->mu);
+    return ctx->ws_bytes;
+}
 
 int thq_matmul(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_act x_type, int64_t m, void* y_dev,
                thq_act y_type, uint32_t flags, void* stream) {

@@ -243,6 +243,19 @@ __host__ __device__ __forceinline__ Q6Layout q6k_layout(int64_t n, int64_t k) {
     return L;
 }
 
+// Last-block tickets (split-K partials, producer epilogues).  Every thread
+// that published data for another block calls ticket_release() after its
+// stores and before the block barrier that precedes the ticket; the ticket
+// is a device-scope acq_rel fetch_add; the block that draws the last ticket
+// calls ticket_acquire() after the barrier that shares the result and before
+// it reads the other blocks' data.  Device ("agent") scope: the blocks may
+// run on different XCDs, whose L2s are not coherent with each other.
+__device__ __forceinline__ void ticket_release() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
+__device__ __forceinline__ void ticket_acquire() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+__device__ __forceinline__ uint32_t ticket_draw(uint32_t* c) {
+    return __hip_atomic_fetch_add(c, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // byte I of w as f32 (selected to v_cvt_f32_ubyteI)
 template <int I>
 __device__ __forceinline__ float ubyte_f32(uint32_t w) {

@@ -54,7 +54,8 @@ EXPORTS = (
     "thq_gguf_metadata_u32", "thq_gguf_metadata_f32", "thq_gguf_metadata_str", "thq_gguf_metadata_array",
     "thq_weight_from_gguf", "thq_q8act_bytes", "thq_q8act_prepare", "thq_matmul_q8act", "thq_gate_up_silu_q8act",
     "thq_plan_gemv_mfma", "thq_plan_gemm", "thq_plan_gemv_wide", "thq_matmul_noalloc", "thq_noalloc_scratch_bytes",
-    "thq_topk", "thq_matmul_topk", "thq_gate_up_silu_q8act_emit", "thq_weight_add_tiles", "thq_plan_gemv_tile",
+    "thq_topk", "thq_matmul_topk", "thq_gate_up_silu_q8act_emit", "thq_weight_add_tiles",
+    "thq_call_scratch_bytes", "thq_reserve", "thq_workspace_bytes", "thq_plan_gemv_tile",
 )
 
 
@@ -168,6 +169,9 @@ def _load():
         "thq_gate_up_silu_q8act_emit": ([P, P, I, P, i64, i64, P, I, P, P], I),
         "thq_matmul_topk": ([P, P, P, I, i64, I, P, P, P, u32, P], I),
         "thq_noalloc_scratch_bytes": ([], C.c_size_t),
+        "thq_call_scratch_bytes": ([P, P, i64, I, u32, I, C.POINTER(C.c_size_t)], I),
+        "thq_reserve": ([P, C.c_size_t, i64], I),
+        "thq_workspace_bytes": ([P], C.c_size_t),
         "thq_plan_gemv_mfma": ([I, i64, i64, i64, I, C.POINTER(GemvPlanInfo)], I),
         "thq_plan_gemm": ([I, I, i64, i64, i64, I, I, C.POINTER(GemmPlanInfo)], I),
         "thq_plan_gemv_wide": ([I, i64, i64, i64, I, C.POINTER(WidePlanInfo)], I),
@@ -232,6 +236,21 @@ class Context:
         if getattr(self, "h", None) and lib is not None:
             lib.thq_destroy(self.h)
             self.h = None
+
+    def reserve(self, workspace_bytes: int, counters: int = 0) -> None:
+        """thq_reserve: grow the workspace and the split-K arrival counters now."""
+        check(lib.thq_reserve(self.h, workspace_bytes, counters))
+
+    def workspace_bytes(self) -> int:
+        return int(lib.thq_workspace_bytes(self.h))
+
+
+def call_scratch_bytes(w: "QTensor", m: int, x_dtype=torch.bfloat16, flags: int = 0, gate_up: bool = False) -> int:
+    """Workspace bytes one thq_matmul / thq_gate_up_silu call of m rows needs (host-side plan)."""
+    out = C.c_size_t()
+    act = ACT_F32 if x_dtype == torch.float32 else ACT_BF16
+    check(lib.thq_call_scratch_bytes(w.ctx.h, w.h, m, act, flags, int(gate_up), C.byref(out)))
+    return int(out.value)
 
 
 class QTensor:
