@@ -265,6 +265,7 @@ struct Call {
     hipStream_t s;
     thq::AmaxOut* am;
     size_t scratch_cap = SIZE_MAX;  // routes needing more scratch are not planned
+    bool counters = true;           // the caller can supply zeroed arrival counters
 };
 
 // an environment switch set to "0" (read on every call)
@@ -300,7 +301,7 @@ int check_call(const Call& c) {
 
 // The kernels a call runs, and the device scratch (split-K partials or the
 // quantized activation planes) they use, known before anything launches.
-enum class Kind { NONE, Q8ACT, Q8ACT_TILE, GEMV1, ROWS, GEMV_TILE, GEMV_MFMA, GEMV_MFMA_GROUPS, WIDE, GEMM, GEMM_DQ, GEMM_FQ, GENERIC };
+enum class Kind { NONE, Q8ACT, Q8ACT_TILE, GEMV1, ROWS, GEMV_TILE, GEMV_MFMA, GEMV_MFMA_GROUPS, WIDE, GEMM, GEMM_DQ, GEMM_FQ, GEMM_RQ, GENERIC };
 struct Route {
     Kind kind = Kind::NONE;
     thq::GemvPlan gp;
@@ -309,6 +310,7 @@ struct Route {
     thq::TilePlan tp;
     thq::GemmPlan gm;
     thq::FqPlan fq;
+    thq::RqPlan rq;
     bool exact = false;
     size_t scratch = 0;
 };
@@ -479,6 +481,31 @@ Route plan_route(const Call& c) {
                 r.scratch = fp.workspace_bytes;
             }
         }
+        // Q4_K / MLX affine with rounded weights from 1024 rows: the GEMM that
+        // dequantizes each wave's 32 weight rows in registers (k_gemm_rq), in
+        // place of the tile GEMM (12288 x 4096 at M = 1024: 116 against 144 us;
+        // 4096 x 12288 at M = 2048: 209 against 219 us) and, for weights with
+        // fewer rows than columns (the down projection), of the dequantize-
+        // then-GEMM route (4096 x 12288 at M = 4096: 369 against 388 us;
+        // 12288 x 4096 keeps that route: 180 against 219 us at M = 2048).  Its
+        // K splits meet in the last block of each tile, so only with arrival
+        // counters.  THQ_GEMM_RQ: 0 never, 1 wherever supported (tests),
+        // unset: that rule
+        const char* rqe = getenv("THQ_GEMM_RQ");
+        const int rq_mode = rqe && *rqe ? atoi(rqe) : -1;
+        const bool rq_default = m >= 1024 && (r.kind == Kind::GEMM ||
+                                              (r.kind == Kind::GEMM_DQ && dq_mode == -1 && w->N < w->K));
+        if (q4 && !r.exact && r.kind != Kind::GEMM_FQ && rq_mode != 0 && (rq_mode == 1 || rq_default) &&
+            c.counters && tickets_on() &&
+            thq::gemm_rq_supported(w->qtype == THQ_MLX_Q4 ? 13 : 12, m, w->N, w->K, c.gu)) {
+            const thq::RqPlan rp = thq::plan_gemm_rq(m, w->N, w->K, c.gu, c.ctx->cus);
+            // the counters thq_reserve documents (one per 32 rows of the weight) cover its tiles
+            if (rp.workspace_bytes <= c.scratch_cap && rp.counters <= (w->N + 31) / 32) {
+                r.kind = Kind::GEMM_RQ;
+                r.rq = rp;
+                r.scratch = rp.workspace_bytes;
+            }
+        }
     } else if (!xf32 && aligned16(c.x) && (q4 || q6) && m > 16 && w->K % 256 == 0 &&
                thq::plan_gemv_mfma(v.qtype, 16, w->N, w->K, c.gu).waves > 0) {
         // exact 4- / 6-bit weights past the decode GEMV's 16 rows (the verify
@@ -551,6 +578,10 @@ int exec_route(const Call& c, const Route& r, void* scratch, uint32_t* cnt = nul
             e = thq::launch_gemm_fq(r.fq, w->qtype == THQ_MLX_Q4, w->q, c.x, c.y, yf32, c.gu, m, w->N, (int)w->K,
                                     static_cast<float*>(scratch), c.s);
             break;
+        case Kind::GEMM_RQ:
+            e = thq::launch_gemm_rq(r.rq, w->qtype == THQ_MLX_Q4, w->q, c.x, c.y, yf32, c.gu, m, w->N, (int)w->K,
+                                    static_cast<float*>(scratch), cnt, c.s);
+            break;
         case Kind::GEMM_DQ:
             // the weight as bf16 [N][K] in the scratch, then x . Wb^T
             e = dequant_any(w, scratch, true, c.s);
@@ -578,6 +609,10 @@ int run_matmul(const Call& c) {
     uint32_t* cnt = nullptr;
     if ((r.kind == Kind::GEMV_TILE || r.kind == Kind::Q8ACT_TILE) && r.tp.splits > 1 && tickets_on())
         cnt = tile_counters(c.ctx, (c.w->N + 31) / 32);  // >= output tiles
+    if (r.kind == Kind::GEMM_RQ && r.rq.splits > 1) {
+        cnt = tile_counters(c.ctx, (c.w->N + 31) / 32);  // >= r.rq.counters (planned so)
+        if (!cnt) return fail(THQ_ENOMEM, "arrival counters: allocation failed");
+    }
     return exec_route(c, r, c.ctx->ws, cnt);
 }
 
@@ -1128,6 +1163,7 @@ int thq_matmul_noalloc(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq
     // cover everything its reduce reads, so nothing needs clearing
     Call c{ctx, w, x_dev, x_type, m, y_dev, y_type, flags, false, static_cast<hipStream_t>(stream), nullptr};
     c.scratch_cap = THQ_NOALLOC_SCRATCH_BYTES;  // e.g. the dequantize-then-GEMM route falls back to the tile GEMM
+    c.counters = false;                         // routes whose splits meet on arrival counters are not planned
     int rc = check_call(c);
     if (rc || m == 0) return rc;
     DeviceGuard g(ctx->device);

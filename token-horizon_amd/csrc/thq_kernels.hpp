@@ -144,6 +144,20 @@ bool gemm_fq_supported(int64_t M, int64_t N_rows, int64_t K, bool gu);
 FqPlan plan_gemm_fq(int64_t M, int64_t N_rows, int64_t K, bool gu, int cus);
 hipError_t launch_gemm_fq(const FqPlan& p, bool aff, const uint8_t* wq, const void* x, void* y, bool yf32, bool gu,
                           int M, int64_t N_rows, int K, float* ws, hipStream_t s);
+// mid-M prefill GEMM with the Q4_K / MLX affine weight dequantized in
+// registers into MFMA operands (k_gemm_rq.hip): block tile, grid and K splits
+struct RqPlan {
+    int bm = 256;  // block rows of M (128 or 256); 128 weight rows per block
+    int tiles_m = 0, tiles_n = 0;
+    int whole = 0;            // tiles computed over all of K (the first blocks); the rest are split
+    int kps = 0, splits = 1;  // 64-wide K steps per split
+    int64_t counters = 0;     // arrival counters the split reduction needs (one per split tile)
+    size_t workspace_bytes = 0;  // split partials, f32, one BM x 128 tile per (tile, split)
+};
+bool gemm_rq_supported(int qtype, int64_t M, int64_t N_rows, int64_t K, bool gu);
+RqPlan plan_gemm_rq(int64_t M, int64_t N_rows, int64_t K, bool gu, int cus);
+hipError_t launch_gemm_rq(const RqPlan& p, bool affine, const uint8_t* wq, const void* x, void* y, bool yf32, bool gu,
+                          int M, int64_t N_rows, int K, float* ws, uint32_t* cnt, hipStream_t s);
 // exact generic kernel, any M, scalar activation loads
 hipError_t launch_generic(const WeightView& w, const void* x, bool xf32, void* y, bool yf32, bool gu, int M,
                           int64_t nout, int64_t up_off, hipStream_t s);
