@@ -44,7 +44,7 @@ def make(kind, n, k, seed):
 
 # (n, k, rows): a ragged last tile in one K split; 32 output tiles (K split
 # four ways); a long K
-CASES = [(1000, 1024, (17, 31, 32, 33, 40, 64)), (4096, 4096, (17, 40, 64)), (300, 12288, (20, 40))]
+CASES = [(1000, 1024, (9, 16, 17, 31, 32, 33, 40, 41, 64)), (4096, 4096, (17, 40, 64)), (300, 12288, (20, 40))]
 
 
 @pytest.mark.parametrize("kind", KINDS)

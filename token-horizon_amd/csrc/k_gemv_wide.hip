@@ -86,17 +86,19 @@ struct WChunk {
 // [s*cps, min((s+1)*cps, K/256)).
 // X is not __restrict__: its loads stay ordered before the weight loads by
 // the compiler barriers.
-template <int QT, int MH, typename YT, bool GU, bool SPLIT, bool AM>
+template <int QT, int MR, typename YT, bool GU, bool SPLIT, bool AM>
 __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict__ Wq, const uint8_t* __restrict__ Wa,
                                                      const bf16_t* X, void* __restrict__ Yv, int M, int K,
                                                      int64_t nout, int64_t up_off, int64_t nrows, int cps,
                                                      float* __restrict__ amv, uint32_t* __restrict__ ami,
                                                      int64_t am_ld) {
-    constexpr int MP = 32 * MH;                 // staged rows (M <= MP)
-    constexpr int NXP = MP * (WV_KC / 8) / 256; // 16-B activation pieces per thread per chunk
+    // MR 8-row groups of activation rows (M <= 8 MR) in MH halves of 32
+    constexpr int MH = (MR + 3) / 4;
+    constexpr int MP = 8 * MR;                  // staged rows (M <= MP)
+    constexpr int NXP = MR;                     // 16-B activation pieces per thread per chunk
     constexpr int NS = WV_KC / 32;  // 32-wide sums per staged row (Q4_K, affine)
     __shared__ __attribute__((aligned(16))) bf16_t xs[2][MP][WV_XR];
-    __shared__ __attribute__((aligned(16))) float Ss[QT == 8 || QT == 14 ? 1 : 2][NS][MP];
+    __shared__ __attribute__((aligned(16))) float Ss[QT == 8 || QT == 14 ? 1 : 2][NS][32 * MH];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -113,63 +115,80 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
     int64_t row = GU && n >= 16 ? orow + up_off : orow;
     if (!valid) row = 0;  // in-bounds reads; the scales are zeroed below
 
-    const uint8_t* pw;
-    const uint8_t* ps;
-    const uint8_t* ph = nullptr;
-    const uint16_t* pd = nullptr;
+    // Every load is a chunk-uniform base (a plane's start plus the chunk's
+    // offset, in scalar registers) plus the lane's 32-bit offset: each plane
+    // and the activations are below 4 GiB (plan_gemv_wide), so the loads take
+    // the scalar-base form and a chunk's addresses cost no vector ALU.
+    const uint8_t* bw = Wq;
+    const uint8_t* bs = Wq;
+    const uint8_t* bh = Wq;
+    const uint8_t* bd = Wq;
+    uint32_t ow, os, oh = 0, od = 0;
     if constexpr (QT == 14) {
         const Q6Layout L = q6k_layout(nrows, K);
-        pw = Wq + row * (K >> 1) + 8 * g;
-        ph = Wq + L.qh + row * (K >> 2) + 8 * g;
-        ps = Wq + L.sc + row * (K >> 4);
-        pd = reinterpret_cast<const uint16_t*>(Wq + L.d) + row * (K >> 8);
+        bh = Wq + L.qh;
+        bs = Wq + L.sc;
+        bd = Wq + L.d;
+        ow = (uint32_t)(row * (K >> 1) + 8 * g);
+        oh = (uint32_t)(row * (K >> 2) + 8 * g);
+        os = (uint32_t)(row * (K >> 4));
+        od = (uint32_t)(row * (K >> 8) * 2);
     } else if constexpr (QT == 8) {
-        // Q8_0 tiles: block b of the row at pw + 1024 b, chunk c's 8 scales at ps + 512 c
-        pw = Wq + q8t_q(row, K >> 5, 0, g);
-        ps = Wa + q8t_d(row, K >> 5, 0) * 2;
+        // Q8_0 tiles: block b of the row at 1024 b, chunk c's 8 scales at 512 c
+        bs = Wa;
+        ow = (uint32_t)q8t_q(row, K >> 5, 0, g);
+        os = (uint32_t)(q8t_d(row, K >> 5, 0) * 2);
     } else {
         const int nsb = K >> 8;
-        pw = Wq + q4k_piece(row, nsb, 0, g, 0);
-        ps = Wq + q4k_hdword(row, nsb, 0, 0);
+        ow = (uint32_t)q4k_piece(row, nsb, 0, g, 0);
+        os = (uint32_t)q4k_hdword(row, nsb, 0, 0);
     }
     auto wload = [&](WChunk<QT>& C, int c) {
         if constexpr (QT == 14) {
-            const uint4 sv = *reinterpret_cast<const uint4*>(ps + (int64_t)c * 16);
+            const uint4 sv = *reinterpret_cast<const uint4*>(bs + (int64_t)c * 16 + os);
             C.s[0] = sv.x; C.s[1] = sv.y; C.s[2] = sv.z; C.s[3] = sv.w;
-            C.d = pd[c];
-            const uint8_t* qlc = pw + (int64_t)c * 128;
-            const uint8_t* qhc = ph + (int64_t)c * 64;
+            C.d = *reinterpret_cast<const uint16_t*>(bd + (int64_t)c * 2 + od);
+            const uint8_t* qlc = bw + (int64_t)c * 128;
+            const uint8_t* qhc = bh + (int64_t)c * 64;
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                const uint2 lo = *reinterpret_cast<const uint2*>(qlc + u * 32);
-                const uint2 hi = *reinterpret_cast<const uint2*>(qlc + u * 32 + 16);
+                const uint2 lo = *reinterpret_cast<const uint2*>(qlc + ow + u * 32);
+                const uint2 hi = *reinterpret_cast<const uint2*>(qlc + ow + u * 32 + 16);
                 C.w[u] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-                C.h[u] = *reinterpret_cast<const uint2*>(qhc + u * 16);
+                C.h[u] = *reinterpret_cast<const uint2*>(qhc + oh + u * 16);
             }
         } else if constexpr (QT == 8) {
-            const uint4 sv = *reinterpret_cast<const uint4*>(ps + (int64_t)c * 512);
+            const uint4 sv = *reinterpret_cast<const uint4*>(bs + (int64_t)c * 512 + os);
             C.s[0] = sv.x; C.s[1] = sv.y; C.s[2] = sv.z; C.s[3] = sv.w;
+            const uint8_t* wc0 = bw + (int64_t)c * 8192;
+            const uint8_t* wc1 = wc0 + 4096;
 #pragma unroll
-            for (int b = 0; b < 8; ++b) C.w[b] = *reinterpret_cast<const uint4*>(pw + (int64_t)c * 8192 + b * 1024);
+            for (int b = 0; b < 8; ++b)
+                C.w[b] = *reinterpret_cast<const uint4*>((b < 4 ? wc0 : wc1) + ow + (b & 3) * 1024);
         } else {
+            const uint8_t* wc = bw + (int64_t)c * 64;
+            const uint8_t* sc = bs + (int64_t)c * 64;
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
-                C.w[u] = *reinterpret_cast<const uint4*>(pw + (int64_t)c * 64 + u * 16);
-                C.s[u] = *reinterpret_cast<const uint32_t*>(ps + (int64_t)c * 64 + u * 16);
+                C.w[u] = *reinterpret_cast<const uint4*>(wc + ow + u * 16);
+                C.s[u] = *reinterpret_cast<const uint32_t*>(sc + os + u * 16);
             }
         }
     };
 
     // activation pieces of chunk c: thread t takes pieces p = t + 256j, row
-    // p / 32, columns 8 * (p % 32) ..; rows past M load row M - 1 (straight-line
-    // loads keep the compiler's wait counts exact) and are not written
+    // p / 32, columns 8 * (p % 32) ..; a thread's piece j is 8 rows below its
+    // piece j - 1 (j < MR: 8 MR >= M rows); rows past M load row M - 1 (in
+    // bounds) and are not written.
+    const uint32_t K2 = (uint32_t)K * 2u;
+    const uint32_t xo0 = (uint32_t)(threadIdx.x >> 5) * K2 + 16u * (threadIdx.x & 31);
+    const uint32_t xomax = (uint32_t)(M - 1) * K2 + 16u * (threadIdx.x & 31);
     auto xload = [&](uint4 (&xv)[NXP], int c) {
+        const uint8_t* xc = reinterpret_cast<const uint8_t*>(X) + (int64_t)c * (WV_KC * 2);
 #pragma unroll
         for (int j = 0; j < NXP; ++j) {
-            const int p = threadIdx.x + 256 * j;
-            int m = p >> 5;
-            m = m < M ? m : M - 1;
-            xv[j] = *reinterpret_cast<const uint4*>(X + (int64_t)m * K + (int64_t)c * WV_KC + 8 * (p & 31));
+            const uint32_t o = xo0 + (uint32_t)j * 8u * K2;
+            xv[j] = *reinterpret_cast<const uint4*>(xc + (o < xomax ? o : xomax));
         }
     };
     auto xstore = [&](const uint4 (&xv)[NXP], int buf) {
@@ -219,6 +238,10 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
         for (int q = 0; q < 4; ++q) S[q] = *reinterpret_cast<const f32x4_t*>(&Ss[QT == 8 ? 0 : buf][col][32 * h + 8 * q + 4 * g]);
     };
 
+    // accumulator e of half h holds activation rows 32h + 8(e / 4) + 4g + e % 4:
+    // the groups of four e past the MR live 8-row groups are never scaled
+    auto live = [](int h, int e) { return 32 * h + 8 * (e >> 2) < 8 * MR; };
+
     auto compute = [&](const WChunk<QT>& C, int buf) {
         if constexpr (QT == 8) {
 #pragma unroll
@@ -234,7 +257,8 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
                     f32x16_t T = wmfma(as_bf16x8(a0), B0, z16);
                     T = wmfma(as_bf16x8(a1), B1, T);
 #pragma unroll
-                    for (int e = 0; e < 16; ++e) acc[h][e] = __builtin_fmaf(d, T[e], acc[h][e]);
+                    for (int e = 0; e < 16; ++e)
+                        if (live(h, e)) acc[h][e] = __builtin_fmaf(d, T[e], acc[h][e]);
                 }
                 pin();
             }
@@ -267,7 +291,8 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
                         f32x16_t T = wmfma(a, B, z16);
                         T = wmfma(a, B160, T);
 #pragma unroll
-                        for (int e = 0; e < 16; ++e) acc[h][e] = __builtin_fmaf(sg, T[e], acc[h][e]);
+                        for (int e = 0; e < 16; ++e)
+                            if (live(h, e)) acc[h][e] = __builtin_fmaf(sg, T[e], acc[h][e]);
                     }
                     pin();
                 }
@@ -312,12 +337,14 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
                     T = wmfma(as_bf16x8(a1), B1, T);
 #pragma unroll
                     for (int e = 0; e < 16; ++e)
-                        acc[h][e] = __builtin_fmaf(-c1, S1[e >> 2][e & 3], __builtin_fmaf(d1, T[e], acc[h][e]));
+                        if (live(h, e))
+                            acc[h][e] = __builtin_fmaf(-c1, S1[e >> 2][e & 3], __builtin_fmaf(d1, T[e], acc[h][e]));
                     T = wmfma(as_bf16x8(a2), B2, z16);
                     T = wmfma(as_bf16x8(a3), B3, T);
 #pragma unroll
                     for (int e = 0; e < 16; ++e)
-                        acc[h][e] = __builtin_fmaf(-c2, S2[e >> 2][e & 3], __builtin_fmaf(d2, T[e], acc[h][e]));
+                        if (live(h, e))
+                            acc[h][e] = __builtin_fmaf(-c2, S2[e >> 2][e & 3], __builtin_fmaf(d2, T[e], acc[h][e]));
                 }
                 pin();
             }
@@ -399,7 +426,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
     }
 }
 
-template <int QT, int MH, bool GU>
+template <int QT, int MR, bool GU>
 hipError_t run_wide(const WidePlan& p, const WeightView& w, const bf16_t* x, void* y, bool yf32, int M, int64_t nout,
                     int64_t up_off, float* ws, hipStream_t s, AmaxOut* am) {
     const int64_t tiles = GU ? (nout + WV_ROWS / 2 - 1) / (WV_ROWS / 2) : (nout + WV_ROWS - 1) / WV_ROWS;
@@ -411,20 +438,20 @@ hipError_t run_wide(const WidePlan& p, const WeightView& w, const bf16_t* x, voi
         const int64_t t32 = (nout + 31) / 32;
         if (t32 > am->ld) return hipErrorInvalidValue;
         am->nb = t32;
-        hipLaunchKernelGGL((k_gemv_wide<QT, MH, float, false, false, true>), grid, block, 0, s, w.q, w.aux, x,
+        hipLaunchKernelGGL((k_gemv_wide<QT, MR, float, false, false, true>), grid, block, 0, s, w.q, w.aux, x,
                            (void*)nullptr, M, K, nout, up_off, w.N, p.cps, am->v, am->i, am->ld);
         return hipGetLastError();
     }
     if (p.splits == 1) {
         if (yf32)
-            hipLaunchKernelGGL((k_gemv_wide<QT, MH, float, GU, false, false>), grid, block, 0, s, w.q, w.aux, x, y, M,
+            hipLaunchKernelGGL((k_gemv_wide<QT, MR, float, GU, false, false>), grid, block, 0, s, w.q, w.aux, x, y, M,
                                K, nout, up_off, w.N, p.cps, (float*)nullptr, (uint32_t*)nullptr, (int64_t)0);
         else
-            hipLaunchKernelGGL((k_gemv_wide<QT, MH, bf16_t, GU, false, false>), grid, block, 0, s, w.q, w.aux, x, y,
+            hipLaunchKernelGGL((k_gemv_wide<QT, MR, bf16_t, GU, false, false>), grid, block, 0, s, w.q, w.aux, x, y,
                                M, K, nout, up_off, w.N, p.cps, (float*)nullptr, (uint32_t*)nullptr, (int64_t)0);
         return hipGetLastError();
     }
-    hipLaunchKernelGGL((k_gemv_wide<QT, MH, float, GU, true, false>), grid, block, 0, s, w.q, w.aux, x, (void*)ws, M,
+    hipLaunchKernelGGL((k_gemv_wide<QT, MR, float, GU, true, false>), grid, block, 0, s, w.q, w.aux, x, (void*)ws, M,
                        K, nout, up_off, w.N, p.cps, (float*)nullptr, (uint32_t*)nullptr, (int64_t)0);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -434,11 +461,16 @@ hipError_t run_wide(const WidePlan& p, const WeightView& w, const bf16_t* x, voi
 template <int QT>
 hipError_t run_wide_q(const WidePlan& p, const WeightView& w, const bf16_t* x, void* y, bool yf32, bool gu, int M,
                       int64_t nout, int64_t up_off, float* ws, hipStream_t s, AmaxOut* am) {
-    if (gu)
-        return M <= 32 ? run_wide<QT, 1, true>(p, w, x, y, yf32, M, nout, up_off, ws, s, am)
-                       : run_wide<QT, 2, true>(p, w, x, y, yf32, M, nout, up_off, ws, s, am);
-    return M <= 32 ? run_wide<QT, 1, false>(p, w, x, y, yf32, M, nout, up_off, ws, s, am)
-                   : run_wide<QT, 2, false>(p, w, x, y, yf32, M, nout, up_off, ws, s, am);
+    // row groups: 2 (M <= 16), 4 (<= 32), 5 (<= 40: the 40-row verify head), 8
+    auto go = [&](auto mr) {
+        constexpr int MR = decltype(mr)::value;
+        return gu ? run_wide<QT, MR, true>(p, w, x, y, yf32, M, nout, up_off, ws, s, am)
+                  : run_wide<QT, MR, false>(p, w, x, y, yf32, M, nout, up_off, ws, s, am);
+    };
+    if (M <= 16) return go(std::integral_constant<int, 2>{});
+    if (M <= 32) return go(std::integral_constant<int, 4>{});
+    if (M <= 40) return go(std::integral_constant<int, 5>{});
+    return go(std::integral_constant<int, 8>{});
 }
 
 }  // namespace
@@ -447,6 +479,11 @@ WidePlan plan_gemv_wide(int qtype, int64_t M, int64_t N, int64_t K, int cus) {
     WidePlan p;
     if (!(qtype == 8 || qtype == 12 || qtype == 13 || qtype == 14)) return p;
     if (M < 1 || M > 64 || N < 1 || K < WV_KC || K % WV_KC || K > (int64_t)1 << 30) return p;
+    // the kernel addresses every plane and the activations with 32-bit lane offsets
+    const uint64_t plane = qtype == 8 ? (uint64_t)q8t_q_bytes(N, K)
+                           : qtype == 14 ? (uint64_t)q6k_layout(N, K).total
+                                         : (uint64_t)((N + 3) / 4) * (uint64_t)(K / 256) * 576u;
+    if (plane >= (1ull << 32) || (uint64_t)M * (uint64_t)K * 2u >= (1ull << 32)) return p;
     const int64_t tiles = (N + WV_ROWS - 1) / WV_ROWS;
     const int64_t nch = K / WV_KC;
     // two resident blocks per CU: split K until the grid fills them, keeping
