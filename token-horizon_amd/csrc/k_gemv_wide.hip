@@ -80,6 +80,21 @@ struct WChunk {
     uint2 h[QT == 14 ? 4 : 1];
     uint32_t d;
 };
+// An empty asm that reads and redefines every register of a chunk (and is
+// ordered with memory operations): the compiler waits for the chunk's loads
+// before it, and later uses depend on it rather than on the loads.
+template <int QT>
+__device__ __forceinline__ void wv_settle(WChunk<QT>& C) {
+#pragma unroll
+    for (int i = 0; i < (QT == 8 ? 8 : 4); ++i)
+        asm volatile("" : "+v"(C.w[i].x), "+v"(C.w[i].y), "+v"(C.w[i].z), "+v"(C.w[i].w)::"memory");
+    asm volatile("" : "+v"(C.s[0]), "+v"(C.s[1]), "+v"(C.s[2]), "+v"(C.s[3])::"memory");
+    if constexpr (QT == 14) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) asm volatile("" : "+v"(C.h[i].x), "+v"(C.h[i].y)::"memory");
+        asm volatile("" : "+v"(C.d)::"memory");
+    }
+}
 
 // Grid (tiles of 128 weight rows, splits); block (t, s) owns rows
 // [128t, 128t + 128) (GU: outputs [64t, 64t + 64)) over chunks
@@ -244,22 +259,32 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
 
     auto compute = [&](const WChunk<QT>& C, int buf) {
         if constexpr (QT == 8) {
+            // software-pipelined by one block: block b's MFMAs (every half)
+            // are issued, block b + 1 is converted while they run, then b's
+            // products are scaled into the accumulators
+            bf16x8_t B0 = wi8(C.w[0].x, C.w[0].y), B1 = wi8(C.w[0].z, C.w[0].w);
 #pragma unroll
             for (int b = 0; b < 8; ++b) {
                 const uint32_t sw = C.s[b >> 1] >> (16 * (b & 1));
                 const float d = valid ? f16_to_f32((uint16_t)sw) : 0.0f;
-                const bf16x8_t B0 = wi8(C.w[b].x, C.w[b].y), B1 = wi8(C.w[b].z, C.w[b].w);
+                f32x16_t T[MH];
 #pragma unroll
                 for (int h = 0; h < MH; ++h) {
                     const bf16_t* xa = &xs[buf][arow[h]][GOFF * g + 32 * b];
                     const uint4 a0 = *reinterpret_cast<const uint4*>(xa);
                     const uint4 a1 = *reinterpret_cast<const uint4*>(xa + 8);
-                    f32x16_t T = wmfma(as_bf16x8(a0), B0, z16);
-                    T = wmfma(as_bf16x8(a1), B1, T);
+                    T[h] = wmfma(as_bf16x8(a0), B0, z16);
+                    T[h] = wmfma(as_bf16x8(a1), B1, T[h]);
+                }
+                if (b < 7) {
+                    B0 = wi8(C.w[b + 1].x, C.w[b + 1].y);
+                    B1 = wi8(C.w[b + 1].z, C.w[b + 1].w);
+                }
+#pragma unroll
+                for (int h = 0; h < MH; ++h)
 #pragma unroll
                     for (int e = 0; e < 16; ++e)
-                        if (live(h, e)) acc[h][e] = __builtin_fmaf(d, T[e], acc[h][e]);
-                }
+                        if (live(h, e)) acc[h][e] = __builtin_fmaf(d, T[h][e], acc[h][e]);
                 pin();
             }
         } else if constexpr (QT == 14) {
@@ -362,15 +387,23 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
     __syncthreads();
 
     // ---- one step: prefetch chunk c + 1 (activations to registers, weights
-    // to Wn), compute chunk c, then stage c + 1 in the other buffer
-    auto step = [&](int c, const WChunk<QT>& Wc, WChunk<QT>& Wn, int buf) {
+    // to Wn), compute chunk c, then stage c + 1 in the other buffer.  Wc
+    // passes through wv_settle first: its loads (issued a step ago) are
+    // waited for there, before the prefetch is issued, and the math then
+    // reads the settled registers, so the compiler's wait counts never make
+    // the math wait for the prefetch.  (Without it the counts lose track of
+    // Wc across the loop's back edge, and each step drained its own prefetch
+    // block by block.)
+    auto step = [&](int c, WChunk<QT>& Wc, WChunk<QT>& Wn, int buf) {
         const bool more = c + 1 < ce;
-        if (more) {
-            xload(xv, c + 1);
-            asm volatile("" ::: "memory");
-            __builtin_amdgcn_sched_barrier(0);
-            wload(Wn, c + 1);
-        }
+        wv_settle(Wc);
+        // unconditional (the last step reloads its own chunk, unused): no
+        // merge of loaded and old register values for the allocator to copy
+        const int cn = more ? c + 1 : c;
+        xload(xv, cn);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        wload(Wn, cn);
         __builtin_amdgcn_sched_barrier(0);
         compute(Wc, buf);
         if (more) xstore(xv, buf ^ 1);
