@@ -290,11 +290,14 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
         } else if constexpr (QT == 14) {
             const float dd = valid ? f16_to_f32((uint16_t)C.d) : 0.0f;
             const uint32_t M4 = 0x0F0F0F0Fu;
-#pragma unroll
-            for (int u = 0; u < 4; ++u) {
+            // bf16(-160) in every element: the second MFMA adds -160 * sum(x)
+            const uint32_t m160 = 0xC320C320u;
+            const bf16x8_t B160 = as_bf16x8(make_uint4(m160, m160, m160, m160));
+            // the 6-bit codes of unit u's four 16-wide groups (bytes of lo / hi)
+            uint32_t lo[4], hi[4];
+            auto unpack = [&](int u) {
                 const uint4 q = C.w[u];
                 const uint2 hb = C.h[u];
-                uint32_t lo[4], hi[4];
                 lo[0] = (q.x & M4) | ((hb.x & 0x03030303u) << 4);
                 hi[0] = (q.y & M4) | ((hb.y & 0x03030303u) << 4);
                 lo[1] = (q.z & M4) | ((hb.x & 0x0C0C0C0Cu) << 2);
@@ -303,24 +306,32 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
                 hi[2] = ((q.y >> 4) & M4) | (hb.y & 0x30303030u);
                 lo[3] = ((q.z >> 4) & M4) | ((hb.x >> 2) & 0x30303030u);
                 hi[3] = ((q.w >> 4) & M4) | ((hb.y >> 2) & 0x30303030u);
-                // bf16(-160) in every element: the second MFMA adds -160 * sum(x)
-                const uint32_t m160 = 0xC320C320u;
-                const bf16x8_t B160 = as_bf16x8(make_uint4(m160, m160, m160, m160));
+            };
+            // software-pipelined by one group: group t's MFMAs are issued,
+            // group t + 1 is converted while they run, then t is scaled
+            unpack(0);
+            bf16x8_t B = wnib(lo[0], hi[0]);
 #pragma unroll
-                for (int G = 0; G < 4; ++G) {
-                    const float sg = dd * (float)(int)(int8_t)(C.s[u] >> (8 * G));
-                    const bf16x8_t B = wnib(lo[G], hi[G]);
+            for (int t = 0; t < 16; ++t) {
+                const int u = t >> 2, G = t & 3;
+                const float sg = dd * (float)(int)(int8_t)(C.s[u] >> (8 * G));
+                f32x16_t T[MH];
 #pragma unroll
-                    for (int h = 0; h < MH; ++h) {
-                        const bf16x8_t a = as_bf16x8(*reinterpret_cast<const uint4*>(&xs[buf][arow[h]][GOFF * g + 64 * u + 16 * G]));
-                        f32x16_t T = wmfma(a, B, z16);
-                        T = wmfma(a, B160, T);
-#pragma unroll
-                        for (int e = 0; e < 16; ++e)
-                            if (live(h, e)) acc[h][e] = __builtin_fmaf(sg, T[e], acc[h][e]);
-                    }
-                    pin();
+                for (int h = 0; h < MH; ++h) {
+                    const bf16x8_t a = as_bf16x8(*reinterpret_cast<const uint4*>(&xs[buf][arow[h]][GOFF * g + 64 * u + 16 * G]));
+                    T[h] = wmfma(a, B, z16);
+                    T[h] = wmfma(a, B160, T[h]);
                 }
+                if (t < 15) {
+                    if (G == 3) unpack(u + 1);
+                    B = wnib(lo[(t + 1) & 3], hi[(t + 1) & 3]);
+                }
+#pragma unroll
+                for (int h = 0; h < MH; ++h)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e)
+                        if (live(h, e)) acc[h][e] = __builtin_fmaf(sg, T[h][e], acc[h][e]);
+                pin();
             }
         } else {
             float d = 0.0f, dm = 0.0f;
@@ -330,8 +341,24 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
                 if (!valid) d = dm = 0.0f;
             }
             const uint32_t M4 = 0x0F0F0F0Fu;
+            // software-pipelined by one unit: unit u's MFMAs (both sub-blocks,
+            // every half) are issued, unit u + 1 is converted while they run,
+            // then u's products are scaled
+            bf16x8_t B0, B1, B2, B3;
+            auto conv = [&](int u) {
+                const uint4 q = C.w[u];
+                B0 = wnib(q.x & M4, q.y & M4);
+                B1 = wnib(q.z & M4, q.w & M4);
+                B2 = wnib((q.x >> 4) & M4, (q.y >> 4) & M4);
+                B3 = wnib((q.z >> 4) & M4, (q.w >> 4) & M4);
+            };
+            // (64 activation rows: no register room for that; unit u is
+            // converted when it starts, and each half is scaled before the next)
+            constexpr bool PIPE = MR <= 5;
+            if constexpr (PIPE) conv(0);
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
+                if constexpr (!PIPE) conv(u);
                 const uint32_t hw = C.s[u];
                 float d1, d2, c1, c2;
                 if constexpr (QT == 13) {
@@ -344,32 +371,59 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
                     c1 = __builtin_fmaf(128.0f, d1, dm * (float)((hw >> 6) & 63u));
                     c2 = __builtin_fmaf(128.0f, d2, dm * (float)((hw >> 18) & 63u));
                 }
-                const uint4 q = C.w[u];
-                const bf16x8_t B0 = wnib(q.x & M4, q.y & M4), B1 = wnib(q.z & M4, q.w & M4);
-                const bf16x8_t B2 = wnib((q.x >> 4) & M4, (q.y >> 4) & M4);
-                const bf16x8_t B3 = wnib((q.z >> 4) & M4, (q.w >> 4) & M4);
+                if constexpr (PIPE) {
+                    f32x16_t T1[MH], T2[MH];
 #pragma unroll
-                for (int h = 0; h < MH; ++h) {
-                    const bf16_t* xa = &xs[buf][arow[h]][GOFF * g + 64 * u];
-                    const uint4 a0 = *reinterpret_cast<const uint4*>(xa);
-                    const uint4 a1 = *reinterpret_cast<const uint4*>(xa + 8);
-                    const uint4 a2 = *reinterpret_cast<const uint4*>(xa + 32);
-                    const uint4 a3 = *reinterpret_cast<const uint4*>(xa + 40);
-                    f32x4_t S1[4], S2[4];
-                    sums(buf, 2 * u, h, S1);
-                    sums(buf, 2 * u + 1, h, S2);
-                    f32x16_t T = wmfma(as_bf16x8(a0), B0, z16);
-                    T = wmfma(as_bf16x8(a1), B1, T);
+                    for (int h = 0; h < MH; ++h) {
+                        const bf16_t* xa = &xs[buf][arow[h]][GOFF * g + 64 * u];
+                        const uint4 a0 = *reinterpret_cast<const uint4*>(xa);
+                        const uint4 a1 = *reinterpret_cast<const uint4*>(xa + 8);
+                        const uint4 a2 = *reinterpret_cast<const uint4*>(xa + 32);
+                        const uint4 a3 = *reinterpret_cast<const uint4*>(xa + 40);
+                        T1[h] = wmfma(as_bf16x8(a0), B0, z16);
+                        T1[h] = wmfma(as_bf16x8(a1), B1, T1[h]);
+                        T2[h] = wmfma(as_bf16x8(a2), B2, z16);
+                        T2[h] = wmfma(as_bf16x8(a3), B3, T2[h]);
+                    }
+                    if (u < 3) conv(u + 1);
 #pragma unroll
-                    for (int e = 0; e < 16; ++e)
-                        if (live(h, e))
-                            acc[h][e] = __builtin_fmaf(-c1, S1[e >> 2][e & 3], __builtin_fmaf(d1, T[e], acc[h][e]));
-                    T = wmfma(as_bf16x8(a2), B2, z16);
-                    T = wmfma(as_bf16x8(a3), B3, T);
+                    for (int h = 0; h < MH; ++h) {
+                        f32x4_t S1[4], S2[4];
+                        sums(buf, 2 * u, h, S1);
+                        sums(buf, 2 * u + 1, h, S2);
 #pragma unroll
-                    for (int e = 0; e < 16; ++e)
-                        if (live(h, e))
-                            acc[h][e] = __builtin_fmaf(-c2, S2[e >> 2][e & 3], __builtin_fmaf(d2, T[e], acc[h][e]));
+                        for (int e = 0; e < 16; ++e)
+                            if (live(h, e))
+                                acc[h][e] = __builtin_fmaf(-c1, S1[e >> 2][e & 3], __builtin_fmaf(d1, T1[h][e], acc[h][e]));
+#pragma unroll
+                        for (int e = 0; e < 16; ++e)
+                            if (live(h, e))
+                                acc[h][e] = __builtin_fmaf(-c2, S2[e >> 2][e & 3], __builtin_fmaf(d2, T2[h][e], acc[h][e]));
+                    }
+                } else {
+#pragma unroll
+                    for (int h = 0; h < MH; ++h) {
+                        const bf16_t* xa = &xs[buf][arow[h]][GOFF * g + 64 * u];
+                        const uint4 a0 = *reinterpret_cast<const uint4*>(xa);
+                        const uint4 a1 = *reinterpret_cast<const uint4*>(xa + 8);
+                        const uint4 a2 = *reinterpret_cast<const uint4*>(xa + 32);
+                        const uint4 a3 = *reinterpret_cast<const uint4*>(xa + 40);
+                        f32x4_t S1[4], S2[4];
+                        sums(buf, 2 * u, h, S1);
+                        sums(buf, 2 * u + 1, h, S2);
+                        f32x16_t T = wmfma(as_bf16x8(a0), B0, z16);
+                        T = wmfma(as_bf16x8(a1), B1, T);
+#pragma unroll
+                        for (int e = 0; e < 16; ++e)
+                            if (live(h, e))
+                                acc[h][e] = __builtin_fmaf(-c1, S1[e >> 2][e & 3], __builtin_fmaf(d1, T[e], acc[h][e]));
+                        T = wmfma(as_bf16x8(a2), B2, z16);
+                        T = wmfma(as_bf16x8(a3), B3, T);
+#pragma unroll
+                        for (int e = 0; e < 16; ++e)
+                            if (live(h, e))
+                                acc[h][e] = __builtin_fmaf(-c2, S2[e >> 2][e & 3], __builtin_fmaf(d2, T[e], acc[h][e]));
+                    }
                 }
                 pin();
             }
