@@ -109,7 +109,12 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
     const int64_t count = FROM_LOGITS ? n : ccount;
     const int64_t base = seg * TK_SEG;
 
-    uint32_t key[TK_EPT], id[TK_EPT];
+    // level 0 recomputes each element's id from its position (thread t
+    // holds base + 16t .. +15) rather than holding them: 16 fewer registers
+    // per thread, so every block of a 151936-wide, 40-row level fits the GPU
+    // at once
+    uint32_t key[TK_EPT], idv[FROM_LOGITS ? 1 : TK_EPT];
+    auto id = [&](int e) { return FROM_LOGITS ? (uint32_t)(base + tid * TK_EPT + e) : idv[e]; };
     if constexpr (FROM_LOGITS) {
         // coalesced loads (position base + e*256 + tid), then thread t takes
         // positions base + 16t .. +15 out of LDS
@@ -136,7 +141,6 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
 #pragma unroll
         for (int e = 0; e < TK_EPT; ++e) {
             key[e] = stage[tid * TK_EPT + e];
-            id[e] = (uint32_t)(base + tid * TK_EPT + e);
         }
     } else {
         // the segment's candidates spread over every thread (epv each, in
@@ -150,7 +154,7 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
             const int64_t pos = base + (int64_t)tid * epv + e;
             const bool ok = e < epv && pos < count;
             key[e] = ok ? kr[pos] : TK_ABSENT;
-            id[e] = ok ? ir[pos] : 0xFFFFFFFFu;
+            idv[e] = ok ? ir[pos] : 0xFFFFFFFFu;
         }
     }
 
@@ -191,7 +195,7 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
             __syncthreads();  // every thread is past its reads of the staged logits
 #pragma unroll
             for (int e = 0; e < TK_EPT; ++e)
-                if (key[e] >= T) cand[pos++] = make_uint2(key[e], id[e]);
+                if (key[e] >= T) cand[pos++] = make_uint2(key[e], id(e));
             // pad to a multiple of 8 with entries that beat nothing
             if (tid < ((nc + 7) & ~7) - nc) cand[nc + tid] = make_uint2(0u, 0xFFFFFFFFu);
             __syncthreads();
@@ -344,7 +348,7 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
         for (int e = 0; e < TK_EPT; ++e)
             if (sel[e]) {
                 ok[pos] = key[e];
-                oi[pos] = id[e];
+                oi[pos] = id(e);
                 ++pos;
             }
         if (tid >= total && tid < k) {
@@ -356,7 +360,7 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
         for (int e = 0; e < TK_EPT; ++e)
             if (sel[e]) {
                 fkey[pos] = key[e];
-                fid[pos] = id[e];
+                fid[pos] = id(e);
                 ++pos;
             }
         __syncthreads();
