@@ -50,6 +50,7 @@ constexpr int WV_WAVES = 4;                // waves per block
 constexpr int WV_ROWS = 32 * WV_WAVES;     // weight rows per block
 constexpr int WV_KC = 256;                 // K chunk
 constexpr int WV_XR = WV_KC + 8;           // LDS row stride (bf16): rows start 16 B apart in bank order
+constexpr int WV_DQ = 16;                  // Q6_K chunks whose d a block stages in LDS
 
 __device__ __forceinline__ f32x16_t wmfma(const bf16x8_t& a, const bf16x8_t& b, const f32x16_t& c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -114,6 +115,10 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
     constexpr int NS = WV_KC / 32;  // 32-wide sums per staged row (Q4_K, affine)
     __shared__ __attribute__((aligned(16))) bf16_t xs[2][MP][WV_XR];
     __shared__ __attribute__((aligned(16))) float Ss[QT == 8 || QT == 14 ? 1 : 2][NS][32 * MH];
+    // Q6_K: the block's rows' f16 d for its chunks (at most WV_DQ), staged once:
+    // read a chunk at a time from HBM, the d plane's lines (4 rows x 16
+    // chunks) left L2 between chunks and were fetched again and again
+    __shared__ uint16_t Dq[QT == 14 ? WV_ROWS * WV_DQ : 1];
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -122,6 +127,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
     const int nch = K >> 8;
     const int cb = blockIdx.y * cps;
     const int ce = cb + cps < nch ? cb + cps : nch;
+    const bool dlds = QT == 14 && ce - cb <= WV_DQ;  // Q6_K d from LDS (staged below)
 
     static_assert(!(GU && AM), "no argmax over gate/up");
     // GU: output o, weight row o (gate, n < 16) or up_off + o (up)
@@ -162,7 +168,8 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
         if constexpr (QT == 14) {
             const uint4 sv = *reinterpret_cast<const uint4*>(bs + (int64_t)c * 16 + os);
             C.s[0] = sv.x; C.s[1] = sv.y; C.s[2] = sv.z; C.s[3] = sv.w;
-            C.d = *reinterpret_cast<const uint16_t*>(bd + (int64_t)c * 2 + od);
+            C.d = dlds ? (uint32_t)Dq[(wave * 32 + n) * WV_DQ + (c - cb)]
+                       : (uint32_t)*reinterpret_cast<const uint16_t*>(bd + (int64_t)c * 2 + od);
             const uint8_t* qlc = bw + (int64_t)c * 128;
             const uint8_t* qhc = bh + (int64_t)c * 64;
 #pragma unroll
@@ -429,6 +436,15 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
             }
         }
     };
+
+    // Q6_K d staging: lanes g = 0 / 1 of a row take alternate chunks
+    if constexpr (QT == 14) {
+        if (dlds) {
+            for (int c = cb + g; c < ce; c += 2)
+                Dq[(wave * 32 + n) * WV_DQ + (c - cb)] = *reinterpret_cast<const uint16_t*>(bd + (int64_t)c * 2 + od);
+            __syncthreads();
+        }
+    }
 
     // ---- prologue: chunk cb staged in buffer 0, its weights in W0
     WChunk<QT> W0, W1;
