@@ -164,20 +164,39 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
         ow = (uint32_t)q4k_piece(row, nsb, 0, g, 0);
         os = (uint32_t)q4k_hdword(row, nsb, 0, 0);
     }
-    auto wload = [&](WChunk<QT>& C, int c) {
+    // Q6_K: a row's QH bytes of chunks 2j, 2j + 1 share a 128-B line, and its
+    // scale bytes of 8 chunks another; one chunk at a time, the second half
+    // came from HBM again once the first had left L2.  So an even chunk of
+    // the block's range (odd = false) also loads the next chunk's QH and
+    // scales into Hod / Sod, and the odd chunk takes them from there.
+    uint2 Hod[QT == 14 ? 4 : 1];
+    uint4 Sod;
+    auto wload = [&](WChunk<QT>& C, int c, bool odd) {
         if constexpr (QT == 14) {
-            const uint4 sv = *reinterpret_cast<const uint4*>(bs + (int64_t)c * 16 + os);
-            C.s[0] = sv.x; C.s[1] = sv.y; C.s[2] = sv.z; C.s[3] = sv.w;
+            const int c1 = c + 1 < ce ? c + 1 : c;
+            if (!odd) {
+                const uint4 sv = *reinterpret_cast<const uint4*>(bs + (int64_t)c * 16 + os);
+                C.s[0] = sv.x; C.s[1] = sv.y; C.s[2] = sv.z; C.s[3] = sv.w;
+                Sod = *reinterpret_cast<const uint4*>(bs + (int64_t)c1 * 16 + os);
+            } else {
+                C.s[0] = Sod.x; C.s[1] = Sod.y; C.s[2] = Sod.z; C.s[3] = Sod.w;
+            }
             C.d = dlds ? (uint32_t)Dq[(wave * 32 + n) * WV_DQ + (c - cb)]
                        : (uint32_t)*reinterpret_cast<const uint16_t*>(bd + (int64_t)c * 2 + od);
             const uint8_t* qlc = bw + (int64_t)c * 128;
             const uint8_t* qhc = bh + (int64_t)c * 64;
+            const uint8_t* qhn = bh + (int64_t)c1 * 64;
 #pragma unroll
             for (int u = 0; u < 4; ++u) {
                 const uint2 lo = *reinterpret_cast<const uint2*>(qlc + ow + u * 32);
                 const uint2 hi = *reinterpret_cast<const uint2*>(qlc + ow + u * 32 + 16);
                 C.w[u] = make_uint4(lo.x, lo.y, hi.x, hi.y);
-                C.h[u] = *reinterpret_cast<const uint2*>(qhc + oh + u * 16);
+                if (!odd) {
+                    C.h[u] = *reinterpret_cast<const uint2*>(qhc + oh + u * 16);
+                    Hod[u] = *reinterpret_cast<const uint2*>(qhn + oh + u * 16);
+                } else {
+                    C.h[u] = Hod[u];
+                }
             }
         } else if constexpr (QT == 8) {
             const uint4 sv = *reinterpret_cast<const uint4*>(bs + (int64_t)c * 512 + os);
@@ -452,7 +471,7 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
     xload(xv, cb);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    wload(W0, cb);
+    wload(W0, cb, false);
     xstore(xv, 0);
     __syncthreads();
 
@@ -467,13 +486,20 @@ __global__ __launch_bounds__(256, 2) void k_gemv_wide(const uint8_t* __restrict_
     auto step = [&](int c, WChunk<QT>& Wc, WChunk<QT>& Wn, int buf) {
         const bool more = c + 1 < ce;
         wv_settle(Wc);
+        if constexpr (QT == 14) {
+            // the next chunk's QH / scales, loaded with Wc (buf 0: the next is odd)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) asm volatile("" : "+v"(Hod[u].x), "+v"(Hod[u].y)::"memory");
+            asm volatile("" : "+v"(Sod.x), "+v"(Sod.y), "+v"(Sod.z), "+v"(Sod.w)::"memory");
+        }
+        const bool odd_next = buf == 0;  // steps alternate even / odd chunks of the range
         // unconditional (the last step reloads its own chunk, unused): no
         // merge of loaded and old register values for the allocator to copy
         const int cn = more ? c + 1 : c;
         xload(xv, cn);
         asm volatile("" ::: "memory");
         __builtin_amdgcn_sched_barrier(0);
-        wload(Wn, cn);
+        wload(Wn, cn, odd_next);
         __builtin_amdgcn_sched_barrier(0);
         compute(Wc, buf);
         if (more) xstore(xv, buf ^ 1);
