@@ -2,8 +2,10 @@
 fresh context (thq_matmul_argmax with logits_dev NULL).
 
 The logits then live in the context workspace together with the scratch of
-the route the call takes: the decode GEMV's split-K partials (M = 3..16 on a
-151936-row head plan two K splits) and the argmax partials.  Both must be
+the route the call takes: the argmax partials, and the split-K partials of
+a route that splits K (on a 151936-row head the wide GEMV takes 5 and 12 rows
+of Q8_0 and 12 of Q6_K with K unsplit; 5 rows of Q6_K take the decode GEMV,
+whose plan splits K in two).  Both must be
 sized from that route before any pointer into the workspace is formed, or
 the logits and the partials overlap (and the first call in a fresh context,
 which grows the workspace, would leave the logits in a retired buffer).
@@ -35,7 +37,7 @@ def _gpu():
     torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("kind,m", [("q8_0", 5), ("q8_0", 12), ("q6_k", 12)])
+@pytest.mark.parametrize("kind,m", [("q8_0", 5), ("q8_0", 12), ("q6_k", 5), ("q6_k", 12)])
 def test_head_without_logits_fresh_context(kind, m):
     if kind == "q8_0":
         qt, b = O.Q8_0, weight_bytes(O.Q8_0, N, K, seed=4)

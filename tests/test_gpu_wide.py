@@ -43,8 +43,10 @@ def make(kind, n, k, seed):
 
 
 # (n, k, rows): a ragged last tile in one K split; 32 output tiles (K split
-# four ways); a long K
-CASES = [(1000, 1024, (9, 16, 17, 31, 32, 33, 40, 41, 64)), (4096, 4096, (17, 40, 64)), (300, 12288, (20, 40))]
+# four ways); a long K; and a vocabulary-wide head (65536 outputs) that the
+# router gives the wide GEMV from 4 (Q8_0), 5 (Q4_K / affine) and 9 (Q6_K) rows
+CASES = [(1000, 1024, (9, 16, 17, 31, 32, 33, 40, 41, 64)), (4096, 4096, (17, 40, 64)), (300, 12288, (20, 40)),
+         (65536, 512, (4, 5, 9, 12, 16))]
 
 
 @pytest.mark.parametrize("kind", KINDS)
@@ -66,12 +68,12 @@ def test_wide_matches_oracle(kind, case):
 
 
 @pytest.mark.parametrize("kind", KINDS)
-def test_wide_fused_argmax(kind):
+@pytest.mark.parametrize("n,k,rows", [(5000, 1024, (17, 40, 64)), (65536, 256, (5, 9, 16))])
+def test_wide_fused_argmax(kind, n, k, rows):
     """Per-32-row (max, lowest index) partials merged to the row argmax equal
     the logits path's argmax and the oracle's argmax of those logits."""
-    n, k = 5000, 1024
     w, _ = make(kind, n, k, seed=990)
-    for m in (17, 40, 64):
+    for m in rows:
         print(f"[wide] fused argmax {kind} m={m}", flush=True)
         xb = torch.from_numpy(O.bf16_round(activations(m, k, seed=m + 77))).cuda().to(torch.bfloat16)
         _, fused = thq.matmul_argmax(w, xb, want_logits=False, flags=thq.MODE_ARGMAX_FUSED)

@@ -365,7 +365,7 @@ Route plan_route(const Call& c) {
         const char* e = getenv("THQ_GEMV_ROWS");
         return !(e && !strcmp(e, "0"));
     }();
-    // 17..64 bf16 rows: the wide exact-weight GEMV where exact weights are
+    // 17..64 bf16 rows (fewer on the widest outputs, below): the wide exact-weight GEMV where exact weights are
     // required (Q8_0 up to 64 rows, THQ_MODE_EXACT_W on 4- / 6-bit weights)
     // and on outputs wide enough to fill the GPU without splitting K (the
     // verify LM head); THQ_GEMV_WIDE=0 turns it off
@@ -373,7 +373,19 @@ Route plan_route(const Call& c) {
         const char* e = getenv("THQ_GEMV_WIDE");
         return !(e && !strcmp(e, "0"));
     }();
-    const thq::WidePlan wp = (wide_on && !xf32 && aligned16(c.x) && m >= 17 && m <= 64)
+    // On outputs that fill the GPU without splitting K (the verify LM head,
+    // 151936 x 4096) it also takes fewer rows, ahead of the MFMA decode GEMV:
+    // from 4 rows of Q8_0, 5 of Q4_K / affine, 9 of Q6_K (151936 x 4096 at
+    // M = 3..16: Q8_0 128-136 against 129-157 us, Q4_K 99-104 against 95-147,
+    // Q6_K 163-167 against 147-198).  THQ_WIDE_MIN_M sets the lowest row count.
+    static const int wide_env = [] {
+        const char* e = getenv("THQ_WIDE_MIN_M");
+        return e && *e ? atoi(e) : 0;
+    }();
+    int wide_min_m = 17;
+    if (nout >= 65536) wide_min_m = w->qtype == THQ_Q8_0 ? 4 : (w->qtype == THQ_Q6_K ? 9 : 5);
+    if (wide_env > 0) wide_min_m = wide_env < 2 ? 2 : wide_env;
+    const thq::WidePlan wp = (wide_on && !xf32 && aligned16(c.x) && m >= wide_min_m && m <= 64)
                                  ? thq::plan_gemv_wide(v.qtype, m, w->N, w->K, c.ctx->cus)
                                  : thq::WidePlan{};
     const bool wide_ok = wp.splits > 0 && (w->qtype == THQ_Q8_0 || (c.flags & THQ_MODE_EXACT_W) || nout >= 65536);
@@ -409,7 +421,7 @@ Route plan_route(const Call& c) {
                // 19.45 against 20.45 us); at 4096 outputs the row kernel is (6.8 against 8.2 us)
                !(m >= 3 && skinny && nout >= 12288)) {
         if (!c.am) r.kind = Kind::ROWS;
-    } else if (skinny) {
+    } else if (skinny && !(wide_ok && m >= wide_min_m)) {
         // the fused epilogue exists on the unsplit plan only (no scratch)
         if (!c.am || gp.splits == 1) {
             r.kind = Kind::GEMV_MFMA;
