@@ -2,8 +2,9 @@
 callers that cannot allocate.  Called through the C ABI and compared with
 thq_matmul on the same inputs, on two calls in a row with the second one
 smaller (the array keeps the first call's contents), for each route that
-uses scratch: the split-K decode GEMV, the split-K GEMM, the split-K wide
-exact-weight GEMV (17..64 rows) and THQ_MODE_Q8ACT.
+uses scratch: the split-K decode GEMV, the split-K tile GEMM, the split-K
+streaming mid-M GEMM, the split-K wide exact-weight GEMV (17..64 rows) and
+THQ_MODE_Q8ACT.
 Both entry points run the same kernels with the same plans, so the outputs
 must agree bit for bit (stricter than the 1e-2 row bar of bf16 rows); the
 oracle's f64 product pins them to the path's tolerance.  A route needing
@@ -47,18 +48,22 @@ def noalloc(w, x, y, flags=0):
                                       C.c_void_p(y.data_ptr()), thq.ACT_F32, flags, s)
 
 
-@pytest.mark.parametrize("route,ms,flags", [
-    ("split-K decode GEMV", (16, 12), 0),
-    ("split-K GEMM", (128, 64), 0),
-    ("split-K wide GEMV", (40, 20), thq.MODE_EXACT_W),
-    ("Q8ACT", (9, 3), thq.MODE_Q8ACT),
+@pytest.mark.parametrize("route,ms,flags,mid", [
+    ("split-K decode GEMV", (16, 12), 0, "0"),
+    ("split-K GEMM", (128, 64), 0, "0"),
+    ("split-K streaming mid GEMM", (128, 100), 0, "1"),
+    ("split-K wide GEMV", (40, 20), thq.MODE_EXACT_W, "0"),
+    ("Q8ACT", (9, 3), thq.MODE_Q8ACT, "0"),
 ])
-def test_noalloc_matches_matmul(weight, route, ms, flags):
+def test_noalloc_matches_matmul(weight, route, ms, flags, mid, monkeypatch):
+    # THQ_GEMM_MID picks between the tile GEMM and the streaming GEMM (whose
+    # planner splits K four ways at 100 and 128 rows of this shape)
+    monkeypatch.setenv("THQ_GEMM_MID", mid)
     b, w = weight
     for m in ms:
         if flags == thq.MODE_EXACT_W:
             assert thq.plan_gemv_wide(thq.Q4_K, m, N, K).splits > 1, f"{route} at M={m} should split K"
-        elif flags == 0:
+        elif flags == 0 and mid == "0":
             plan = thq.plan_gemv_mfma(thq.Q4_K, m, N, K) if m <= 16 else thq.plan_gemm(thq.Q4_K, m, N, K)
             assert plan.splits > 1, f"{route} at M={m} should split K"
         xf = O.bf16_round(activations(m, K, seed=m))

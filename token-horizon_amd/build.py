@@ -32,7 +32,7 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 SOURCES = [
     "thq_api.cpp", "k_weights.hip", "k_gemv.hip", "k_gemv_mfma.hip", "k_gemm.hip", "k_argmax.hip", "k_q8act.hip",
     "k_q6k.hip", "k_topk.hip", "k_gemv_wide.hip", "k_gemv_tile.hip", "k_gemm_b16.hip",
-    "k_gemm_fq.hip", "k_gemm_rq.hip", "thq_gguf.cpp",
+    "k_gemm_fq.hip", "k_gemm_rq.hip", "k_gemm_mid.hip", "thq_gguf.cpp",
 ]
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", "--offload-arch=gfx950", "-ffp-contract=off",

@@ -301,7 +301,7 @@ int check_call(const Call& c) {
 
 // The kernels a call runs, and the device scratch (split-K partials or the
 // quantized activation planes) they use, known before anything launches.
-enum class Kind { NONE, Q8ACT, Q8ACT_TILE, GEMV1, ROWS, GEMV_TILE, GEMV_MFMA, GEMV_MFMA_GROUPS, WIDE, GEMM, GEMM_DQ, GEMM_FQ, GEMM_RQ, GENERIC };
+enum class Kind { NONE, Q8ACT, Q8ACT_TILE, GEMV1, ROWS, GEMV_TILE, GEMV_MFMA, GEMV_MFMA_GROUPS, WIDE, GEMM, GEMM_DQ, GEMM_FQ, GEMM_RQ, GEMM_MID, GENERIC };
 struct Route {
     Kind kind = Kind::NONE;
     thq::GemvPlan gp;
@@ -311,6 +311,7 @@ struct Route {
     thq::GemmPlan gm;
     thq::FqPlan fq;
     thq::RqPlan rq;
+    thq::MidPlan mp;
     bool exact = false;
     size_t scratch = 0;
 };
@@ -518,6 +519,27 @@ Route plan_route(const Call& c) {
                 r.scratch = rp.workspace_bytes;
             }
         }
+        // Q4_K / MLX affine with rounded weights at tens of rows: the
+        // streaming GEMM (k_gemm_mid: each wave's weight rows straight into
+        // registers, the activation rows copied into LDS), from 17 rows up to
+        // 128 on weights with at least as many rows as columns and up to 64
+        // on the others (12288 x 4096 at M = 17 / 64 / 96 / 128: 22.3 / 25.9 /
+        // 33.6 / 34.7 against 25.3 / 28.9 / 42.0 / 37.2 us; gate/up 2 x 12288
+        // x 4096 at M = 32 / 128: 35.7 / 51.1 against 44.5 / 56.9 us; 4096 x
+        // 12288 at M = 64: 26.3 against 28.8 us, at M = 128: 35.2 against
+        // 33.0 us).  THQ_GEMM_MID: 0 never, 1 wherever supported (tests),
+        // unset: that rule
+        const char* mde = getenv("THQ_GEMM_MID");
+        const int mid_mode = mde && *mde ? atoi(mde) : -1;
+        const bool mid_default = m >= 17 && m <= (w->N >= w->K ? 128 : 64) && r.kind == Kind::GEMM;
+        if (q4 && !r.exact && mid_mode != 0 && (mid_mode == 1 || mid_default)) {
+            const thq::MidPlan mp = thq::plan_gemm_mid(v.qtype, m, w->N, w->K, c.gu, c.ctx->cus);
+            if (mp.mh > 0 && mp.workspace_bytes <= c.scratch_cap) {
+                r.kind = Kind::GEMM_MID;
+                r.mp = mp;
+                r.scratch = mp.workspace_bytes;
+            }
+        }
     } else if (!xf32 && aligned16(c.x) && (q4 || q6) && m > 16 && w->K % 256 == 0 &&
                thq::plan_gemv_mfma(v.qtype, 16, w->N, w->K, c.gu).waves > 0) {
         // exact 4- / 6-bit weights past the decode GEMV's 16 rows (the verify
@@ -593,6 +615,9 @@ int exec_route(const Call& c, const Route& r, void* scratch, uint32_t* cnt = nul
         case Kind::GEMM_RQ:
             e = thq::launch_gemm_rq(r.rq, w->qtype == THQ_MLX_Q4, w->q, c.x, c.y, yf32, c.gu, m, w->N, (int)w->K,
                                     static_cast<float*>(scratch), cnt, c.s);
+            break;
+        case Kind::GEMM_MID:
+            e = thq::launch_gemm_mid(r.mp, v, c.x, c.y, yf32, c.gu, m, nout, up_off, static_cast<float*>(scratch), c.s);
             break;
         case Kind::GEMM_DQ:
             // the weight as bf16 [N][K] in the scratch, then x . Wb^T

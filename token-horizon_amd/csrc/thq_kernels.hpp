@@ -107,6 +107,17 @@ struct WidePlan {
 WidePlan plan_gemv_wide(int qtype, int64_t M, int64_t N, int64_t K, int cus);
 hipError_t launch_gemv_wide(const WidePlan& p, const WeightView& w, const void* x, void* y, bool yf32, bool gu,
                             int M, int64_t nout, int64_t up_off, float* ws, hipStream_t s, AmaxOut* am = nullptr);
+// prefill / verify GEMM with rounded weights for Q4_K / MLX affine on the
+// row-quad plane (k_gemm_mid.hip): bf16 rows (16-B aligned), K % 256 == 0,
+// plain or gate/up; activation rows in groups of 32 mh (grid.z)
+struct MidPlan {
+    int mh = 0, nt = 1, nw = 4, groups = 0;  // 32-row halves per group (2 or 4; 0: unsupported), column tiles per wave, waves per block, groups
+    int splits = 0, cps = 0;      // K splits, 256-wide chunks per split
+    size_t workspace_bytes = 0;   // split partials (f32 [splits][M][N])
+};
+MidPlan plan_gemm_mid(int qtype, int64_t M, int64_t N, int64_t K, bool gu, int cus);
+hipError_t launch_gemm_mid(const MidPlan& p, const WeightView& w, const void* x, void* y, bool yf32, bool gu, int M,
+                           int64_t nout, int64_t up_off, float* ws, hipStream_t s);
 // Q4_K / MLX affine tile plane (thq_dev.hpp, q4t_record), k_gemv_tile.hip:
 // its size, its construction from the row-quad plane, and the 3..8-row
 // decode GEMV over it (bf16 rows, 16-B aligned; plain or gate/up)
