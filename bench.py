@@ -329,7 +329,7 @@ def main():
     ap.add_argument("--no-configs", action="store_true", help="skip the per-configuration object")
     ap.add_argument("--extra", action="store_true", help="also time the other workloads (formats, modes, layers)")
     ap.add_argument("--only", default=None,
-                    help="with --extra: only the sections whose name contains this (gemv_q8_0, q4k, affine, q6k, "
+                    help="with --extra: only the sections whose name contains this (gemv_q8_0, q4k, gemm_mid, affine, q6k, "
                          "lm_head_q6k, lm_head_q8_0, topk, decoder), e.g. for a profile of one workload")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="after the run, stream a 28,311,552-byte buffer through an elementwise kernel 24 times "
@@ -621,7 +621,8 @@ def q6k_bytes(n, k):
 def run_extra(torch, thq, g, only=None):
     """Every other configuration: decode GEMV M in {1,2,4,8} (and M in
     {3,4,5,8} on weights with a tile plane) and prefill GEMM
-    M in {128,512,2048} on both Qwen3-8B MLP weight shapes (plus Q8ACT GEMV,
+    M in {128,512,2048} on both Qwen3-8B MLP weight shapes, M in
+    {32,...,512} on them and on the fused gate/up (plus Q8ACT GEMV,
     also on the tile plane at M in {2,5,8} with the dot alone over a
     prepared Q8_K buffer, and the MLX affine format on the gate/up shape), Q8_0 decode GEMV at
     M in {1,8} on both shapes, the Q8_0 LM head with argmax at M in {1,5,40}
@@ -692,6 +693,25 @@ def run_extra(torch, thq, g, only=None):
             fns = [lambda w=w, pre=pre: pre.matmul(w, torch.float32) for w in ws]
             planes = m * (k + k // 256 * 4 + k // 32 * 2)
             res[f"gemv_q4k_tiles_q8act_dot_n{n}_k{k}_m{m}"] = gemv_line(fns, q4k_bytes(n, k) + planes + 4 * m * n)
+        del ws
+
+    # tens to hundreds of rows on Q4_K (the streaming mid-M GEMM's range up
+    # to 128 rows, the tile / dequantize GEMMs past it): both MLP shapes and
+    # the fused gate/up, 12 weight copies rotated (> MALL)
+    for (n, k, gu) in [(12288, 4096, False), (4096, 12288, False), (24576, 4096, True)] if want("gemm_mid") else []:
+        log(f"extra: Q4_K {n}x{k}{' gate/up' if gu else ''} at 32..512 rows")
+        ws = make_weights(thq, torch, n, k, 12, seed=9 + n)
+        nout = n // 2 if gu else n
+        for m in (32, 64, 96, 128, 256, 512):
+            x = torch.randn((m, k), generator=g, device="cuda").to(torch.bfloat16)
+            y = torch.empty((m, nout), dtype=torch.bfloat16, device="cuda")
+            if gu:
+                fns = [lambda w=w, x=x, y=y: thq.gate_up_silu(w, x, out=y) for w in ws]
+            else:
+                fns = [lambda w=w, x=x, y=y: thq.matmul(w, x, out=y) for w in ws]
+            dt = time_eager(torch, fns, 120, 12) / 120
+            res[f"gemm_mid_q4k_n{n}_k{k}{'_gu' if gu else ''}_m{m}"] = {
+                "us": round(dt * 1e6, 1), "TFLOPs": round(2.0 * m * n * k / dt / 1e12, 1)}
         del ws
 
     if want("affine"):

@@ -8,29 +8,31 @@
 // M x N output is too small for 256-wide GEMM tiles to fill the GPU without
 // splitting K several ways.
 //
-// Structure (one block = 4 waves):
-//   weights      each wave owns 32 weight rows (gate/up: 16 gate rows and the
-//                16 up rows of the same outputs); each lane streams its row's
-//                16-B nibble pieces and header dwords of a 256-wide chunk
-//                straight into registers (k_gemv_wide's loads), one chunk
-//                ahead of the math, so every weight byte is read once per
-//                group of activation rows;
-//   activations  a group of up to MP = 32 MH rows (grid.z) is copied chunk by
-//                chunk into LDS by direct-to-LDS copies
-//                (global_load_lds_dwordx4), the next chunk while the current
-//                one computes: two buffers of MP x 256 bf16.  One copy
-//                instruction fills two 512-B rows; the 16-B piece p of row r
-//                sits at slot p ^ (r & 15), so the MFMA operand reads of 16
-//                consecutive rows hit 16 distinct bank groups.  Rows past M
-//                copy row M - 1 and are never stored;
-//   math         per 64-wide unit the lane's 32 weights become bf16
+// Structure (a block = NW waves, 4 or 8; its instances and the planner are
+// below):
+//   weights      each wave owns NT 32-row column tiles of weight rows
+//                (gate/up: 16 gate rows and the 16 up rows of the same
+//                outputs per tile); each lane streams its rows' 16-B nibble
+//                pieces and header dwords of a 256-wide chunk straight into
+//                registers (k_gemv_wide's loads), two chunks ahead of the
+//                math, so every weight byte is read once per group of
+//                activation rows;
+//   activations  a group of up to MP = 32 MH rows is copied chunk by chunk
+//                into LDS by direct-to-LDS copies (global_load_lds_dwordx4),
+//                the next chunk while the current one computes: two buffers
+//                of MP x 256 bf16.  One copy instruction fills two 512-B
+//                rows; the 16-B piece p of row r sits at slot p ^ (r & 15),
+//                so the MFMA operand reads of 16 consecutive rows hit 16
+//                distinct bank groups.  Rows past M copy row M - 1 and are
+//                never stored;
+//   math         per 64-wide unit the lane's 32 weights per tile become bf16
 //                fma(d1, 128 + q, -(128 d1 + m1)) (k_gemm's rounded tile,
 //                bit for bit: Q4_K d1 = d sc, m1 = dmin m; affine d1 = scale,
 //                m1 = -bias) and feed one v_mfma_f32_32x32x16_bf16 per 16 K
-//                per 32-row half of the group, accumulating across all of K
-//                (no per-sub-block scaling);
-//   K splits     grid.y: f32 partials into the workspace, summed in split
-//                order by k_split_reduce (deterministic).
+//                per 32-row half of the group and tile, accumulating across
+//                all of K (no per-sub-block scaling);
+//   K splits     f32 partials into the workspace, summed in split order by
+//                k_split_reduce (deterministic).
 // Offsets are 32-bit: the host checks the plane and x sizes (< 4 GiB).
 #include "thq_dev.hpp"
 #include "thq_kernels.hpp"
