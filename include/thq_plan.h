@@ -2,7 +2,7 @@
  * thq_plan.h — host-only planner introspection of libthq.so.
  *
  * What thq_matmul would launch for a shape, computed on the host with no
- * device work and no context: the decode GEMV's and the GEMM's plans, the
+ * device work and no context: the decode GEMVs' and the GEMMs' plans, the
  * kernel instance a plan selects, and the kernels' LDS staging limits.  For
  * tests (bounds of every plan are checked off-GPU against these limits) and
  * for tuning.  No counterpart in the reference (its Metal pipelines size
@@ -80,6 +80,23 @@ typedef struct thq_tile_plan_info {
 
 int thq_plan_gemv_tile(int dtype, int64_t m, int64_t n, int64_t k, int gate_up, int cus,
                        thq_tile_plan_info* out);
+
+/* Streaming mid-M GEMM with rounded weights (Q4_K / MLX affine on the
+ * row-quad plane, bf16 rows, K a multiple of 256), for a device with `cus`
+ * compute units; gate_up: the fused [gate; up] weight (n rows, n / 2
+ * outputs).  The router takes it for 17..128 rows (17..64 where n < k).
+ * group_halves 0 for shapes it does not cover. */
+typedef struct thq_mid_plan_info {
+    int32_t group_halves;     /* 32-row halves per activation group (2 or 4; 0: no plan) */
+    int32_t col_tiles;        /* 32-row column tiles per wave                       */
+    int32_t waves;            /* waves per block (4 or 8)                           */
+    int32_t groups;           /* activation groups (blocks along M)                 */
+    int32_t splits;           /* K splits (partials summed by a reduce launch)      */
+    int32_t chunks_per_split; /* 256-wide K chunks per split                        */
+    int64_t workspace_bytes;  /* split partials, f32 [splits][M][N]                 */
+} thq_mid_plan_info;
+
+int thq_plan_gemm_mid(int dtype, int64_t m, int64_t n, int64_t k, int gate_up, int cus, thq_mid_plan_info* out);
 
 #ifdef __cplusplus
 }

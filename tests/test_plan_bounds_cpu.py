@@ -174,6 +174,40 @@ def test_wide_plans():
     assert thq.plan_gemv_wide(thq.Q4_K, 40, 151936, 4096).splits == 1
 
 
+def test_mid_plans():
+    """The streaming mid-M GEMM's plan: an instance the launcher has (groups of
+    64 or 128 rows; 1 or 2 column tiles per wave; 4 or 8 waves, 8 with one
+    column tile), groups that cover M, splits that cover K exactly and are
+    non-empty, and a workspace of the split partials; shapes it cannot
+    address with 32-bit offsets, K not a multiple of 256 and odd gate/up
+    weights plan nothing; the measured picks of the two MLP shapes."""
+    for dt in (thq.Q4_K, thq.MLX_Q4):
+        for gu in (False, True):
+            for m in (1, 17, 33, 64, 65, 100, 128, 129, 300, 512, 2048):
+                for n in (256, 600, 4096, 12288, 24576):
+                    for k in (256, 1024, 4096, 12288):
+                        p = thq.plan_gemm_mid(dt, m, n, k, gu)
+                        nch = k // 256
+                        assert p.group_halves in (2, 4), (dt, gu, m, n, k)
+                        assert (p.col_tiles, p.waves) in ((1, 4), (2, 4), (1, 8))
+                        assert p.groups == -(-m // (32 * p.group_halves))
+                        assert p.splits >= 1 and p.chunks_per_split >= 1
+                        assert p.splits * p.chunks_per_split >= nch > (p.splits - 1) * p.chunks_per_split
+                        assert p.workspace_bytes == (p.splits * m * n * 4 if p.splits > 1 else 0)
+        assert thq.plan_gemm_mid(dt, 64, 4096, 1000).group_halves == 0
+        assert thq.plan_gemm_mid(dt, 64, 301, 1024, gate_up=True).group_halves == 0
+        assert thq.plan_gemm_mid(dt, 64, 1 << 20, 1 << 14).group_halves == 0  # 9.7 GB plane
+        assert thq.plan_gemm_mid(dt, 1 << 18, 4096, 8192).group_halves == 0   # 4 GiB of x
+    p = thq.plan_gemm_mid(thq.Q4_K, 128, 12288, 4096)
+    assert (p.group_halves, p.col_tiles, p.waves, p.splits) == (4, 1, 8, 4)
+    p = thq.plan_gemm_mid(thq.Q4_K, 64, 12288, 4096)
+    assert (p.group_halves, p.col_tiles, p.waves, p.splits) == (2, 1, 8, 4)
+    o = thq.MidPlanInfo()
+    assert thq.lib.thq_plan_gemm_mid(thq.Q8_0, 64, 4096, 4096, 0, 256, o) == thq.EDTYPE
+    assert thq.lib.thq_plan_gemm_mid(thq.Q4_K, 0, 4096, 4096, 0, 256, o) == thq.ESHAPE
+    assert thq.lib.thq_plan_gemm_mid(thq.Q4_K, 64, 4096, 4096, 0, 256, None) == thq.EINVAL
+
+
 def tile_lds_bytes(kw: int, m: int, nt: int) -> int:
     """k_gemv_q4t's LDS (token-horizon_amd/csrc/k_gemv_tile.hip, tile_lds_bytes):
     x rows of the block's K range with an 8-column pad, the 32-wide sums of 8

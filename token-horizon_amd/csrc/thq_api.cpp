@@ -1439,6 +1439,24 @@ int thq_plan_gemv_wide(int dtype, int64_t m, int64_t n, int64_t k, int cus, thq_
     return THQ_OK;
 }
 
+int thq_plan_gemm_mid(int dtype, int64_t m, int64_t n, int64_t k, int gate_up, int cus, thq_mid_plan_info* out) {
+    if (dtype != THQ_Q4_K && dtype != THQ_MLX_Q4)
+        return fail(THQ_EDTYPE, "the streaming GEMM: Q4_K or MLX affine (%d)", dtype);
+    if (!out) return fail(THQ_EINVAL, "null out");
+    if (m < 1 || n < 1 || k < 1) return fail(THQ_ESHAPE, "shape [%lld, %lld, %lld]", (long long)m, (long long)n,
+                                             (long long)k);
+    const thq::MidPlan p = thq::plan_gemm_mid(kernel_qtype(dtype), m, n, k, gate_up != 0, cus);
+    *out = thq_mid_plan_info{};
+    out->group_halves = p.mh;
+    out->col_tiles = p.nt;
+    out->waves = p.nw;
+    out->groups = p.groups;
+    out->splits = p.splits;
+    out->chunks_per_split = p.cps;
+    out->workspace_bytes = (int64_t)p.workspace_bytes;
+    return THQ_OK;
+}
+
 int thq_plan_gemv_tile(int dtype, int64_t m, int64_t n, int64_t k, int gate_up, int cus,
                        thq_tile_plan_info* out) {
     if (dtype != THQ_Q4_K && dtype != THQ_MLX_Q4) return fail(THQ_EDTYPE, "tile planes: Q4_K or MLX affine (%d)", dtype);

@@ -53,7 +53,7 @@ EXPORTS = (
     "thq_gguf_find_tensor", "thq_gguf_tensor_info", "thq_gguf_tensor_data", "thq_gguf_metadata_key",
     "thq_gguf_metadata_u32", "thq_gguf_metadata_f32", "thq_gguf_metadata_str", "thq_gguf_metadata_array",
     "thq_weight_from_gguf", "thq_q8act_bytes", "thq_q8act_prepare", "thq_matmul_q8act", "thq_gate_up_silu_q8act",
-    "thq_plan_gemv_mfma", "thq_plan_gemm", "thq_plan_gemv_wide", "thq_matmul_noalloc", "thq_noalloc_scratch_bytes",
+    "thq_plan_gemv_mfma", "thq_plan_gemm", "thq_plan_gemv_wide", "thq_plan_gemm_mid", "thq_matmul_noalloc", "thq_noalloc_scratch_bytes",
     "thq_topk", "thq_matmul_topk", "thq_gate_up_silu_q8act_emit", "thq_weight_add_tiles",
     "thq_call_scratch_bytes", "thq_reserve", "thq_workspace_bytes", "thq_plan_gemv_tile",
 )
@@ -94,6 +94,18 @@ def plan_gemv_wide(dtype: int, m: int, n: int, k: int, cus: int = 256) -> WidePl
     """The wide exact-weight GEMV's plan (thq_plan_gemv_wide); splits == 0: no plan."""
     out = WidePlanInfo()
     check(lib.thq_plan_gemv_wide(dtype, m, n, k, cus, C.byref(out)))
+    return out
+
+
+class MidPlanInfo(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("group_halves", "col_tiles", "waves", "groups", "splits",
+                                         "chunks_per_split")] + [("workspace_bytes", C.c_int64)]
+
+
+def plan_gemm_mid(dtype: int, m: int, n: int, k: int, gate_up: bool = False, cus: int = 256) -> MidPlanInfo:
+    """The streaming mid-M GEMM's plan (thq_plan_gemm_mid); group_halves == 0: no plan."""
+    out = MidPlanInfo()
+    check(lib.thq_plan_gemm_mid(dtype, m, n, k, int(gate_up), cus, C.byref(out)))
     return out
 
 
@@ -175,6 +187,7 @@ def _load():
         "thq_plan_gemv_mfma": ([I, i64, i64, i64, I, C.POINTER(GemvPlanInfo)], I),
         "thq_plan_gemm": ([I, I, i64, i64, i64, I, I, C.POINTER(GemmPlanInfo)], I),
         "thq_plan_gemv_wide": ([I, i64, i64, i64, I, C.POINTER(WidePlanInfo)], I),
+        "thq_plan_gemm_mid": ([I, i64, i64, i64, I, I, C.POINTER(MidPlanInfo)], I),
         "thq_plan_gemv_tile": ([I, i64, i64, i64, I, I, C.POINTER(TilePlanInfo)], I),
     }
     for name, (args, res) in sig.items():
