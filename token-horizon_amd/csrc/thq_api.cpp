@@ -389,7 +389,15 @@ Route plan_route(const Call& c) {
     const thq::WidePlan wp = (wide_on && !xf32 && aligned16(c.x) && m >= wide_min_m && m <= 64)
                                  ? thq::plan_gemv_wide(v.qtype, m, w->N, w->K, c.ctx->cus)
                                  : thq::WidePlan{};
-    const bool wide_ok = wp.splits > 0 && (w->qtype == THQ_Q8_0 || (c.flags & THQ_MODE_EXACT_W) || nout >= 65536);
+    // 17..32 rows of Q4_K / MLX affine: the wide GEMV (exact weights) is
+    // also the fastest route (12288 x 4096 / 4096 x 12288 / gate/up 2 x 12288
+    // x 4096 at M = 17..32: 19.2-20.5 / 21.0-21.5 / 30.2-31.1 us against the
+    // streaming GEMM's 24.5-25.0 / 26.3-26.6 / 36.1-43.8; from 48 rows it is
+    // slower); THQ_GEMM_MID=1 keeps those rows on the streaming GEMM
+    const char* mde0 = getenv("THQ_GEMM_MID");
+    const bool mid_forced = mde0 && !strcmp(mde0, "1");
+    const bool wide_ok = wp.splits > 0 && (w->qtype == THQ_Q8_0 || (c.flags & THQ_MODE_EXACT_W) || nout >= 65536 ||
+                                           (q4 && m <= 32 && !mid_forced));
     // Q8_0 at M = 1 from 12288 outputs: the MFMA GEMV on the tile layout beats
     // the VALU kernel (bf16 x; 12288 / 24576 x 4096: 13.7 / 21.9 vs 14.0 /
     // 23.1 us; LM head 151936 x 4096: 111 vs 125 us); below, the VALU kernel
@@ -519,16 +527,16 @@ Route plan_route(const Call& c) {
                 r.scratch = rp.workspace_bytes;
             }
         }
-        // Q4_K / MLX affine with rounded weights at tens of rows: the
-        // streaming GEMM (k_gemm_mid: each wave's weight rows straight into
-        // registers, the activation rows copied into LDS), from 17 rows up to
-        // 128 on weights with at least as many rows as columns and up to 64
-        // on the others (12288 x 4096 at M = 17 / 64 / 96 / 128: 22.3 / 25.9 /
-        // 33.6 / 34.7 against 25.3 / 28.9 / 42.0 / 37.2 us; gate/up 2 x 12288
-        // x 4096 at M = 32 / 128: 35.7 / 51.1 against 44.5 / 56.9 us; 4096 x
-        // 12288 at M = 64: 26.3 against 28.8 us, at M = 128: 35.2 against
-        // 33.0 us).  THQ_GEMM_MID: 0 never, 1 wherever supported (tests),
-        // unset: that rule
+        // Q4_K / MLX affine with rounded weights at tens of rows (past the
+        // 32 the wide GEMV takes): the streaming GEMM (k_gemm_mid: each wave's
+        // weight rows straight into registers, the activation rows copied
+        // into LDS), up to 128 rows on weights with at least as many rows as
+        // columns and up to 64 on the others (12288 x 4096 at M = 48 / 64 /
+        // 96 / 128: 25.2 / 25.9 / 33.6 / 34.7 against 28.1 / 28.9 / 42.0 /
+        // 37.2 us; gate/up 2 x 12288 x 4096 at M = 64 / 128: 38.8 / 51.1
+        // against 46.2 / 56.9 us; 4096 x 12288 at M = 64: 26.3 against 28.8 us,
+        // at M = 128: 35.2 against 33.0 us).  THQ_GEMM_MID: 0 never, 1
+        // wherever supported (tests), unset: that rule
         const char* mde = getenv("THQ_GEMM_MID");
         const int mid_mode = mde && *mde ? atoi(mde) : -1;
         const bool mid_default = m >= 17 && m <= (w->N >= w->K ? 128 : 64) && r.kind == Kind::GEMM;
