@@ -389,15 +389,17 @@ Route plan_route(const Call& c) {
     const thq::WidePlan wp = (wide_on && !xf32 && aligned16(c.x) && m >= wide_min_m && m <= 64)
                                  ? thq::plan_gemv_wide(v.qtype, m, w->N, w->K, c.ctx->cus)
                                  : thq::WidePlan{};
-    // 17..32 rows of Q4_K / MLX affine: the wide GEMV (exact weights) is
-    // also the fastest route (12288 x 4096 / 4096 x 12288 / gate/up 2 x 12288
-    // x 4096 at M = 17..32: 19.2-20.5 / 21.0-21.5 / 30.2-31.1 us against the
-    // streaming GEMM's 24.5-25.0 / 26.3-26.6 / 36.1-43.8; from 48 rows it is
-    // slower); THQ_GEMM_MID=1 keeps those rows on the streaming GEMM
+    // 17..32 rows of Q4_K / MLX affine / Q6_K: the wide GEMV (exact
+    // weights) is also the fastest route (12288 x 4096 / 4096 x 12288 /
+    // gate/up 2 x 12288 x 4096 at M = 17..32: Q4_K 19.2-20.5 / 21.0-21.5 /
+    // 30.2-31.1 us against the streaming GEMM's 24.5-25.0 / 26.3-26.6 /
+    // 36.1-43.8; Q6_K 27.0-27.7 / 27.0-27.4 against the tile GEMM's 30.0-30.1
+    // / 32.4-33.2; from 40-48 rows it is slower); THQ_GEMM_MID=1 keeps the
+    // 4-bit formats' rows on the streaming GEMM
     const char* mde0 = getenv("THQ_GEMM_MID");
     const bool mid_forced = mde0 && !strcmp(mde0, "1");
     const bool wide_ok = wp.splits > 0 && (w->qtype == THQ_Q8_0 || (c.flags & THQ_MODE_EXACT_W) || nout >= 65536 ||
-                                           (q4 && m <= 32 && !mid_forced));
+                                           (((q4 && !mid_forced) || q6) && m <= 32));
     // Q8_0 at M = 1 from 12288 outputs: the MFMA GEMV on the tile layout beats
     // the VALU kernel (bf16 x; 12288 / 24576 x 4096: 13.7 / 21.9 vs 14.0 /
     // 23.1 us; LM head 151936 x 4096: 111 vs 125 us); below, the VALU kernel
