@@ -782,9 +782,59 @@ __global__ __launch_bounds__(256) void k_split_reduce(const float* __restrict__ 
     store_y<YT>(y + m * nout + o, GU ? silu_mul(g, u) : g);
 }
 
+// The same sums, four outputs per thread with 16-B loads (nout, ldp and
+// up_off multiples of 4, P and y 16-B aligned), the loads of four splits
+// issued before their adds: each element is still summed in split order
+// from 0, so the bits equal k_split_reduce's.
+template <bool GU, typename YT>
+__global__ __launch_bounds__(256) void k_split_reduce4(const float* __restrict__ P, YT* __restrict__ y, int M,
+                                                      int64_t nout, int64_t up_off, int64_t ldp, int splits) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t q = nout >> 2;
+    if (t >= (int64_t)M * q) return;
+    const int64_t m = t / q, o = (t - m * q) * 4;
+    const float* base = P + m * ldp + o;
+    const int64_t ss = (int64_t)M * ldp;  // split stride
+    f32x4_t g = {0.0f, 0.0f, 0.0f, 0.0f}, u = {0.0f, 0.0f, 0.0f, 0.0f};
+    int sp = 0;
+    for (; sp + 4 <= splits; sp += 4) {
+        f32x4_t a[4], b[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            a[j] = *reinterpret_cast<const f32x4_t*>(base + (int64_t)(sp + j) * ss);
+            if (GU) b[j] = *reinterpret_cast<const f32x4_t*>(base + (int64_t)(sp + j) * ss + up_off);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            g += a[j];
+            if (GU) u += b[j];
+        }
+    }
+    for (; sp < splits; ++sp) {
+        g += *reinterpret_cast<const f32x4_t*>(base + (int64_t)sp * ss);
+        if (GU) u += *reinterpret_cast<const f32x4_t*>(base + (int64_t)sp * ss + up_off);
+    }
+    YT* yo = y + m * nout + o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_y<YT>(yo + i, GU ? silu_mul(g[i], u[i]) : g[i]);
+}
+
 hipError_t launch_split_reduce(const float* P, void* y, bool yf32, bool gu, int M, int64_t nout, int64_t up_off,
                                int64_t ldp, int splits, hipStream_t s) {
     const int64_t total = (int64_t)M * nout;
+    const bool vec = nout % 4 == 0 && ldp % 4 == 0 && up_off % 4 == 0 && (uintptr_t)P % 16 == 0 &&
+                     (uintptr_t)y % 16 == 0;
+    if (vec) {
+        const dim3 grid4((unsigned)((total / 4 + 255) / 256));
+        if (gu) {
+            if (yf32) hipLaunchKernelGGL((k_split_reduce4<true, float>), grid4, dim3(256), 0, s, P, (float*)y, M, nout, up_off, ldp, splits);
+            else hipLaunchKernelGGL((k_split_reduce4<true, bf16_t>), grid4, dim3(256), 0, s, P, (bf16_t*)y, M, nout, up_off, ldp, splits);
+        } else {
+            if (yf32) hipLaunchKernelGGL((k_split_reduce4<false, float>), grid4, dim3(256), 0, s, P, (float*)y, M, nout, up_off, ldp, splits);
+            else hipLaunchKernelGGL((k_split_reduce4<false, bf16_t>), grid4, dim3(256), 0, s, P, (bf16_t*)y, M, nout, up_off, ldp, splits);
+        }
+        return hipGetLastError();
+    }
     const dim3 grid((unsigned)((total + 255) / 256));
     if (gu) {
         if (yf32) hipLaunchKernelGGL((k_split_reduce<true, float>), grid, dim3(256), 0, s, P, (float*)y, M, nout, up_off, ldp, splits);
@@ -900,10 +950,10 @@ static hipError_t gemm_t(const GemmPlan& p, const WeightView& w, const bf16_t* x
         hipLaunchKernelGGL((k_gemm_dma<QT, BM, WM, GU, float, true>), dim3(nb), dim3(128 * WM), 0, s, w.q, w.aux, x,
                            (void*)ws, M, (int)w.K, nout, up_off, (int64_t)w.N, p.kps, (int)p.tiles_n,
                            (int)p.tiles_m);
-        const int64_t total = (int64_t)M * nout;
-        hipLaunchKernelGGL((k_split_reduce<GU, YT>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ws,
-                           static_cast<YT*>(y), M, nout, up_off, (int64_t)w.N, p.splits);
-        return hipGetLastError();
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_split_reduce(ws, y, std::is_same<YT, float>::value, GU, M, nout, up_off, (int64_t)w.N,
+                                   p.splits, s);
     }
     if constexpr (QT == 14) {
         return hipErrorInvalidValue;
@@ -916,10 +966,10 @@ static hipError_t gemm_t(const GemmPlan& p, const WeightView& w, const bf16_t* x
         // partials in natural weight-row order: ld = N rows
         hipLaunchKernelGGL((k_gemm<QT, EXACT, BM, GU, float, true>), grid, dim3(256), 0, s, w.q, w.aux, x, (void*)ws,
                            M, (int)w.K, nout, up_off, (int64_t)w.N, p.kps);
-        const int64_t total = (int64_t)M * nout;
-        hipLaunchKernelGGL((k_split_reduce<GU, YT>), dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, ws,
-                           static_cast<YT*>(y), M, nout, up_off, (int64_t)w.N, p.splits);
-        return hipGetLastError();
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        return launch_split_reduce(ws, y, std::is_same<YT, float>::value, GU, M, nout, up_off, (int64_t)w.N,
+                                   p.splits, s);
     }
 }
 
