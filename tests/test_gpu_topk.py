@@ -31,6 +31,18 @@ def _gpu():
     torch.cuda.synchronize()
 
 
+@pytest.fixture(params=["one launch", "two launches"])
+def path(request, monkeypatch):
+    """Rows of up to 4096 / k segments take one launch whose last block per
+    row merges the segments' candidates (arrival counters); THQ_TILE_TICKET=0
+    gives the counter-free form, a second launch per merge level."""
+    if request.param == "two launches":
+        monkeypatch.setenv("THQ_TILE_TICKET", "0")
+    else:
+        monkeypatch.delenv("THQ_TILE_TICKET", raising=False)
+    return request.param
+
+
 def check(v: np.ndarray, k: int, tag: str):
     vals, idx = thq.topk(torch.from_numpy(np.ascontiguousarray(v, np.float32)).cuda(), k)
     torch.cuda.synchronize()
@@ -50,13 +62,13 @@ def ref_rows():
 
 @pytest.mark.parametrize("n", [5000, 151936])
 @pytest.mark.parametrize("k", [1, 20, 32, 64])
-def test_topk_reference_generator(ref_rows, n, k):
-    print(f"topk lm_row n={n} k={k}", flush=True)
+def test_topk_reference_generator(ref_rows, n, k, path):
+    print(f"topk lm_row n={n} k={k} {path}", flush=True)
     check(ref_rows[n], k, f"lm_row n={n} k={k}")
 
 
 @pytest.mark.parametrize("n", [1, 100, 4095, 4096, 4097, 20011, 300000])
-def test_topk_ties_across_segments(n):
+def test_topk_ties_across_segments(n, path):
     """Small-integer rows: the k-th value has copies in many 4096-wide
     segments, so the lowest ids among them must win across the merge."""
     rng = np.random.default_rng(n)
@@ -64,12 +76,12 @@ def test_topk_ties_across_segments(n):
     v[1] = 1.0                       # every element tied: ids 0..k-1
     v[2, rng.integers(0, n, 5)] = np.nan
     for k in (1, 7, 64):
-        print(f"topk ties n={n} k={k}", flush=True)
+        print(f"topk ties n={n} k={k} {path}", flush=True)
         check(v, k, f"ties n={n} k={k}")
 
 
 @pytest.mark.parametrize("n", [3000, 9000])
-def test_topk_every_k(n):
+def test_topk_every_k(n, path):
     """Every k from 1 to 64 on normal and bf16-rounded rows: the fast path's
     candidate count (keys at or above the threshold) then takes many values,
     including every remainder of its 8-wide batches."""
@@ -80,9 +92,9 @@ def test_topk_every_k(n):
         check(v, k, f"every k n={n} k={k}")
 
 
-def test_topk_special_rows():
+def test_topk_special_rows(path):
     n = 9000
-    v = np.zeros((5, n), np.float32)
+    v = np.zeros((8, n), np.float32)
     v[0] = np.nan                    # all NaN: keys -inf, ids 0..k-1
     v[1] = -np.inf
     v[2, ::2] = -0.0                 # -0.0 ties with +0.0
@@ -90,6 +102,13 @@ def test_topk_special_rows():
     v[3, 17] = np.inf
     v[4] = np.nan
     v[4, 8999] = -5.0                # the only real value ranks first
+    rng = np.random.default_rng(9)
+    # subnormals of both signs around +-0 (the filter compares floats)
+    v[5] = (rng.integers(-2000, 2000, n) * np.float32(1e-42)).astype(np.float32)
+    v[6] = -np.abs(rng.normal(0, 1, n)).astype(np.float32) - 1.0  # negatives only
+    v[7] = rng.normal(0, 1, n).astype(np.float32)
+    v[7, rng.integers(0, n, 200)] = np.nan  # NaNs in most lanes of a segment
+    v[7, 4096:4096 + 4096:2] = np.nan
     check(v, 64, "special")
 
 
@@ -101,11 +120,22 @@ def test_topk_k_beyond_row():
     check(v, 8, "k > n")
 
 
-def test_topk_many_rows():
+def test_topk_many_rows(path):
     """More rows than one launch's grid dimension holds (65535)."""
     rng = np.random.default_rng(3)
     v = rng.integers(-4, 5, (70000, 8)).astype(np.float32)
     check(v, 4, "70000 rows")
+
+
+def test_topk_rows_beyond_one_launch(path):
+    """More rows than the one-launch form takes per launch (2048), each row
+    several segments long, with ties: every launch's counters and pool."""
+    rng = np.random.default_rng(4)
+    v = rng.integers(-40, 41, (2100, 5000)).astype(np.float32)
+    v[::7] = rng.normal(0, 2, (300, 5000)).astype(np.float32)
+    for k in (8, 64):
+        print(f"topk 2100 rows k={k} {path}", flush=True)
+        check(v, k, f"2100 rows k={k}")
 
 
 def test_topk_rejects_bad_k():

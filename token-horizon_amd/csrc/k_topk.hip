@@ -47,6 +47,11 @@ constexpr int TK_EPT = 16;
 constexpr int TK_SEG = TK_THREADS * TK_EPT;
 constexpr uint32_t TK_ABSENT = 0u;
 constexpr int TK_CAP = 256;  // candidates the fast path ranks
+// the one-launch form's arrival counters sit 128 B apart (row m: cnt[32 m]):
+// device-scope atomics on one line serialize (40 rows of 38 blocks on
+// adjacent counters: 7.6 us more), and launches take at most TK_ROWS1 rows
+constexpr int TK_CNT_STRIDE = 32;
+constexpr int TK_ROWS1 = 2048;
 
 __device__ __forceinline__ uint32_t topk_key(float v) {
     uint32_t b = __float_as_uint(v);
@@ -79,85 +84,96 @@ __device__ __forceinline__ int block_scan(int v, int* lds, int& total) {
     return base + x - v;
 }
 
-// Grid: (segments, rows).  Level 0 reads logits rows [m][n] (ids = column);
-// later levels read candidate rows ckey / cid [m][ccount] (kept in id order).
-// Non-final: the segment's k selected (key, id) go to okey / oid at
-// m * ostride + seg * k, in id order, padded with absent entries.  FINAL (a
-// single segment): vals / idx [m][k] in rank order, unused slots -inf /
-// 0xFFFFFFFF.
-template <bool FROM_LOGITS, bool FINAL>
-__global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restrict__ logits, int64_t n,
-                                                           const uint32_t* __restrict__ ckey,
-                                                           const uint32_t* __restrict__ cid, int64_t ccount, int k,
-                                                           uint32_t* __restrict__ okey, uint32_t* __restrict__ oid,
-                                                           int64_t ostride, float* __restrict__ vals,
-                                                           uint32_t* __restrict__ idx) {
-    // level 0 stages the segment's logits here (transposed to thread order);
-    // after the keys are in registers the same bytes hold the fast path's
-    // candidates or the fallback's histograms
-    __shared__ uint32_t stage[TK_SEG];
-    uint32_t* const hist = stage;
-    __shared__ int scan_lds[TK_THREADS / 64];
-    __shared__ uint32_t sh_prefix;
-    __shared__ int sh_kk;
-    __shared__ uint32_t fkey[64], fid[64];
-    __shared__ uint32_t wthr[TK_THREADS / 64];
+// One block's LDS.
+struct TkLds {
+    uint32_t buf[TK_SEG];  // staged logits, then candidates (key, id) or radix histograms
+    int scan[TK_THREADS / 64];
+    uint32_t prefix;
+    int kk;
+    uint32_t fkey[64], fid[64];
+    uint32_t wthr[TK_THREADS / 64];
+    uint32_t thr;
+    int last;
+};
 
+// Ranks the nc <= TK_CAP candidates (key, id) in cand (LDS, TK_CAP + 64
+// entries) by (key desc, id asc) and emits the first k.  FINAL: vr / xr [k]
+// in rank order, unused slots -inf / 0xFFFFFFFF.  Else: ok / oi [k] in id
+// order, padded with absent entries, as device-scope stores (a block of the
+// same launch may read them).  Every thread of the block calls it.
+template <bool FINAL>
+__device__ void tk_emit(uint2* cand, int nc, int k, float* vr, uint32_t* xr, uint32_t* ok, uint32_t* oi) {
     const int tid = threadIdx.x;
-    const int64_t m = blockIdx.y;
-    const int64_t seg = blockIdx.x;
-    const int64_t count = FROM_LOGITS ? n : ccount;
-    const int64_t base = seg * TK_SEG;
-
-    // level 0 recomputes each element's id from its position (thread t
-    // holds base + 16t .. +15) rather than holding them: 16 fewer registers
-    // per thread, so every block of a 151936-wide, 40-row level fits the GPU
-    // at once
-    uint32_t key[TK_EPT], idv[FROM_LOGITS ? 1 : TK_EPT];
-    auto id = [&](int e) { return FROM_LOGITS ? (uint32_t)(base + tid * TK_EPT + e) : idv[e]; };
-    if constexpr (FROM_LOGITS) {
-        // coalesced loads (position base + e*256 + tid), then thread t takes
-        // positions base + 16t .. +15 out of LDS
-        const float* row = logits + m * n;
-        if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && base + TK_SEG <= n) {
-            // a whole segment of a 16-B aligned row: 16-B loads
-#pragma unroll
-            for (int e = 0; e < TK_EPT / 4; ++e) {
-                const int o = 4 * (e * TK_THREADS + tid);
-                const float4 v = *reinterpret_cast<const float4*>(row + base + o);
-                stage[o] = topk_key(v.x);
-                stage[o + 1] = topk_key(v.y);
-                stage[o + 2] = topk_key(v.z);
-                stage[o + 3] = topk_key(v.w);
-            }
-        } else {
-#pragma unroll
-            for (int e = 0; e < TK_EPT; ++e) {
-                const int64_t pos = base + e * TK_THREADS + tid;
-                stage[e * TK_THREADS + tid] = pos < n ? topk_key(row[pos]) : TK_ABSENT;
-            }
+    uint2* sel = cand + TK_CAP;  // [64] selected, by rank
+    // pad to a multiple of 8 with entries that beat nothing
+    if (tid < ((nc + 7) & ~7) - nc) cand[nc + tid] = make_uint2(0u, 0xFFFFFFFFu);
+    __syncthreads();
+    // rank = number of candidates ahead in (key desc, id asc); 8 per LDS
+    // round trip (4 x 16-B broadcast reads)
+    auto ahead = [](uint2 a, uint2 me) { return (int)(a.x > me.x || (a.x == me.x && a.y < me.y)); };
+    int rank = k;  // k: not selected
+    uint2 me = make_uint2(0u, 0u);
+    if (tid < nc) {
+        me = cand[tid];
+        const uint4* c4 = reinterpret_cast<const uint4*>(cand);
+        int r0 = 0, r1 = 0;
+        auto batch = [&](int j) {
+            const uint4 q0 = c4[j / 2], q1 = c4[j / 2 + 1], q2 = c4[j / 2 + 2], q3 = c4[j / 2 + 3];
+            r0 += ahead(make_uint2(q0.x, q0.y), me) + ahead(make_uint2(q0.z, q0.w), me) +
+                  ahead(make_uint2(q1.x, q1.y), me) + ahead(make_uint2(q1.z, q1.w), me);
+            r1 += ahead(make_uint2(q2.x, q2.y), me) + ahead(make_uint2(q2.z, q2.w), me) +
+                  ahead(make_uint2(q3.x, q3.y), me) + ahead(make_uint2(q3.z, q3.w), me);
+        };
+        int j = 0;
+        for (; j + 16 <= nc; j += 16) {  // two batches' reads in flight together
+            batch(j);
+            batch(j + 8);
         }
-        __syncthreads();
-#pragma unroll
-        for (int e = 0; e < TK_EPT; ++e) {
-            key[e] = stage[tid * TK_EPT + e];
+        for (; j < nc; j += 8) batch(j);  // the rest (up to 15, in batches of 8)
+        rank = r0 + r1;
+    }
+    const int nsel = nc < k ? nc : k;
+    if constexpr (FINAL) {
+        if (rank < k) {
+            vr[rank] = topk_value(me.x);
+            xr[rank] = me.y;
+        }
+        if (tid >= nsel && tid < k) {
+            vr[tid] = -INFINITY;
+            xr[tid] = 0xFFFFFFFFu;
         }
     } else {
-        // the segment's candidates spread over every thread (epv each, in
-        // position order, so thread order stays id order)
-        const uint32_t* kr = ckey + m * ccount;
-        const uint32_t* ir = cid + m * ccount;
-        const int64_t here = count - base < TK_SEG ? count - base : TK_SEG;
-        const int epv = (int)((here + TK_THREADS - 1) / TK_THREADS);
-#pragma unroll
-        for (int e = 0; e < TK_EPT; ++e) {
-            const int64_t pos = base + (int64_t)tid * epv + e;
-            const bool ok = e < epv && pos < count;
-            key[e] = ok ? kr[pos] : TK_ABSENT;
-            idv[e] = ok ? ir[pos] : 0xFFFFFFFFu;
+        // id-order position among the selected: count smaller ids among them
+        if (rank < k) sel[rank] = me;
+        __syncthreads();
+        if (tid < nsel) {
+            const uint2 mine = sel[tid];
+            const uint4* s4 = reinterpret_cast<const uint4*>(sel);
+            int opos = 0, j = 0;
+            for (; j + 8 <= nsel; j += 8) {
+                const uint4 q0 = s4[j / 2], q1 = s4[j / 2 + 1], q2 = s4[j / 2 + 2], q3 = s4[j / 2 + 3];
+                opos += (q0.y < mine.y) + (q0.w < mine.y) + (q1.y < mine.y) + (q1.w < mine.y) + (q2.y < mine.y) +
+                        (q2.w < mine.y) + (q3.y < mine.y) + (q3.w < mine.y);
+            }
+            for (; j < nsel; ++j) opos += sel[j].y < mine.y;
+            __hip_atomic_store(ok + opos, mine.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(oi + opos, mine.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        if (tid >= nsel && tid < k) {
+            __hip_atomic_store(ok + tid, TK_ABSENT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(oi + tid, 0xFFFFFFFFu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
+}
 
+// The top k of one segment held as key[TK_EPT] per thread, thread order =
+// id order (element e of thread t: id(e)); emits as tk_emit.  Every thread
+// of the block calls it; L.buf may hold staged logits that the threads have
+// already read into key.
+template <bool FINAL, typename IdF>
+__device__ void tk_select(const uint32_t (&key)[TK_EPT], IdF id, int k, TkLds& L, float* vr, uint32_t* xr,
+                          uint32_t* ok, uint32_t* oi) {
+    const int tid = threadIdx.x;
     // ---- fast path: threshold from the waves' lane maxima
     {
         uint32_t v0 = 0u, v1 = 0u, v2 = 0u, v3 = 0u;  // the lane's 4 largest keys, v0 >= v1 >= v2 >= v3
@@ -178,97 +194,35 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
                             __popcll(__ballot(v2 >= c)) + __popcll(__ballot(v3 >= c));
             if (cnt >= k) tw = c;
         }
-        if ((tid & 63) == 0) wthr[tid >> 6] = tw;
+        if ((tid & 63) == 0) L.wthr[tid >> 6] = tw;
         __syncthreads();
-        uint32_t T = wthr[0];
+        uint32_t T = L.wthr[0];
 #pragma unroll
-        for (int w = 1; w < TK_THREADS / 64; ++w) T = wthr[w] > T ? wthr[w] : T;
+        for (int w = 1; w < TK_THREADS / 64; ++w) T = L.wthr[w] > T ? L.wthr[w] : T;
         if (T == TK_ABSENT) T = 1u;  // present keys only
         int c = 0;
 #pragma unroll
         for (int e = 0; e < TK_EPT; ++e) c += key[e] >= T;
         int nc;
-        int pos = block_scan(c, scan_lds, nc);
+        int pos = block_scan(c, L.scan, nc);
         if (nc <= TK_CAP) {
-            uint2* cand = reinterpret_cast<uint2*>(hist);             // [TK_CAP] (key, id)
-            uint2* sel = cand + TK_CAP;                               // [64] selected, by rank
+            uint2* cand = reinterpret_cast<uint2*>(L.buf);
             __syncthreads();  // every thread is past its reads of the staged logits
 #pragma unroll
             for (int e = 0; e < TK_EPT; ++e)
                 if (key[e] >= T) cand[pos++] = make_uint2(key[e], id(e));
-            // pad to a multiple of 8 with entries that beat nothing
-            if (tid < ((nc + 7) & ~7) - nc) cand[nc + tid] = make_uint2(0u, 0xFFFFFFFFu);
-            __syncthreads();
-            // rank = number of candidates ahead in (key desc, id asc); 8 per
-            // LDS round trip (4 x 16-B broadcast reads)
-            auto ahead = [](uint2 a, uint2 me) { return (int)(a.x > me.x || (a.x == me.x && a.y < me.y)); };
-            int rank = k;  // k: not selected
-            uint2 me = make_uint2(0u, 0u);
-            if (tid < nc) {
-                me = cand[tid];
-                const uint4* c4 = reinterpret_cast<const uint4*>(cand);
-                int r0 = 0, r1 = 0;
-                auto batch = [&](int j) {
-                    const uint4 q0 = c4[j / 2], q1 = c4[j / 2 + 1], q2 = c4[j / 2 + 2], q3 = c4[j / 2 + 3];
-                    r0 += ahead(make_uint2(q0.x, q0.y), me) + ahead(make_uint2(q0.z, q0.w), me) +
-                          ahead(make_uint2(q1.x, q1.y), me) + ahead(make_uint2(q1.z, q1.w), me);
-                    r1 += ahead(make_uint2(q2.x, q2.y), me) + ahead(make_uint2(q2.z, q2.w), me) +
-                          ahead(make_uint2(q3.x, q3.y), me) + ahead(make_uint2(q3.z, q3.w), me);
-                };
-                int j = 0;
-                for (; j + 16 <= nc; j += 16) {  // two batches' reads in flight together
-                    batch(j);
-                    batch(j + 8);
-                }
-                for (; j < nc; j += 8) batch(j);  // the rest (up to 15, in batches of 8)
-                rank = r0 + r1;
-            }
-            const int nsel = nc < k ? nc : k;
-            if constexpr (FINAL) {
-                float* vr = vals + m * k;
-                uint32_t* xr = idx + m * k;
-                if (rank < k) {
-                    vr[rank] = topk_value(me.x);
-                    xr[rank] = me.y;
-                }
-                if (tid >= nsel && tid < k) {
-                    vr[tid] = -INFINITY;
-                    xr[tid] = 0xFFFFFFFFu;
-                }
-            } else {
-                // id-order position among the selected: count smaller ids among them
-                if (rank < k) sel[rank] = me;
-                __syncthreads();
-                uint32_t* ok = okey + m * ostride + seg * k;
-                uint32_t* oi = oid + m * ostride + seg * k;
-                if (tid < nsel) {
-                    const uint2 mine = sel[tid];
-                    const uint4* s4 = reinterpret_cast<const uint4*>(sel);
-                    int opos = 0, j = 0;
-                    for (; j + 8 <= nsel; j += 8) {
-                        const uint4 q0 = s4[j / 2], q1 = s4[j / 2 + 1], q2 = s4[j / 2 + 2], q3 = s4[j / 2 + 3];
-                        opos += (q0.y < mine.y) + (q0.w < mine.y) + (q1.y < mine.y) + (q1.w < mine.y) +
-                                (q2.y < mine.y) + (q2.w < mine.y) + (q3.y < mine.y) + (q3.w < mine.y);
-                    }
-                    for (; j < nsel; ++j) opos += sel[j].y < mine.y;
-                    ok[opos] = mine.x;
-                    oi[opos] = mine.y;
-                }
-                if (tid >= nsel && tid < k) {
-                    ok[tid] = TK_ABSENT;
-                    oi[tid] = 0xFFFFFFFFu;
-                }
-            }
+            tk_emit<FINAL>(cand, nc, k, vr, xr, ok, oi);
             return;
         }
     }
 
     // ---- fallback: exact radix select over the whole segment
+    uint32_t* const hist = L.buf;
     int present = 0;
 #pragma unroll
     for (int e = 0; e < TK_EPT; ++e) present += key[e] != TK_ABSENT;
     int P;
-    (void)block_scan(present, scan_lds, P);
+    (void)block_scan(present, L.scan, P);
 
     // radix select: tau = the k-th largest present key, need = how many of
     // the keys equal to tau belong to the top k
@@ -294,22 +248,22 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
             int cnt = 0;
             for (int j = 0; j < per; ++j) cnt += (int)hist[nb - 1 - per * tid - j];
             int tot;
-            int ex = block_scan(cnt, scan_lds, tot);
+            int ex = block_scan(cnt, L.scan, tot);
             if (ex < kk && kk <= ex + cnt) {
                 for (int j = 0; j < per; ++j) {
                     const int b = nb - 1 - per * tid - j;
                     const int c = (int)hist[b];
                     if (ex + c >= kk) {
-                        sh_prefix = prefix | ((uint32_t)b << shift);
-                        sh_kk = kk - ex;
+                        L.prefix = prefix | ((uint32_t)b << shift);
+                        L.kk = kk - ex;
                         break;
                     }
                     ex += c;
                 }
             }
             __syncthreads();
-            prefix = sh_prefix;
-            kk = sh_kk;
+            prefix = L.prefix;
+            kk = L.kk;
             pmask |= (uint32_t)(nb - 1) << shift;
         }
         tau = prefix;
@@ -324,7 +278,7 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
         for (int e = 0; e < TK_EPT; ++e) eq += key[e] == tau;
     }
     int eq_total;
-    int eq_rank = block_scan(eq, scan_lds, eq_total);
+    int eq_rank = block_scan(eq, L.scan, eq_total);
     bool sel[TK_EPT];
     int nsel = 0;
 #pragma unroll
@@ -339,38 +293,34 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
         nsel += sel[e];
     }
     int total;
-    int pos = block_scan(nsel, scan_lds, total);  // total == min(P, k)
+    int pos = block_scan(nsel, L.scan, total);  // total == min(P, k)
 
     if constexpr (!FINAL) {
-        uint32_t* ok = okey + m * ostride + seg * k;
-        uint32_t* oi = oid + m * ostride + seg * k;
 #pragma unroll
         for (int e = 0; e < TK_EPT; ++e)
             if (sel[e]) {
-                ok[pos] = key[e];
-                oi[pos] = id(e);
+                __hip_atomic_store(ok + pos, key[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(oi + pos, id(e), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 ++pos;
             }
         if (tid >= total && tid < k) {
-            ok[tid] = TK_ABSENT;
-            oi[tid] = 0xFFFFFFFFu;
+            __hip_atomic_store(ok + tid, TK_ABSENT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(oi + tid, 0xFFFFFFFFu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     } else {
 #pragma unroll
         for (int e = 0; e < TK_EPT; ++e)
             if (sel[e]) {
-                fkey[pos] = key[e];
-                fid[pos] = id(e);
+                L.fkey[pos] = key[e];
+                L.fid[pos] = id(e);
                 ++pos;
             }
         __syncthreads();
         if (tid < k) {
-            float* vr = vals + m * k;
-            uint32_t* xr = idx + m * k;
             if (tid < total) {
-                const uint32_t kt = fkey[tid], it = fid[tid];
+                const uint32_t kt = L.fkey[tid], it = L.fid[tid];
                 int rank = 0;
-                for (int j = 0; j < total; ++j) rank += fkey[j] > kt || (fkey[j] == kt && fid[j] < it);
+                for (int j = 0; j < total; ++j) rank += L.fkey[j] > kt || (L.fkey[j] == kt && L.fid[j] < it);
                 vr[rank] = topk_value(kt);
                 xr[rank] = it;
             } else {
@@ -379,6 +329,237 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
             }
         }
     }
+}
+
+// The candidates of row m (count of them, in id order) spread over the
+// block's threads, epv each in position order, so thread order stays id
+// order.  Device-scope loads: other blocks of the same launch may have
+// written them.
+__device__ __forceinline__ void tk_load_candidates(const uint32_t* kr, const uint32_t* ir, int64_t base,
+                                                   int64_t count, uint32_t (&key)[TK_EPT], uint32_t (&idv)[TK_EPT]) {
+    const int tid = threadIdx.x;
+    const int64_t here = count - base < TK_SEG ? count - base : TK_SEG;
+    const int epv = (int)((here + TK_THREADS - 1) / TK_THREADS);
+#pragma unroll
+    for (int e = 0; e < TK_EPT; ++e) {
+        const int64_t pos = base + (int64_t)tid * epv + e;
+        const bool ok = e < epv && pos < count;
+        key[e] = ok ? __hip_atomic_load(kr + pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : TK_ABSENT;
+        idv[e] = ok ? __hip_atomic_load(ir + pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0xFFFFFFFFu;
+    }
+}
+
+// Grid: (segments, rows).  Level 0 reads logits rows [m][n] (ids = column);
+// later levels read candidate rows ckey / cid [m][ccount] (kept in id order).
+// Non-final: the segment's k selected (key, id) go to okey / oid at
+// m * ostride + seg * k, in id order, padded with absent entries.  FINAL (a
+// single segment): vals / idx [m][k] in rank order, unused slots -inf /
+// 0xFFFFFFFF.
+template <bool FROM_LOGITS, bool FINAL>
+__global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restrict__ logits, int64_t n,
+                                                           const uint32_t* __restrict__ ckey,
+                                                           const uint32_t* __restrict__ cid, int64_t ccount, int k,
+                                                           uint32_t* __restrict__ okey, uint32_t* __restrict__ oid,
+                                                           int64_t ostride, float* __restrict__ vals,
+                                                           uint32_t* __restrict__ idx) {
+    __shared__ TkLds L;
+    const int tid = threadIdx.x;
+    const int64_t m = blockIdx.y;
+    const int64_t seg = blockIdx.x;
+    const int64_t base = seg * TK_SEG;
+    float* const vr = FINAL ? vals + m * k : nullptr;
+    uint32_t* const xr = FINAL ? idx + m * k : nullptr;
+    uint32_t* const ok = FINAL ? nullptr : okey + m * ostride + seg * k;
+    uint32_t* const oi = FINAL ? nullptr : oid + m * ostride + seg * k;
+
+    uint32_t key[TK_EPT];
+    if constexpr (FROM_LOGITS) {
+        // level 0 recomputes each element's id from its position (thread t
+        // holds base + 16t .. +15) rather than holding them: 16 fewer
+        // registers per thread.  Coalesced loads (position base + e*256 +
+        // tid), then thread t takes positions base + 16t .. +15 out of LDS.
+        const float* row = logits + m * n;
+        if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && base + TK_SEG <= n) {
+            // a whole segment of a 16-B aligned row: 16-B loads
+#pragma unroll
+            for (int e = 0; e < TK_EPT / 4; ++e) {
+                const int o = 4 * (e * TK_THREADS + tid);
+                const float4 v = *reinterpret_cast<const float4*>(row + base + o);
+                L.buf[o] = topk_key(v.x);
+                L.buf[o + 1] = topk_key(v.y);
+                L.buf[o + 2] = topk_key(v.z);
+                L.buf[o + 3] = topk_key(v.w);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < TK_EPT; ++e) {
+                const int64_t pos = base + e * TK_THREADS + tid;
+                L.buf[e * TK_THREADS + tid] = pos < n ? topk_key(row[pos]) : TK_ABSENT;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < TK_EPT; ++e) key[e] = L.buf[tid * TK_EPT + e];
+        tk_select<FINAL>(key, [&](int e) { return (uint32_t)(base + tid * TK_EPT + e); }, k, L, vr, xr, ok, oi);
+    } else {
+        uint32_t idv[TK_EPT];
+        tk_load_candidates(ckey + m * ccount, cid + m * ccount, base, ccount, key, idv);
+        tk_select<FINAL>(key, [&](int e) { return idv[e]; }, k, L, vr, xr, ok, oi);
+    }
+}
+
+// The block's 256 lane maxima (keys, one per thread) -> the k-th largest,
+// rounded down to 16 key bits, found by one wave with ballots: at least k of
+// the lane maxima are >= the result.  L.buf[0..255] holds the lane keys on
+// return; every thread of the block calls it.
+__device__ __forceinline__ uint32_t tk_lane_threshold(uint32_t lane_key, int k, TkLds& L) {
+    const int tid = threadIdx.x;
+    L.buf[tid] = lane_key;
+    __syncthreads();
+    if (tid < 64) {
+        const uint32_t a0 = L.buf[tid], a1 = L.buf[tid + 64], a2 = L.buf[tid + 128], a3 = L.buf[tid + 192];
+        uint32_t t = 0u;
+        for (int b = 31; b >= 16; --b) {
+            const uint32_t c = t | (1u << b);
+            const int nge = __popcll(__ballot(a0 >= c)) + __popcll(__ballot(a1 >= c)) + __popcll(__ballot(a2 >= c)) +
+                            __popcll(__ballot(a3 >= c));
+            if (nge >= k) t = c;
+        }
+        if (tid == 0) L.thr = t;
+    }
+    __syncthreads();
+    return L.thr;
+}
+
+// The exact top k of a row's pool (count <= TK_SEG entries, id order) into
+// vr / xr [k], rank order.  The filter of level 0 on keys: T = the k-th
+// largest lane maximum (16 key bits), the candidates are the keys >= T;
+// real keys are at least the -inf key (0x007fffff), so T > 0 means at least
+// k real entries pass.  Otherwise, or past TK_CAP candidates, tk_select.
+__device__ void tk_merge(const uint32_t* kr, const uint32_t* ir, int64_t count, int k, TkLds& L, float* vr,
+                         uint32_t* xr) {
+    const int tid = threadIdx.x;
+    uint32_t key[TK_EPT], idv[TK_EPT];
+    tk_load_candidates(kr, ir, 0, count, key, idv);
+    uint32_t lm = key[0];
+#pragma unroll
+    for (int e = 1; e < TK_EPT; ++e) lm = key[e] > lm ? key[e] : lm;
+    const uint32_t t = tk_lane_threshold(lm, k, L);
+    int c = 0;
+#pragma unroll
+    for (int e = 0; e < TK_EPT; ++e) c += key[e] >= t;
+    int nc;
+    int pos = block_scan(c, L.scan, nc);  // its barriers order wave 0's reads of the lane keys first
+    if (t != 0u && nc <= TK_CAP) {
+        uint2* cand = reinterpret_cast<uint2*>(L.buf);
+#pragma unroll
+        for (int e = 0; e < TK_EPT; ++e)
+            if (key[e] >= t) cand[pos++] = make_uint2(key[e], idv[e]);
+        tk_emit<true>(cand, nc, k, vr, xr, nullptr, nullptr);
+    } else {
+        tk_select<true>(key, [&](int e) { return idv[e]; }, k, L, vr, xr, nullptr, nullptr);
+    }
+}
+
+// Rows whose segments' candidates fit one block (segments * k <= TK_SEG) in
+// one launch.  Grid (segments >= 2, rows).  Each block selects its
+// segment's top k into the pool (okey / oid [m][segments * k], in id order,
+// device-scope stores) and draws a ticket on the row's arrival counter
+// cnt[TK_CNT_STRIDE m] (zero before the launch); the block that draws the
+// last ticket selects the row's top k from the pool (tk_merge) into vals /
+// idx and zeroes the counter.
+//
+// A segment's selection first tries a filter: thread t holds the elements
+// at offsets 1024 j + 4t + c (j, c < 4: four 16-B loads, no staging), the
+// block's threshold T is the k-th largest of its 256 lane maxima, rounded
+// down to 16 key bits (one wave, by ballots), and the candidates are the
+// elements >= T in float order.  T is a lane maximum, so at least k elements
+// pass and the segment's top k are among them; ranking those (at most
+// TK_CAP) exactly gives the segment's top k.  Where no such T exists (fewer
+// than k lanes hold a value above -inf) or more than TK_CAP elements pass
+// (long runs of equal logits), the segment takes tk_select over its keys in
+// id order instead (its own fast path, else the radix select).
+// (80 VGPRs: six blocks per CU, so 40 rows of 38 segments run in one round)
+__global__ __launch_bounds__(TK_THREADS, 6) void k_topk_rows(const float* __restrict__ logits, int64_t n, int k,
+                                                         uint32_t* __restrict__ pkey, uint32_t* __restrict__ pid,
+                                                         uint32_t* __restrict__ cnt, float* __restrict__ vals,
+                                                         uint32_t* __restrict__ idx) {
+    __shared__ TkLds L;
+    const int tid = threadIdx.x;
+    const int64_t m = blockIdx.y, seg = blockIdx.x, segs = gridDim.x;
+    const int64_t base = seg * TK_SEG;
+    const int64_t pstride = segs * k;
+    const float* row = logits + m * n;
+    uint32_t* const ok = pkey + m * pstride + seg * k;
+    uint32_t* const oi = pid + m * pstride + seg * k;
+
+    float xv[TK_EPT];  // element 4j + c: offset 1024 j + 4 tid + c
+    if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && base + TK_SEG <= n) {
+#pragma unroll
+        for (int j = 0; j < TK_EPT / 4; ++j) {
+            const float4 v = *reinterpret_cast<const float4*>(row + base + j * 4 * TK_THREADS + 4 * tid);
+            xv[4 * j] = v.x;
+            xv[4 * j + 1] = v.y;
+            xv[4 * j + 2] = v.z;
+            xv[4 * j + 3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < TK_EPT; ++e) {
+            const int64_t pos = base + (e >> 2) * 4 * TK_THREADS + 4 * tid + (e & 3);
+            xv[e] = pos < n ? row[pos] : __builtin_nanf("");  // NaN: never passes the filter
+        }
+    }
+    // lane maximum: v_max_f32 returns the non-NaN operand, and a NaN result
+    // maps to the -inf key, so the key is at most the lane's largest key
+    float lm = xv[0];
+#pragma unroll
+    for (int e = 1; e < TK_EPT; ++e) asm("v_max_f32 %0, %0, %1" : "+v"(lm) : "v"(xv[e]));
+    const uint32_t t = tk_lane_threshold(topk_key(lm), k, L);
+    // above the -inf key (0x007fffff), t (low 16 bits clear) is the key of a
+    // real float tf, and for a non-NaN x, key(x) >= t exactly when x >= tf
+    const bool valid = t > 0x007fffffu;
+    const float tf = valid ? topk_value(t) : INFINITY;
+    int c = 0;
+#pragma unroll
+    for (int e = 0; e < TK_EPT; ++e) c += xv[e] >= tf;
+    int nc;
+    int pos = block_scan(c, L.scan, nc);  // its barriers order wave 0's reads of the lane keys first
+    if (valid && nc <= TK_CAP) {
+        uint2* cand = reinterpret_cast<uint2*>(L.buf);
+#pragma unroll
+        for (int e = 0; e < TK_EPT; ++e)
+            if (xv[e] >= tf)
+                cand[pos++] = make_uint2(topk_key(xv[e]), (uint32_t)(base + (e >> 2) * 4 * TK_THREADS + 4 * tid + (e & 3)));
+        tk_emit<false>(cand, nc, k, nullptr, nullptr, ok, oi);
+    } else {
+        uint32_t key[TK_EPT];
+#pragma unroll
+        for (int e = 0; e < TK_EPT; ++e) {
+            const int64_t p = base + tid * TK_EPT + e;
+            key[e] = p < n ? topk_key(row[p]) : TK_ABSENT;
+        }
+        tk_select<false>(key, [&](int e) { return (uint32_t)(base + tid * TK_EPT + e); }, k, L, nullptr, nullptr,
+                         ok, oi);
+    }
+
+    // The last block of the row to arrive merges the pool.  Every pool
+    // access is an agent-scope (sc1) store or load, performed at the level
+    // where all XCDs' L2s are coherent, so no cache maintenance is needed: a
+    // thread's stores have reached that level when its s_waitcnt vmcnt(0)
+    // returns, which precedes the block barrier and the device-scope
+    // ticket, and the last block loads only after its ticket has returned.
+    // (Release / acquire fences write back and invalidate a whole L2 per
+    // block: 84.5 against 24.9 us for the two-launch form at 40 rows.)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0)
+        L.last = __hip_atomic_fetch_add(cnt + TK_CNT_STRIDE * m, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (uint32_t)(segs - 1);
+    __syncthreads();
+    if (!L.last) return;
+    tk_merge(pkey + m * pstride, pid + m * pstride, pstride, k, L, vals + m * k, idx + m * k);
+    if (tid == 0) __hip_atomic_store(cnt + TK_CNT_STRIDE * m, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
@@ -391,12 +572,19 @@ size_t topk_workspace_bytes(int64_t m, int64_t n, int k) {
     return 2 * one;
 }
 
+int64_t topk_counters(int64_t m) { return (m < TK_ROWS1 ? m : TK_ROWS1) * TK_CNT_STRIDE; }
+
 hipError_t launch_topk(const float* v, int64_t m, int64_t n, int k, float* vals, uint32_t* idx, void* ws,
-                       hipStream_t s) {
+                       uint32_t* cnt, int64_t ncnt, hipStream_t s) {
     if (k < 1 || k > 64 || m < 0) return hipErrorInvalidValue;
     if (m == 0) return hipSuccess;
-    for (int64_t r0 = 0; r0 < m; r0 += 65535) {
-        const int64_t rows = m - r0 < 65535 ? m - r0 : 65535;
+    const int64_t seg0 = (n + TK_SEG - 1) / TK_SEG;
+    // the one-launch form: counters for a launch of TK_ROWS1 rows (or all of them)
+    const int64_t rows1 = m < TK_ROWS1 ? m : TK_ROWS1;
+    const bool one = n > TK_SEG && seg0 * k <= TK_SEG && cnt && ncnt >= rows1 * TK_CNT_STRIDE;
+    const int64_t chunk = one ? TK_ROWS1 : 65535;
+    for (int64_t r0 = 0; r0 < m; r0 += chunk) {
+        const int64_t rows = m - r0 < chunk ? m - r0 : chunk;
         float* vr = vals + r0 * k;
         uint32_t* ir = idx + r0 * k;
         if (n <= TK_SEG) {
@@ -405,26 +593,31 @@ hipError_t launch_topk(const float* v, int64_t m, int64_t n, int k, float* vals,
                                (uint32_t*)nullptr, (uint32_t*)nullptr, (int64_t)0, vr, ir);
             continue;
         }
-        const int64_t seg0 = (n + TK_SEG - 1) / TK_SEG;
-        const size_t one = ((size_t)m * (size_t)seg0 * (size_t)k * 8 + 255) & ~(size_t)255;
-        uint32_t* buf[2] = {static_cast<uint32_t*>(ws), reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + one)};
-        // each buffer: keys [rows][cnt] then ids [rows][cnt]
-        int64_t cnt = seg0 * k;
+        const size_t half = ((size_t)m * (size_t)seg0 * (size_t)k * 8 + 255) & ~(size_t)255;
+        uint32_t* buf[2] = {static_cast<uint32_t*>(ws), reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + half)};
+        if (one) {
+            // one launch: the pool [rows][seg0 * k] keys then ids in buf[0]
+            hipLaunchKernelGGL(k_topk_rows, dim3((unsigned)seg0, (unsigned)rows), dim3(TK_THREADS), 0, s, v + r0 * n,
+                               n, k, buf[0], buf[0] + rows * seg0 * k, cnt, vr, ir);
+            continue;
+        }
+        // each buffer: keys [rows][count] then ids [rows][count]
+        int64_t count = seg0 * k;
         hipLaunchKernelGGL((k_topk_select<true, false>), dim3((unsigned)seg0, (unsigned)rows), dim3(TK_THREADS), 0, s,
                            v + r0 * n, n, (const uint32_t*)nullptr, (const uint32_t*)nullptr, (int64_t)0, k, buf[0],
-                           buf[0] + rows * cnt, cnt, (float*)nullptr, (uint32_t*)nullptr);
+                           buf[0] + rows * count, count, (float*)nullptr, (uint32_t*)nullptr);
         int cur = 0;
-        while (cnt > TK_SEG) {
-            const int64_t segs = (cnt + TK_SEG - 1) / TK_SEG;
+        while (count > TK_SEG) {
+            const int64_t segs = (count + TK_SEG - 1) / TK_SEG;
             const int64_t nc = segs * k;
             hipLaunchKernelGGL((k_topk_select<false, false>), dim3((unsigned)segs, (unsigned)rows), dim3(TK_THREADS),
-                               0, s, (const float*)nullptr, (int64_t)0, buf[cur], buf[cur] + rows * cnt, cnt, k,
+                               0, s, (const float*)nullptr, (int64_t)0, buf[cur], buf[cur] + rows * count, count, k,
                                buf[cur ^ 1], buf[cur ^ 1] + rows * nc, nc, (float*)nullptr, (uint32_t*)nullptr);
             cur ^= 1;
-            cnt = nc;
+            count = nc;
         }
         hipLaunchKernelGGL((k_topk_select<false, true>), dim3(1, (unsigned)rows), dim3(TK_THREADS), 0, s,
-                           (const float*)nullptr, (int64_t)0, buf[cur], buf[cur] + rows * cnt, cnt, k,
+                           (const float*)nullptr, (int64_t)0, buf[cur], buf[cur] + rows * count, count, k,
                            (uint32_t*)nullptr, (uint32_t*)nullptr, (int64_t)0, vr, ir);
     }
     return hipGetLastError();

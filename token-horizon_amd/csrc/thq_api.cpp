@@ -279,6 +279,18 @@ bool env_flag_off(const char* name) {
 // (partials summed by a separate k_split_reduce launch, bit for bit the same)
 bool tickets_on() { return !env_flag_off("THQ_TILE_TICKET"); }
 
+// Arrival counters for the one-launch top-k (32 per row of a launch of at
+// most 2048 rows), or null with THQ_TILE_TICKET=0 or when they cannot be
+// allocated (the two-launch form then runs; same results).
+uint32_t* topk_counters(thq_ctx* ctx, int64_t m, int64_t* n) {
+    *n = 0;
+    if (!tickets_on()) return nullptr;
+    const int64_t want = thq::topk_counters(m);
+    uint32_t* p = tile_counters(ctx, want);
+    if (p) *n = want;
+    return p;
+}
+
 int check_call(const Call& c) {
     if (!c.ctx || !c.w) return fail(THQ_EINVAL, "null context or weight");
     if (c.xt != THQ_ACT_F32 && c.xt != THQ_ACT_BF16) return fail(THQ_EINVAL, "bad x_type %d", c.xt);
@@ -1296,7 +1308,10 @@ int thq_topk(thq_ctx* ctx, const float* v_dev, int64_t m, int64_t n, int k, floa
     std::lock_guard<std::mutex> lk(ctx->mu);
     int rc = ensure_ws(ctx, thq::topk_workspace_bytes(m, n, k));
     if (rc) return rc;
-    hipError_t e = thq::launch_topk(v_dev, m, n, k, vals_dev, idx_dev, ctx->ws, static_cast<hipStream_t>(stream));
+    int64_t ncnt = 0;
+    uint32_t* cnt = topk_counters(ctx, m, &ncnt);
+    hipError_t e =
+        thq::launch_topk(v_dev, m, n, k, vals_dev, idx_dev, ctx->ws, cnt, ncnt, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return fail(THQ_EHIP, "topk: %s", hipGetErrorString(e));
     return THQ_OK;
 }
@@ -1326,7 +1341,9 @@ int thq_matmul_topk(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_ac
     c.y = logits;
     rc = exec_route(c, r, scratch);
     if (rc) return rc;
-    hipError_t e = thq::launch_topk(logits, m, w->N, k, vals_dev, idx_dev, scratch, s);
+    int64_t ncnt = 0;
+    uint32_t* cnt = topk_counters(ctx, m, &ncnt);
+    hipError_t e = thq::launch_topk(logits, m, w->N, k, vals_dev, idx_dev, scratch, cnt, ncnt, s);
     if (e != hipSuccess) return fail(THQ_EHIP, "topk: %s", hipGetErrorString(e));
     return THQ_OK;
 }
