@@ -127,6 +127,21 @@ def test_topk_many_rows(path):
     check(v, 4, "70000 rows")
 
 
+@pytest.mark.parametrize("k", [1, 32, 64])
+def test_topk_wide_rows_many(path, k):
+    """30 rows of 151936: past 1024 blocks of 4096 logits, so the one-launch
+    form takes 8192-logit segments; smooth, bf16-tied, integer-tied and
+    NaN-heavy rows."""
+    rng = np.random.default_rng(k)
+    v = rng.normal(0, 3, (30, 151936)).astype(np.float32)
+    v[1::4] = O.bf16_round(v[1::4])
+    v[2::4] = np.round(v[2::4])
+    v[3, :100000] = np.nan
+    v[7, 5:] = -np.inf
+    print(f"topk 30 x 151936 k={k} {path}", flush=True)
+    check(v, k, f"30 wide rows k={k}")
+
+
 def test_topk_rows_beyond_one_launch(path):
     """More rows than the one-launch form takes per launch (2048), each row
     several segments long, with ties: every launch's counters and pool."""

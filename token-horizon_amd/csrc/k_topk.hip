@@ -52,6 +52,19 @@ constexpr int TK_CAP = 256;  // candidates the fast path ranks
 // adjacent counters: 7.6 us more), and launches take at most TK_ROWS1 rows
 constexpr int TK_CNT_STRIDE = 32;
 constexpr int TK_ROWS1 = 2048;
+// The one-launch form takes 16 logits per thread (4096-logit segments) up
+// to this many blocks per launch, else 32 (8192-logit segments: half the
+// blocks, pool stores and merge input; 151936-wide rows, k = 32: 5 rows
+// 9.0 against 10.0 us, 40 rows 13.3 against 11.0 us)
+#ifndef TK_RE16_BLOCKS
+#define TK_RE16_BLOCKS 1024
+#endif
+// pool entries per segment in the one-launch form: room for the filter's
+// candidates as they are (about k + 8 for smooth logits), 16-aligned, and
+// for the exact fallback's k per 4096-logit part
+__host__ __device__ constexpr int tk_pslot(int k, int re) {
+    return ((k + 31) & ~15) > re / TK_EPT * k ? ((k + 31) & ~15) : re / TK_EPT * k;
+}
 
 __device__ __forceinline__ uint32_t topk_key(float v) {
     uint32_t b = __float_as_uint(v);
@@ -102,7 +115,7 @@ struct TkLds {
 // order, padded with absent entries, as device-scope stores (a block of the
 // same launch may read them).  Every thread of the block calls it.
 template <bool FINAL>
-__device__ void tk_emit(uint2* cand, int nc, int k, float* vr, uint32_t* xr, uint32_t* ok, uint32_t* oi) {
+__device__ __forceinline__ void tk_emit(uint2* cand, int nc, int k, float* vr, uint32_t* xr, uint32_t* ok, uint32_t* oi) {
     const int tid = threadIdx.x;
     uint2* sel = cand + TK_CAP;  // [64] selected, by rank
     // pad to a multiple of 8 with entries that beat nothing
@@ -166,13 +179,16 @@ __device__ void tk_emit(uint2* cand, int nc, int k, float* vr, uint32_t* xr, uin
     }
 }
 
-// The top k of one segment held as key[TK_EPT] per thread, thread order =
-// id order (element e of thread t: id(e)); emits as tk_emit.  Every thread
-// of the block calls it; L.buf may hold staged logits that the threads have
-// already read into key.
-template <bool FINAL, typename IdF>
-__device__ void tk_select(const uint32_t (&key)[TK_EPT], IdF id, int k, TkLds& L, float* vr, uint32_t* xr,
+// The top k of one segment held as key[TK_EPT] per thread (element e of
+// thread t: id(e)); emits as tk_emit.  ORDERED: thread order = id order.
+// Else (FINAL only) the ids may sit in any order, and the fallback takes
+// the lowest ids among the keys equal to the k-th largest by a radix select
+// over the ids.  Every thread of the block calls it; L.buf may hold staged
+// logits that the threads have already read into key.
+template <bool FINAL, bool ORDERED = true, typename IdF>
+__device__ __forceinline__ void tk_select(const uint32_t (&key)[TK_EPT], IdF id, int k, TkLds& L, float* vr, uint32_t* xr,
                           uint32_t* ok, uint32_t* oi) {
+    static_assert(ORDERED || FINAL, "unordered candidates only for the final selection");
     const int tid = threadIdx.x;
     // ---- fast path: threshold from the waves' lane maxima
     {
@@ -272,25 +288,75 @@ __device__ void tk_select(const uint32_t (&key)[TK_EPT], IdF id, int k, TkLds& L
 
     // select: every key above tau, and the `need` lowest ids among keys equal
     // to tau (P <= k: every present element)
-    int eq = 0;
-    if (P > k) {
-#pragma unroll
-        for (int e = 0; e < TK_EPT; ++e) eq += key[e] == tau;
-    }
-    int eq_total;
-    int eq_rank = block_scan(eq, L.scan, eq_total);
     bool sel[TK_EPT];
     int nsel = 0;
-#pragma unroll
-    for (int e = 0; e < TK_EPT; ++e) {
+    if constexpr (ORDERED) {
+        int eq = 0;
         if (P > k) {
-            const bool is_eq = key[e] == tau;
-            sel[e] = key[e] > tau || (is_eq && eq_rank < need);
-            eq_rank += is_eq;
-        } else {
-            sel[e] = key[e] != TK_ABSENT;
+#pragma unroll
+            for (int e = 0; e < TK_EPT; ++e) eq += key[e] == tau;
         }
-        nsel += sel[e];
+        int eq_total;
+        int eq_rank = block_scan(eq, L.scan, eq_total);
+#pragma unroll
+        for (int e = 0; e < TK_EPT; ++e) {
+            if (P > k) {
+                const bool is_eq = key[e] == tau;
+                sel[e] = key[e] > tau || (is_eq && eq_rank < need);
+                eq_rank += is_eq;
+            } else {
+                sel[e] = key[e] != TK_ABSENT;
+            }
+            nsel += sel[e];
+        }
+    } else {
+        // id_cut = the need-th smallest id among the keys equal to tau (ids
+        // are distinct): a radix select from the bottom, 12 + 10 + 10 bits
+        uint32_t id_cut = 0u;
+        if (P > k) {
+            uint32_t prefix = 0u, pmask = 0u;
+            int kk = need;
+#pragma unroll
+            for (int pass = 0; pass < 3; ++pass) {
+                const int width = pass == 0 ? 12 : 10;
+                const int shift = pass == 0 ? 20 : (pass == 1 ? 10 : 0);
+                const int nb = 1 << width, per = nb / TK_THREADS;
+                for (int i = tid; i < nb; i += TK_THREADS) hist[i] = 0u;
+                __syncthreads();
+#pragma unroll
+                for (int e = 0; e < TK_EPT; ++e)
+                    if (key[e] == tau && (id(e) & pmask) == prefix)
+                        atomicAdd(&hist[(id(e) >> shift) & (uint32_t)(nb - 1)], 1u);
+                __syncthreads();
+                // thread t owns bins per*t .. per*(t+1)-1 (from the bottom)
+                int cnt = 0;
+                for (int j = 0; j < per; ++j) cnt += (int)hist[per * tid + j];
+                int tot;
+                int ex = block_scan(cnt, L.scan, tot);
+                if (ex < kk && kk <= ex + cnt) {
+                    for (int j = 0; j < per; ++j) {
+                        const int b = per * tid + j;
+                        const int c = (int)hist[b];
+                        if (ex + c >= kk) {
+                            L.prefix = prefix | ((uint32_t)b << shift);
+                            L.kk = kk - ex;
+                            break;
+                        }
+                        ex += c;
+                    }
+                }
+                __syncthreads();
+                prefix = L.prefix;
+                kk = L.kk;
+                pmask |= (uint32_t)(nb - 1) << shift;
+            }
+            id_cut = prefix;
+        }
+#pragma unroll
+        for (int e = 0; e < TK_EPT; ++e) {
+            sel[e] = P > k ? key[e] > tau || (key[e] == tau && id(e) <= id_cut) : key[e] != TK_ABSENT;
+            nsel += sel[e];
+        }
     }
     int total;
     int pos = block_scan(nsel, L.scan, total);  // total == min(P, k)
@@ -431,16 +497,23 @@ __device__ __forceinline__ uint32_t tk_lane_threshold(uint32_t lane_key, int k, 
     return L.thr;
 }
 
-// The exact top k of a row's pool (count <= TK_SEG entries, id order) into
-// vr / xr [k], rank order.  The filter of level 0 on keys: T = the k-th
+// The exact top k of a row's pool (count <= TK_SEG entries (key, id) in any
+// order, absent entries key 0) into vr / xr [k], rank order.  The filter of level 0 on keys: T = the k-th
 // largest lane maximum (16 key bits), the candidates are the keys >= T;
 // real keys are at least the -inf key (0x007fffff), so T > 0 means at least
 // k real entries pass.  Otherwise, or past TK_CAP candidates, tk_select.
-__device__ void tk_merge(const uint32_t* kr, const uint32_t* ir, int64_t count, int k, TkLds& L, float* vr,
+__device__ __forceinline__ void tk_merge(const uint32_t* kr, const uint32_t* ir, int64_t count, int k, TkLds& L, float* vr,
                          uint32_t* xr) {
     const int tid = threadIdx.x;
+    // entry tid + 256 e: every load covers 1 KB contiguous (the order is free)
     uint32_t key[TK_EPT], idv[TK_EPT];
-    tk_load_candidates(kr, ir, 0, count, key, idv);
+#pragma unroll
+    for (int e = 0; e < TK_EPT; ++e) {
+        const int64_t pos = (int64_t)e * TK_THREADS + tid;
+        const bool ok = pos < count;
+        key[e] = ok ? __hip_atomic_load(kr + pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : TK_ABSENT;
+        idv[e] = ok ? __hip_atomic_load(ir + pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0xFFFFFFFFu;
+    }
     uint32_t lm = key[0];
 #pragma unroll
     for (int e = 1; e < TK_EPT; ++e) lm = key[e] > lm ? key[e] : lm;
@@ -457,46 +530,59 @@ __device__ void tk_merge(const uint32_t* kr, const uint32_t* ir, int64_t count, 
             if (key[e] >= t) cand[pos++] = make_uint2(key[e], idv[e]);
         tk_emit<true>(cand, nc, k, vr, xr, nullptr, nullptr);
     } else {
-        tk_select<true>(key, [&](int e) { return idv[e]; }, k, L, vr, xr, nullptr, nullptr);
+        tk_select<true, false>(key, [&](int e) { return idv[e]; }, k, L, vr, xr, nullptr, nullptr);
     }
 }
 
-// Rows whose segments' candidates fit one block (segments * k <= TK_SEG) in
-// one launch.  Grid (segments >= 2, rows).  Each block selects its
-// segment's top k into the pool (okey / oid [m][segments * k], in id order,
+// Rows whose segments' candidates fit one block (segments * pslot <= TK_SEG)
+// in one launch.  Grid (segments >= 2, rows); a segment is 256 * RE logits
+// (RE elements per thread).  Each block writes a set of at most pslot
+// elements that holds its segment's top k into its slot of the pool (okey /
+// oid [m][segments * pslot], any order, absent entries after them;
 // device-scope stores) and draws a ticket on the row's arrival counter
 // cnt[TK_CNT_STRIDE m] (zero before the launch); the block that draws the
 // last ticket selects the row's top k from the pool (tk_merge) into vals /
 // idx and zeroes the counter.
 //
 // A segment's selection first tries a filter: thread t holds the elements
-// at offsets 1024 j + 4t + c (j, c < 4: four 16-B loads, no staging), the
-// block's threshold T is the k-th largest of its 256 lane maxima, rounded
-// down to 16 key bits (one wave, by ballots), and the candidates are the
-// elements >= T in float order.  T is a lane maximum, so at least k elements
-// pass and the segment's top k are among them; ranking those (at most
-// TK_CAP) exactly gives the segment's top k.  Where no such T exists (fewer
-// than k lanes hold a value above -inf) or more than TK_CAP elements pass
-// (long runs of equal logits), the segment takes tk_select over its keys in
-// id order instead (its own fast path, else the radix select).
-// (80 VGPRs: six blocks per CU, so 40 rows of 38 segments run in one round)
-__global__ __launch_bounds__(TK_THREADS, 6) void k_topk_rows(const float* __restrict__ logits, int64_t n, int k,
-                                                         uint32_t* __restrict__ pkey, uint32_t* __restrict__ pid,
-                                                         uint32_t* __restrict__ cnt, float* __restrict__ vals,
-                                                         uint32_t* __restrict__ idx) {
+// at offsets 1024 j + 4t + c (j < RE / 4, c < 4: 16-B loads, no staging),
+// the block's threshold T is the k-th largest of its 256 lane maxima,
+// rounded down to 16 key bits (one wave, by ballots), and the candidates are
+// the elements >= T in float order.  T is a lane maximum, so at least k
+// elements pass and the segment's top k are among them: up to pslot of them
+// go to the pool as they are; up to TK_CAP are ranked exactly and the top k
+// go.  Where no such T exists (fewer than k lanes hold a value above -inf)
+// or more than TK_CAP elements pass (long runs of equal logits), each
+// 4096-logit part of the segment takes tk_select over its keys in id order
+// (its own fast path, else the radix select), into slot entries [h k, h k +
+// k) (pslot >= RE / 16 * k).  No scratch: the selection helpers are inlined
+// (called, their register arrays went to the stack) and the bounds leave
+// RE = 16 94 VGPRs (five blocks per CU, its 1024 blocks in one round), RE =
+// 32 135 (three).
+template <int RE>
+__global__ __launch_bounds__(TK_THREADS, RE == 16 ? 4 : 3) void k_topk_rows(const float* __restrict__ logits,
+                                                                          int64_t n, int k, int pslot,
+                                                                          uint32_t* __restrict__ pkey,
+                                                                          uint32_t* __restrict__ pid,
+                                                                          uint32_t* __restrict__ cnt,
+                                                                          float* __restrict__ vals,
+                                                                          uint32_t* __restrict__ idx) {
+    static_assert(RE % 16 == 0 && RE <= 32, "RE: 16 or 32");
+    constexpr int SEG = TK_THREADS * RE;
     __shared__ TkLds L;
     const int tid = threadIdx.x;
     const int64_t m = blockIdx.y, seg = blockIdx.x, segs = gridDim.x;
-    const int64_t base = seg * TK_SEG;
-    const int64_t pstride = segs * k;
+    const int64_t base = seg * SEG;
+    const int64_t pstride = segs * pslot;
     const float* row = logits + m * n;
-    uint32_t* const ok = pkey + m * pstride + seg * k;
-    uint32_t* const oi = pid + m * pstride + seg * k;
+    uint32_t* const ok = pkey + m * pstride + seg * pslot;
+    uint32_t* const oi = pid + m * pstride + seg * pslot;
+    auto at = [&](int e) { return base + (e >> 2) * 4 * TK_THREADS + 4 * tid + (e & 3); };
 
-    float xv[TK_EPT];  // element 4j + c: offset 1024 j + 4 tid + c
-    if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && base + TK_SEG <= n) {
+    float xv[RE];  // element 4j + c: offset 1024 j + 4 tid + c
+    if ((n & 3) == 0 && (reinterpret_cast<uintptr_t>(logits) & 15) == 0 && base + SEG <= n) {
 #pragma unroll
-        for (int j = 0; j < TK_EPT / 4; ++j) {
+        for (int j = 0; j < RE / 4; ++j) {
             const float4 v = *reinterpret_cast<const float4*>(row + base + j * 4 * TK_THREADS + 4 * tid);
             xv[4 * j] = v.x;
             xv[4 * j + 1] = v.y;
@@ -505,8 +591,8 @@ __global__ __launch_bounds__(TK_THREADS, 6) void k_topk_rows(const float* __rest
         }
     } else {
 #pragma unroll
-        for (int e = 0; e < TK_EPT; ++e) {
-            const int64_t pos = base + (e >> 2) * 4 * TK_THREADS + 4 * tid + (e & 3);
+        for (int e = 0; e < RE; ++e) {
+            const int64_t pos = at(e);
             xv[e] = pos < n ? row[pos] : __builtin_nanf("");  // NaN: never passes the filter
         }
     }
@@ -514,7 +600,7 @@ __global__ __launch_bounds__(TK_THREADS, 6) void k_topk_rows(const float* __rest
     // maps to the -inf key, so the key is at most the lane's largest key
     float lm = xv[0];
 #pragma unroll
-    for (int e = 1; e < TK_EPT; ++e) asm("v_max_f32 %0, %0, %1" : "+v"(lm) : "v"(xv[e]));
+    for (int e = 1; e < RE; ++e) asm("v_max_f32 %0, %0, %1" : "+v"(lm) : "v"(xv[e]));
     const uint32_t t = tk_lane_threshold(topk_key(lm), k, L);
     // above the -inf key (0x007fffff), t (low 16 bits clear) is the key of a
     // real float tf, and for a non-NaN x, key(x) >= t exactly when x >= tf
@@ -522,25 +608,46 @@ __global__ __launch_bounds__(TK_THREADS, 6) void k_topk_rows(const float* __rest
     const float tf = valid ? topk_value(t) : INFINITY;
     int c = 0;
 #pragma unroll
-    for (int e = 0; e < TK_EPT; ++e) c += xv[e] >= tf;
+    for (int e = 0; e < RE; ++e) c += xv[e] >= tf;
     int nc;
     int pos = block_scan(c, L.scan, nc);  // its barriers order wave 0's reads of the lane keys first
+    int filled = k;                       // pool entries written below (the rest: absent)
     if (valid && nc <= TK_CAP) {
         uint2* cand = reinterpret_cast<uint2*>(L.buf);
 #pragma unroll
-        for (int e = 0; e < TK_EPT; ++e)
-            if (xv[e] >= tf)
-                cand[pos++] = make_uint2(topk_key(xv[e]), (uint32_t)(base + (e >> 2) * 4 * TK_THREADS + 4 * tid + (e & 3)));
-        tk_emit<false>(cand, nc, k, nullptr, nullptr, ok, oi);
-    } else {
-        uint32_t key[TK_EPT];
-#pragma unroll
-        for (int e = 0; e < TK_EPT; ++e) {
-            const int64_t p = base + tid * TK_EPT + e;
-            key[e] = p < n ? topk_key(row[p]) : TK_ABSENT;
+        for (int e = 0; e < RE; ++e)
+            if (xv[e] >= tf) cand[pos++] = make_uint2(topk_key(xv[e]), (uint32_t)at(e));
+        if (nc <= pslot) {
+            // as they are: the slot in coalesced stores, absent after them
+            __syncthreads();
+            if (tid < pslot) {
+                const uint2 cv = tid < nc ? cand[tid] : make_uint2(TK_ABSENT, 0xFFFFFFFFu);
+                __hip_atomic_store(ok + tid, cv.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(oi + tid, cv.y, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+            filled = pslot;
+        } else {
+            tk_emit<false>(cand, nc, k, nullptr, nullptr, ok, oi);
         }
-        tk_select<false>(key, [&](int e) { return (uint32_t)(base + tid * TK_EPT + e); }, k, L, nullptr, nullptr,
-                         ok, oi);
+    } else {
+#pragma unroll 1
+        for (int h = 0; h < RE / TK_EPT; ++h) {
+            const int64_t hb = base + (int64_t)h * TK_SEG;
+            uint32_t key[TK_EPT];
+#pragma unroll
+            for (int e = 0; e < TK_EPT; ++e) {
+                const int64_t p = hb + tid * TK_EPT + e;
+                key[e] = p < n ? topk_key(row[p]) : TK_ABSENT;
+            }
+            if (h > 0) __syncthreads();  // the previous part is done with L
+            tk_select<false>(key, [&](int e) { return (uint32_t)(hb + tid * TK_EPT + e); }, k, L, nullptr, nullptr,
+                             ok + h * k, oi + h * k);
+        }
+        filled = RE / TK_EPT * k;
+    }
+    if (tid >= filled && tid < pslot) {
+        __hip_atomic_store(ok + tid, TK_ABSENT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(oi + tid, 0xFFFFFFFFu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
     // The last block of the row to arrive merges the pool.  Every pool
@@ -567,9 +674,15 @@ __global__ __launch_bounds__(TK_THREADS, 6) void k_topk_rows(const float* __rest
 size_t topk_workspace_bytes(int64_t m, int64_t n, int k) {
     const int64_t seg0 = (n + TK_SEG - 1) / TK_SEG;
     if (seg0 <= 1) return 0;
-    // two candidate buffers of [m][seg0 * k] (key, id) pairs, 256-B aligned
+    // two candidate buffers of [m][seg0 * k] (key, id) pairs, 256-B aligned;
+    // the one-launch form's pool [m][seg0 * TK_PSLOT] in their place
     const size_t one = ((size_t)m * (size_t)seg0 * (size_t)k * 8 + 255) & ~(size_t)255;
-    return 2 * one;
+    // the one-launch form's pool [m][segments * pslot], the larger of its two shapes
+    const int64_t s32 = (n + 2 * TK_SEG - 1) / (2 * TK_SEG);
+    const int64_t e16 = seg0 * tk_pslot(k, 16) <= TK_SEG ? seg0 * tk_pslot(k, 16) : 0;
+    const int64_t e32 = s32 * tk_pslot(k, 32) <= TK_SEG ? s32 * tk_pslot(k, 32) : 0;
+    const size_t pool = (size_t)m * (size_t)(e16 > e32 ? e16 : e32) * 8;
+    return 2 * one > pool ? 2 * one : pool;
 }
 
 int64_t topk_counters(int64_t m) { return (m < TK_ROWS1 ? m : TK_ROWS1) * TK_CNT_STRIDE; }
@@ -581,7 +694,9 @@ hipError_t launch_topk(const float* v, int64_t m, int64_t n, int k, float* vals,
     const int64_t seg0 = (n + TK_SEG - 1) / TK_SEG;
     // the one-launch form: counters for a launch of TK_ROWS1 rows (or all of them)
     const int64_t rows1 = m < TK_ROWS1 ? m : TK_ROWS1;
-    const bool one = n > TK_SEG && seg0 * k <= TK_SEG && cnt && ncnt >= rows1 * TK_CNT_STRIDE;
+    const int64_t s32 = (n + 2 * TK_SEG - 1) / (2 * TK_SEG);
+    const bool fit16 = seg0 * tk_pslot(k, 16) <= TK_SEG, fit32 = s32 * tk_pslot(k, 32) <= TK_SEG;
+    const bool one = n > TK_SEG && (fit16 || fit32) && cnt && ncnt >= rows1 * TK_CNT_STRIDE;
     const int64_t chunk = one ? TK_ROWS1 : 65535;
     for (int64_t r0 = 0; r0 < m; r0 += chunk) {
         const int64_t rows = m - r0 < chunk ? m - r0 : chunk;
@@ -596,9 +711,17 @@ hipError_t launch_topk(const float* v, int64_t m, int64_t n, int k, float* vals,
         const size_t half = ((size_t)m * (size_t)seg0 * (size_t)k * 8 + 255) & ~(size_t)255;
         uint32_t* buf[2] = {static_cast<uint32_t*>(ws), reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + half)};
         if (one) {
-            // one launch: the pool [rows][seg0 * k] keys then ids in buf[0]
-            hipLaunchKernelGGL(k_topk_rows, dim3((unsigned)seg0, (unsigned)rows), dim3(TK_THREADS), 0, s, v + r0 * n,
-                               n, k, buf[0], buf[0] + rows * seg0 * k, cnt, vr, ir);
+            // one launch: the pool [rows][segments * pslot] keys then ids at ws
+            uint32_t* pool = static_cast<uint32_t*>(ws);
+            if (fit16 && (!fit32 || rows * seg0 <= TK_RE16_BLOCKS)) {
+                const int pslot = tk_pslot(k, 16);
+                hipLaunchKernelGGL((k_topk_rows<16>), dim3((unsigned)seg0, (unsigned)rows), dim3(TK_THREADS), 0, s,
+                                   v + r0 * n, n, k, pslot, pool, pool + rows * seg0 * pslot, cnt, vr, ir);
+            } else {
+                const int pslot = tk_pslot(k, 32);
+                hipLaunchKernelGGL((k_topk_rows<32>), dim3((unsigned)s32, (unsigned)rows), dim3(TK_THREADS), 0, s,
+                                   v + r0 * n, n, k, pslot, pool, pool + rows * s32 * pslot, cnt, vr, ir);
+            }
             continue;
         }
         // each buffer: keys [rows][count] then ids [rows][count]

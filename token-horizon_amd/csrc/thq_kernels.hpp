@@ -225,8 +225,8 @@ hipError_t launch_argmax_partials(const float* v, const uint32_t* i, int64_t m, 
 
 // exact per-row top-k (k <= 64) by (logit desc, id asc), k_topk.hip.  cnt:
 // ncnt zeroed arrival counters (left zero), or null; with at least
-// topk_counters(m) of them, rows of up to 4096 / k segments of 4096 logits
-// take one launch per 2048 rows
+// topk_counters(m) of them, rows of up to 64 segments of 4096 logits take
+// one launch per 2048 rows
 size_t topk_workspace_bytes(int64_t m, int64_t n, int k);
 int64_t topk_counters(int64_t m);
 hipError_t launch_topk(const float* v, int64_t m, int64_t n, int k, float* vals, uint32_t* idx, void* ws,
