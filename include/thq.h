@@ -297,7 +297,7 @@ size_t thq_noalloc_scratch_bytes(void);
  * work.  thq_reserve grows the context workspace to at least
  * workspace_bytes and the context's zeroed split-K arrival counters to at
  * least `counters` entries (one per 32-row output tile of the widest
- * weight), synchronously (hipMalloc, hipMemset, device synchronize); calls
+ * weight, and 32 per row of a top-k call, at most 65536), synchronously (hipMalloc, hipMemset, device synchronize); calls
  * whose needs fit then allocate nothing.  thq_workspace_bytes returns the
  * current workspace size. */
 int thq_call_scratch_bytes(thq_ctx* ctx, const thq_weight* w, int64_t m, thq_act x_type, uint32_t flags,
@@ -340,7 +340,12 @@ int thq_matmul_argmax(thq_ctx* ctx, const thq_weight* w, const void* x_dev, thq_
  * ts_topk (engine/src/sample_kernel.rs:725-796, CPU form sorted_row_dist
  * :326-347) consuming the verify logits in place (engine/src/engine.rs:
  * 2424-2436); that kernel bounds its candidate pool, this one is exact for
- * any row. */
+ * any row.  Rows of up to 64 segments of 4096 logits run in one launch per
+ * 2048 rows whose last block per row merges the segments' candidates; it
+ * needs 32 zeroed arrival counters per row of a launch (thq_reserve's
+ * `counters`; grown on demand, so a graph-captured call reserves them first).
+ * THQ_TILE_TICKET=0, longer rows or counters that cannot be allocated take a
+ * second launch per merge level instead: the same results. */
 int thq_topk(thq_ctx* ctx, const float* v_dev, int64_t m, int64_t n, int k, float* vals_dev, uint32_t* idx_dev,
              void* stream);
 

@@ -153,6 +153,32 @@ def test_topk_rows_beyond_one_launch(path):
         check(v, k, f"2100 rows k={k}")
 
 
+def test_topk_graph_replays():
+    """The one-launch form inside a captured HIP graph: its arrival counters
+    are left zero by the kernel itself, so every replay, with eager calls
+    and synchronizations between them, gives the eager result."""
+    rng = np.random.default_rng(12)
+    v = torch.from_numpy(rng.normal(0, 3, (40, 151936)).astype(np.float32)).cuda()
+    want_v, want_i = thq.topk(v, 32)  # eager; also reserves the counters before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            gv, gi = thq.topk(v, 32)
+    torch.cuda.current_stream().wait_stream(s)
+    for r in range(3):
+        gv.fill_(float("nan"))
+        gi.fill_(-1)
+        ev, ei = thq.topk(v[:5].contiguous(), 32)  # eager work between replays
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gi, want_i) and torch.equal(gv, want_v), r
+        assert torch.equal(ei, want_i[:5]), r
+
+
 def test_topk_rejects_bad_k():
     v = torch.zeros((2, 10), dtype=torch.float32, device="cuda")
     for k in (0, 65):
