@@ -122,9 +122,9 @@ __device__ __forceinline__ void tile_finish(float (&tot)[NT][4], float* red, YT*
             if (4 * g + e < M)
                 store_y<YT>(Y + (int64_t)(4 * g + e) * nout + row, GU ? silu_mul(tot[0][e], tot[NT - 1][e]) : tot[0][e]);
     } else {
-        // partials as device-scope stores when the last block sums them; a
-        // release fence orders them before the ticket (device-scope acq_rel)
-        // and the last block's acquire fence orders its loads after it
+        // partials as device-scope (sc1) stores when the last block sums them,
+        // published before the ticket (ticket_publish, thq_dev.hpp) and read
+        // back with device-scope loads after it
         const int64_t ldp = NT * nout;
         if (wave == 0 && row < nout) {
 #pragma unroll
@@ -142,12 +142,11 @@ __device__ __forceinline__ void tile_finish(float (&tot)[NT][4], float* red, YT*
         }
         if (!cnt) return;
         __shared__ int last;
-        ticket_release();
+        ticket_publish();
         __syncthreads();
         if (threadIdx.x == 0) last = ticket_draw(cnt + tile) == gridDim.y - 1;
         __syncthreads();
         if (!last) return;
-        ticket_acquire();
         // the tile's outputs, one per thread: the splits' partials in split
         // order (k_split_reduce's sums, bit for bit), loads batched 8 deep
         const int splits = (int)gridDim.y;

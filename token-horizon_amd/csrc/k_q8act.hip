@@ -423,18 +423,17 @@ __global__ __launch_bounds__(256) void k_q8act_q4k(const uint8_t* __restrict__ W
     for (int i = 0; i < NR * MT; ++i) acc[i] = p == 0 ? acc[i] : 0.0f;  // one lane per quad
     q8act_store<MT, GU, YT, EMIT>(acc, lane, y, o0, nout, m0, mrows, ldy);
     if constexpr (EMIT) {
-        // the outputs went out as device-scope stores; a release fence orders
-        // them before the ticket (device-scope acq_rel) and the last block's
-        // acquire fence orders its loads after it
+        // the outputs went out as device-scope (sc1) stores, published before
+        // the ticket (ticket_publish, thq_dev.hpp) and read back with
+        // device-scope loads after it
         __shared__ int last;
         const int64_t seg = blockIdx.x >> 4;  // 256-wide segment of the outputs
         uint32_t* c = cnt + (int64_t)blockIdx.y * (nout >> 8) + seg;
-        ticket_release();
+        ticket_publish();
         __syncthreads();
         if (threadIdx.x == 0) last = ticket_draw(c) == 15u;
         __syncthreads();
         if (last) {
-            ticket_acquire();
             const int wave = threadIdx.x >> 6;
             const int nsb = (int)(nout >> 8);
             for (int m = wave; m < mrows; m += 4) {

@@ -650,19 +650,12 @@ __global__ __launch_bounds__(TK_THREADS, RE == 16 ? 4 : 3) void k_topk_rows(cons
         __hip_atomic_store(oi + tid, 0xFFFFFFFFu, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
-    // The last block of the row to arrive merges the pool.  Every pool
-    // access is an agent-scope (sc1) store or load, performed at the level
-    // where all XCDs' L2s are coherent, so no cache maintenance is needed: a
-    // thread's stores have reached that level when its s_waitcnt vmcnt(0)
-    // returns, which precedes the block barrier and the device-scope
-    // ticket, and the last block loads only after its ticket has returned.
-    // (Release / acquire fences write back and invalidate a whole L2 per
-    // block: 84.5 against 24.9 us for the two-launch form at 40 rows.)
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // The last block of the row to arrive merges the pool: every pool access
+    // is an agent-scope (sc1) store or load, published before the ticket
+    // (ticket_publish, thq_dev.hpp)
+    ticket_publish();
     __syncthreads();
-    if (tid == 0)
-        L.last = __hip_atomic_fetch_add(cnt + TK_CNT_STRIDE * m, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                 (uint32_t)(segs - 1);
+    if (tid == 0) L.last = ticket_draw(cnt + TK_CNT_STRIDE * m) == (uint32_t)(segs - 1);
     __syncthreads();
     if (!L.last) return;
     tk_merge(pkey + m * pstride, pid + m * pstride, pstride, k, L, vals + m * k, idx + m * k);
