@@ -522,14 +522,21 @@ Route plan_route(const Call& c) {
         // 4096 x 12288 at M = 2048: 209 against 219 us) and, for weights with
         // fewer rows than columns (the down projection), of the dequantize-
         // then-GEMM route (4096 x 12288 at M = 4096: 369 against 388 us;
-        // 12288 x 4096 keeps that route: 180 against 219 us at M = 2048).  Its
+        // 12288 x 4096 keeps that route: 180 against 219 us at M = 2048); on
+        // weights of at least 12288 x 4096 elements also from 768 rows, and
+        // gate/up from 384 (12288 x 4096 / 4096 x 12288 at M = 768: 107.6 /
+        // 106.7 against 136.3 / 115.4 us; gate/up 2 x 12288 x 4096 at M = 384
+        // / 512: 128.4 / 130.4 against 146.5 / 151.3 us; at M = 512 the plain
+        // shapes keep the tile GEMM: 72.0 / 70.9 against 78.8 / 84.9).  Its
         // K splits meet in the last block of each tile, so only with arrival
         // counters.  THQ_GEMM_RQ: 0 never, 1 wherever supported (tests),
         // unset: that rule
         const char* rqe = getenv("THQ_GEMM_RQ");
         const int rq_mode = rqe && *rqe ? atoi(rqe) : -1;
-        const bool rq_default = m >= 1024 && (r.kind == Kind::GEMM ||
-                                              (r.kind == Kind::GEMM_DQ && dq_mode == -1 && w->N < w->K));
+        const bool rq_big = w->N * w->K >= (int64_t)12288 * 4096 && r.kind == Kind::GEMM &&
+                            (m >= 768 || (c.gu && m >= 384));
+        const bool rq_default = rq_big || (m >= 1024 && (r.kind == Kind::GEMM ||
+                                                         (r.kind == Kind::GEMM_DQ && dq_mode == -1 && w->N < w->K)));
         if (q4 && !r.exact && r.kind != Kind::GEMM_FQ && rq_mode != 0 && (rq_mode == 1 || rq_default) &&
             c.counters && tickets_on() &&
             thq::gemm_rq_supported(w->qtype == THQ_MLX_Q4 ? 13 : 12, m, w->N, w->K, c.gu)) {
@@ -549,11 +556,15 @@ Route plan_route(const Call& c) {
         // 96 / 128: 25.2 / 25.9 / 33.6 / 34.7 against 28.1 / 28.9 / 42.0 /
         // 37.2 us; gate/up 2 x 12288 x 4096 at M = 64 / 128: 38.8 / 51.1
         // against 46.2 / 56.9 us; 4096 x 12288 at M = 64: 26.3 against 28.8 us,
-        // at M = 128: 35.2 against 33.0 us).  THQ_GEMM_MID: 0 never, 1
-        // wherever supported (tests), unset: that rule
+        // at M = 128: 35.2 against 33.0 us), and up to 384 rows on square
+        // weights of at most 4096 rows, where the tile GEMM's few tiles leave
+        // CUs idle (4096 x 4096 at M = 160 / 256 / 384: 23.6 / 26.1 / 31.9
+        // against 27.5 / 31.0 / 34.6 us; at 512: 36.9 against 35.6).
+        // THQ_GEMM_MID: 0 never, 1 wherever supported (tests), unset: that rule
         const char* mde = getenv("THQ_GEMM_MID");
         const int mid_mode = mde && *mde ? atoi(mde) : -1;
-        const bool mid_default = m >= 17 && m <= (w->N >= w->K ? 128 : 64) && r.kind == Kind::GEMM;
+        const int mid_max = w->N >= w->K ? (w->N == w->K && w->N <= 4096 ? 384 : 128) : 64;
+        const bool mid_default = m >= 17 && m <= mid_max && r.kind == Kind::GEMM;
         if (q4 && !r.exact && mid_mode != 0 && (mid_mode == 1 || mid_default)) {
             const thq::MidPlan mp = thq::plan_gemm_mid(v.qtype, m, w->N, w->K, c.gu, c.ctx->cus);
             if (mp.mh > 0 && mp.workspace_bytes <= c.scratch_cap) {
