@@ -474,10 +474,17 @@ __global__ __launch_bounds__(TK_THREADS) void k_topk_select(const float* __restr
     }
 }
 
-// The block's 256 lane maxima (keys, one per thread) -> the k-th largest,
-// rounded down to 16 key bits, found by one wave with ballots: at least k of
-// the lane maxima are >= the result.  L.buf[0..255] holds the lane keys on
-// return; every thread of the block calls it.
+// The block's 256 lane maxima (keys, one per thread) -> a threshold t with
+// at least k of them >= t, found by one wave with ballots over 16 key bits:
+// the k-th largest lane maximum rounded down, or (QUAD) the k-th largest of
+// the 64 maxima of lane quads (lanes l, l + 64, l + 128, l + 192), one ballot
+// a step instead of four, a lower t that lets a few more candidates pass.
+// QUAD in the merge and for 8192-logit segments (151936-wide rows, k = 32:
+// 5 / 20 / 27 / 40 / 64 rows 8.9 / 9.4 / 9.9 / 10.8 / 16.1 against 9.0 / 9.8
+// / 10.7 / 11.3 / 17.3 us); not for 4096-logit segments, whose 48-entry
+// slots it overflows (10.2 against 9.0 us at 5 rows).  L.buf[0..255] holds
+// the lane keys on return; every thread of the block calls it.
+template <bool QUAD = false>
 __device__ __forceinline__ uint32_t tk_lane_threshold(uint32_t lane_key, int k, TkLds& L) {
     const int tid = threadIdx.x;
     L.buf[tid] = lane_key;
@@ -485,11 +492,21 @@ __device__ __forceinline__ uint32_t tk_lane_threshold(uint32_t lane_key, int k, 
     if (tid < 64) {
         const uint32_t a0 = L.buf[tid], a1 = L.buf[tid + 64], a2 = L.buf[tid + 128], a3 = L.buf[tid + 192];
         uint32_t t = 0u;
-        for (int b = 31; b >= 16; --b) {
-            const uint32_t c = t | (1u << b);
-            const int nge = __popcll(__ballot(a0 >= c)) + __popcll(__ballot(a1 >= c)) + __popcll(__ballot(a2 >= c)) +
-                            __popcll(__ballot(a3 >= c));
-            if (nge >= k) t = c;
+        if constexpr (QUAD) {
+            uint32_t q = a0 > a1 ? a0 : a1;
+            const uint32_t r = a2 > a3 ? a2 : a3;
+            q = q > r ? q : r;
+            for (int b = 31; b >= 16; --b) {
+                const uint32_t c = t | (1u << b);
+                if (__popcll(__ballot(q >= c)) >= k) t = c;
+            }
+        } else {
+            for (int b = 31; b >= 16; --b) {
+                const uint32_t c = t | (1u << b);
+                const int nge = __popcll(__ballot(a0 >= c)) + __popcll(__ballot(a1 >= c)) +
+                                __popcll(__ballot(a2 >= c)) + __popcll(__ballot(a3 >= c));
+                if (nge >= k) t = c;
+            }
         }
         if (tid == 0) L.thr = t;
     }
@@ -517,7 +534,7 @@ __device__ __forceinline__ void tk_merge(const uint32_t* kr, const uint32_t* ir,
     uint32_t lm = key[0];
 #pragma unroll
     for (int e = 1; e < TK_EPT; ++e) lm = key[e] > lm ? key[e] : lm;
-    const uint32_t t = tk_lane_threshold(lm, k, L);
+    const uint32_t t = tk_lane_threshold<true>(lm, k, L);
     int c = 0;
 #pragma unroll
     for (int e = 0; e < TK_EPT; ++e) c += key[e] >= t;
@@ -546,10 +563,9 @@ __device__ __forceinline__ void tk_merge(const uint32_t* kr, const uint32_t* ir,
 //
 // A segment's selection first tries a filter: thread t holds the elements
 // at offsets 1024 j + 4t + c (j < RE / 4, c < 4: 16-B loads, no staging),
-// the block's threshold T is the k-th largest of its 256 lane maxima,
-// rounded down to 16 key bits (one wave, by ballots), and the candidates are
-// the elements >= T in float order.  T is a lane maximum, so at least k
-// elements pass and the segment's top k are among them: up to pslot of them
+// the block's threshold T (tk_lane_threshold) has at least k lane maxima at
+// or above it, and the candidates are the elements >= T in float order:
+// at least k elements pass and the segment's top k are among them: up to pslot of them
 // go to the pool as they are; up to TK_CAP are ranked exactly and the top k
 // go.  Where no such T exists (fewer than k lanes hold a value above -inf)
 // or more than TK_CAP elements pass (long runs of equal logits), each
@@ -601,7 +617,7 @@ __global__ __launch_bounds__(TK_THREADS, RE == 16 ? 4 : 3) void k_topk_rows(cons
     float lm = xv[0];
 #pragma unroll
     for (int e = 1; e < RE; ++e) asm("v_max_f32 %0, %0, %1" : "+v"(lm) : "v"(xv[e]));
-    const uint32_t t = tk_lane_threshold(topk_key(lm), k, L);
+    const uint32_t t = tk_lane_threshold<RE == 32>(topk_key(lm), k, L);
     // above the -inf key (0x007fffff), t (low 16 bits clear) is the key of a
     // real float tf, and for a non-NaN x, key(x) >= t exactly when x >= tf
     const bool valid = t > 0x007fffffu;
