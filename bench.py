@@ -4,7 +4,8 @@ Headline metric: Q4_K decode GEMV HBM GB/s at M=1 and prefill GEMM TFLOP/s at
 M=2048, both on the Qwen3-8B-class gate/up projection (N=12288, K=4096).
 A "step" is one GEMV call (M=1, bf16 x, f32 y) on the next of 24 distinct
 weight copies (680 MB in rotation, so weights stream from HBM, not from the
-256 MB MALL).  --warmup untimed steps run first; then exactly --steps steps
+256 MB MALL), each read once after it is written (page_in).  --warmup
+untimed steps run first; then exactly --steps steps
 are launched on one stream behind a GPU spin that lasts longer than the host
 takes to launch all of them, so the GPU runs them back to back with no host
 gap, and HIP events on that stream bracket exactly those steps.  The bench
@@ -75,6 +76,21 @@ def log(msg: str):
 
 def q4k_bytes(n, k):
     return n * (k // 256) * Q4K_BYTES_PER_256
+
+
+def page_in(thq, torch, ws):
+    """One read pass over each weight copy (thq_dequantize_bf16 into one
+    scratch buffer), as a decode loop's weights have had before any step:
+    a GEMV's first pass over freshly written copies runs about 0.3 us per
+    step slower (first 20-step timing in fresh processes: 7.17-7.23 us
+    without, 6.88-6.98 us with; the 2400-step default run: 6.87-6.92).
+    Setup, not a call of the timed operation."""
+    n, k = ws[0].shape
+    tmp = torch.empty((n, k), dtype=torch.bfloat16, device="cuda")
+    for w in ws:
+        thq.check(thq.lib.thq_dequantize_bf16(w.ctx.h, w.h, thq._ptr(tmp), thq._stream()))
+    torch.cuda.synchronize()
+    del tmp
 
 
 def make_weights(thq, torch, n, k, copies, seed=0):
@@ -356,6 +372,7 @@ def main():
         sys.exit(2)
     log(f"quantizing {copies} copies of Q4_K {N}x{K} ({copies * q4k_bytes(N, K) / 1e6:.0f} MB)")
     ws = make_weights(thq, torch, N, K, copies)
+    page_in(thq, torch, ws)
     g = torch.Generator(device="cuda").manual_seed(1)
     x1 = torch.randn((1, K), generator=g, device="cuda").to(torch.bfloat16)
     y1 = torch.empty((1, N), dtype=torch.float32, device="cuda")
@@ -426,6 +443,7 @@ def main():
         "config": {"workload": "Q4_K decode GEMV M=1, N=12288, K=4096 (Qwen3-8B-class gate/up projection)",
                    "rotating_weight_copies": copies, "launch": ("queued behind a GPU spin that outlasts the host's launches" if launch == "queued"
                               else "hip-graph, uploaded before timing"),
+                   "page_in": "each copy read once (thq_dequantize_bf16) after it is written, before the warmup steps",
                    "algorithmic_bytes_per_call": gemv_bytes},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic.get("gemv"),
