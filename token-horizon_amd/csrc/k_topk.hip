@@ -515,12 +515,13 @@ __device__ __forceinline__ uint32_t tk_lane_threshold(uint32_t lane_key, int k, 
 }
 
 // The exact top k of a row's pool (count <= TK_SEG entries (key, id) in any
-// order, absent entries key 0) into vr / xr [k], rank order.  The filter of level 0 on keys: T = the k-th
-// largest lane maximum (16 key bits), the candidates are the keys >= T;
-// real keys are at least the -inf key (0x007fffff), so T > 0 means at least
-// k real entries pass.  Otherwise, or past TK_CAP candidates, tk_select.
-__device__ __forceinline__ void tk_merge(const uint32_t* kr, const uint32_t* ir, int64_t count, int k, TkLds& L, float* vr,
-                         uint32_t* xr) {
+// order, absent entries key 0) into vr / xr [k], rank order.  Level 0's
+// filter on keys: T from the lane maxima (tk_lane_threshold, over lane
+// quads), the candidates are the keys >= T; real keys are at least the -inf
+// key (0x007fffff), so T > 0 means at least k real entries pass.
+// Otherwise, or past TK_CAP candidates, tk_select (order-free ties).
+__device__ __forceinline__ void tk_merge(const uint32_t* kr, const uint32_t* ir, int64_t count, int k, TkLds& L,
+                                         float* vr, uint32_t* xr) {
     const int tid = threadIdx.x;
     // entry tid + 256 e: every load covers 1 KB contiguous (the order is free)
     uint32_t key[TK_EPT], idv[TK_EPT];
@@ -564,10 +565,10 @@ __device__ __forceinline__ void tk_merge(const uint32_t* kr, const uint32_t* ir,
 // A segment's selection first tries a filter: thread t holds the elements
 // at offsets 1024 j + 4t + c (j < RE / 4, c < 4: 16-B loads, no staging),
 // the block's threshold T (tk_lane_threshold) has at least k lane maxima at
-// or above it, and the candidates are the elements >= T in float order:
-// at least k elements pass and the segment's top k are among them: up to pslot of them
-// go to the pool as they are; up to TK_CAP are ranked exactly and the top k
-// go.  Where no such T exists (fewer than k lanes hold a value above -inf)
+// or above it, and the candidates are the elements >= T in float order: at
+// least k elements pass and the segment's top k are among them.  Up to pslot
+// of them go to the pool as they are; up to TK_CAP are ranked exactly and
+// the top k go.  Where no such T exists (fewer than k lanes hold a value above -inf)
 // or more than TK_CAP elements pass (long runs of equal logits), each
 // 4096-logit part of the segment takes tk_select over its keys in id order
 // (its own fast path, else the radix select), into slot entries [h k, h k +
