@@ -572,12 +572,14 @@ __device__ __forceinline__ void tk_merge(const uint32_t* kr, const uint32_t* ir,
 // or more than TK_CAP elements pass (long runs of equal logits), each
 // 4096-logit part of the segment takes tk_select over its keys in id order
 // (its own fast path, else the radix select), into slot entries [h k, h k +
-// k) (pslot >= RE / 16 * k).  No scratch: the selection helpers are inlined
-// (called, their register arrays went to the stack) and the bounds leave
-// RE = 16 94 VGPRs (five blocks per CU, its 1024 blocks in one round), RE =
-// 32 135 (three).
-template <int RE>
-__global__ __launch_bounds__(TK_THREADS, RE == 16 ? 4 : 3) void k_topk_rows(const float* __restrict__ logits,
+// k) (pslot >= RE / 16 * k).  The selection helpers are inlined (called,
+// their register arrays went to the stack).  MINB blocks per CU: RE = 16 at
+// 4 (94 VGPRs, five blocks per CU: its 1024 blocks in one round); RE = 32 at
+// 3 (135 VGPRs, no scratch) up to 768 blocks, at 4 (128 VGPRs, 20 B of
+// spills) past them (64 rows of 19 segments: 15.4 against 16.3 us; 40 rows:
+// 11.2 against 10.9).
+template <int RE, int MINB>
+__global__ __launch_bounds__(TK_THREADS, MINB) void k_topk_rows(const float* __restrict__ logits,
                                                                           int64_t n, int k, int pslot,
                                                                           uint32_t* __restrict__ pkey,
                                                                           uint32_t* __restrict__ pid,
@@ -725,12 +727,16 @@ hipError_t launch_topk(const float* v, int64_t m, int64_t n, int k, float* vals,
             uint32_t* pool = static_cast<uint32_t*>(ws);
             if (fit16 && (!fit32 || rows * seg0 <= TK_RE16_BLOCKS)) {
                 const int pslot = tk_pslot(k, 16);
-                hipLaunchKernelGGL((k_topk_rows<16>), dim3((unsigned)seg0, (unsigned)rows), dim3(TK_THREADS), 0, s,
+                hipLaunchKernelGGL((k_topk_rows<16, 4>), dim3((unsigned)seg0, (unsigned)rows), dim3(TK_THREADS), 0, s,
                                    v + r0 * n, n, k, pslot, pool, pool + rows * seg0 * pslot, cnt, vr, ir);
             } else {
                 const int pslot = tk_pslot(k, 32);
-                hipLaunchKernelGGL((k_topk_rows<32>), dim3((unsigned)s32, (unsigned)rows), dim3(TK_THREADS), 0, s,
-                                   v + r0 * n, n, k, pslot, pool, pool + rows * s32 * pslot, cnt, vr, ir);
+                if (rows * s32 <= 768)
+                    hipLaunchKernelGGL((k_topk_rows<32, 3>), dim3((unsigned)s32, (unsigned)rows), dim3(TK_THREADS), 0,
+                                       s, v + r0 * n, n, k, pslot, pool, pool + rows * s32 * pslot, cnt, vr, ir);
+                else
+                    hipLaunchKernelGGL((k_topk_rows<32, 4>), dim3((unsigned)s32, (unsigned)rows), dim3(TK_THREADS), 0,
+                                       s, v + r0 * n, n, k, pslot, pool, pool + rows * s32 * pslot, cnt, vr, ir);
             }
             continue;
         }
